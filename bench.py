@@ -1,0 +1,203 @@
+#!/usr/bin/env python3
+"""Benchmark of the Q4_K / Q6_K dequant-GEMV hot path on one MI355X.
+
+A step is one pass of the hot path over one batch of synthetic input: one
+Q6_K GEMV over the tied LM head, 128256 x 2048 (215.5 MB of super-blocks),
+batch 1, fp32 activations.  Four weight copies of that matrix (862 MB) rotate
+from step to step so that the ~256 MB last-level cache cannot serve them;
+all inputs are resident in HBM before timing starts.
+
+value = algorithmic bytes per step (weights + x + y) * steps / wall time of
+the timed region (barrier + synchronize on both sides).  roofline.achieved
+divides the same bytes by the average kernel duration from HIP events
+recorded around every launch on the launch stream.  cpu_baseline times the
+oracle's OpenMP restatement of the reference's FP32 GEMV (inferencer.cu:
+645-661) on the host cores over a bounded row sample of the same matrix.
+"""
+from __future__ import annotations
+
+import argparse
+import importlib.util
+import json
+import os
+import pathlib
+import re
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+PKG_NAME = "inferencer_jetson_amd"
+HBM_PEAK_GBPS = 8000.0
+METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak); batched decode tokens/s (1 GPU)"
+
+
+def load_package():
+    if PKG_NAME in sys.modules:
+        return sys.modules[PKG_NAME]
+    pkg_dir = ROOT / "inferencer-jetson_amd"
+    spec = importlib.util.spec_from_file_location(PKG_NAME, pkg_dir / "__init__.py",
+                                                  submodule_search_locations=[str(pkg_dir)])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[PKG_NAME] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary
+    (profiles/<name>.md, a line 'traffic_bytes_per_launch: N'), or None."""
+    path = ROOT / "profiles" / f"{name}.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def time_launches(torch, launch, steps: int, warmup: int, stream):
+    """Runs warmup + timed launches; returns (wall seconds of the timed
+    region, mean per-launch kernel ms from events on `stream`)."""
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        events[i][0].record(stream)
+        launch(warmup + i)
+        events[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [a.elapsed_time(b) for a, b in events]
+    return wall, sum(per) / len(per)
+
+
+def cpu_baseline_lm_head(workloads, sample_rows: int, target_s: float) -> dict:
+    """The oracle's OpenMP restatement of gemv_quant<14> on a row sample."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle  # noqa: E402  (the CPU baseline leg only)
+    import numpy as np
+    w, x = workloads.lm_head_q6k()
+    row_bytes = 8 * 210
+    ws = np.ascontiguousarray(w[: sample_rows * row_bytes])
+    oracle.gemv_f32_ref(14, ws, x, 2048, sample_rows)           # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.gemv_f32_ref(14, ws, x, 2048, sample_rows)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= target_s:
+            break
+    sample_bytes = sample_rows * row_bytes + 2048 * 4 + sample_rows * 4
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(sample_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"Q6_K GEMV over the first {sample_rows} rows (x 2048) of the LM-head matrix, "
+                      f"{reps} repetitions in {el:.1f} s, OpenMP static rows, nproc={os.cpu_count()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=4, help="rotating weight copies (>= 2x the last-level cache)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the GEMV shards by rows with no communication; see DESIGN.md).", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    qk = load_package()
+    import inferencer_jetson_amd.workloads as wl
+
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    cols, rows = 2048, 128256
+    log(f"[bench] building {args.copies} LM-head copies ({rows}x{cols} Q6_K)")
+    copies = []
+    x_host = None
+    for c in range(args.copies):
+        w, x_host = wl.lm_head_q6k(copy=c)
+        copies.append(torch.from_numpy(w).to("cuda"))
+    x = torch.from_numpy(x_host).to("cuda")
+    y = torch.empty(rows, dtype=torch.float32, device="cuda")
+    tensors = [qk.Tensor((cols, rows), qk.Q6_K, wc) for wc in copies]
+
+    def launch(i):
+        qk.matvec(tensors[i % len(tensors)], x, y, cols, rows, stream)
+
+    weight_bytes = qk.tensor_bytes(qk.Q6_K, cols, rows)
+    step_bytes = weight_bytes + cols * 4 + rows * 4
+    log(f"[bench] timing {args.steps} steps after {args.warmup} warmup")
+    wall, kern_ms = time_launches(torch, launch, args.steps, args.warmup, stream)
+    value = step_bytes * args.steps / wall / 1e9
+    achieved = step_bytes / (kern_ms * 1e-3) / 1e9
+    traffic = measured_traffic("gemv_q6k_lm_head_128256x2048")
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / args.steps * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random Q6_K super-blocks, x ~ N(0,1))",
+        "config": {"workload": "lm_head_q6k: Q6_K GEMV 128256x2048 (tied LM head), batch 1, "
+                               f"{args.copies} rotating weight copies",
+                   "rows": rows, "cols": cols, "bytes_per_step": step_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
+    }
+    log(f"[bench] lm_head_q6k: {value:.1f} GB/s wall, kernel {kern_ms * 1e3:.2f} us = {achieved:.1f} GB/s")
+
+    if args.secondary:
+        sec = {}
+        # Q4_K 2048x2048 (Llama-3.2-1B attn_q): launch-bound at this size.
+        w1, x1 = wl.gemv_q4k_2048()
+        w1d, x1d = torch.from_numpy(w1).to("cuda"), torch.from_numpy(x1).to("cuda")
+        y1 = torch.empty(2048, device="cuda")
+        t1 = qk.Tensor((2048, 2048), qk.Q4_K, w1d)
+        wall1, k1 = time_launches(torch, lambda i: qk.matvec(t1, x1d, y1, 2048, 2048, stream), 200, 20, stream)
+        b1 = qk.tensor_bytes(qk.Q4_K, 2048, 2048) + 2048 * 8
+        sec["gemv_q4k_2048x2048"] = {"kernel_us": round(k1 * 1e3, 2), "GBps_kernel": round(b1 / (k1 * 1e-3) / 1e9, 1)}
+        # Q4_K at scale: fused gate/up (2 x 8192 x 2048) over 16 layers' weights.
+        gu = []
+        for l in range(16):
+            wg = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 4, 0.02)
+            wu = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 5, 0.02)
+            gu.append((qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wg).to("cuda")),
+                       qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wu).to("cuda"))))
+        g = torch.empty(8192, device="cuda")
+        u = torch.empty(8192, device="cuda")
+        xg = torch.from_numpy(wl.synth.normal_f32(2048, 2, 7)).to("cuda")
+        wall2, k2 = time_launches(
+            torch, lambda i: qk.gate_up(gu[i % 16][0], gu[i % 16][1], xg, g, u, 2048, 8192, stream), 320, 32, stream)
+        b2 = 2 * qk.tensor_bytes(qk.Q4_K, 2048, 8192) + 2048 * 4 + 2 * 8192 * 4
+        sec["gemv_q4k_gate_up_1b_2x8192x2048"] = {
+            "kernel_us": round(k2 * 1e3, 2), "GBps_kernel": round(b2 / (k2 * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(b2 / (k2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        result["secondary"] = sec
+        log(f"[bench] secondary: {json.dumps(sec)}")
+
+    if not args.no_cpu_baseline:
+        log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
+        result["cpu_baseline"] = cpu_baseline_lm_head(wl, sample_rows=16384, target_s=args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

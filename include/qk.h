@@ -1,0 +1,223 @@
+/*
+ * qk.h - C ABI of the MI355X (gfx950) Q4_K / Q6_K dequant-GEMV library.
+ *
+ * Drop-in boundary for inferencer.cu's quantized matrix path.  The reference
+ * has no plugin layer: its kernels are launched from FastGPU / FastRunner.
+ * Each entry point below names the reference code it replaces.  Conventions
+ * shared by every call:
+ *
+ *  - Weights are GGUF/GGML super-block bytes, rows contiguous, row stride
+ *    (cols/256) * 144 B for Q4_K (type 12) and (cols/256) * 210 B for Q6_K
+ *    (type 14) (inferencer.cu:252-259, 652).  cols = dims[0] is a multiple
+ *    of 256, rows = dims[1] (inferencer.cu:184-185).
+ *  - Activations and outputs are fp32.  Outputs are overwritten, never
+ *    accumulated (inferencer.cu:660); inputs and outputs must not alias.
+ *  - Device pointers only.  Weight bases must be 16-byte aligned (GGUF tensor
+ *    data is aligned to general.alignment, default 32: inferencer.cu:270-272);
+ *    fp32 activation bases and leading dimensions must keep 16-byte alignment.
+ *  - stream is a hipStream_t (NULL selects the null stream).  Calls are
+ *    asynchronous, allocate nothing and keep no per-call state: they are
+ *    reentrant and may be issued from several host threads.
+ *  - Every call validates its arguments on the host before any launch and
+ *    returns a qk status (QK_OK = 0).  Nothing throws across the ABI; the
+ *    reference's runtime_error texts (inferencer.cu:126-128, 1157-1158) map
+ *    to the status plus qk_last_error(), a thread-local message.
+ */
+#ifndef QK_H
+#define QK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage type ids: the GGUF type numbers of storage_name (inferencer.cu:194-202). */
+#define QK_TYPE_F32 0
+#define QK_TYPE_F16 1
+#define QK_TYPE_Q4_K 12
+#define QK_TYPE_Q6_K 14
+
+/* Status codes. */
+#define QK_OK 0
+#define QK_ERR_INVALID_ARG 1   /* null pointer, negative count, bad leading dimension */
+#define QK_ERR_SHAPE 2         /* cols not a positive multiple of 256, rows < 1 */
+#define QK_ERR_TYPE 3          /* storage type other than Q4_K / Q6_K */
+#define QK_ERR_ALIGN 4         /* base pointer or leading dimension misaligned */
+#define QK_ERR_DEVICE 5        /* HIP runtime error at launch */
+#define QK_ERR_LIMIT 6         /* size beyond what the kernels index */
+
+typedef void *qk_stream;
+
+/* ------------------------------------------------------------ utility -- */
+
+/* Status text; replaces the cuda_check / runtime_error messages
+   (inferencer.cu:126-128). */
+const char *qk_status_string(int status);
+/* Detail of the last failing call on this host thread ("" if none). */
+const char *qk_last_error(void);
+/* Bytes per 256-value super-block (144 / 210; 0 for other types) and bytes of
+   a cols x rows tensor: the size rule of inferencer.cu:252-259. */
+int qk_block_bytes(int type);
+int64_t qk_tensor_bytes(int type, int64_t cols, int64_t rows);
+
+/* ------------------------------------------------ FP32 dequant-GEMV -- */
+
+/* y[r] = sum_c W[r][c] * x[c] for r < rows.
+   Replaces FastGPU::matvec's FP32 branch (inferencer.cu:1156-1171) and the
+   gemv_quant<12|14> kernel (inferencer.cu:645-661) it launches. */
+int qk_gemv_f32(int type, const void *w, const float *x, float *y, int cols, int rows,
+                qk_stream stream);
+
+/* One matrix of a fused launch. */
+typedef struct qk_matrix {
+    int type;          /* QK_TYPE_Q4_K or QK_TYPE_Q6_K */
+    int rows;
+    const void *w;
+    float *y;          /* rows outputs */
+} qk_matrix;
+
+/* Several matrices that share x and cols, in one launch: y_m = W_m x.
+   Replaces qkv_cuda (inferencer.cu:753-784: Q, K and a Q4_K or Q6_K V) and
+   gate_up_cuda (inferencer.cu:786-804).  At most QK_MAX_FUSED matrices. */
+#define QK_MAX_FUSED 8
+int qk_gemv_multi_f32(const qk_matrix *mats, int n_mats, const float *x, int cols,
+                      qk_stream stream);
+
+/* Device workspace the multi-token calls need for n_tokens tokens of cols
+   activations (the packed activation tile; 0 when none is needed).  It plays
+   the part of the reference's preallocated batch_xq / batch_xscale buffers
+   (inferencer.cu:1237-1238). */
+size_t qk_gemv_batched_workspace_bytes(int cols, int n_tokens);
+
+/* Multi-token variant: y[t*ldy + r] = sum_c W[r][c] * x[t*ldx + c] for
+   t < n_tokens (token-major like inferencer.cu:698).  FP32 semantics of the
+   reference's INT8-only batched path FastRunner::batch_matvec +
+   gemv_batch_dp4a (inferencer.cu:1265-1278, 678-699), without its 32-token
+   cap; n_tokens = 0 is a no-op.  workspace holds at least
+   qk_gemv_batched_workspace_bytes(cols, n_tokens) device bytes and must not
+   be shared by calls in flight at the same time. */
+int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float *y, int ldy,
+                        int cols, int rows, int n_tokens, void *workspace,
+                        size_t workspace_bytes, qk_stream stream);
+
+/* Fused multi-token launch over matrices sharing x: y_m[t*rows_m + r].
+   Replaces qkv_batch_cuda (inferencer.cu:701-731) and gate_up_batch_cuda
+   (inferencer.cu:733-751). */
+int qk_gemv_multi_batched_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx,
+                              int cols, int n_tokens, void *workspace, size_t workspace_bytes,
+                              qk_stream stream);
+
+/* ------------------------------------------------------------ dequant -- */
+
+/* out[r*cols + c] = W[row0 + r][c] as fp32, bit-exact with q4_value /
+   q6_value (inferencer.cu:454-487). */
+int qk_dequant_rows(int type, const void *w, float *out, int cols, int row0, int nrows,
+                    qk_stream stream);
+
+/* out[t*cols + c] = W[tokens[t]][c]; tokens is a device array of n_tokens
+   ids in [0, vocab).  Replaces embedding_cuda / embedding_batch_cuda
+   (inferencer.cu:806-819); any Q4_K or Q6_K table. */
+int qk_embedding(int type, const void *w, const int32_t *tokens, int n_tokens, float *out,
+                 int cols, int vocab, qk_stream stream);
+
+/* ---------------------------------------------------------- INT8 mode -- */
+
+/* Per 32 values: scale = amax/127 (1 if amax == 0), xq = clamp(rne(x/scale),
+   -127, 127).  Token t reads x + t*ldx and writes xq + t*ldxq, xscale +
+   t*ldscale (the reference's fixed strides are 8192 and 256,
+   inferencer.cu:687-688).  Replaces quantize_x32_cuda (inferencer.cu:544-556)
+   and quantize_batch_cuda (inferencer.cu:891-904). */
+int qk_quantize_x32(const float *x, int ldx, int8_t *xq, int ldxq, float *xscale, int ldscale,
+                    int cols, int n_tokens, qk_stream stream);
+
+/* INT8-activation GEMV for n_tokens tokens (1 = decode): exact integer
+   sub-block dots, fp32 combine.  Replaces gemv_q4_dp4a / gemv_q6_dp4a
+   (inferencer.cu:558-569, 663-674) and gemv_batch_dp4a
+   (inferencer.cu:678-699). */
+int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale,
+               int ldscale, float *y, int ldy, int cols, int rows, int n_tokens,
+               qk_stream stream);
+
+/* -------------------------------------------------------- step kernels -- */
+
+/* out = x * 1/sqrt(mean(x^2) + eps) * weight per token of n values.
+   Replaces rmsnorm_cuda (inferencer.cu:821-834). */
+int qk_rmsnorm_f32(const float *x, const float *weight, float *out, int n, int n_tokens,
+                   float eps, qk_stream stream);
+
+/* Rotates q (heads*head_dim) and k (kv_heads*head_dim) in adjacent pairs at
+   position pos, writes rotated k and v into the caches at
+   [(layer*context + pos)*kv_dim].  Tables are [context][head_dim/2].
+   Replaces rope_cache_cuda / rope_cuda + cache_cuda (inferencer.cu:906-951),
+   generalised from head_dim 128. */
+int qk_rope_kv_write(float *q, const float *k, const float *v, const float *cosine,
+                     const float *sine, float *key_cache, float *value_cache, int layer, int pos,
+                     int context, int heads, int kv_heads, int head_dim, qk_stream stream);
+
+/* GQA attention of one query token over cache positions 0..pos of a layer.
+   Replaces attention_cuda (inferencer.cu:981-1009), generalised head_dim. */
+int qk_attention_f32(const float *q, const float *key_cache, const float *value_cache,
+                     float *out, int layer, int pos, int context, int heads, int kv_heads,
+                     int head_dim, qk_stream stream);
+
+/* x += y (add_cuda, inferencer.cu:1043-1046). */
+int qk_add_f32(float *x, const float *y, int n, qk_stream stream);
+
+/* gate = gate / (1 + exp(-gate)) * up (silu_cuda, inferencer.cu:1053-1056). */
+int qk_silu_mul_f32(float *gate, const float *up, int n, qk_stream stream);
+
+/* Index of the maximum of v[0..n), lowest index among equal maxima, into
+   *out (device).  workspace holds qk_argmax_workspace_bytes(n) device bytes.
+   Replaces argmax_blocks_cuda + argmax_final_cuda (inferencer.cu:1063-1099). */
+size_t qk_argmax_workspace_bytes(int n);
+int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_stream stream);
+
+/* ---------------------------------------------------- decode-step driver -- */
+
+/* Llama configuration (the llama.* GGUF keys read at inferencer.cu:1205-1214). */
+typedef struct qk_llama_config {
+    int dim, layers, heads, kv_heads, hidden, vocab, context;
+    float eps, rope_theta;
+} qk_llama_config;
+
+/* Device pointers to one layer's tensors (blk.N.* names of inferencer.cu:1434-1502). */
+typedef struct qk_llama_layer {
+    int q_type, k_type, v_type, o_type, gate_type, up_type, down_type;
+    const void *q, *k, *v, *o, *gate, *up, *down;
+    const float *attn_norm, *ffn_norm;
+} qk_llama_layer;
+
+typedef struct qk_llama_weights {
+    int embd_type;
+    const void *token_embd;
+    int output_type;
+    const void *output;            /* NULL: tied to token_embd (inferencer.cu:1521-1522) */
+    const float *output_norm;
+    const qk_llama_layer *layers;  /* host array of cfg.layers entries */
+} qk_llama_weights;
+
+typedef struct qk_llama qk_llama;
+
+/* Allocates the step buffers, KV cache and RoPE tables once (the FastGPU /
+   FastRunner constructors, inferencer.cu:1115-1142, 1196-1249).  The weights
+   stay owned by the caller. */
+int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream,
+                    qk_llama **out);
+int qk_llama_destroy(qk_llama *m);
+/* Device pointers to the fp32 caches, [layer][context][kv_dim]. */
+int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
+/* Device pointer to the fp32 logits of the last step with need_logits. */
+int qk_llama_logits(qk_llama *m, const float **logits);
+/* One decode step at position pos (FastRunner::forward, inferencer.cu:1424-1531).
+   With need_logits, *next_token receives the greedy token (synchronises the
+   stream like the reference's 4-byte copy, inferencer.cu:1529); otherwise
+   the step stays asynchronous and *next_token is -1. */
+int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next_token);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,255 @@
+"""MI355X (gfx950) Q4_K / Q6_K dequant-GEMV: Python host mirror of the C ABI.
+
+libqk.so (built from csrc/ by the Makefile) exports the C ABI declared in
+include/qk.h.  This module binds it with ctypes and mirrors the reference's
+host-side interface for the path (inferencer.cu:178-186 Tensor,
+1101-1180 FastGPU, 1265-1278 batch_matvec): the same names, argument meaning
+and error behaviour -- a failing call raises QKError("where: message") like
+cuda_check (inferencer.cu:126-128).
+
+Device buffers are passed as raw pointers; torch tensors (or anything with
+data_ptr()) are accepted for convenience, torch being only the allocator and
+stream provider.  There is no CPU fallback: if libqk.so is missing, loading
+raises ImportError.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+from dataclasses import dataclass
+from typing import Sequence
+
+_HERE = pathlib.Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libqk.so"
+
+F32, F16, Q4_K, Q6_K = 0, 1, 12, 14
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
+STORAGE_NAMES = {F32: "FP32", F16: "FP16", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+MAX_FUSED = 8
+
+QK_OK = 0
+QK_ERR_INVALID_ARG = 1
+QK_ERR_SHAPE = 2
+QK_ERR_TYPE = 3
+QK_ERR_ALIGN = 4
+QK_ERR_DEVICE = 5
+QK_ERR_LIMIT = 6
+
+
+class QKError(RuntimeError):
+    """A non-zero qk status; .status holds the code."""
+
+    def __init__(self, where: str, status: int, detail: str):
+        super().__init__(f"{where}: {detail}")
+        self.status = status
+
+
+class qk_matrix(ctypes.Structure):
+    _fields_ = [("type", ctypes.c_int), ("rows", ctypes.c_int),
+                ("w", ctypes.c_void_p), ("y", ctypes.c_void_p)]
+
+
+class qk_llama_config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab", "context")] + \
+               [("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class qk_llama_layer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("q_type", "k_type", "v_type", "o_type", "gate_type", "up_type",
+                                             "down_type")] + \
+               [(n, ctypes.c_void_p) for n in ("q", "k", "v", "o", "gate", "up", "down", "attn_norm", "ffn_norm")]
+
+
+class qk_llama_weights(ctypes.Structure):
+    _fields_ = [("embd_type", ctypes.c_int), ("token_embd", ctypes.c_void_p), ("output_type", ctypes.c_int),
+                ("output", ctypes.c_void_p), ("output_norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(qk_llama_layer))]
+
+
+_i, _vp, _f = ctypes.c_int, ctypes.c_void_p, ctypes.c_float
+# name -> (restype, argtypes), exactly the declarations of include/qk.h.
+SIGNATURES = {
+    "qk_status_string": (ctypes.c_char_p, [_i]),
+    "qk_last_error": (ctypes.c_char_p, []),
+    "qk_block_bytes": (_i, [_i]),
+    "qk_tensor_bytes": (ctypes.c_int64, [_i, ctypes.c_int64, ctypes.c_int64]),
+    "qk_gemv_f32": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
+    "qk_gemv_multi_f32": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _vp]),
+    "qk_gemv_batched_workspace_bytes": (ctypes.c_size_t, [_i, _i]),
+    "qk_gemv_batched_f32": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
+    "qk_gemv_multi_batched_f32": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
+    "qk_dequant_rows": (_i, [_i, _vp, _vp, _i, _i, _i, _vp]),
+    "qk_embedding": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _vp]),
+    "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "qk_rope_kv_write": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "qk_attention_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
+    "qk_add_f32": (_i, [_vp, _vp, _i, _vp]),
+    "qk_silu_mul_f32": (_i, [_vp, _vp, _i, _vp]),
+    "qk_argmax_workspace_bytes": (ctypes.c_size_t, [_i]),
+    "qk_argmax_f32": (_i, [_vp, _i, _vp, _vp, _vp]),
+    "qk_llama_create": (_i, [ctypes.POINTER(qk_llama_config), ctypes.POINTER(qk_llama_weights), _vp,
+                             ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_destroy": (_i, [_vp]),
+    "qk_llama_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_forward": (_i, [_vp, _i, _i, _i, ctypes.POINTER(ctypes.c_int)]),
+}
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded libqk.so with every signature bound (raises if unbuilt)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build()")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def check(status: int, where: str) -> None:
+    """Raise QKError for a non-zero status (the cuda_check convention)."""
+    if status != QK_OK:
+        detail = lib().qk_last_error().decode() or lib().qk_status_string(status).decode()
+        raise QKError(where, status, detail)
+
+
+def ptr(a) -> int | None:
+    """Device address of a tensor-like (data_ptr()), an int, or None."""
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    return a.data_ptr()
+
+
+def stream_handle(stream) -> int | None:
+    """hipStream_t of a torch stream / raw handle; None = null stream."""
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def tensor_bytes(qtype: int, cols: int, rows: int) -> int:
+    """Bytes of a quantized tensor: the size rule of inferencer.cu:252-259."""
+    if qtype not in BLOCK_BYTES or cols % 256 or cols <= 0 or rows < 0:
+        raise QKError("tensor_bytes", QK_ERR_SHAPE, "Invalid quantized tensor shape")
+    return cols // 256 * BLOCK_BYTES[qtype] * rows
+
+
+@dataclass
+class Tensor:
+    """A quantized weight view: Tensor{dims, type, gpu} of inferencer.cu:178-186.
+
+    dims[0] = cols (contiguous), dims[1] = rows; data is a device buffer."""
+    dims: Sequence[int]
+    type: int
+    data: object
+
+    def cols(self) -> int:
+        return int(self.dims[0])
+
+    def rows(self) -> int:
+        return int(self.dims[1])
+
+    @property
+    def gpu(self) -> int:
+        return ptr(self.data)
+
+
+def matvec(t: Tensor, inp, out, expected_cols: int, expected_rows: int, stream=None) -> None:
+    """FastGPU::matvec (inferencer.cu:1156-1171), FP32 mode: out = W inp."""
+    if t.cols() != expected_cols or t.rows() != expected_rows or t.type not in (Q4_K, Q6_K):
+        raise QKError("matvec", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
+    check(lib().qk_gemv_f32(t.type, t.gpu, ptr(inp), ptr(out), expected_cols, expected_rows,
+                            stream_handle(stream)), "quantized matrix launch")
+
+
+def _matrices(pairs) -> ctypes.Array:
+    arr = (qk_matrix * len(pairs))()
+    for i, (t, out) in enumerate(pairs):
+        arr[i].type, arr[i].rows, arr[i].w, arr[i].y = t.type, t.rows(), t.gpu, ptr(out)
+    return arr
+
+
+def multi_matvec(pairs, inp, cols: int, stream=None) -> None:
+    """One fused launch of out_m = W_m inp over (Tensor, out) pairs sharing inp."""
+    for t, _ in pairs:
+        if t.cols() != cols:
+            raise QKError("multi_matvec", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
+    arr = _matrices(pairs)
+    check(lib().qk_gemv_multi_f32(arr, len(pairs), ptr(inp), cols, stream_handle(stream)),
+          "fused quantized matrix launch")
+
+
+def qkv(wq: Tensor, wk: Tensor, wv: Tensor, x, q, k, v, dim: int, kv_dim: int, stream=None) -> None:
+    """qkv_cuda (inferencer.cu:753-784), FP32 mode: Q4_K q/k, Q4_K or Q6_K v."""
+    if (wq.rows(), wk.rows(), wv.rows()) != (dim, kv_dim, kv_dim) or wq.type != Q4_K or wk.type != Q4_K \
+            or wv.type not in (Q4_K, Q6_K):
+        raise QKError("qkv", QK_ERR_SHAPE, "Unexpected QKV quantization")
+    multi_matvec([(wq, q), (wk, k), (wv, v)], x, dim, stream)
+
+
+def gate_up(wgate: Tensor, wup: Tensor, x, gate, up, dim: int, hidden: int, stream=None) -> None:
+    """gate_up_cuda (inferencer.cu:786-804), FP32 mode."""
+    if wgate.type != Q4_K or wup.type != Q4_K or wgate.rows() != hidden or wup.rows() != hidden:
+        raise QKError("gate_up", QK_ERR_SHAPE, "Unexpected feedforward quantization")
+    multi_matvec([(wgate, gate), (wup, up)], x, dim, stream)
+
+
+def batch_workspace_bytes(cols: int, count: int) -> int:
+    return int(lib().qk_gemv_batched_workspace_bytes(cols, count))
+
+
+def batch_matvec(t: Tensor, inp, out, cols: int, rows: int, count: int, workspace=None,
+                 workspace_bytes: int = 0, stream=None) -> None:
+    """FastRunner::batch_matvec (inferencer.cu:1265-1278) with FP32 semantics:
+    out[t*rows + r] = sum_c W[r][c] inp[t*cols + c] for t < count."""
+    if t.cols() != cols or t.rows() != rows or t.type not in (Q4_K, Q6_K):
+        raise QKError("batch_matvec", QK_ERR_SHAPE, "Unexpected batched matrix shape")
+    check(lib().qk_gemv_batched_f32(t.type, t.gpu, ptr(inp), cols, ptr(out), rows, cols, rows, count,
+                                    ptr(workspace), workspace_bytes, stream_handle(stream)),
+          "batched matrix launch")
+
+
+def dequant_rows(t: Tensor, out, row0: int, nrows: int, stream=None) -> None:
+    check(lib().qk_dequant_rows(t.type, t.gpu, ptr(out), t.cols(), row0, nrows, stream_handle(stream)),
+          "dequant launch")
+
+
+def embedding(t: Tensor, tokens, out, n_tokens: int, stream=None) -> None:
+    """embedding_cuda / embedding_batch_cuda (inferencer.cu:806-819)."""
+    check(lib().qk_embedding(t.type, t.gpu, ptr(tokens), n_tokens, ptr(out), t.cols(), t.rows(),
+                             stream_handle(stream)), "embedding launch")
+
+
+def quantize(x, xq, xscale, cols: int, n_tokens: int = 1, ldx: int | None = None, ldxq: int | None = None,
+             ldscale: int | None = None, stream=None) -> None:
+    """FastGPU::quantize / quantize_batch_cuda (inferencer.cu:1151-1155, 891-904)."""
+    ldx = cols if ldx is None else ldx
+    ldxq = cols if ldxq is None else ldxq
+    ldscale = (cols + 31) // 32 if ldscale is None else ldscale
+    check(lib().qk_quantize_x32(ptr(x), ldx, ptr(xq), ldxq, ptr(xscale), ldscale, cols, n_tokens,
+                                stream_handle(stream)), "activation quantization launch")
+
+
+def matvec_i8(t: Tensor, xq, xscale, out, cols: int, rows: int, n_tokens: int = 1, ldxq: int | None = None,
+              ldscale: int | None = None, ldy: int | None = None, stream=None) -> None:
+    """gemv_q4_dp4a / gemv_q6_dp4a / gemv_batch_dp4a (inferencer.cu:558-569, 663-699)."""
+    if t.cols() != cols or t.rows() != rows or t.type not in (Q4_K, Q6_K):
+        raise QKError("matvec_i8", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
+    ldxq = cols if ldxq is None else ldxq
+    ldscale = cols // 32 if ldscale is None else ldscale
+    ldy = rows if ldy is None else ldy
+    check(lib().qk_gemv_i8(t.type, t.gpu, ptr(xq), ldxq, ptr(xscale), ldscale, ptr(out), ldy, cols, rows,
+                           n_tokens, stream_handle(stream)), "INT8 matrix launch")

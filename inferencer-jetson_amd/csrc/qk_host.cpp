@@ -1,0 +1,97 @@
+// qk_host.cpp - status codes, thread-local error text, argument validation
+// and cached device properties shared by every entry point of libqk.so.
+#include "qk_internal.h"
+
+#include <mutex>
+#include <vector>
+
+namespace qk {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int status, const std::string &message) {
+    g_last_error = message;
+    return status;
+}
+
+int ok() {
+    g_last_error.clear();
+    return QK_OK;
+}
+
+int launch_status(const char *where) {
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess)
+        return fail(QK_ERR_DEVICE, std::string(where) + ": " + hipGetErrorString(err));
+    return ok();
+}
+
+int block_bytes(int type) {
+    return type == QK_TYPE_Q4_K ? 144 : type == QK_TYPE_Q6_K ? 210 : 0;
+}
+
+int check_weights(const char *where, int type, const void *w, int cols, int rows) {
+    // Mirrors FastGPU::matvec's checks (inferencer.cu:1157-1158) and the
+    // quantized shape rule (inferencer.cu:254-256), plus the alignment the
+    // GGUF data section guarantees (inferencer.cu:270-272).
+    if (type != QK_TYPE_Q4_K && type != QK_TYPE_Q6_K)
+        return fail(QK_ERR_TYPE, std::string(where) + ": unsupported storage type " + std::to_string(type));
+    if (cols <= 0 || cols % 256 != 0 || rows < 1)
+        return fail(QK_ERR_SHAPE, std::string(where) + ": unexpected quantized matrix shape " +
+                                      std::to_string(cols) + " x " + std::to_string(rows));
+    if (!w) return fail(QK_ERR_INVALID_ARG, std::string(where) + ": null weight pointer");
+    if (!aligned(w, 16)) return fail(QK_ERR_ALIGN, std::string(where) + ": weight base not 16-byte aligned");
+    return QK_OK;
+}
+
+const DeviceInfo &device_info() {
+    static std::mutex mutex;
+    static std::vector<DeviceInfo> cache;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) device = 0;
+    std::lock_guard<std::mutex> lock(mutex);
+    if (cache.size() <= static_cast<size_t>(device)) cache.resize(device + 1);
+    DeviceInfo &info = cache[device];
+    if (info.device < 0) {
+        hipDeviceProp_t prop{};
+        if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+            info.cus = prop.multiProcessorCount;
+            info.max_threads = prop.maxThreadsPerBlock;
+        } else {
+            info.cus = 256;
+        }
+        info.device = device;
+    }
+    return info;
+}
+
+}  // namespace qk
+
+extern "C" {
+
+const char *qk_status_string(int status) {
+    switch (status) {
+        case QK_OK: return "ok";
+        case QK_ERR_INVALID_ARG: return "invalid argument";
+        case QK_ERR_SHAPE: return "unexpected quantized matrix shape";
+        case QK_ERR_TYPE: return "unsupported storage type";
+        case QK_ERR_ALIGN: return "misaligned pointer or leading dimension";
+        case QK_ERR_DEVICE: return "HIP device error";
+        case QK_ERR_LIMIT: return "size beyond kernel limits";
+        default: return "unknown status";
+    }
+}
+
+const char *qk_last_error(void) { return qk::g_last_error.c_str(); }
+
+int qk_block_bytes(int type) { return qk::block_bytes(type); }
+
+int64_t qk_tensor_bytes(int type, int64_t cols, int64_t rows) {
+    int bpb = qk::block_bytes(type);
+    if (!bpb || cols <= 0 || cols % 256 || rows < 0) return -1;
+    return cols / 256 * bpb * rows;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// qk_internal.h - shared host plumbing and device helpers of libqk.so.
+//
+// Super-block layouts (GGML, decoded by inferencer.cu:453-497):
+//   Q4_K, 144 B: fp16 d @0, fp16 dmin @2, 12 packed 6-bit scale/min bytes @4,
+//                128 bytes of nibbles @16.  w = d*sc*q - dmin*m.
+//   Q6_K, 210 B: ql[128] @0, qh[64] @128, int8 scales[16] @192, fp16 d @208.
+//                w = d*scale*(code - 32).
+//
+// The GEMV kernels cut every row into "pieces" of 64 weights, one piece per
+// lane.  Piece p of a row covers block b = p/4, g = (p/2)%2, h = p%2 and the
+// columns b*256 + g*128 + part*32 + h*16 + k for part 0..3, k 0..15.  The
+// same column set serves both formats:
+//   Q4_K: 16 B of nibbles at 16 + g*64 + h*16 (parts 0/1 = low/high nibbles)
+//         and at 16 + g*64 + 32 + h*16 (parts 2/3), plus the 16 B header.
+//   Q6_K: 16 B of ql at g*64 + h*16 (parts 0/2), at g*64 + 32 + h*16
+//         (parts 1/3), 16 B of qh at 128 + g*32 + h*16, the four scales
+//         scales[g*8 + part*2 + h] and d.
+// so a lane's 64 activations are fixed for every row of a matrix and for
+// every matrix of a fused launch, whatever their types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/qk.h"
+
+namespace qk {
+
+// ------------------------------------------------------------------ host --
+
+// Records a thread-local message and returns the status (never throws).
+int fail(int status, const std::string &message);
+// Clears the thread-local message; returns QK_OK.
+int ok();
+// Maps a HIP error after launches to QK_ERR_DEVICE.
+int launch_status(const char *where);
+
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int block_bytes(int type);
+// Validates a Q4_K / Q6_K weight operand shape; returns QK_OK or a status.
+int check_weights(const char *where, int type, const void *w, int cols, int rows);
+
+// Dynamic LDS of the attention kernel for positions 0..pos.
+size_t attention_lds_bytes(int pos, int head_dim);
+
+// Per-device properties, cached once per device (thread-safe).
+struct DeviceInfo {
+    int device = -1;
+    int cus = 0;          // compute units
+    int max_threads = 1024;
+};
+const DeviceInfo &device_info();
+
+// ---------------------------------------------------------------- device --
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+    _Float16 h = __builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16));
+    return static_cast<float>(h);
+}
+
+// Byte j of v as a float; the backend emits v_cvt_f32_ubyte{0..3}.
+__device__ __forceinline__ float ubyte0(uint32_t v) { return static_cast<float>(v & 0xFFu); }
+__device__ __forceinline__ float ubyte1(uint32_t v) { return static_cast<float>((v >> 8) & 0xFFu); }
+__device__ __forceinline__ float ubyte2(uint32_t v) { return static_cast<float>((v >> 16) & 0xFFu); }
+__device__ __forceinline__ float ubyte3(uint32_t v) { return static_cast<float>(v >> 24); }
+
+// 16 / 8 / 2 byte loads at any 2-byte alignment.  gfx950 global loads
+// tolerate unaligned addresses (Q6_K blocks are 210 B, so odd blocks are
+// only 2-byte aligned); memcpy keeps the C++ side free of misaligned
+// pointer dereferences.
+__device__ __forceinline__ uint4 load16(const uint8_t *p) {
+    uint4 v;
+    __builtin_memcpy(&v, p, 16);
+    return v;
+}
+__device__ __forceinline__ uint2 load8(const uint8_t *p) {
+    uint2 v;
+    __builtin_memcpy(&v, p, 8);
+    return v;
+}
+__device__ __forceinline__ uint32_t load2(const uint8_t *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+// Scalar decode of element i of a block: the bit-exact semantics of
+// q4_value / q6_value (inferencer.cu:454-487).
+__device__ __forceinline__ float q4k_value(const uint8_t *block, int i) {
+    float d = f16_bits_to_f32(load2(block));
+    float dmin = f16_bits_to_f32(load2(block + 2));
+    const uint8_t *s = block + 4;
+    const uint8_t *qs = block + 16;
+    int sub = i >> 5;
+    int qi = (i >> 6) * 32 + (i & 31);
+    int q = (i & 63) < 32 ? (qs[qi] & 15) : (qs[qi] >> 4);
+    int sc, m;
+    if (sub < 4) {
+        sc = s[sub] & 63;
+        m = s[sub + 4] & 63;
+    } else {
+        sc = (s[sub + 4] & 15) | ((s[sub - 4] >> 6) << 4);
+        m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
+    }
+    // Products are exact in fp32; the subtraction is the only rounding.
+    return d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
+}
+
+__device__ __forceinline__ float q6k_value(const uint8_t *block, int i) {
+    int group = i >> 7, p = i & 127, lane = p & 31, part = p >> 5;
+    int low = block[group * 64 + (part & 1) * 32 + lane];
+    low = part < 2 ? (low & 15) : (low >> 4);
+    int high = (block[128 + group * 32 + lane] >> (part * 2)) & 3;
+    int q = (low | (high << 4)) - 32;
+    float d = f16_bits_to_f32(load2(block + 208));
+    int sc = static_cast<int8_t>(block[192 + group * 8 + part * 2 + (lane >> 4)]);
+    return d * static_cast<float>(sc) * static_cast<float>(q);
+}
+
+}  // namespace qk

@@ -1,0 +1,207 @@
+// qk_llama.cpp - Llama decode-step driver over the qk C ABI.
+//
+// The counterpart of FastGPU / FastRunner (inferencer.cu:1101-1150,
+// 1182-1532): buffers, KV cache and RoPE tables are allocated once in
+// qk_llama_create; qk_llama_forward issues one step in the order of
+// FastRunner::forward (inferencer.cu:1424-1531).  The step is generalised
+// past the reference's Llama-3.2-3B hard-coding (inferencer.cu:1215-1217):
+// any head_dim dividing 256, GQA group and layer count.
+//
+// The greedy token of a step stays on the device; when the caller feeds it
+// back as the next input token the embedding reads it there, so a decode
+// loop moves 4 bytes device->host per token (the reference's copy,
+// inferencer.cu:1529) and nothing host->device.
+#include "qk_internal.h"
+
+#include <cmath>
+#include <vector>
+
+struct qk_llama {
+    qk_llama_config cfg{};
+    qk_llama_weights w{};
+    std::vector<qk_llama_layer> layers;
+    hipStream_t stream = nullptr;
+    int head_dim = 0, kv_dim = 0;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr;
+    float *attn = nullptr, *tmp = nullptr, *gate = nullptr, *up = nullptr, *logits = nullptr;
+    float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
+    void *argmax_ws = nullptr;
+    int32_t *d_next = nullptr, *d_token = nullptr;
+    int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
+    int last_next = -1;
+};
+
+namespace {
+
+template <class T>
+int dev_alloc(T **p, size_t count, const char *what) {
+    if (hipMalloc(reinterpret_cast<void **>(p), count * sizeof(T)) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, std::string("qk_llama_create: cannot allocate ") + what);
+    return QK_OK;
+}
+
+void release(qk_llama *m) {
+    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
+                    m->value_cache, m->cosine, m->sine, m->argmax_ws, m->d_next, m->d_token};
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->h_token) (void)hipHostFree(m->h_token);
+    delete m;
+}
+
+bool quant_type(int t) { return t == QK_TYPE_Q4_K || t == QK_TYPE_Q6_K; }
+
+}  // namespace
+
+extern "C" {
+
+int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream, qk_llama **out) {
+    if (!cfg || !w || !out || !w->layers || !w->token_embd || !w->output_norm)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_create: null argument");
+    const qk_llama_config &c = *cfg;
+    if (c.dim < 256 || c.dim % 256 || c.hidden % 256 || c.hidden < 256 || c.layers < 1 || c.heads < 1 ||
+        c.kv_heads < 1 || c.dim % c.heads || c.heads % c.kv_heads || c.vocab < 1 || c.context < 1)
+        return qk::fail(QK_ERR_SHAPE, "qk_llama_create: unsupported model shape");
+    const int head_dim = c.dim / c.heads;
+    if (head_dim % 4 || 256 % head_dim)
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_create: head_dim must be a multiple of 4 dividing 256");
+    if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
+        return qk::fail(QK_ERR_TYPE, "qk_llama_create: embedding and output must be Q4_K or Q6_K");
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = w->layers[l];
+        if (!quant_type(L.q_type) || !quant_type(L.k_type) || !quant_type(L.v_type) || !quant_type(L.o_type) ||
+            !quant_type(L.gate_type) || !quant_type(L.up_type) || !quant_type(L.down_type))
+            return qk::fail(QK_ERR_TYPE, "qk_llama_create: layer " + std::to_string(l) + " has a non-K-quant tensor");
+        if (!L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down || !L.attn_norm || !L.ffn_norm)
+            return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_create: layer " + std::to_string(l) + " is incomplete");
+    }
+    if (qk::attention_lds_bytes(c.context - 1, head_dim) > 150 * 1024)
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_create: context beyond the attention kernel's LDS budget");
+
+    qk_llama *m = new qk_llama();
+    m->cfg = c;
+    m->w = *w;
+    m->layers.assign(w->layers, w->layers + c.layers);
+    m->w.layers = m->layers.data();
+    m->stream = static_cast<hipStream_t>(stream);
+    m->head_dim = head_dim;
+    m->kv_dim = head_dim * c.kv_heads;
+    const size_t cache = static_cast<size_t>(c.layers) * c.context * m->kv_dim;
+    const int half = head_dim / 2;
+    int st = QK_OK;
+    if ((st = dev_alloc(&m->x, c.dim, "residual")) || (st = dev_alloc(&m->xn, c.dim, "normalized state")) ||
+        (st = dev_alloc(&m->q, c.dim, "query")) || (st = dev_alloc(&m->k, m->kv_dim, "key")) ||
+        (st = dev_alloc(&m->v, m->kv_dim, "value")) || (st = dev_alloc(&m->attn, c.dim, "attention")) ||
+        (st = dev_alloc(&m->tmp, c.dim, "residual update")) || (st = dev_alloc(&m->gate, c.hidden, "gate")) ||
+        (st = dev_alloc(&m->up, c.hidden, "up projection")) || (st = dev_alloc(&m->logits, c.vocab, "logits")) ||
+        (st = dev_alloc(&m->key_cache, cache, "key cache")) ||
+        (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
+        (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
+        (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
+        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_workspace_bytes(c.vocab),
+                        "argmax workspace")) ||
+        (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token"))) {
+        release(m);
+        return st;
+    }
+    if (hipHostMalloc(reinterpret_cast<void **>(&m->h_token), 2 * sizeof(int32_t), hipHostMallocDefault) !=
+        hipSuccess) {
+        release(m);
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_create: cannot allocate pinned staging");
+    }
+    // RoPE tables exactly as the reference builds them on the host
+    // (inferencer.cu:1218-1226): float powf, float angle, cosf / sinf.
+    std::vector<float> cosines(static_cast<size_t>(c.context) * half), sines(cosines.size()), freq(half);
+    for (int i = 0; i < half; ++i) freq[i] = std::pow(c.rope_theta, -2.f * static_cast<float>(i) / head_dim);
+    for (int pos = 0; pos < c.context; ++pos)
+        for (int i = 0; i < half; ++i) {
+            const float angle = static_cast<float>(pos) * freq[i];
+            cosines[static_cast<size_t>(pos) * half + i] = std::cos(angle);
+            sines[static_cast<size_t>(pos) * half + i] = std::sin(angle);
+        }
+    if (hipMemcpy(m->cosine, cosines.data(), cosines.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sine, sines.data(), sines.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(m->key_cache, 0, cache * sizeof(float)) != hipSuccess ||
+        hipMemset(m->value_cache, 0, cache * sizeof(float)) != hipSuccess) {
+        release(m);
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_create: table upload failed");
+    }
+    *out = m;
+    return qk::ok();
+}
+
+int qk_llama_destroy(qk_llama *m) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_destroy: null handle");
+    (void)hipStreamSynchronize(m->stream);
+    release(m);
+    return qk::ok();
+}
+
+int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache) {
+    if (!m || !key_cache || !value_cache) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_kv_cache: null argument");
+    *key_cache = m->key_cache;
+    *value_cache = m->value_cache;
+    return qk::ok();
+}
+
+int qk_llama_logits(qk_llama *m, const float **logits) {
+    if (!m || !logits) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_logits: null argument");
+    *logits = m->logits;
+    return qk::ok();
+}
+
+int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next_token) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_forward: null handle");
+    const qk_llama_config &c = m->cfg;
+    if (pos < 0 || pos >= c.context || token < 0 || token >= c.vocab)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_forward: token or position outside model context");
+    hipStream_t s = m->stream;
+    const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
+    int st;
+    const int32_t *tok = m->d_next;
+    if (token != m->last_next) {
+        m->h_token[0] = token;
+        if (hipMemcpyAsync(m->d_token, m->h_token, sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess)
+            return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: token upload failed");
+        tok = m->d_token;
+    }
+    m->last_next = -1;
+    if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        if ((st = qk_rmsnorm_f32(m->x, L.attn_norm, m->xn, dim, 1, c.eps, s))) return st;
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = qk_gemv_multi_f32(qkv, 3, m->xn, dim, s))) return st;
+        if ((st = qk_rope_kv_write(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l, pos,
+                                   c.context, c.heads, c.kv_heads, hd, s)))
+            return st;
+        if ((st = qk_attention_f32(m->q, m->key_cache, m->value_cache, m->attn, l, pos, c.context, c.heads,
+                                   c.kv_heads, hd, s)))
+            return st;
+        if ((st = qk_gemv_f32(L.o_type, L.o, m->attn, m->tmp, dim, dim, s))) return st;
+        if ((st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
+        if ((st = qk_rmsnorm_f32(m->x, L.ffn_norm, m->xn, dim, 1, c.eps, s))) return st;
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+        if ((st = qk_gemv_multi_f32(gu, 2, m->xn, dim, s))) return st;
+        if ((st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s))) return st;
+        if ((st = qk_gemv_f32(L.down_type, L.down, m->gate, m->tmp, c.hidden, dim, s))) return st;
+        if ((st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
+    }
+    if (!need_logits) {
+        if (next_token) *next_token = -1;
+        return qk::ok();
+    }
+    if ((st = qk_rmsnorm_f32(m->x, m->w.output_norm, m->xn, dim, 1, c.eps, s))) return st;
+    const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
+    const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
+    if ((st = qk_gemv_f32(out_type, out_w, m->xn, m->logits, dim, c.vocab, s))) return st;
+    if ((st = qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s))) return st;
+    if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");
+    m->last_next = m->h_token[1];
+    if (next_token) *next_token = m->last_next;
+    return qk::ok();
+}
+
+}  // extern "C"

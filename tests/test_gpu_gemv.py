@@ -1,0 +1,127 @@
+"""GPU parity of the batch-1 FP32 dequant-GEMV (qk_gemv_f32, qk_gemv_multi_f32)
+against the fp64 oracle.  Bar: relative L2 error <= 1e-5 (fp32 accumulation
+against fp64 truth); one-hot activations must reproduce dequantized columns
+bit for bit."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+Q4_K, Q6_K = 12, 14
+TOL = 1e-5
+
+
+def run_gemv(qk, torch, qtype, w, x, cols, rows):
+    wd, xd = to_dev(torch, w), to_dev(torch, x)
+    yd = torch.full((rows,), float("nan"), dtype=torch.float32, device="cuda")
+    qk.matvec(qk.Tensor((cols, rows), qtype, wd), xd, yd, cols, rows)
+    torch.cuda.synchronize()
+    return yd.cpu().numpy()
+
+
+def test_config1_q4k_2048(qk, torch_gpu, oracle, workloads):
+    w, x = workloads.gemv_q4k_2048()
+    y = run_gemv(qk, torch_gpu, Q4_K, w, x, 2048, 2048)
+    assert rel_l2(y, oracle.gemv_f64(Q4_K, w, x, 2048, 2048)) < TOL
+
+
+def test_config2_lm_head_q6k(qk, torch_gpu, oracle, workloads):
+    w, x = workloads.lm_head_q6k()
+    y = run_gemv(qk, torch_gpu, Q6_K, w, x, 2048, 128256)
+    y64 = oracle.gemv_f64(Q6_K, w, x, 2048, 128256)
+    assert np.all(np.isfinite(y))
+    assert rel_l2(y, y64) < TOL
+    assert int(np.argmax(y)) == int(np.argmax(y64))
+
+
+# Block counts covering every launch shape: chunk count 1 (P | 64), split
+# tiles with LDS (C = 2..16, incl. odd nb), and rows too long for chunks.
+NB = [1, 2, 3, 4, 5, 7, 8, 12, 16, 17, 24, 32, 56]
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("nb", NB)
+def test_shapes(qk, torch_gpu, oracle, workloads, qtype, nb):
+    cols = 256 * nb
+    for rows in (1, 3, 65, 257):
+        w, x = workloads.gemv_case(qtype, cols, rows, seed=100 + nb, x_stream=rows)
+        y = run_gemv(qk, torch_gpu, qtype, w, x, cols, rows)
+        assert rel_l2(y, oracle.gemv_f64(qtype, w, x, cols, rows)) < TOL, (nb, rows)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_one_hot_is_bit_exact_column(qk, torch_gpu, oracle, workloads, qtype):
+    cols, rows = 2048, 130
+    w, _ = workloads.gemv_case(qtype, cols, rows, seed=41)
+    W = oracle.dequant(qtype, w, cols, rows)
+    for c in (0, 17, 31, 32, 100, 255, 256, 1023, 2047):
+        e = np.zeros(cols, dtype=np.float32)
+        e[c] = 1.0
+        y = run_gemv(qk, torch_gpu, qtype, w, e, cols, rows)
+        assert np.array_equal(y.view(np.uint32), W[:, c].view(np.uint32)), c
+
+
+def test_multi_qkv_mixed_types(qk, torch_gpu, oracle, workloads, synth):
+    dim, kv = 2048, 512
+    wq, x = workloads.gemv_case(Q4_K, dim, dim, seed=42)
+    wk, _ = workloads.gemv_case(Q4_K, dim, kv, seed=43)
+    wv, _ = workloads.gemv_case(Q6_K, dim, kv, seed=44)
+    t = torch_gpu
+    q = t.empty(dim, device="cuda")
+    k = t.empty(kv, device="cuda")
+    v = t.empty(kv, device="cuda")
+    T = qk.Tensor
+    qk.qkv(T((dim, dim), Q4_K, to_dev(t, wq)), T((dim, kv), Q4_K, to_dev(t, wk)), T((dim, kv), Q6_K, to_dev(t, wv)),
+           to_dev(t, x), q, k, v, dim, kv)
+    t.cuda.synchronize()
+    assert rel_l2(q.cpu().numpy(), oracle.gemv_f64(Q4_K, wq, x, dim, dim)) < TOL
+    assert rel_l2(k.cpu().numpy(), oracle.gemv_f64(Q4_K, wk, x, dim, kv)) < TOL
+    assert rel_l2(v.cpu().numpy(), oracle.gemv_f64(Q6_K, wv, x, dim, kv)) < TOL
+
+
+def test_multi_gate_up(qk, torch_gpu, oracle, workloads):
+    dim, hidden = 2048, 8192
+    wg, x = workloads.gemv_case(Q4_K, dim, hidden, seed=45)
+    wu, _ = workloads.gemv_case(Q4_K, dim, hidden, seed=46)
+    t = torch_gpu
+    g = t.empty(hidden, device="cuda")
+    u = t.empty(hidden, device="cuda")
+    T = qk.Tensor
+    qk.gate_up(T((dim, hidden), Q4_K, to_dev(t, wg)), T((dim, hidden), Q4_K, to_dev(t, wu)), to_dev(t, x), g, u,
+               dim, hidden)
+    t.cuda.synchronize()
+    assert rel_l2(g.cpu().numpy(), oracle.gemv_f64(Q4_K, wg, x, dim, hidden)) < TOL
+    assert rel_l2(u.cpu().numpy(), oracle.gemv_f64(Q4_K, wu, x, dim, hidden)) < TOL
+
+
+def test_ffn_down_q6k_8192(qk, torch_gpu, oracle, workloads):
+    w, x = workloads.gemv_case(Q6_K, 8192, 2048, seed=47)
+    assert rel_l2(run_gemv(qk, torch_gpu, Q6_K, w, x, 8192, 2048), oracle.gemv_f64(Q6_K, w, x, 8192, 2048)) < TOL
+
+
+def test_output_overwritten_and_bounded(qk, torch_gpu, workloads):
+    # y is overwritten (never accumulated) and nothing past rows is written.
+    t = torch_gpu
+    w, x = workloads.gemv_case(Q4_K, 512, 70, seed=48)
+    wd, xd = to_dev(t, w), to_dev(t, x)
+    y = t.full((80,), 12345.0, device="cuda")
+    qk.matvec(qk.Tensor((512, 70), Q4_K, wd), xd, y, 512, 70)
+    first = y.clone()
+    qk.matvec(qk.Tensor((512, 70), Q4_K, wd), xd, y, 512, 70)
+    t.cuda.synchronize()
+    assert t.equal(first, y)
+    assert t.all(y[70:] == 12345.0)
+
+
+def test_validation_errors(qk, torch_gpu):
+    t = torch_gpu
+    x = t.zeros(256, device="cuda")
+    y = t.zeros(4, device="cuda")
+    w = t.zeros(144 * 4, dtype=t.uint8, device="cuda")
+    with pytest.raises(qk.QKError):
+        qk.matvec(qk.Tensor((256, 4), 13, w), x, y, 256, 4)
+    with pytest.raises(qk.QKError):
+        qk.matvec(qk.Tensor((256, 4), Q4_K, w), x, y, 256, 5)
+    rc = qk.lib().qk_gemv_f32(Q4_K, w.data_ptr() + 2, x.data_ptr(), y.data_ptr(), 256, 4, None)
+    assert rc == qk.QK_ERR_ALIGN
