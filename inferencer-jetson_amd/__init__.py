@@ -223,6 +223,9 @@ def batch_matvec(t: Tensor, inp, out, cols: int, rows: int, count: int, workspac
 
 
 def dequant_rows(t: Tensor, out, row0: int, nrows: int, stream=None) -> None:
+    """Rows row0 .. row0+nrows-1 of t as fp32 (q4_value / q6_value, inferencer.cu:454-487)."""
+    if row0 < 0 or nrows < 0 or row0 + nrows > t.rows():
+        raise QKError("dequant_rows", QK_ERR_INVALID_ARG, "row range outside the tensor")
     check(lib().qk_dequant_rows(t.type, t.gpu, ptr(out), t.cols(), row0, nrows, stream_handle(stream)),
           "dequant launch")
 
@@ -253,3 +256,107 @@ def matvec_i8(t: Tensor, xq, xscale, out, cols: int, rows: int, n_tokens: int = 
     ldy = rows if ldy is None else ldy
     check(lib().qk_gemv_i8(t.type, t.gpu, ptr(xq), ldxq, ptr(xscale), ldscale, ptr(out), ldy, cols, rows,
                            n_tokens, stream_handle(stream)), "INT8 matrix launch")
+
+
+class Runner:
+    """FastRunner (inferencer.cu:1182-1532) over the C ABI's decode driver.
+
+    weights is a dict of host numpy arrays (workloads.llama_weights layout);
+    they are copied to device memory owned by this object."""
+
+    def __init__(self, cfg: dict, weights: dict, stream=None):
+        import numpy as np
+        import torch
+        self.cfg = cfg
+        self._dev = []
+
+        def up(a):
+            t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+            self._dev.append(t)
+            return t.data_ptr()
+
+        layers = (qk_llama_layer * cfg["layers"])()
+        for i, L in enumerate(weights["layers"]):
+            for name in ("q", "k", "v", "o", "gate", "up", "down"):
+                setattr(layers[i], name + "_type", L[name + "_type"])
+                setattr(layers[i], name, up(L[name]))
+            layers[i].attn_norm = up(L["attn_norm"])
+            layers[i].ffn_norm = up(L["ffn_norm"])
+        self._layers = layers
+        out = weights.get("output")
+        w = qk_llama_weights(embd_type=weights["embd_type"], token_embd=up(weights["token_embd"]),
+                             output_type=weights.get("output_type", 0), output=up(out) if out is not None else None,
+                             output_norm=up(weights["output_norm"]), layers=layers)
+        c = qk_llama_config(**{k: cfg[k] for k in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab",
+                                                    "context")}, eps=cfg["eps"], rope_theta=cfg["rope_theta"])
+        h = ctypes.c_void_p()
+        check(lib().qk_llama_create(ctypes.byref(c), ctypes.byref(w), stream_handle(stream), ctypes.byref(h)),
+              "FastRunner")
+        self.handle = h
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().qk_llama_destroy(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def kv_cache(self) -> tuple[int, int]:
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib().qk_llama_kv_cache(self.handle, ctypes.byref(k), ctypes.byref(v)), "kv_cache")
+        return k.value, v.value
+
+    def logits_ptr(self) -> int:
+        p = ctypes.c_void_p()
+        check(lib().qk_llama_logits(self.handle, ctypes.byref(p)), "logits")
+        return p.value
+
+    def forward(self, token: int, pos: int, need_logits: bool = True) -> int:
+        nxt = ctypes.c_int(-1)
+        check(lib().qk_llama_forward(self.handle, token, pos, int(need_logits), ctypes.byref(nxt)), "forward")
+        return nxt.value
+
+
+_HIP = None
+
+
+def _hip() -> ctypes.CDLL:
+    """libamdhip64 for plain device<->host copies of buffers the C ABI owns."""
+    global _HIP
+    if _HIP is None:
+        h = ctypes.CDLL("libamdhip64.so")
+        h.hipMemcpy.argtypes = [_vp, _vp, ctypes.c_size_t, _i]
+        h.hipMemcpy.restype = _i
+        _HIP = h
+    return _HIP
+
+
+def copy_to_device(dst: int, host_array) -> None:
+    import numpy as np
+    a = np.ascontiguousarray(host_array)
+    if _hip().hipMemcpy(dst, a.ctypes.data, a.nbytes, 1) != 0:
+        raise QKError("copy_to_device", QK_ERR_DEVICE, "hipMemcpy host->device failed")
+
+
+def copy_to_host(src: int, count: int, dtype) -> "object":
+    import numpy as np
+    out = np.empty(count, dtype=dtype)
+    if _hip().hipMemcpy(out.ctypes.data, src, out.nbytes, 2) != 0:
+        raise QKError("copy_to_host", QK_ERR_DEVICE, "hipMemcpy device->host failed")
+    return out
+
+
+def _runner_load_kv(self, key_cache, value_cache) -> None:
+    """Copy fp32 caches laid out [layer][context][kv_dim] into the runner."""
+    k, v = self.kv_cache()
+    copy_to_device(k, key_cache)
+    copy_to_device(v, value_cache)
+
+
+def _runner_logits(self):
+    import numpy as np
+    return copy_to_host(self.logits_ptr(), self.cfg["vocab"], np.float32)
+
+
+Runner.load_kv = _runner_load_kv
+Runner.logits = _runner_logits

@@ -32,11 +32,16 @@
 #include "qk_internal.h"
 
 #include <algorithm>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace qk {
 namespace {
 
 constexpr int kMaxChunks = 16;
+// Activations staged per workgroup plus the split kernels' reduction slots.
+constexpr size_t kMaxLds = 64 * 1024;
 
 struct GemvMatrix {
     const uint8_t *w;
@@ -92,24 +97,6 @@ __device__ __forceinline__ TileRef locate(const GemvParams &p, int tile, int rit
     return t;
 }
 
-__device__ __forceinline__ Raw fetch(const TileRef &t, int g, int h) {
-    Raw r;
-    if (t.type == QK_TYPE_Q4_K) {
-        r.a = load16(t.blk);                              // d, dmin, scales
-        r.b = load16(t.blk + 16 + g * 64 + h * 16);      // parts 0 / 1
-        r.c = load16(t.blk + 48 + g * 64 + h * 16);      // parts 2 / 3
-        r.s = make_uint2(0, 0);
-        r.d = 0;
-    } else {
-        r.a = load16(t.blk + g * 64 + h * 16);           // ql: parts 0 / 2
-        r.b = load16(t.blk + 32 + g * 64 + h * 16);      // ql: parts 1 / 3
-        r.c = load16(t.blk + 128 + g * 32 + h * 16);     // qh
-        r.s = load8(t.blk + 192 + g * 8);                // scales[g*8 .. g*8+7]
-        r.d = load2(t.blk + 208);
-    }
-    return r;
-}
-
 // 6-bit scale / min of Q4_K sub-blocks 4g + part (q4_scale_min,
 // inferencer.cu:489-497), one per byte.
 __device__ __forceinline__ void q4k_scale_min4(const uint4 &hdr, int g, uint32_t &sc, uint32_t &mn) {
@@ -140,58 +127,150 @@ __device__ __forceinline__ void q6k_scales(const uint2 &s, int h, float *sc) {
 }
 
 // ------------------------------------------------------------ FP32 path --
+//
+// fp32 activations become exact integer work: each 16-column group of x is
+// written as X = rint(x * 2^(21-e)) with e = ilogb(max|x| of the group), so
+// |X| <= 2^22, then split into three signed bytes X = L2*65536 + L1*256 + L0
+// (L0, L1 in [-128, 127], L2 in [-64, 64]).  A part's dot with 16 codes
+// (0..63) is three exact v_dot4_i32_i8 sums, recombined in fp32 and scaled
+// by 2^(e-21): 22 significant bits of every activation relative to its
+// group maximum, i.e. a relative error of at most 2^-22 of the group's
+// largest value per activation, far inside the 1e-5 rel-L2 budget, at a
+// quarter of the VALU work of a convert + fma per weight.  Each workgroup
+// prepares the groups of its token once in LDS (64 B per group); every lane
+// then copies the four groups of its piece into registers.
+
+extern __shared__ __align__(16) unsigned char qk_smem[];
+
+struct XGroup {
+    int limb[12];   // L0 x16, L1 x16, L2 x16 as int8, four per dword
+    float scale;    // 2^(e-21); 0 for an all-zero group, NaN/inf if x is not finite
+    float sum;      // fp32 sum of the 16 activations (min / code-offset terms)
+    int pad[2];
+};
+static_assert(sizeof(XGroup) == 64, "XGroup is one 64-byte LDS record");
+
+__device__ __forceinline__ XGroup make_group(const float *x16) {
+    float v[16];
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 q = *reinterpret_cast<const float4 *>(x16 + 4 * k);
+        v[4 * k] = q.x;
+        v[4 * k + 1] = q.y;
+        v[4 * k + 2] = q.z;
+        v[4 * k + 3] = q.w;
+    }
+    float m = 0.f, s = 0.f;
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        s += v[i];
+    }
+    XGroup gr;
+    gr.sum = s;
+    gr.pad[0] = gr.pad[1] = 0;
+    if (!(m > 0.f) || !isfinite(m)) {
+        #pragma unroll
+        for (int i = 0; i < 12; ++i) gr.limb[i] = 0;
+        gr.scale = m == 0.f ? 0.f : __builtin_nanf("");   // a non-finite input poisons its rows
+        return gr;
+    }
+    // v_frexp_exp gives e+1 for m in [2^e, 2^(e+1)).
+    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
+    uint32_t l0[4] = {0, 0, 0, 0}, l1[4] = {0, 0, 0, 0}, l2[4] = {0, 0, 0, 0};
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int X = static_cast<int>(rintf(ldexpf(v[i], 21 - e)));
+        const int b0 = (X << 24) >> 24;
+        const int X1 = (X - b0) >> 8;
+        const int b1 = (X1 << 24) >> 24;
+        const int b2 = (X1 - b1) >> 8;
+        l0[i >> 2] |= (static_cast<uint32_t>(b0) & 0xFFu) << (8 * (i & 3));
+        l1[i >> 2] |= (static_cast<uint32_t>(b1) & 0xFFu) << (8 * (i & 3));
+        l2[i >> 2] |= (static_cast<uint32_t>(b2) & 0xFFu) << (8 * (i & 3));
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        gr.limb[k] = static_cast<int>(l0[k]);
+        gr.limb[4 + k] = static_cast<int>(l1[k]);
+        gr.limb[8 + k] = static_cast<int>(l2[k]);
+    }
+    gr.scale = ldexpf(1.f, e - 21);
+    return gr;
+}
+
+// sum_i code_i * x_i of one part: codes are four dwords of byte codes 0..63.
+__device__ __forceinline__ float limb_dot(const uint32_t *codes, const int *limb, float scale) {
+    int d0 = 0, d1 = 0, d2 = 0;
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        d0 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[k], d0, false);
+        d1 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[4 + k], d1, false);
+        d2 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[8 + k], d2, false);
+    }
+    return fmaf(static_cast<float>(d2), 65536.f, fmaf(static_cast<float>(d1), 256.f, static_cast<float>(d0))) * scale;
+}
 
 struct F32Policy {
+    static constexpr bool kPrepLds = true;
+
     struct Lane {
-        float xr[64];
+        int limb[4][12];
+        float scale[4];
         float X[4];
     };
 
-    __device__ static void load(Lane &L, const GemvParams &p, int token, int piece) {
-        const int b = piece >> 2, g = (piece >> 1) & 1, h = piece & 1;
-        const float *xs = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx + b * 256 + g * 128 +
-                          h * 16;
+    // LDS bytes of the prepared activations of one token.
+    __host__ __device__ static size_t lds_bytes(int cols) { return static_cast<size_t>(cols / 16) * sizeof(XGroup); }
+
+    // Cooperative: the block writes every 16-column group of its token.
+    __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
+        const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
+        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) lds[gi] = make_group(x + gi * 16);
+    }
+
+    __device__ static void set_part(Lane &L, int part, const XGroup &gr) {
         #pragma unroll
-        for (int part = 0; part < 4; ++part) {
-            float s = 0.f;
-            #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                float4 v = *reinterpret_cast<const float4 *>(xs + part * 32 + k * 4);
-                L.xr[part * 16 + 4 * k + 0] = v.x;
-                L.xr[part * 16 + 4 * k + 1] = v.y;
-                L.xr[part * 16 + 4 * k + 2] = v.z;
-                L.xr[part * 16 + 4 * k + 3] = v.w;
-                s += (v.x + v.y) + (v.z + v.w);
-            }
-            L.X[part] = s;
-        }
+        for (int i = 0; i < 12; ++i) L.limb[part][i] = gr.limb[i];
+        L.scale[part] = gr.scale;
+        L.X[part] = gr.sum;
+    }
+
+    // Group of part `part` of a piece: column b*256 + g*128 + part*32 + h*16.
+    __device__ static int group_of(int piece, int part) {
+        return 16 * (piece >> 2) + 8 * ((piece >> 1) & 1) + 2 * part + (piece & 1);
+    }
+
+    __device__ static void load(Lane &L, const GemvParams &, int, int piece, const XGroup *lds) {
+        #pragma unroll
+        for (int part = 0; part < 4; ++part) set_part(L, part, lds[group_of(piece, part)]);
+    }
+
+    // Without LDS (rows too long to stage): each lane builds its own groups.
+    __device__ static void load_direct(Lane &L, const GemvParams &p, int token, int piece) {
+        const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
+        #pragma unroll
+        for (int part = 0; part < 4; ++part) set_part(L, part, make_group(x + 16 * group_of(piece, part)));
     }
 
     __device__ static float q4k(const Raw &r, const Lane &L, int g) {
         const uint32_t M = 0x0F0F0F0Fu;
-        float S[4] = {0.f, 0.f, 0.f, 0.f};
-        const uint32_t qa[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-        const uint32_t qb[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
-        #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t c[4] = {qa[k] & M, (qa[k] >> 4) & M, qb[k] & M, (qb[k] >> 4) & M};
-            #pragma unroll
-            for (int part = 0; part < 4; ++part) {
-                const float *x = L.xr + part * 16 + 4 * k;
-                S[part] = fmaf(ubyte0(c[part]), x[0], S[part]);
-                S[part] = fmaf(ubyte1(c[part]), x[1], S[part]);
-                S[part] = fmaf(ubyte2(c[part]), x[2], S[part]);
-                S[part] = fmaf(ubyte3(c[part]), x[3], S[part]);
-            }
-        }
+        const uint32_t c0[4] = {r.b.x & M, r.b.y & M, r.b.z & M, r.b.w & M};
+        const uint32_t c1[4] = {(r.b.x >> 4) & M, (r.b.y >> 4) & M, (r.b.z >> 4) & M, (r.b.w >> 4) & M};
+        const uint32_t c2[4] = {r.c.x & M, r.c.y & M, r.c.z & M, r.c.w & M};
+        const uint32_t c3[4] = {(r.c.x >> 4) & M, (r.c.y >> 4) & M, (r.c.z >> 4) & M, (r.c.w >> 4) & M};
+        const float S0 = limb_dot(c0, L.limb[0], L.scale[0]);
+        const float S1 = limb_dot(c1, L.limb[1], L.scale[1]);
+        const float S2 = limb_dot(c2, L.limb[2], L.scale[2]);
+        const float S3 = limb_dot(c3, L.limb[3], L.scale[3]);
         uint32_t sc, mn;
         q4k_scale_min4(r.a, g, sc, mn);
         const float d = f16_bits_to_f32(r.a.x & 0xFFFFu);
         const float dmin = f16_bits_to_f32(r.a.x >> 16);
-        float a = ubyte0(sc) * S[0];
-        a = fmaf(ubyte1(sc), S[1], a);
-        a = fmaf(ubyte2(sc), S[2], a);
-        a = fmaf(ubyte3(sc), S[3], a);
+        float a = ubyte0(sc) * S0;
+        a = fmaf(ubyte1(sc), S1, a);
+        a = fmaf(ubyte2(sc), S2, a);
+        a = fmaf(ubyte3(sc), S3, a);
         float b = ubyte0(mn) * L.X[0];
         b = fmaf(ubyte1(mn), L.X[1], b);
         b = fmaf(ubyte2(mn), L.X[2], b);
@@ -200,29 +279,18 @@ struct F32Policy {
     }
 
     __device__ static float q6k(const Raw &r, const Lane &L, int h) {
-        float S[4] = {0.f, 0.f, 0.f, 0.f};
         const uint32_t la[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
         const uint32_t lb[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
         const uint32_t qh[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+        uint32_t c[4][4];
         #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            uint32_t c[4];
-            q6k_codes(la[k], lb[k], qh[k], c[0], c[1], c[2], c[3]);
-            #pragma unroll
-            for (int part = 0; part < 4; ++part) {
-                const float *x = L.xr + part * 16 + 4 * k;
-                S[part] = fmaf(ubyte0(c[part]), x[0], S[part]);
-                S[part] = fmaf(ubyte1(c[part]), x[1], S[part]);
-                S[part] = fmaf(ubyte2(c[part]), x[2], S[part]);
-                S[part] = fmaf(ubyte3(c[part]), x[3], S[part]);
-            }
-        }
+        for (int k = 0; k < 4; ++k) q6k_codes(la[k], lb[k], qh[k], c[0][k], c[1][k], c[2][k], c[3][k]);
         float sc[4];
         q6k_scales(r.s, h, sc);
-        float a = sc[0] * fmaf(-32.f, L.X[0], S[0]);
-        a = fmaf(sc[1], fmaf(-32.f, L.X[1], S[1]), a);
-        a = fmaf(sc[2], fmaf(-32.f, L.X[2], S[2]), a);
-        a = fmaf(sc[3], fmaf(-32.f, L.X[3], S[3]), a);
+        float a = 0.f;
+        #pragma unroll
+        for (int part = 0; part < 4; ++part)
+            a = fmaf(sc[part], fmaf(-32.f, L.X[part], limb_dot(c[part], L.limb[part], L.scale[part])), a);
         return f16_bits_to_f32(r.d) * a;
     }
 };
@@ -230,13 +298,21 @@ struct F32Policy {
 // ------------------------------------------------------------ INT8 path --
 
 struct I8Policy {
+    static constexpr bool kPrepLds = false;
+    __host__ __device__ static size_t lds_bytes(int) { return 0; }
+    __device__ static void prep(const GemvParams &, int, int, XGroup *) {}
+
     struct Lane {
         int xq[16];       // the piece's 64 int8 activations, 4 per dword
         int xs[4];        // sum of the 16 int8 values of each part
         float scale[4];   // activation scale of each part's 32-value group
     };
 
-    __device__ static void load(Lane &L, const GemvParams &p, int token, int piece) {
+    __device__ static void load(Lane &L, const GemvParams &p, int token, int piece, const XGroup *) {
+        load_direct(L, p, token, piece);
+    }
+
+    __device__ static void load_direct(Lane &L, const GemvParams &p, int token, int piece) {
         const int b = piece >> 2, g = (piece >> 1) & 1, h = piece & 1;
         const int8_t *xq = static_cast<const int8_t *>(p.x) + static_cast<int64_t>(token) * p.ldx + b * 256 + g * 128 +
                            h * 16;
@@ -307,60 +383,147 @@ struct I8Policy {
     }
 };
 
-template <class Policy>
-__device__ __forceinline__ float piece_dot(const TileRef &t, const Raw &r, const typename Policy::Lane &L, int g,
-                                           int h) {
-    return t.type == QK_TYPE_Q4_K ? Policy::q4k(r, L, g) : Policy::q6k(r, L, h);
+// Type dispatch of one piece: TYPE is the storage type when every matrix of
+// the launch shares it, 0 for fused launches over mixed types (then `type`
+// is wave-uniform and the branch is scalar).
+template <int TYPE>
+__device__ __forceinline__ bool is_q4k(int type) {
+    return TYPE == QK_TYPE_Q4_K || (TYPE == 0 && type == QK_TYPE_Q4_K);
 }
 
-__device__ __forceinline__ float group_sum(float v, int group_lanes) {
-    #pragma unroll 1
-    for (int off = group_lanes >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off);
+template <int TYPE>
+__device__ __forceinline__ Raw fetch_typed(const TileRef &t, int g, int h) {
+    Raw r;
+    if (is_q4k<TYPE>(t.type)) {
+        r.a = load16(t.blk);                              // d, dmin, scales
+        r.b = load16(t.blk + 16 + g * 64 + h * 16);      // parts 0 / 1
+        r.c = load16(t.blk + 48 + g * 64 + h * 16);      // parts 2 / 3
+        r.s = make_uint2(0, 0);
+        r.d = 0;
+    } else {
+        r.a = load16(t.blk + g * 64 + h * 16);           // ql: parts 0 / 2
+        r.b = load16(t.blk + 32 + g * 64 + h * 16);      // ql: parts 1 / 3
+        r.c = load16(t.blk + 128 + g * 32 + h * 16);     // qh
+        r.s = load8(t.blk + 192 + g * 8);                // scales[g*8 .. g*8+7]
+        r.d = load2(t.blk + 208);
+    }
+    return r;
+}
+
+template <class Policy, int TYPE>
+__device__ __forceinline__ float piece_dot(int type, const Raw &r, const typename Policy::Lane &L, int g, int h) {
+    return is_q4k<TYPE>(type) ? Policy::q4k(r, L, g) : Policy::q6k(r, L, h);
+}
+
+__device__ __forceinline__ float dpp_add(float v, int ctrl_id) {
+    int moved;
+    const int bits = __builtin_bit_cast(int, v);
+    switch (ctrl_id) {
+        case 0: moved = __builtin_amdgcn_update_dpp(0, bits, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
+        case 1: moved = __builtin_amdgcn_update_dpp(0, bits, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
+        case 2: moved = __builtin_amdgcn_update_dpp(0, bits, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
+        default: moved = __builtin_amdgcn_update_dpp(0, bits, 0x140, 0xF, 0xF, true); break; // row_mirror
+    }
+    return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum over aligned groups of GROUP lanes; every lane of a group receives
+// the group's total.  DPP covers groups up to a 16-lane row; wider groups
+// finish with cross-row shuffles.
+template <int GROUP>
+__device__ __forceinline__ float group_sum(float v) {
+    if (GROUP >= 2) v = dpp_add(v, 0);
+    if (GROUP >= 4) v = dpp_add(v, 1);
+    if (GROUP >= 8) v = dpp_add(v, 2);
+    if (GROUP >= 16) v = dpp_add(v, 3);
+    if (GROUP >= 32) v += __shfl_xor(v, 16);
+    if (GROUP >= 64) v += __shfl_xor(v, 32);
     return v;
 }
 
-// C == 1: every tile lives inside one wave; no LDS, no barriers.
-template <class Policy>
+// One prefetched tile: where its result goes and its raw bytes.
+struct Slot {
+    TileRef t;
+    Raw r;
+};
+
+template <int TYPE>
+__device__ __forceinline__ Slot prep(const GemvParams &p, int tile, int rit, int piece, int token, int g, int h) {
+    Slot s;
+    s.t = locate(p, tile, rit, piece >> 2, token);
+    s.r = fetch_typed<TYPE>(s.t, g, h);
+    return s;
+}
+
+// C == 1 (P divides 64): every tile lives inside one wave; no LDS, no
+// barriers.  GROUP == P lanes per row, 64/P rows per tile.  Each wave keeps
+// two tiles in flight; the prefetch index is clamped to the last tile so the
+// loads are unconditional (a wave's last prefetches re-read a valid tile).
+template <class Policy, int TYPE, int GROUP>
 __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n_waves = blockDim.x >> 6;
     const int token = blockIdx.y;
-    const int rit = lane / p.pieces;
-    const int piece = lane - rit * p.pieces;
+    const int rit = lane / GROUP;
+    const int piece = lane & (GROUP - 1);
     const int g = (piece >> 1) & 1, h = piece & 1;
+    XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
+    if (Policy::kPrepLds) {
+        Policy::prep(p, token, p.pieces * 64, xg);
+        __syncthreads();
+    }
     typename Policy::Lane L;
-    Policy::load(L, p, token, piece);
+    Policy::load(L, p, token, piece, xg);
 
     const int stride = gridDim.x * n_waves;
-    int tile = blockIdx.x * n_waves + wave;
-    if (tile >= p.total_tiles) return;
-    TileRef cur = locate(p, tile, rit, piece >> 2, token);
-    Raw rc = fetch(cur, g, h);
+    const int first = blockIdx.x * n_waves + wave;
+    if (first >= p.total_tiles) return;
+    const int last = p.total_tiles - 1;
+    const int n_iter = (last - first) / stride + 1;
+    Slot a = prep<TYPE>(p, first, rit, piece, token, g, h);
+    Slot b = prep<TYPE>(p, min(first + stride, last), rit, piece, token, g, h);
+    int k = 0;
     while (true) {
-        const int next = tile + stride;
-        const bool more = next < p.total_tiles;
-        TileRef nt;
-        Raw rn;
-        if (more) {
-            nt = locate(p, next, rit, piece >> 2, token);
-            rn = fetch(nt, g, h);
-        }
-        const float v = group_sum(piece_dot<Policy>(cur, rc, L, g, h), p.group_lanes);
-        if (piece == 0 && cur.valid) cur.y[cur.row] = v;
-        if (!more) break;
-        tile = next;
-        cur = nt;
-        rc = rn;
+        float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(a.t.type, a.r, L, g, h));
+        if (piece == 0 && a.t.valid) a.t.y[a.t.row] = v;
+        a = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
+        if (++k == n_iter) break;
+        v = group_sum<GROUP>(piece_dot<Policy, TYPE>(b.t.type, b.r, L, g, h));
+        if (piece == 0 && b.t.valid) b.t.y[b.t.row] = v;
+        b = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
+        if (++k == n_iter) break;
     }
 }
 
-// C > 1: the C waves of a wave-group share each tile; group sums meet in LDS.
-template <class Policy>
+// C > 1: the C waves of a wave-group share each tile; the group sums of a
+// tile meet in LDS (double-buffered, one barrier per tile) and lane t of the
+// group's first wave adds row t's C sums in chunk order.
+template <class Policy, int TYPE, int GROUP>
+__device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, const typename Policy::Lane &L,
+                                           float *red, int k, int tile, int wgroup, int chunk, int lane, int q,
+                                           int g, int h, int token) {
+    const int slots = p.tile_rows * p.chunks;
+    float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(s.t.type, s.r, L, g, h));
+    float *buf = red + (wgroup * 2 + (k & 1)) * slots;
+    if ((lane & (GROUP - 1)) == 0) buf[q / GROUP] = v;
+    __syncthreads();
+    if (tile < p.total_tiles && chunk == 0 && lane < p.tile_rows) {
+        const TileRef rowref = locate(p, tile, lane, 0, token);
+        if (rowref.valid) {
+            float sum = 0.f;
+            for (int c = 0; c < p.chunks; ++c) sum += buf[lane * p.chunks + c];
+            rowref.y[rowref.row] = sum;
+        }
+    }
+}
+
+template <class Policy, int TYPE, int GROUP>
 __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
-    extern __shared__ float red[];
+    XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
+    float *red = reinterpret_cast<float *>(qk_smem + Policy::lds_bytes(p.pieces * 64));
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int token = blockIdx.y;
     const int chunk = wave % p.chunks;
     const int wgroup = wave / p.chunks;
@@ -369,47 +532,27 @@ __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
     const int rit = q / p.pieces;
     const int piece = q - rit * p.pieces;
     const int g = (piece >> 1) & 1, h = piece & 1;
-    const int slots = p.tile_rows * p.chunks;      // group sums per tile
+    if (Policy::kPrepLds) {
+        Policy::prep(p, token, p.pieces * 64, xg);
+        __syncthreads();
+    }
     typename Policy::Lane L;
-    Policy::load(L, p, token, piece);
+    Policy::load(L, p, token, piece, xg);
 
     const int per_iter = gridDim.x * n_wgroups;
-    const int iters = (p.total_tiles + per_iter - 1) / per_iter;
-    int tile = blockIdx.x * n_wgroups + wgroup;
-    bool have = tile < p.total_tiles;
-    TileRef cur{};
-    Raw rc{};
-    if (have) {
-        cur = locate(p, tile, rit, piece >> 2, token);
-        rc = fetch(cur, g, h);
-    }
-    for (int it = 0; it < iters; ++it) {
-        const int next = tile + per_iter;
-        const bool have_next = next < p.total_tiles;
-        TileRef nt{};
-        Raw rn{};
-        if (have_next) {
-            nt = locate(p, next, rit, piece >> 2, token);
-            rn = fetch(nt, g, h);
-        }
-        float v = have ? piece_dot<Policy>(cur, rc, L, g, h) : 0.f;
-        v = group_sum(v, p.group_lanes);
-        float *buf = red + (wgroup * 2 + (it & 1)) * slots;
-        if ((lane & (p.group_lanes - 1)) == 0) buf[q / p.group_lanes] = v;
-        __syncthreads();
-        if (have && chunk == 0 && lane < p.tile_rows) {
-            // Row `lane` of the tile: its C group sums, added in chunk order.
-            const TileRef rowref = locate(p, tile, lane, 0, token);
-            if (rowref.valid) {
-                float s = 0.f;
-                for (int c = 0; c < p.chunks; ++c) s += buf[lane * p.chunks + c];
-                rowref.y[rowref.row] = s;
-            }
-        }
-        tile = next;
-        have = have_next;
-        cur = nt;
-        rc = rn;
+    const int iters = (p.total_tiles + per_iter - 1) / per_iter;   // same for every wave of the block
+    const int first = blockIdx.x * n_wgroups + wgroup;
+    const int last = p.total_tiles - 1;
+    Slot a = prep<TYPE>(p, min(first, last), rit, piece, token, g, h);
+    Slot b = prep<TYPE>(p, min(first + per_iter, last), rit, piece, token, g, h);
+    int k = 0;
+    while (true) {
+        split_step<Policy, TYPE, GROUP>(p, a, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token);
+        a = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
+        if (++k == iters) break;
+        split_step<Policy, TYPE, GROUP>(p, b, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token);
+        b = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
+        if (++k == iters) break;
     }
 }
 
@@ -418,7 +561,7 @@ __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
 template <class Policy>
 __global__ __launch_bounds__(256) void gemv_long(GemvParams p) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n_waves = blockDim.x >> 6;
     const int token = blockIdx.y;
     for (int tile = blockIdx.x * n_waves + wave; tile < p.total_tiles; tile += gridDim.x * n_waves) {
@@ -426,12 +569,12 @@ __global__ __launch_bounds__(256) void gemv_long(GemvParams p) {
         for (int piece = lane; piece < p.pieces; piece += 64) {
             const int g = (piece >> 1) & 1, h = piece & 1;
             typename Policy::Lane L;
-            Policy::load(L, p, token, piece);
+            Policy::load_direct(L, p, token, piece);
             const TileRef t = locate(p, tile, 0, piece >> 2, token);
-            const Raw r = fetch(t, g, h);
-            acc += piece_dot<Policy>(t, r, L, g, h);
+            const Raw r = fetch_typed<0>(t, g, h);
+            acc += piece_dot<Policy, 0>(t.type, r, L, g, h);
         }
-        acc = group_sum(acc, 64);
+        acc = group_sum<64>(acc);
         const TileRef t = locate(p, tile, 0, 0, token);
         if (lane == 0 && t.valid) t.y[t.row] = acc;
     }
@@ -446,11 +589,65 @@ int gcd_int(int a, int b) {
     return a;
 }
 
+// Resident workgroups of a kernel on the current device, cached per
+// (device, kernel, block size, LDS bytes): the occupancy query costs
+// microseconds of host time, more than a small GEMV runs.
 int resident_blocks(const void *kernel, int block, size_t lds) {
+    struct Key {
+        int device;
+        const void *kernel;
+        int block;
+        size_t lds;
+        bool operator==(const Key &o) const {
+            return device == o.device && kernel == o.kernel && block == o.block && lds == o.lds;
+        }
+    };
+    static std::mutex mutex;
+    static std::vector<std::pair<Key, int>> cache;
+    const Key key{device_info().device, kernel, block, lds};
+    {
+        std::lock_guard<std::mutex> lock(mutex);
+        for (const auto &e : cache)
+            if (e.first == key) return e.second;
+    }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
-    return per_cu * device_info().cus;
+    const int total = per_cu * device_info().cus;
+    std::lock_guard<std::mutex> lock(mutex);
+    cache.emplace_back(key, total);
+    return total;
+}
+
+template <class Policy, int TYPE, int GROUP>
+void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
+    const size_t x_lds = Policy::lds_bytes(p.pieces * 64);
+    if (p.chunks == 1) {
+        const int block = 256, waves = block / 64;
+        const void *k = reinterpret_cast<const void *>(gemv_wave<Policy, TYPE, GROUP>);
+        const int cap = std::max(1, resident_blocks(k, block, x_lds) / n_tokens);
+        const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
+        hipLaunchKernelGGL((gemv_wave<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
+    } else {
+        const int wgroups = std::max(1, 4 / p.chunks);
+        const int block = wgroups * p.chunks * 64;
+        const size_t lds = x_lds + static_cast<size_t>(wgroups) * 2 * p.tile_rows * p.chunks * sizeof(float);
+        const void *k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP>);
+        const int cap = std::max(1, resident_blocks(k, block, lds) / n_tokens);
+        const int grid = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
+        hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
+    }
+}
+
+template <class Policy, int TYPE>
+void launch_group(const GemvParams &p, int n_tokens, hipStream_t stream) {
+    switch (p.group_lanes) {
+        case 4: launch_tiled<Policy, TYPE, 4>(p, n_tokens, stream); break;
+        case 8: launch_tiled<Policy, TYPE, 8>(p, n_tokens, stream); break;
+        case 16: launch_tiled<Policy, TYPE, 16>(p, n_tokens, stream); break;
+        case 32: launch_tiled<Policy, TYPE, 32>(p, n_tokens, stream); break;
+        default: launch_tiled<Policy, TYPE, 64>(p, n_tokens, stream); break;
+    }
 }
 
 template <class Policy>
@@ -462,9 +659,10 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
     p.group_lanes = gcd_int(p.pieces, 64);
     p.tile_rows = 64 / p.group_lanes;
     p.chunks = p.pieces / p.group_lanes;
-    const bool long_rows = p.chunks > kMaxChunks;
+    const bool long_rows = p.chunks > kMaxChunks || Policy::lds_bytes(cols) + 4096 > kMaxLds;
     if (long_rows) p.tile_rows = 1;
     int64_t tiles = 0;
+    int type = mats[0].type;
     for (int m = 0; m < n_mats; ++m) {
         GemvMatrix &M = p.mat[m];
         M.w = static_cast<const uint8_t *>(mats[m].w);
@@ -477,6 +675,7 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
         tiles += (M.rows + p.tile_rows - 1) / p.tile_rows;
         if (static_cast<int64_t>(M.rows) * M.row_bytes > (int64_t(1) << 40))
             return fail(QK_ERR_LIMIT, std::string(where) + ": matrix too large");
+        if (M.type != type) type = 0;
     }
     if (tiles > (1 << 30)) return fail(QK_ERR_LIMIT, std::string(where) + ": too many rows");
     if (n_tokens > 65535) return fail(QK_ERR_LIMIT, std::string(where) + ": too many tokens in one launch");
@@ -486,20 +685,12 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
         const int block = 256, waves = block / 64;
         const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, device_info().cus * 8));
         hipLaunchKernelGGL(gemv_long<Policy>, dim3(grid, n_tokens), dim3(block), 0, stream, p);
-    } else if (p.chunks == 1) {
-        const int block = 256, waves = block / 64;
-        const int cap = std::max(1, resident_blocks(reinterpret_cast<const void *>(gemv_wave<Policy>), block, 0) /
-                                        n_tokens);
-        const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
-        hipLaunchKernelGGL(gemv_wave<Policy>, dim3(grid, n_tokens), dim3(block), 0, stream, p);
+    } else if (type == QK_TYPE_Q4_K) {
+        launch_group<Policy, QK_TYPE_Q4_K>(p, n_tokens, stream);
+    } else if (type == QK_TYPE_Q6_K) {
+        launch_group<Policy, QK_TYPE_Q6_K>(p, n_tokens, stream);
     } else {
-        const int wgroups = std::max(1, 4 / p.chunks);
-        const int block = wgroups * p.chunks * 64;
-        const size_t lds = static_cast<size_t>(wgroups) * 2 * p.tile_rows * p.chunks * sizeof(float);
-        const int cap = std::max(1, resident_blocks(reinterpret_cast<const void *>(gemv_split<Policy>), block, lds) /
-                                        n_tokens);
-        const int grid = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
-        hipLaunchKernelGGL(gemv_split<Policy>, dim3(grid, n_tokens), dim3(block), lds, stream, p);
+        launch_group<Policy, 0>(p, n_tokens, stream);
     }
     return launch_status(where);
 }

@@ -92,12 +92,44 @@ float oq_q6k_value(const uint8_t *block, int i) {
     return d * (float)scales[group * 8 + part * 2 + lane / 16] * (float)q;
 }
 
+/* Whole-block forms of oq_q4k_value / oq_q6k_value: the same operations in
+   the same order per element (so the same bits), with the block header
+   decoded once. */
+static void q4k_block(const uint8_t *blk, float *out) {
+    float d = load_f16(blk), dmin = load_f16(blk + 2);
+    for (int sub = 0; sub < 8; ++sub) {
+        int sc, m;
+        oq_q4k_scale_min(blk + 4, sub, &sc, &m);
+        float dsc = d * (float)sc, dm = dmin * (float)m;
+        const uint8_t *q = blk + 16 + (sub / 2) * 32;
+        for (int l = 0; l < 32; ++l) {
+            int code = (sub & 1) ? (q[l] >> 4) : (q[l] & 15);
+            out[sub * 32 + l] = dsc * (float)code - dm;
+        }
+    }
+}
+
+static void q6k_block(const uint8_t *blk, float *out) {
+    const int8_t *scales = (const int8_t *)(blk + 192);
+    float d = load_f16(blk + 208);
+    for (int group = 0; group < 2; ++group)
+        for (int part = 0; part < 4; ++part)
+            for (int lane = 0; lane < 32; ++lane) {
+                int low = blk[group * 64 + (part % 2) * 32 + lane];
+                low = part < 2 ? (low & 15) : (low >> 4);
+                int high = (blk[128 + group * 32 + lane] >> (part * 2)) & 3;
+                int q = (low | (high << 4)) - 32;
+                out[group * 128 + part * 32 + lane] = d * (float)scales[group * 8 + part * 2 + lane / 16] * (float)q;
+            }
+}
+
 static void dequant_row(int type, const uint8_t *row, float *out, int64_t cols) {
     int bpb = oq_block_bytes(type);
     for (int64_t b = 0; b < cols / 256; ++b) {
-        const uint8_t *blk = row + b * bpb;
-        for (int i = 0; i < 256; ++i)
-            out[b * 256 + i] = type == OQ_Q4_K ? oq_q4k_value(blk, i) : oq_q6k_value(blk, i);
+        if (type == OQ_Q4_K)
+            q4k_block(row + b * bpb, out + b * 256);
+        else
+            q6k_block(row + b * bpb, out + b * 256);
     }
 }
 
