@@ -99,6 +99,37 @@ def cpu_baseline_lm_head(workloads, sample_rows: int, target_s: float) -> dict:
                       f"{reps} repetitions in {el:.1f} s, OpenMP static rows, nproc={os.cpu_count()}"}
 
 
+def reference_kernels(torch, args) -> int:
+    """Plain copy / streaming read of 256 MiB buffers (4 rotating sources)."""
+    import ctypes
+    lib = ctypes.CDLL(str(ROOT / "inferencer-jetson_amd" / "libqkbench.so"))
+    vp, sz = ctypes.c_void_p, ctypes.c_size_t
+    lib.qkb_copy.argtypes, lib.qkb_copy.restype = [vp, vp, sz, vp], ctypes.c_int
+    lib.qkb_stream_read.argtypes, lib.qkb_stream_read.restype = [vp, sz, vp, vp], ctypes.c_int
+    lib.qkb_sink_words.restype = ctypes.c_int
+    nbytes = 256 << 20
+    srcs = [torch.full((nbytes // 4,), float(i + 1), device="cuda") for i in range(4)]
+    dst = torch.empty(nbytes // 4, device="cuda")
+    sink = torch.zeros(lib.qkb_sink_words(), dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def launch(i):
+        if args.only == "copy":
+            rc = lib.qkb_copy(srcs[i % 4].data_ptr(), dst.data_ptr(), nbytes, stream.cuda_stream)
+        else:
+            rc = lib.qkb_stream_read(srcs[i % 4].data_ptr(), nbytes, sink.data_ptr(), stream.cuda_stream)
+        if rc:
+            raise RuntimeError(f"bench kernel failed ({rc})")
+
+    wall, kern_ms = time_launches(torch, launch, args.steps, args.warmup, stream)
+    moved = nbytes * (2 if args.only == "copy" else 1)
+    print(json.dumps({"kernel": args.only, "bytes_per_launch": moved, "read_bytes": nbytes,
+                      "write_bytes": nbytes if args.only == "copy" else 0,
+                      "kernel_us": round(kern_ms * 1e3, 2), "GBps": round(moved / (kern_ms * 1e-3) / 1e9, 1)}),
+          flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -108,10 +139,14 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
+    ap.add_argument("--only", choices=["gemv", "copy", "stream"], default="gemv",
+                    help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
+                         "(a plain 256 MiB copy calibrates FETCH_SIZE / WRITE_SIZE; a streaming read gives "
+                         "the practical read ceiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
-              "(the GEMV shards by rows with no communication; see DESIGN.md).", file=sys.stderr)
+              "(the GEMV shards by rows with no communication between GPUs).", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -120,6 +155,8 @@ def main() -> int:
     import inferencer_jetson_amd.workloads as wl
 
     torch.cuda.set_device(0)
+    if args.only != "gemv":
+        return reference_kernels(torch, args)
     stream = torch.cuda.current_stream()
     cols, rows = 2048, 128256
     log(f"[bench] building {args.copies} LM-head copies ({rows}x{cols} Q6_K)")
