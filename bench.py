@@ -8,9 +8,10 @@ from step to step so that the ~256 MB last-level cache cannot serve them;
 all inputs are resident in HBM before timing starts.
 
 value = algorithmic bytes per step (weights + x + y) * steps / wall time of
-the timed region (barrier + synchronize on both sides).  roofline.achieved
-divides the same bytes by the average kernel duration from HIP events
-recorded around every launch on the launch stream.  cpu_baseline times the
+the timed region (synchronize on both sides).  roofline.achieved divides the
+same bytes by the average kernel duration: the span of a HIP event pair
+recorded on the launch stream around the timed launches, divided by the
+number of launches.  cpu_baseline times the
 oracle's OpenMP restatement of the reference's FP32 GEMV (inferencer.cu:
 645-661) on the host cores over a bounded row sample of the same matrix.
 """
@@ -59,21 +60,22 @@ def measured_traffic(name: str):
 
 def time_launches(torch, launch, steps: int, warmup: int, stream):
     """Runs warmup + timed launches; returns (wall seconds of the timed
-    region, mean per-launch kernel ms from events on `stream`)."""
+    region, mean ms per launch from one pair of HIP events recorded on
+    `stream` around the timed launches).  The launches are queued faster
+    than they run, so the event span is the kernels back to back plus the
+    dispatch gaps between them."""
     for i in range(warmup):
         launch(i)
-    torch.cuda.synchronize()
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    start.record(stream)
     for i in range(steps):
-        events[i][0].record(stream)
         launch(warmup + i)
-        events[i][1].record(stream)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [a.elapsed_time(b) for a, b in events]
-    return wall, sum(per) / len(per)
+    return wall, start.elapsed_time(end) / steps
 
 
 def cpu_baseline_lm_head(workloads, sample_rows: int, target_s: float) -> dict:
@@ -145,7 +147,7 @@ def main() -> int:
                          "the practical read ceiling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
               "(the GEMV shards by rows with no communication between GPUs).", file=sys.stderr)
         return 2
 
