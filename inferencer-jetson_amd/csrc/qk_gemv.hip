@@ -97,15 +97,6 @@ __device__ __forceinline__ TileRef locate(const GemvParams &p, int tile, int rit
     return t;
 }
 
-// 6-bit scale / min of Q4_K sub-blocks 4g + part (q4_scale_min,
-// inferencer.cu:489-497), one per byte.
-__device__ __forceinline__ void q4k_scale_min4(const uint4 &hdr, int g, uint32_t &sc, uint32_t &mn) {
-    const uint32_t M = 0x0F0F0F0Fu;
-    const uint32_t s03 = hdr.y, s47 = hdr.z, s811 = hdr.w;
-    sc = g ? ((s811 & M) | ((s03 >> 2) & 0x30303030u)) : (s03 & 0x3F3F3F3Fu);
-    mn = g ? (((s811 >> 4) & M) | ((s47 >> 2) & 0x30303030u)) : (s47 & 0x3F3F3F3Fu);
-}
-
 // Q6_K codes 0..63 of the four parts, one byte each, for dword k.
 __device__ __forceinline__ void q6k_codes(uint32_t la, uint32_t lb, uint32_t qh, uint32_t &c0, uint32_t &c1,
                                           uint32_t &c2, uint32_t &c3) {

@@ -119,4 +119,13 @@ __device__ __forceinline__ float q6k_value(const uint8_t *block, int i) {
     return d * static_cast<float>(sc) * static_cast<float>(q);
 }
 
+// 6-bit scale / min of Q4_K sub-blocks 4g + part (q4_scale_min,
+// inferencer.cu:489-497), one per byte.
+__device__ __forceinline__ void q4k_scale_min4(const uint4 &hdr, int g, uint32_t &sc, uint32_t &mn) {
+    const uint32_t M = 0x0F0F0F0Fu;
+    const uint32_t s03 = hdr.y, s47 = hdr.z, s811 = hdr.w;
+    sc = g ? ((s811 & M) | ((s03 >> 2) & 0x30303030u)) : (s03 & 0x3F3F3F3Fu);
+    mn = g ? (((s811 >> 4) & M) | ((s47 >> 2) & 0x30303030u)) : (s47 & 0x3F3F3F3Fu);
+}
+
 }  // namespace qk

@@ -54,7 +54,7 @@ def test_ffn_3b_ragged_batch(qk, torch_gpu, oracle, workloads):
     wu = oracle.gemv_f64(Q4_K, c["up"], x, dim, hidden)
     for k in range(x.shape[0]):
         assert rel_l2(yg[k], wg[k]) < TOL and rel_l2(yu[k], wu[k]) < TOL
-    h = (wg / (1.0 + np.exp(-wg)) * wu).astype(np.float32)
+    h = (wg / (1.0 + np.exp(-np.clip(wg, -80, 80))) * wu).astype(np.float32)
     yd = run_batched(qk, t, Q6_K, c["down"], h, hidden, dim)
     wd = oracle.gemv_f64(Q6_K, c["down"], h, hidden, dim)
     for k in range(x.shape[0]):
@@ -83,3 +83,100 @@ def test_multi_batched_gate_up(qk, torch_gpu, oracle, workloads):
     for k in range(ntok):
         assert rel_l2(g[k].cpu().numpy(), want_g[k]) < TOL
         assert rel_l2(u[k].cpu().numpy(), want_u[k]) < TOL
+
+
+# ------------------------------------------------ matrix-core path (T >= 8) --
+
+def _fused(qk, t, mats, x, cols, ntok):
+    """qk_gemv_multi_batched_f32 over [(type, w, rows)]; returns the outputs."""
+    arr = (qk.qk_matrix * len(mats))()
+    keep, outs = [], []
+    for i, (qtype, w, rows) in enumerate(mats):
+        wd = to_dev(t, w)
+        y = t.full((ntok, rows), float("nan"), device="cuda")
+        keep.append(wd)
+        outs.append(y)
+        arr[i].type, arr[i].rows, arr[i].w, arr[i].y = qtype, rows, wd.data_ptr(), y.data_ptr()
+    ws_bytes = qk.batch_workspace_bytes(cols, ntok)
+    ws = t.empty(ws_bytes, dtype=t.uint8, device="cuda")
+    xd = to_dev(t, x)
+    qk.check(qk.lib().qk_gemv_multi_batched_f32(arr, len(mats), xd.data_ptr(), cols, cols, ntok, ws.data_ptr(),
+                                                ws_bytes, None), "multi batched")
+    t.cuda.synchronize()
+    return [y.cpu().numpy() for y in outs]
+
+
+@pytest.mark.parametrize("ntok", [8, 40])
+def test_mfma_fused_qkv_mixed_types(qk, torch_gpu, oracle, workloads, ntok):
+    """Llama-3.2-1B QKV: Q4_K q/k, Q6_K v in one launch (mixed-type kernel)."""
+    dim, kv = 2048, 512
+    wq, x = workloads.gemv_case(Q4_K, dim, dim, seed=90, n_tokens=ntok)
+    wk, _ = workloads.gemv_case(Q4_K, dim, kv, seed=91)
+    wv, _ = workloads.gemv_case(Q6_K, dim, kv, seed=92)
+    outs = _fused(qk, torch_gpu, [(Q4_K, wq, dim), (Q4_K, wk, kv), (Q6_K, wv, kv)], x, dim, ntok)
+    for (qtype, w, rows), y in zip([(Q4_K, wq, dim), (Q4_K, wk, kv), (Q6_K, wv, kv)], outs):
+        want = oracle.gemv_f64(qtype, w, x, dim, rows)
+        for k in range(ntok):
+            assert rel_l2(y[k], want[k]) < TOL, (qtype, rows, k)
+
+
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+@pytest.mark.parametrize("cols,rows,ntok", [(8192, 300, 8), (3072, 130, 64), (256, 64, 9)])
+def test_mfma_shapes(qk, torch_gpu, oracle, workloads, qtype, cols, rows, ntok):
+    w, x = workloads.gemv_case(qtype, cols, rows, seed=93 + ntok, n_tokens=ntok)
+    y = run_batched(qk, torch_gpu, qtype, w, x, cols, rows)
+    want = oracle.gemv_f64(qtype, w, x, cols, rows)
+    for k in range(ntok):
+        assert rel_l2(y[k], want[k]) < TOL, k
+
+
+def test_mfma_scaled_and_zero_tokens(qk, torch_gpu, oracle, workloads):
+    """Per-(token, block) scaling: tokens of very different magnitudes, an
+    all-zero token (exact zeros) and a token with one huge outlier."""
+    cols, rows, ntok = 2048, 256, 12
+    w, x = workloads.gemv_case(Q4_K, cols, rows, seed=97, n_tokens=ntok)
+    x = x.copy()
+    x[1] *= 1e-30
+    x[2] *= 1e30
+    x[3] = 0.0
+    x[4, 77] = 1e6
+    x[5, :256] = 0.0
+    y = run_batched(qk, torch_gpu, Q4_K, w, x, cols, rows)
+    want = oracle.gemv_f64(Q4_K, w, x, cols, rows)
+    assert np.all(y[3] == 0.0)
+    for k in range(ntok):
+        if k != 3:
+            assert rel_l2(y[k], want[k]) < TOL, k
+
+
+def test_mfma_nonfinite_token_is_isolated(qk, torch_gpu, oracle, workloads):
+    cols, rows, ntok = 512, 64, 9
+    w, x = workloads.gemv_case(Q6_K, cols, rows, seed=98, n_tokens=ntok)
+    x = x.copy()
+    x[4, 300] = np.inf
+    y = run_batched(qk, torch_gpu, Q6_K, w, x, cols, rows)
+    want = oracle.gemv_f64(Q6_K, w, x, cols, rows)
+    assert np.all(np.isnan(y[4]))
+    for k in range(ntok):
+        if k != 4:
+            assert rel_l2(y[k], want[k]) < TOL, k
+
+
+def test_mfma_deterministic(qk, torch_gpu, workloads):
+    cols, rows, ntok = 8192, 200, 32
+    w, x = workloads.gemv_case(Q6_K, cols, rows, seed=99, n_tokens=ntok)
+    a = run_batched(qk, torch_gpu, Q6_K, w, x, cols, rows)
+    b = run_batched(qk, torch_gpu, Q6_K, w, x, cols, rows)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_mfma_needs_workspace(qk, torch_gpu, workloads):
+    t = torch_gpu
+    cols, rows, ntok = 512, 64, 8
+    w, x = workloads.gemv_case(Q4_K, cols, rows, seed=100, n_tokens=ntok)
+    need = qk.batch_workspace_bytes(cols, ntok)
+    ws = t.empty(need, dtype=t.uint8, device="cuda")
+    y = t.empty((ntok, rows), device="cuda")
+    with pytest.raises(qk.QKError) as e:
+        qk.batch_matvec(qk.Tensor((cols, rows), Q4_K, to_dev(t, w)), to_dev(t, x), y, cols, rows, ntok, ws, need - 16)
+    assert e.value.status == qk.QK_ERR_INVALID_ARG
