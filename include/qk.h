@@ -85,19 +85,24 @@ typedef struct qk_matrix {
 int qk_gemv_multi_f32(const qk_matrix *mats, int n_mats, const float *x, int cols,
                       qk_stream stream);
 
-/* Device workspace the multi-token calls need for n_tokens tokens of cols
-   activations (the packed activation tile; 0 when none is needed).  It plays
-   the part of the reference's preallocated batch_xq / batch_xscale buffers
-   (inferencer.cu:1237-1238). */
-size_t qk_gemv_batched_workspace_bytes(int cols, int n_tokens);
+/* Device workspace a multi-token call needs: cols activations, `rows` output
+   rows in total (the sum over the matrices of a fused call) and n_tokens
+   tokens.  From 8 tokens on it holds the activations packed for the matrix
+   cores (4.1 KiB per token and 256 columns, tokens rounded up to 32) and,
+   when one row group's blocks are split over several workgroups, their
+   partial sums; below 8 tokens it is 0 and the pointer may be NULL.  It
+   plays the part of the reference's preallocated batch buffers
+   (inferencer.cu:1237-1238) and never needs clearing.  Base alignment 256
+   bytes. */
+size_t qk_gemv_batched_workspace_bytes(int cols, int rows, int n_tokens);
 
 /* Multi-token variant: y[t*ldy + r] = sum_c W[r][c] * x[t*ldx + c] for
    t < n_tokens (token-major like inferencer.cu:698).  FP32 semantics of the
    reference's INT8-only batched path FastRunner::batch_matvec +
    gemv_batch_dp4a (inferencer.cu:1265-1278, 678-699), without its 32-token
    cap; n_tokens = 0 is a no-op.  workspace holds at least
-   qk_gemv_batched_workspace_bytes(cols, n_tokens) device bytes and must not
-   be shared by calls in flight at the same time. */
+   qk_gemv_batched_workspace_bytes(cols, rows, n_tokens) device bytes and
+   must not be shared by calls in flight at the same time. */
 int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float *y, int ldy,
                         int cols, int rows, int n_tokens, void *workspace,
                         size_t workspace_bytes, qk_stream stream);

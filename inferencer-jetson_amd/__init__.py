@@ -75,7 +75,7 @@ SIGNATURES = {
     "qk_tensor_bytes": (ctypes.c_int64, [_i, ctypes.c_int64, ctypes.c_int64]),
     "qk_gemv_f32": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
     "qk_gemv_multi_f32": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _vp]),
-    "qk_gemv_batched_workspace_bytes": (ctypes.c_size_t, [_i, _i]),
+    "qk_gemv_batched_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i]),
     "qk_gemv_batched_f32": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
     "qk_gemv_multi_batched_f32": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
     "qk_dequant_rows": (_i, [_i, _vp, _vp, _i, _i, _i, _vp]),
@@ -207,8 +207,9 @@ def gate_up(wgate: Tensor, wup: Tensor, x, gate, up, dim: int, hidden: int, stre
     multi_matvec([(wgate, gate), (wup, up)], x, dim, stream)
 
 
-def batch_workspace_bytes(cols: int, count: int) -> int:
-    return int(lib().qk_gemv_batched_workspace_bytes(cols, count))
+def batch_workspace_bytes(cols: int, rows: int, count: int) -> int:
+    """Workspace bytes of a multi-token call (rows: total output rows)."""
+    return int(lib().qk_gemv_batched_workspace_bytes(cols, rows, count))
 
 
 def batch_matvec(t: Tensor, inp, out, cols: int, rows: int, count: int, workspace=None,

@@ -20,15 +20,23 @@
 // (and dmin with the sub-block sums X, through v_mfma_f32_32x32x8_f16) and
 // the activation scale are applied in fp32 when the block is done.
 //
-// Two kernels:
-//   pack_activations  x -> per (32-token tile, block) records in the caller's
-//                     workspace, laid out as MFMA A operands.
-//   batch_mfma        one wave = 64 weight rows x 32 tokens over a run of
-//                     blocks; the waves of a workgroup split the row's blocks
-//                     and meet in LDS (fixed order, deterministic).
-// The weights are MFMA B operands decoded in registers from the raw block
-// bytes: lane l owns weight row l%32 and block half l/32.
+// Three kernels:
+//   pack_activations  once per (block, 32-token tile): x -> the record of
+//                     MFMA A operands (fp16 hi / lo, sub-block sums, scales)
+//                     in the caller's workspace.
+//   batch_mfma        a workgroup (4 waves) owns 128 weight rows x one token
+//                     tile x a run of blocks.  Per block it copies the record
+//                     into LDS (double-buffered: the next record and the next
+//                     block's weight bytes load while this block computes) and
+//                     each wave decodes the raw bytes of its 32 rows into MFMA
+//                     B operands in registers (lane l: row l%32, block half
+//                     l/32).  When one row group's blocks are split over
+//                     several workgroups (to put enough waves on the chip),
+//                     each writes its partial sums to the workspace;
+//   reduce_splits     adds them in split order, so results are deterministic.
 #include "qk_internal.h"
+
+#include <algorithm>
 
 namespace qk {
 int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
@@ -44,21 +52,22 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaMinTokens = 8;
 constexpr int kTokTile = 32;            // tokens per MFMA tile (the A rows)
-constexpr int kRowTiles = 2;            // 32-row MFMA column tiles per wave
-constexpr int kGroupRows = 32 * kRowTiles;
-constexpr int kMaxSplit = 8;            // waves per workgroup splitting the blocks
+constexpr int kGroupRows = 128;         // weight rows per workgroup (4 waves x 32)
+constexpr int kMaxSplit = 4;            // workgroups splitting one row group's blocks
+constexpr int kTargetGroups = 512;      // two workgroups per CU
 
-// One (token tile, block) record of packed activations.
+// LDS tile of one block's activations for one 32-token tile, in MFMA A
+// operand order:
 //   hi   [16 steps][2 halves][32 tokens][8]  fp16   16 KiB
 //   lo   same                                fp16   16 KiB
 //   mhi  [2 halves][32 tokens][4]            fp16   512 B  (sub-block sums / 64)
 //   mlo  same                                fp16   512 B
-//   f    [2 halves][16]                      fp32   128 B  (2^e per token, lane order)
-constexpr size_t kRecA = 16384;
-constexpr size_t kRecM = 512;
-constexpr size_t kRecF = 128;
-constexpr size_t kRecBytes = 2 * kRecA + 2 * kRecM + kRecF;
-static_assert(kRecBytes % 16 == 0, "records keep 16-byte alignment");
+//   f    [2 halves][16]                      fp32   128 B  (2^-shift per token, lane order)
+constexpr int kTileA = 16384;
+constexpr int kTileM = 512;
+constexpr int kTileF = 128;
+constexpr int kTileBytes = 2 * kTileA + 2 * kTileM + kTileF;
+static_assert(kTileBytes % 16 == 0, "tiles keep 16-byte alignment");
 
 // K order of the A / B operands inside a block.  Step s (0..15) and half kh
 // (lane / 32) hold eight columns of the 64-column group G = 2*kh + s/8:
@@ -67,92 +76,6 @@ static_assert(kRecBytes % 16 == 0, "records keep 16-byte alignment");
 // i.e. the low nibbles (e < 4) and high nibbles (e >= 4) of Q4_K qs bytes
 // G*32 + 4*(s%8) .. +3, even bytes first; Q6_K uses the same columns.
 
-// ------------------------------------------------------------- packing --
-
-__global__ __launch_bounds__(256) void pack_activations(const float *__restrict__ x, int ldx, int n_tokens, int nb,
-                                                        uint8_t *__restrict__ ws) {
-    const int b = blockIdx.x, tile = blockIdx.y;
-    const int tl = threadIdx.x >> 3;           // token within the tile
-    const int q = threadIdx.x & 7;             // 32-column sub-block of the block
-    const int t = tile * kTokTile + tl;
-    float v[32];
-    if (t < n_tokens) {
-        const float4 *src = reinterpret_cast<const float4 *>(x + static_cast<int64_t>(t) * ldx + b * 256 + q * 32);
-        #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 u = src[i];
-            v[4 * i] = u.x;
-            v[4 * i + 1] = u.y;
-            v[4 * i + 2] = u.z;
-            v[4 * i + 3] = u.w;
-        }
-    } else {
-        #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = 0.f;
-    }
-    float m = 0.f;
-    #pragma unroll
-    for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(v[i]));
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    // x' = x * 2^(14-e), e = floor(log2 max): the block maximum in [2^14, 2^15).
-    // The shift is capped at 140 so that 2^-shift stays a finite nonzero fp32.
-    int shift = 0;
-    float f = 0.f;
-    bool bad = false;
-    #pragma unroll
-    for (int i = 0; i < 32; ++i) bad |= !isfinite(v[i]);
-    if (m > 0.f && isfinite(m)) {
-        shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
-        f = ldexpf(1.f, -shift);
-    }
-    bad = __shfl_xor(static_cast<int>(bad), 1) | bad;
-    bad = __shfl_xor(static_cast<int>(bad), 2) | bad;
-    bad = __shfl_xor(static_cast<int>(bad), 4) | bad;
-    if (bad) f = __builtin_nanf("");            // a non-finite input poisons the token's outputs
-
-    uint8_t *rec = ws + (static_cast<size_t>(tile) * nb + b) * kRecBytes;
-    _Float16 *hi = reinterpret_cast<_Float16 *>(rec);
-    _Float16 *lo = reinterpret_cast<_Float16 *>(rec + kRecA);
-    const int G = q >> 1, half = q & 1, kh = G >> 1, hf = G & 1;
-    float sum = 0.f;
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int s = hf * 8 + j;
-        half4 h4, l4;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float xs = bad ? 0.f : ldexpf(v[4 * j + i], shift);
-            sum += xs;
-            const _Float16 h = static_cast<_Float16>(xs);
-            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
-            h4[e] = h;
-            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
-        }
-        const size_t at = (static_cast<size_t>((s * 2 + kh) * 32 + tl)) * 8 + half * 4;
-        *reinterpret_cast<half4 *>(hi + at) = h4;
-        *reinterpret_cast<half4 *>(lo + at) = l4;
-    }
-    // Sub-block sums for the Q4_K min term: K index j = q, lane half q/4.
-    _Float16 *mhi = reinterpret_cast<_Float16 *>(rec + 2 * kRecA);
-    _Float16 *mlo = reinterpret_cast<_Float16 *>(rec + 2 * kRecA + kRecM);
-    // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
-    const float s64 = sum * (1.f / 64.f);
-    const _Float16 sh = static_cast<_Float16>(s64);
-    const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
-    mhi[mat] = sh;
-    mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
-    // Token scales in the accumulator lane order: lane half kh' = (tl/4)%2,
-    // register k = 4*(tl/8) + tl%4.
-    if (q == 0) {
-        float *fr = reinterpret_cast<float *>(rec + 2 * kRecA + 2 * kRecM);
-        fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
-    }
-}
-
-// ---------------------------------------------------------------- GEMM --
-
 struct BatchMatrix {
     const uint8_t *w;
     float *y;
@@ -160,23 +83,130 @@ struct BatchMatrix {
     int type;
     int row_bytes;
     int ldy;
-    int group_begin;   // first 64-row group of this matrix in the launch
+    int group_begin;   // first 128-row group of this matrix in the launch
 };
 
 struct BatchParams {
     BatchMatrix mat[QK_MAX_FUSED];
     int n_mats;
-    const uint8_t *ws;
-    int nb;
+    const float *x;
+    int ldx;
     int n_tokens;
-    int blocks_per_wave;
+    int nb;
+    int tiles;
+    int splits;             // workgroups sharing one row group's blocks
+    int blocks_per_split;
+    float *partials;        // [group][tile][split][4096] when splits > 1
+    const uint8_t *records; // packed activations, [tile][block][kTileBytes]
 };
+
+// ---------------------------------------------------- activation staging --
+//
+// Thread (tl = tid/8, q = tid%8) owns token tl of the tile and the 32
+// columns q*32 .. q*32+31 (Q4_K sub-block q) of the block.
+
+struct XStage {
+    float v[32];
+};
+
+__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, XStage &s) {
+    const int tl = threadIdx.x >> 3, q = threadIdx.x & 7;
+    const int t = tile * kTokTile + tl;
+    if (t < p.n_tokens) {
+        const float4 *src = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32);
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 u = src[i];
+            s.v[4 * i] = u.x;
+            s.v[4 * i + 1] = u.y;
+            s.v[4 * i + 2] = u.z;
+            s.v[4 * i + 3] = u.w;
+        }
+    } else {
+        #pragma unroll
+        for (int i = 0; i < 32; ++i) s.v[i] = 0.f;
+    }
+}
+
+// x' = x * 2^shift with the block maximum of the token in [2^14, 2^15)
+// (shift capped at 140 so 2^-shift stays a nonzero fp32), split into fp16
+// hi + lo; a non-finite activation makes the token's scale NaN.
+__device__ __forceinline__ void stage_store(const XStage &s, uint8_t *tile) {
+    const int tl = threadIdx.x >> 3, q = threadIdx.x & 7;
+    float m = 0.f;
+    bool bad = false;
+    #pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        m = fmaxf(m, fabsf(s.v[i]));
+        bad |= !isfinite(s.v[i]);
+    }
+    m = fmaxf(m, __shfl_xor(m, 1));
+    m = fmaxf(m, __shfl_xor(m, 2));
+    m = fmaxf(m, __shfl_xor(m, 4));
+    int nb_bad = bad ? 1 : 0;
+    nb_bad |= __shfl_xor(nb_bad, 1);
+    nb_bad |= __shfl_xor(nb_bad, 2);
+    nb_bad |= __shfl_xor(nb_bad, 4);
+    int shift = 0;
+    float f = 0.f;
+    if (m > 0.f && isfinite(m)) {
+        shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
+        f = ldexpf(1.f, -shift);
+    }
+    if (nb_bad) f = __builtin_nanf("");
+
+    _Float16 *hi = reinterpret_cast<_Float16 *>(tile);
+    _Float16 *lo = reinterpret_cast<_Float16 *>(tile + kTileA);
+    const int G = q >> 1, half = q & 1, kh = G >> 1, hf = G & 1;
+    float sum = 0.f;
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int st = hf * 8 + j;
+        half4 h4, l4;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float xs = nb_bad ? 0.f : ldexpf(s.v[4 * j + i], shift);
+            sum += xs;
+            const _Float16 h = static_cast<_Float16>(xs);
+            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
+            h4[e] = h;
+            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
+        }
+        const int at = ((st * 2 + kh) * 32 + tl) * 8 + half * 4;
+        *reinterpret_cast<half4 *>(hi + at) = h4;
+        *reinterpret_cast<half4 *>(lo + at) = l4;
+    }
+    // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
+    const float s64 = sum * (1.f / 64.f);
+    const _Float16 sh = static_cast<_Float16>(s64);
+    _Float16 *mhi = reinterpret_cast<_Float16 *>(tile + 2 * kTileA);
+    _Float16 *mlo = reinterpret_cast<_Float16 *>(tile + 2 * kTileA + kTileM);
+    const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
+    mhi[mat] = sh;
+    mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
+    // Token scales in accumulator lane order: lane half (tl/4)%2, register 4*(tl/8) + tl%4.
+    if (q == 0) {
+        float *fr = reinterpret_cast<float *>(tile + 2 * kTileA + 2 * kTileM);
+        fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
+    }
+}
+
+// One workgroup per (block, 32-token tile): the tile's activations of the
+// block, packed once into the workspace record the GEMM copies into LDS.
+__global__ __launch_bounds__(256) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
+    const int b = blockIdx.x, tile = blockIdx.y;
+    XStage xs;
+    stage_load(p, tile, b, xs);
+    stage_store(xs, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
+}
+
+// ------------------------------------------------------- weight operands --
 
 // Raw bytes of one block of one row that lane half kh needs.
 struct RawBlock {
     uint4 q[4];        // Q4_K: qs[kh*64 .. +64); Q6_K: ql[kh*64 .. +64)
     uint4 h[2];        // Q6_K: qh[kh*32 .. +32)
-    uint4 hdr;         // Q4_K: d, dmin, scales; Q6_K: x = scales[kh*8 .. +4), y = scales[kh*8+4 .. +8), z = d
+    uint4 hdr;         // Q4_K: d, dmin, scales; Q6_K: x, y = scales[kh*8 .. +8), z = d
 };
 
 template <int TYPE>
@@ -197,8 +227,8 @@ __device__ __forceinline__ RawBlock load_block(const uint8_t *blk, int type, int
         for (int i = 0; i < 4; ++i) r.q[i] = load16(blk + kh * 64 + 16 * i);
         r.h[0] = load16(blk + 128 + kh * 32);
         r.h[1] = load16(blk + 128 + kh * 32 + 16);
-        const uint2 s = load8(blk + 192 + kh * 8);
-        r.hdr = make_uint4(s.x, s.y, load2(blk + 208), 0);
+        const uint2 sc = load8(blk + 192 + kh * 8);
+        r.hdr = make_uint4(sc.x, sc.y, load2(blk + 208), 0);
     }
     return r;
 }
@@ -208,61 +238,159 @@ __device__ __forceinline__ uint32_t word(const uint4 *v, int i) {
     return (i & 3) == 0 ? u.x : (i & 3) == 1 ? u.y : (i & 3) == 2 ? u.z : u.w;
 }
 
-// Two bytes (0 and 2, or 1 and 3 after a shift) of v as two fp16 integers
-// minus `bias`: 0x6400 | n is the fp16 1024 + n.
-__device__ __forceinline__ uint32_t bytes_to_h2(uint32_t v, _Float16 bias) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const uint32_t bits = (v & 0x00FF00FFu) | 0x64006400u;
-    h2 r = __builtin_bit_cast(h2, bits);
-    const h2 b = {bias, bias};
-    r = r - b;
-    return __builtin_bit_cast(uint32_t, r);
-}
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t mul_h2(uint32_t a, _Float16 s) {
-    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-    const h2 m = {s, s};
-    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, a) * m);
+// Bytes 0 and 2 (sel 0x04020400) or 1 and 3 (sel 0x04030401) of v as the
+// fp16 halves 0x64nn = 1024 + n, then fma(1024 + n, s, bias) with bias =
+// -(1024 + offset) * s: the exact product (n - offset) * s, rounded once.
+__device__ __forceinline__ uint32_t nib_h2(uint32_t v, uint32_t sel, half2v s, half2v bias) {
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, v, sel);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(half2v, h), s, bias));
 }
 
 // B operand of step j (0..7) of block half hf: eight exact fp16 integer
-// weights in the K order above.
+// weights in the K order above; (sa, ba) scale columns e < 4 and (sb, bb)
+// columns e >= 4.
 template <int TYPE>
-__device__ __forceinline__ half8 decode_b(const RawBlock &r, int type, int hf, int j, _Float16 sa, _Float16 sb) {
+__device__ __forceinline__ half8 decode_b(const RawBlock &r, int type, int hf, int j, half2v sa, half2v ba,
+                                          half2v sb, half2v bb) {
     uint32_t c0, c1;
-    _Float16 bias;
     if (is_q4<TYPE>(type)) {
         const uint32_t w = word(r.q, hf * 8 + j);
         c0 = w & 0x0F0F0F0Fu;
         c1 = (w >> 4) & 0x0F0F0F0Fu;
-        bias = static_cast<_Float16>(1024.f);
     } else {
         const uint32_t la = word(r.q, j), lb = word(r.q, 8 + j), hq = word(r.h, j);
         const int sh = 4 * hf;
         c0 = ((la >> sh) & 0x0F0F0F0Fu) | (((hq >> sh) & 0x03030303u) << 4);
         c1 = ((lb >> sh) & 0x0F0F0F0Fu) | (((hq >> (sh + 2)) & 0x03030303u) << 4);
-        bias = static_cast<_Float16>(1056.f);   // 1024 + 32: code - 32
     }
     uint4 out;
-    out.x = mul_h2(bytes_to_h2(c0, bias), sa);
-    out.y = mul_h2(bytes_to_h2(c0 >> 8, bias), sa);
-    out.z = mul_h2(bytes_to_h2(c1, bias), sb);
-    out.w = mul_h2(bytes_to_h2(c1 >> 8, bias), sb);
+    out.x = nib_h2(c0, 0x04020400u, sa, ba);
+    out.y = nib_h2(c0, 0x04030401u, sa, ba);
+    out.z = nib_h2(c1, 0x04020400u, sb, bb);
+    out.w = nib_h2(c1, 0x04030401u, sb, bb);
     return __builtin_bit_cast(half8, out);
 }
 
-__device__ __forceinline__ float16v mfma16(half8 a, half8 b, float16v c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ _Float16 u8_to_h(uint32_t v) { return static_cast<_Float16>(static_cast<float>(v & 0xFFu)); }
+__device__ __forceinline__ _Float16 s8_to_h(uint32_t v) {
+    return static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(v & 0xFFu)));
+}
+
+// acc += this block's contribution (32 tokens x the lane's row).
+template <int TYPE>
+__device__ __forceinline__ void block_mfma(const RawBlock &r, int type, const uint8_t *tile_lds, int kh, int col,
+                                           float16v &acc) {
+    const float4 *fr = reinterpret_cast<const float4 *>(tile_lds + 2 * kTileA + 2 * kTileM) + kh * 4;
+    float f[16];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 u = fr[i];
+        f[4 * i] = u.x;
+        f[4 * i + 1] = u.y;
+        f[4 * i + 2] = u.z;
+        f[4 * i + 3] = u.w;
+    }
+    float d, dmin = 0.f;
+    uint32_t sc4 = 0, mn4 = 0;
+    if (is_q4<TYPE>(type)) {
+        d = f16_bits_to_f32(r.hdr.x & 0xFFFFu);
+        dmin = f16_bits_to_f32(r.hdr.x >> 16);
+        q4k_scale_min4(r.hdr, kh, sc4, mn4);
+    } else {
+        d = f16_bits_to_f32(r.hdr.z);
+    }
+    const half8 *ahp = reinterpret_cast<const half8 *>(tile_lds) + kh * 32 + col;
+    const half8 *alp = reinterpret_cast<const half8 *>(tile_lds + kTileA) + kh * 32 + col;
+    float16v t;
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) t[k] = 0.f;
+    #pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+        #pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            _Float16 sa, sb, off;
+            if (is_q4<TYPE>(type)) {
+                sa = u8_to_h(sc4 >> (16 * hf));
+                sb = u8_to_h(sc4 >> (16 * hf + 8));
+                off = static_cast<_Float16>(-1024.f);
+            } else {
+                // scales[kh*8 + 4*hf + 2*half + j/4]
+                const uint32_t sw = hf ? r.hdr.y : r.hdr.x;
+                sa = s8_to_h(sw >> (8 * (j >> 2)));
+                sb = s8_to_h(sw >> (8 * (j >> 2) + 16));
+                off = static_cast<_Float16>(-1056.f);   // code - 32
+            }
+            const half2v sa2 = {sa, sa}, sb2 = {sb, sb};
+            const half2v ba2 = {static_cast<_Float16>(off * sa), static_cast<_Float16>(off * sa)};
+            const half2v bb2 = {static_cast<_Float16>(off * sb), static_cast<_Float16>(off * sb)};
+            const half8 bw = decode_b<TYPE>(r, type, hf, j, sa2, ba2, sb2, bb2);
+            const int st = hf * 8 + j;
+            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahp[st * 64], bw, t, 0, 0, 0);
+            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(alp[st * 64], bw, t, 0, 0, 0);
+        }
+    }
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] = fmaf(d * f[k], t[k], acc[k]);
+    if (is_q4<TYPE>(type)) {
+        const half4 mh = reinterpret_cast<const half4 *>(tile_lds + 2 * kTileA)[kh * 32 + col];
+        const half4 ml = reinterpret_cast<const half4 *>(tile_lds + 2 * kTileA + kTileM)[kh * 32 + col];
+        half4 bm;
+        #pragma unroll
+        for (int e = 0; e < 4; ++e) bm[e] = u8_to_h(mn4 >> (8 * e));
+        float16v tm;
+        #pragma unroll
+        for (int k = 0; k < 16; ++k) tm[k] = 0.f;
+        tm = __builtin_amdgcn_mfma_f32_32x32x8f16(mh, bm, tm, 0, 0, 0);
+        tm = __builtin_amdgcn_mfma_f32_32x32x8f16(ml, bm, tm, 0, 0, 0);
+        #pragma unroll
+        for (int k = 0; k < 16; ++k) acc[k] = fmaf(-64.f * dmin * f[k], tm[k], acc[k]);
+    }
+}
+
+// ---------------------------------------------------------------- GEMM --
+//
+// Workgroup = 4 waves = 128 weight rows (32 per wave, lane l -> row l%32,
+// block half l/32) x one 32-token tile x a run of blocks.  Per block the
+// workgroup stages the activations once in LDS (double-buffered) and each
+// wave decodes its rows' raw block bytes into MFMA B operands; the next
+// block's activations and weight bytes are loaded while this one computes.
+
+// Copy of one packed record into LDS in 16-byte chunks: the 2048 chunks of
+// the fp16 operands, eight per thread, then the 72 chunks of sums and
+// scales (every thread loads one, clamped; the first 72 store theirs).
+constexpr int kChunks = kTileBytes / 16;
+constexpr int kMainChunks = 2 * kTileA / 16;
+constexpr int kTailChunks = kChunks - kMainChunks;
+static_assert(kMainChunks == 8 * 256 && kTailChunks <= 256, "record copy layout");
+
+struct RecordStage {
+    uint4 v[8];
+    uint4 tail;
+};
+
+__device__ __forceinline__ void record_load(const uint8_t *rec, RecordStage &s) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(rec);
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) s.v[i] = src[i * 256 + threadIdx.x];
+    s.tail = src[kMainChunks + min(static_cast<int>(threadIdx.x), kTailChunks - 1)];
+}
+
+__device__ __forceinline__ void record_store(const RecordStage &s, uint8_t *tile_lds) {
+    uint4 *dst = reinterpret_cast<uint4 *>(tile_lds);
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i * 256 + threadIdx.x] = s.v[i];
+    if (threadIdx.x < kTailChunks) dst[kMainChunks + threadIdx.x] = s.tail;
 }
 
 template <int TYPE>
-__global__ __launch_bounds__(64 * kMaxSplit) void batch_mfma(BatchParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void batch_mfma(BatchParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n_waves = blockDim.x >> 6;
     const int kh = lane >> 5, col = lane & 31;
-    const int group = blockIdx.x, tile = blockIdx.y;
+    const int split = blockIdx.x % p.splits, group = blockIdx.x / p.splits, tile = blockIdx.y;
 
     int m = 0;
     #pragma unroll
@@ -270,135 +398,75 @@ __global__ __launch_bounds__(64 * kMaxSplit) void batch_mfma(BatchParams p) {
     m = __builtin_amdgcn_readfirstlane(m);
     const BatchMatrix &M = p.mat[m];
     const int type = TYPE ? TYPE : M.type;
-    const int row0 = (group - M.group_begin) * kGroupRows;
-    const uint8_t *wrow[kRowTiles];
-    #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt)
-        wrow[rt] = M.w + static_cast<size_t>(min(row0 + rt * 32 + col, M.rows - 1)) * M.row_bytes;
     const int bpb = is_q4<TYPE>(type) ? 144 : 210;
+    const int row = (group - M.group_begin) * kGroupRows + wave * 32 + col;
+    const uint8_t *wrow = M.w + static_cast<size_t>(min(row, M.rows - 1)) * M.row_bytes;
+    const uint8_t *recs = p.records + static_cast<size_t>(tile) * p.nb * kTileBytes;
 
-    float16v acc[kRowTiles];
+    const int b0 = split * p.blocks_per_split;
+    const int b1 = min(p.nb, b0 + p.blocks_per_split);
+    RecordStage rs;
+    record_load(recs + static_cast<size_t>(b0) * kTileBytes, rs);
+    RawBlock cur = load_block<TYPE>(wrow + b0 * bpb, type, kh);
+    record_store(rs, lds);
+    __syncthreads();
+
+    float16v acc;
     #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt)
-        #pragma unroll
-        for (int k = 0; k < 16; ++k) acc[rt][k] = 0.f;
-
-    const int b_begin = wave * p.blocks_per_wave;
-    const int b_end = min(p.nb, b_begin + p.blocks_per_wave);
-    for (int b = b_begin; b < b_end; ++b) {
-        RawBlock raw[kRowTiles];
-        #pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) raw[rt] = load_block<TYPE>(wrow[rt] + b * bpb, type, kh);
-        const uint8_t *rec = p.ws + (static_cast<size_t>(tile) * p.nb + b) * kRecBytes;
-        const float4 *fr = reinterpret_cast<const float4 *>(rec + 2 * kRecA + 2 * kRecM) + kh * 4;
-        float f[16];
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float4 u = fr[i];
-            f[4 * i] = u.x;
-            f[4 * i + 1] = u.y;
-            f[4 * i + 2] = u.z;
-            f[4 * i + 3] = u.w;
-        }
-        // Per-row block scales.
-        float d[kRowTiles], dmin[kRowTiles];
-        uint32_t sc4[kRowTiles], mn4[kRowTiles];
-        #pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) {
-            if (is_q4<TYPE>(type)) {
-                d[rt] = f16_bits_to_f32(raw[rt].hdr.x & 0xFFFFu);
-                dmin[rt] = f16_bits_to_f32(raw[rt].hdr.x >> 16);
-                q4k_scale_min4(raw[rt].hdr, kh, sc4[rt], mn4[rt]);
-            } else {
-                d[rt] = f16_bits_to_f32(raw[rt].hdr.z);
-                dmin[rt] = 0.f;
-                sc4[rt] = mn4[rt] = 0;
-            }
-        }
-        #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-            half8 ah[8], al[8];
-            const half8 *ahp = reinterpret_cast<const half8 *>(rec) + (hf * 8 * 2 + kh) * 32 + col;
-            const half8 *alp = reinterpret_cast<const half8 *>(rec + kRecA) + (hf * 8 * 2 + kh) * 32 + col;
-            #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                ah[j] = ahp[j * 64];
-                al[j] = alp[j * 64];
-            }
-            #pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
-                float16v t;
-                #pragma unroll
-                for (int k = 0; k < 16; ++k) t[k] = 0.f;
-                #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    _Float16 sa, sb;
-                    if (is_q4<TYPE>(type)) {
-                        sa = static_cast<_Float16>(static_cast<float>((sc4[rt] >> (16 * hf)) & 0xFFu));
-                        sb = static_cast<_Float16>(static_cast<float>((sc4[rt] >> (16 * hf + 8)) & 0xFFu));
-                    } else {
-                        // scales[kh*8 + 4*hf + 2*half + j/4] (int8)
-                        const uint32_t sw = hf ? raw[rt].hdr.y : raw[rt].hdr.x;
-                        const int sh = 8 * (j >> 2);
-                        sa = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((sw >> sh) & 0xFFu)));
-                        sb = static_cast<_Float16>(static_cast<float>(static_cast<int8_t>((sw >> (sh + 16)) & 0xFFu)));
-                    }
-                    const half8 bw = decode_b<TYPE>(raw[rt], type, hf, j, sa, sb);
-                    t = mfma16(ah[j], bw, t);
-                    t = mfma16(al[j], bw, t);
-                }
-                #pragma unroll
-                for (int k = 0; k < 16; ++k) acc[rt][k] = fmaf(d[rt] * f[k], t[k], acc[rt][k]);
-            }
-        }
-        if (is_q4<TYPE>(type)) {
-            const half4 mh = reinterpret_cast<const half4 *>(rec + 2 * kRecA)[kh * 32 + col];
-            const half4 ml = reinterpret_cast<const half4 *>(rec + 2 * kRecA + kRecM)[kh * 32 + col];
-            #pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
-                half4 bm;
-                #pragma unroll
-                for (int e = 0; e < 4; ++e) bm[e] = static_cast<_Float16>(static_cast<float>((mn4[rt] >> (8 * e)) & 0xFFu));
-                float16v t;
-                #pragma unroll
-                for (int k = 0; k < 16; ++k) t[k] = 0.f;
-                t = __builtin_amdgcn_mfma_f32_32x32x8f16(mh, bm, t, 0, 0, 0);
-                t = __builtin_amdgcn_mfma_f32_32x32x8f16(ml, bm, t, 0, 0, 0);
-                #pragma unroll
-                for (int k = 0; k < 16; ++k) acc[rt][k] = fmaf(-64.f * dmin[rt] * f[k], t[k], acc[rt][k]);
-            }
-        }
+    for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+    for (int b = b0; b < b1; ++b) {
+        const int buf = (b - b0) & 1;
+        // The last iteration reloads its own block (unconditional, in bounds).
+        const int bn = min(b + 1, b1 - 1);
+        record_load(recs + static_cast<size_t>(bn) * kTileBytes, rs);
+        const RawBlock nxt = load_block<TYPE>(wrow + bn * bpb, type, kh);
+        block_mfma<TYPE>(cur, type, lds + buf * kTileBytes, kh, col, acc);
+        record_store(rs, lds + (buf ^ 1) * kTileBytes);
+        cur = nxt;
+        __syncthreads();
     }
 
-    // Token k of the accumulators: 8*(k/4) + 4*kh + k%4 of the tile.
-    const int t0 = tile * kTokTile + 4 * kh;
-    if (n_waves == 1) {
-        #pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) {
-            const int row = row0 + rt * 32 + col;
-            if (row >= M.rows) continue;
+    // Accumulator register k holds token 8*(k/4) + 4*kh + k%4 of the tile.
+    const int tbase = tile * kTokTile + 4 * kh;
+    if (p.splits == 1) {
+        if (row < M.rows) {
             #pragma unroll
             for (int k = 0; k < 16; ++k) {
-                const int t = t0 + 8 * (k >> 2) + (k & 3);
-                if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = acc[rt][k];
+                const int t = tbase + 8 * (k >> 2) + (k & 3);
+                if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = acc[k];
             }
         }
         return;
     }
-    // Split blocks: partial sums meet in LDS, added in wave order.
-    float *red = reinterpret_cast<float *>(lds);
+
+    // Split blocks: the partial sums go to the workspace in accumulator
+    // order; reduce_splits adds them.
+    const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
+    float *mine = p.partials + (slot * p.splits + split) * 4096 + wave * 1024 + lane;
     #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt)
-        #pragma unroll
-        for (int k = 0; k < 16; ++k) red[((wave * kRowTiles + rt) * 16 + k) * 64 + lane] = acc[rt][k];
-    __syncthreads();
-    constexpr int kOut = kRowTiles * 16 * 64;
-    for (int o = threadIdx.x; o < kOut; o += blockDim.x) {
+    for (int k = 0; k < 16; ++k) mine[k * 64] = acc[k];
+}
+
+// y = the sum of a row group's split partials, in split order (deterministic).
+// One workgroup per (row group, tile); thread (wave, lane) owns the 16
+// outputs the same thread of batch_mfma produced.
+__global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
+    const int group = blockIdx.x, tile = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int kh = lane >> 5, col = lane & 31;
+    int m = 0;
+    #pragma unroll
+    for (int i = 1; i < QK_MAX_FUSED; ++i) m += (i < p.n_mats && group >= p.mat[i].group_begin) ? 1 : 0;
+    const BatchMatrix &M = p.mat[m];
+    const int row = (group - M.group_begin) * kGroupRows + wave * 32 + col;
+    const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
+    const float *part = p.partials + slot * p.splits * 4096 + wave * 1024 + lane;
+    const int tbase = tile * kTokTile + 4 * kh;
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) {
         float s = 0.f;
-        for (int w = 0; w < n_waves; ++w) s += red[w * kOut + o];
-        const int ln = o & 63, k = (o >> 6) & 15, rt = o >> 10;
-        const int row = row0 + rt * 32 + (ln & 31);
-        const int t = tile * kTokTile + 4 * (ln >> 5) + 8 * (k >> 2) + (k & 3);
+        for (int sp = 0; sp < p.splits; ++sp) s += part[sp * 4096 + k * 64];
+        const int t = tbase + 8 * (k >> 2) + (k & 3);
         if (row < M.rows && t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = s;
     }
 }
@@ -411,28 +479,48 @@ int check_batched(const char *where, const float *x, int ldx, int cols, int n_to
     return QK_OK;
 }
 
-size_t workspace_bytes(int cols, int n_tokens) {
-    if (cols <= 0 || cols % 256 || n_tokens <= 0) return 0;
-    const size_t tiles = (static_cast<size_t>(n_tokens) + kTokTile - 1) / kTokTile;
-    return tiles * static_cast<size_t>(cols / 256) * kRecBytes;
+int tile_count(int n_tokens) { return (n_tokens + kTokTile - 1) / kTokTile; }
+
+// Workgroups sharing a row group's blocks: enough that about kTargetGroups
+// workgroups run, at most kMaxSplit, at least two blocks each.
+void split_plan(int64_t rows_total, int nb, int tiles, int &splits, int &per_split) {
+    const int64_t groups = std::max<int64_t>(1, (rows_total + kGroupRows - 1) / kGroupRows);
+    const int64_t want = (kTargetGroups + groups * tiles - 1) / (groups * tiles);
+    int s = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want, 1), std::min(kMaxSplit, std::max(1, nb / 2))));
+    per_split = (nb + s - 1) / s;
+    splits = (nb + per_split - 1) / per_split;
+}
+
+size_t records_bytes(int cols, int n_tokens) {
+    return static_cast<size_t>(tile_count(n_tokens)) * (cols / 256) * kTileBytes;
+}
+
+// Workspace: packed activation records, then (when blocks are split) one
+// counter per (row group, tile) and the partial sums.
+size_t workspace_bytes(int cols, int64_t rows_total, int n_tokens) {
+    if (cols <= 0 || cols % 256 || rows_total <= 0 || n_tokens < kMfmaMinTokens) return 0;
+    const int tiles = tile_count(n_tokens);
+    size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
+    int splits, per_split;
+    split_plan(rows_total, cols / 256, tiles, splits, per_split);
+    if (splits == 1) return bytes;
+    const int64_t groups = (rows_total + kGroupRows - 1) / kGroupRows + QK_MAX_FUSED - 1;
+    return bytes + static_cast<size_t>(groups) * tiles * splits * 4096 * sizeof(float);
 }
 
 int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *x, int ldx, int cols, int n_tokens,
                 void *workspace, size_t workspace_size, hipStream_t stream, const char *where) {
-    const size_t need = workspace_bytes(cols, n_tokens);
-    if (!workspace || workspace_size < need)
-        return fail(QK_ERR_INVALID_ARG, std::string(where) + ": workspace smaller than " + std::to_string(need) +
-                                            " bytes (qk_gemv_batched_workspace_bytes)");
-    if (!aligned(workspace, 16)) return fail(QK_ERR_ALIGN, std::string(where) + ": workspace not 16-byte aligned");
     const int nb = cols / 256;
-    const int tiles = (n_tokens + kTokTile - 1) / kTokTile;
+    const int tiles = tile_count(n_tokens);
     if (tiles > 65535) return fail(QK_ERR_LIMIT, std::string(where) + ": too many tokens in one launch");
     BatchParams p{};
     p.n_mats = n_mats;
-    p.ws = static_cast<const uint8_t *>(workspace);
-    p.nb = nb;
+    p.x = x;
+    p.ldx = ldx;
     p.n_tokens = n_tokens;
-    int64_t groups = 0;
+    p.nb = nb;
+    p.tiles = tiles;
+    int64_t groups = 0, rows_total = 0;
     int type = mats[0].type;
     for (int i = 0; i < n_mats; ++i) {
         BatchMatrix &M = p.mat[i];
@@ -444,29 +532,32 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         M.ldy = ldy[i];
         M.group_begin = static_cast<int>(groups);
         groups += (M.rows + kGroupRows - 1) / kGroupRows;
+        rows_total += M.rows;
         if (static_cast<int64_t>(M.rows) * M.row_bytes > (int64_t(1) << 40))
             return fail(QK_ERR_LIMIT, std::string(where) + ": matrix too large");
         if (M.type != type) type = 0;
     }
-    if (groups > (1 << 30)) return fail(QK_ERR_LIMIT, std::string(where) + ": too many rows");
-    // Split a row group's blocks over up to kMaxSplit waves until about 2048
-    // waves are in flight.
-    const int64_t base = groups * tiles;
-    int split = static_cast<int>(std::min<int64_t>(kMaxSplit, std::max<int64_t>(1, 2048 / std::max<int64_t>(1, base))));
-    split = std::min(split, nb);
-    p.blocks_per_wave = (nb + split - 1) / split;
-    split = (nb + p.blocks_per_wave - 1) / p.blocks_per_wave;
-    const size_t lds = split > 1 ? static_cast<size_t>(split) * kRowTiles * 16 * 64 * sizeof(float) : 0;
-
-    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles), dim3(256), 0, stream, x, ldx, n_tokens, nb,
-                       static_cast<uint8_t *>(workspace));
-    const dim3 grid(static_cast<unsigned>(groups), tiles), block(64 * split);
+    split_plan(rows_total, nb, tiles, p.splits, p.blocks_per_split);
+    if (groups * p.splits > (1 << 30)) return fail(QK_ERR_LIMIT, std::string(where) + ": too many rows");
+    const size_t need = workspace_bytes(cols, rows_total, n_tokens);
+    if (!workspace || workspace_size < need)
+        return fail(QK_ERR_INVALID_ARG, std::string(where) + ": workspace smaller than " + std::to_string(need) +
+                                            " bytes (qk_gemv_batched_workspace_bytes)");
+    if (!aligned(workspace, 256)) return fail(QK_ERR_ALIGN, std::string(where) + ": workspace not 256-byte aligned");
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    p.records = ws;
+    if (p.splits > 1) p.partials = reinterpret_cast<float *>(ws + (records_bytes(cols, n_tokens) + 255) / 256 * 256);
+    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles), dim3(256), 0, stream, p, ws);
+    const dim3 grid(static_cast<unsigned>(groups * p.splits), tiles), block(256);
+    const size_t lds = 2 * kTileBytes;
     if (type == QK_TYPE_Q4_K)
         hipLaunchKernelGGL(batch_mfma<QK_TYPE_Q4_K>, grid, block, lds, stream, p);
     else if (type == QK_TYPE_Q6_K)
         hipLaunchKernelGGL(batch_mfma<QK_TYPE_Q6_K>, grid, block, lds, stream, p);
     else
         hipLaunchKernelGGL(batch_mfma<0>, grid, block, lds, stream, p);
+    if (p.splits > 1)
+        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups), tiles), dim3(256), 0, stream, p);
     return launch_status(where);
 }
 
@@ -475,8 +566,8 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
 
 extern "C" {
 
-size_t qk_gemv_batched_workspace_bytes(int cols, int n_tokens) {
-    return qk::workspace_bytes(cols, n_tokens);
+size_t qk_gemv_batched_workspace_bytes(int cols, int rows, int n_tokens) {
+    return qk::workspace_bytes(cols, rows, n_tokens);
 }
 
 int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float *y, int ldy, int cols, int rows,

@@ -119,10 +119,14 @@ def test_int8_validation(qk):
 
 def test_batched_workspace_sizes(qk):
     lib = qk.lib()
-    assert lib.qk_gemv_batched_workspace_bytes(0, 4) == 0
-    assert lib.qk_gemv_batched_workspace_bytes(2048, 0) == 0
-    a = lib.qk_gemv_batched_workspace_bytes(3072, 32)
-    assert a > 0 and a == lib.qk_gemv_batched_workspace_bytes(3072, 17)
+    assert lib.qk_gemv_batched_workspace_bytes(0, 64, 32) == 0
+    assert lib.qk_gemv_batched_workspace_bytes(2048, 64, 0) == 0
+    assert lib.qk_gemv_batched_workspace_bytes(2048, 64, 4) == 0         # below the matrix-core path
+    # Packed records: 33,920 B per (32-token tile, 256 columns).
+    big = lib.qk_gemv_batched_workspace_bytes(3072, 16384, 256)          # fills the chip unsplit
+    assert big == 8 * 12 * 33920
+    a = lib.qk_gemv_batched_workspace_bytes(8192, 3072, 32)              # split: records + partials
+    assert a > 32 * 33920 and a % 256 == 0 and a == lib.qk_gemv_batched_workspace_bytes(8192, 3072, 17)
     assert lib.qk_argmax_workspace_bytes(128256) > 0
 
 

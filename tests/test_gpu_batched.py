@@ -12,8 +12,8 @@ TOL = 1e-5
 
 def run_batched(qk, t, qtype, w, x, cols, rows):
     ntok = x.shape[0]
-    ws_bytes = qk.batch_workspace_bytes(cols, ntok)
-    ws = t.empty(max(ws_bytes, 16), dtype=t.uint8, device="cuda")
+    ws_bytes = qk.batch_workspace_bytes(cols, rows, ntok)
+    ws = t.empty(max(ws_bytes, 256), dtype=t.uint8, device="cuda")
     y = t.full((ntok, rows), float("nan"), device="cuda")
     qk.batch_matvec(qk.Tensor((cols, rows), qtype, to_dev(t, w)), to_dev(t, x), y, cols, rows, ntok, ws, ws_bytes)
     t.cuda.synchronize()
@@ -72,8 +72,8 @@ def test_multi_batched_gate_up(qk, torch_gpu, oracle, workloads):
     wgd, wud = to_dev(t, wg), to_dev(t, wu)
     arr[0].type, arr[0].rows, arr[0].w, arr[0].y = Q4_K, hidden, wgd.data_ptr(), g.data_ptr()
     arr[1].type, arr[1].rows, arr[1].w, arr[1].y = Q6_K, hidden, wud.data_ptr(), u.data_ptr()
-    ws_bytes = qk.batch_workspace_bytes(dim, ntok)
-    ws = t.empty(ws_bytes, dtype=t.uint8, device="cuda")
+    ws_bytes = qk.batch_workspace_bytes(dim, 2 * hidden, ntok)
+    ws = t.empty(max(ws_bytes, 256), dtype=t.uint8, device="cuda")
     xd = to_dev(t, x)
     qk.check(qk.lib().qk_gemv_multi_batched_f32(arr, 2, xd.data_ptr(), dim, dim, ntok, ws.data_ptr(), ws_bytes, None),
              "multi batched")
@@ -97,8 +97,8 @@ def _fused(qk, t, mats, x, cols, ntok):
         keep.append(wd)
         outs.append(y)
         arr[i].type, arr[i].rows, arr[i].w, arr[i].y = qtype, rows, wd.data_ptr(), y.data_ptr()
-    ws_bytes = qk.batch_workspace_bytes(cols, ntok)
-    ws = t.empty(ws_bytes, dtype=t.uint8, device="cuda")
+    ws_bytes = qk.batch_workspace_bytes(cols, sum(r for _, _, r in mats), ntok)
+    ws = t.empty(max(ws_bytes, 256), dtype=t.uint8, device="cuda")
     xd = to_dev(t, x)
     qk.check(qk.lib().qk_gemv_multi_batched_f32(arr, len(mats), xd.data_ptr(), cols, cols, ntok, ws.data_ptr(),
                                                 ws_bytes, None), "multi batched")
@@ -172,9 +172,10 @@ def test_mfma_deterministic(qk, torch_gpu, workloads):
 
 def test_mfma_needs_workspace(qk, torch_gpu, workloads):
     t = torch_gpu
-    cols, rows, ntok = 512, 64, 8
+    cols, rows, ntok = 2048, 64, 8
     w, x = workloads.gemv_case(Q4_K, cols, rows, seed=100, n_tokens=ntok)
-    need = qk.batch_workspace_bytes(cols, ntok)
+    need = qk.batch_workspace_bytes(cols, rows, ntok)
+    assert need > 0          # 64 rows x 8 blocks: the blocks split over several workgroups
     ws = t.empty(need, dtype=t.uint8, device="cuda")
     y = t.empty((ntok, rows), device="cuda")
     with pytest.raises(qk.QKError) as e:
