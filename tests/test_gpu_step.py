@@ -14,8 +14,10 @@ def test_rmsnorm(qk, torch_gpu, oracle, synth):
     x = synth.normal_f32(n * ntok, 91, 1).reshape(ntok, n) * np.float32(50.0)
     w = synth.normal_f32(n, 91, 2)
     out = t.empty((ntok, n), device="cuda")
-    qk.check(qk.lib().qk_rmsnorm_f32(to_dev(t, x).data_ptr(), to_dev(t, w).data_ptr(), out.data_ptr(), n, ntok,
-                                     1e-5, None), "rmsnorm")
+    # Device copies stay bound to names until the launch has finished: a
+    # temporary freed before the kernel runs lets the allocator reuse it.
+    xd, wd = to_dev(t, x), to_dev(t, w)
+    qk.check(qk.lib().qk_rmsnorm_f32(xd.data_ptr(), wd.data_ptr(), out.data_ptr(), n, ntok, 1e-5, None), "rmsnorm")
     t.cuda.synchronize()
     for k in range(ntok):
         assert rel_l2(out[k].cpu().numpy(), oracle.rmsnorm(x[k], w, 1e-5)) < 1e-6
@@ -32,10 +34,10 @@ def test_rope_kv_write(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim):
     v = synth.normal_f32(kv, 92, 3)
     kc = t.zeros((layers, ctx, kv), device="cuda")
     vc = t.zeros((layers, ctx, kv), device="cuda")
-    qd = to_dev(t, q)
-    qk.check(qk.lib().qk_rope_kv_write(qd.data_ptr(), to_dev(t, k).data_ptr(), to_dev(t, v).data_ptr(),
-                                       to_dev(t, cos).data_ptr(), to_dev(t, sin).data_ptr(), kc.data_ptr(),
-                                       vc.data_ptr(), layer, pos, ctx, heads, kv_heads, head_dim, None), "rope")
+    qd, kd, vd, cd, sd = (to_dev(t, a) for a in (q, k, v, cos, sin))
+    qk.check(qk.lib().qk_rope_kv_write(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                       kc.data_ptr(), vc.data_ptr(), layer, pos, ctx, heads, kv_heads, head_dim,
+                                       None), "rope")
     t.cuda.synchronize()
     assert np.max(np.abs(qd.cpu().numpy() - oracle.rope(q, cos, sin, pos, head_dim))) < 1e-5
     assert np.max(np.abs(kc[layer, pos].cpu().numpy() - oracle.rope(k, cos, sin, pos, head_dim))) < 1e-5
@@ -55,8 +57,9 @@ def test_attention(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim, pos)
     kc = synth.normal_f32(layers * ctx * kv, 93, 2).reshape(layers, ctx, kv)
     vc = synth.normal_f32(layers * ctx * kv, 93, 3).reshape(layers, ctx, kv)
     out = t.empty(heads * head_dim, device="cuda")
-    qk.check(qk.lib().qk_attention_f32(to_dev(t, q).data_ptr(), to_dev(t, kc).data_ptr(), to_dev(t, vc).data_ptr(),
-                                       out.data_ptr(), layer, pos, ctx, heads, kv_heads, head_dim, None), "attention")
+    qd, kd, vd = to_dev(t, q), to_dev(t, kc), to_dev(t, vc)
+    qk.check(qk.lib().qk_attention_f32(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(), layer, pos, ctx,
+                                       heads, kv_heads, head_dim, None), "attention")
     t.cuda.synchronize()
     want = oracle.attention(q, kc[layer, : pos + 1], vc[layer, : pos + 1], pos, heads, kv_heads, head_dim)
     assert rel_l2(out.cpu().numpy(), want) < 1e-5
@@ -88,6 +91,7 @@ def test_argmax_lowest_index(qk, torch_gpu, oracle, synth, n):
         v[[7, n // 2, n - 1]] = 50.0
     ws = t.empty(max(qk.lib().qk_argmax_workspace_bytes(n), 8), dtype=t.uint8, device="cuda")
     out = t.full((1,), -1, dtype=t.int32, device="cuda")
-    qk.check(qk.lib().qk_argmax_f32(to_dev(t, v).data_ptr(), n, out.data_ptr(), ws.data_ptr(), None), "argmax")
+    vd = to_dev(t, v)
+    qk.check(qk.lib().qk_argmax_f32(vd.data_ptr(), n, out.data_ptr(), ws.data_ptr(), None), "argmax")
     t.cuda.synchronize()
     assert int(out.item()) == oracle.argmax(v)
