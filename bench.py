@@ -29,6 +29,7 @@ import time
 ROOT = pathlib.Path(__file__).resolve().parent
 PKG_NAME = "inferencer_jetson_amd"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0   # dense fp16 / bf16 matrix-core peak of MI355X
 METRIC = "Q4_K/Q6_K GEMV HBM GB/s (% of peak); batched decode tokens/s (1 GPU)"
 
 
@@ -99,6 +100,177 @@ def cpu_baseline_lm_head(workloads, sample_rows: int, target_s: float) -> dict:
     return {"value": round(sample_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"Q6_K GEMV over the first {sample_rows} rows (x 2048) of the LM-head matrix, "
                       f"{reps} repetitions in {el:.1f} s, OpenMP static rows, nproc={os.cpu_count()}"}
+
+
+def bench_small_gemvs(torch, qk, wl, stream) -> dict:
+    """Q4_K 2048x2048 (launch-bound) and the fused 1B gate/up over 16 layers."""
+    sec = {}
+    w1, x1 = wl.gemv_q4k_2048()
+    w1d, x1d = torch.from_numpy(w1).to("cuda"), torch.from_numpy(x1).to("cuda")
+    y1 = torch.empty(2048, device="cuda")
+    t1 = qk.Tensor((2048, 2048), qk.Q4_K, w1d)
+    _, k1 = time_launches(torch, lambda i: qk.matvec(t1, x1d, y1, 2048, 2048, stream), 200, 20, stream)
+    b1 = qk.tensor_bytes(qk.Q4_K, 2048, 2048) + 2048 * 8
+    sec["gemv_q4k_2048x2048"] = {"kernel_us": round(k1 * 1e3, 2), "GBps_kernel": round(b1 / (k1 * 1e-3) / 1e9, 1)}
+    gu = []
+    for l in range(16):
+        wg = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 4, 0.02)
+        wu = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 5, 0.02)
+        gu.append((qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wg).to("cuda")),
+                   qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wu).to("cuda"))))
+    g = torch.empty(8192, device="cuda")
+    u = torch.empty(8192, device="cuda")
+    xg = torch.from_numpy(wl.synth.normal_f32(2048, 2, 7)).to("cuda")
+    _, k2 = time_launches(
+        torch, lambda i: qk.gate_up(gu[i % 16][0], gu[i % 16][1], xg, g, u, 2048, 8192, stream), 320, 32, stream)
+    b2 = 2 * qk.tensor_bytes(qk.Q4_K, 2048, 8192) + 2048 * 4 + 2 * 8192 * 4
+    sec["gemv_q4k_gate_up_1b_2x8192x2048"] = {
+        "kernel_us": round(k2 * 1e3, 2), "GBps_kernel": round(b2 / (k2 * 1e-3) / 1e9, 1),
+        "frac_of_peak": round(b2 / (k2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+    return sec
+
+
+def _workspace(torch, qk, cols, rows, ntok):
+    n = qk.batch_workspace_bytes(cols, rows, ntok)
+    return torch.empty(max(n, 256), dtype=torch.uint8, device="cuda"), n
+
+
+def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200, warmup: int = 16) -> dict:
+    """Llama-3.2-3B FFN for 32 decode tokens of 32 sequences (ragged context
+    lengths 64..2048 in the batch descriptor; the FFN reads only the token
+    count): fused gate/up (Q4_K 2 x 8192 x 3072), SiLU * up, down (Q6_K
+    3072 x 8192).  `copies` weight sets rotate so the last-level cache cannot
+    hold them (8 x 49 MB)."""
+    dim, hidden, ntok = 3072, 8192, 32
+    sets = []
+    x_host = None
+    for c in range(copies):
+        case = wl.ffn_3b_ragged(copy=c)
+        x_host = case["x"] if x_host is None else x_host
+        sets.append(tuple(torch.from_numpy(case[k]).to("cuda") for k in ("gate", "up", "down")))
+    x = torch.from_numpy(x_host).to("cuda")
+    gate = torch.empty((ntok, hidden), device="cuda")
+    up = torch.empty((ntok, hidden), device="cuda")
+    y = torch.empty((ntok, dim), device="cuda")
+    ws_gu, n_gu = _workspace(torch, qk, dim, 2 * hidden, ntok)
+    ws_d, n_d = _workspace(torch, qk, hidden, dim, ntok)
+    L = qk.lib()
+    s = qk.stream_handle(stream)
+
+    def step(i):
+        wg, wu, wd = sets[i % copies]
+        arr = qk._matrices([(qk.Tensor((dim, hidden), qk.Q4_K, wg), gate), (qk.Tensor((dim, hidden), qk.Q4_K, wu), up)])
+        qk.check(L.qk_gemv_multi_batched_f32(arr, 2, x.data_ptr(), dim, dim, ntok, ws_gu.data_ptr(), n_gu, s), "gate/up")
+        qk.check(L.qk_silu_mul_f32(gate.data_ptr(), up.data_ptr(), ntok * hidden, s), "silu")
+        qk.check(L.qk_gemv_batched_f32(qk.Q6_K, wd.data_ptr(), gate.data_ptr(), hidden, y.data_ptr(), dim, hidden,
+                                       dim, ntok, ws_d.data_ptr(), n_d, s), "down")
+
+    wall, ms = time_launches(torch, step, steps, warmup, stream)
+    weights = 2 * qk.tensor_bytes(qk.Q4_K, dim, hidden) + qk.tensor_bytes(qk.Q6_K, hidden, dim)
+    # x, gate/up outputs, down input (h), down output, fp32, once each.
+    act = 4 * ntok * (dim + 2 * hidden + hidden + dim)
+    return {"tokens": ntok, "ms_per_step": round(ms, 4), "tokens_per_s": round(ntok / (ms * 1e-3), 1),
+            "bytes_per_step": weights + act, "GBps": round((weights + act) / (ms * 1e-3) / 1e9, 1),
+            "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "weight_copies": copies, "launches_per_step": 3}
+
+
+def bench_mixed_1b_256(torch, qk, wl, stream, steps: int = 20, warmup: int = 3) -> dict:
+    """256 packed tokens (2 prefill chunks of 96 + 64 decodes) through the
+    seven projections of all 16 Llama-3.2-1B layers on the matrix cores:
+    fused QKV (Q4_K q/k, Q6_K v), o (Q4_K), fused gate/up (Q4_K), SiLU * up,
+    down (Q6_K).  Useful flops = 2 * 256 * (weights per layer) * 16."""
+    cfg = wl.LLAMA_1B
+    dim, hidden, ntok = cfg["dim"], cfg["hidden"], 256
+    kv = dim // cfg["heads"] * cfg["kv_heads"]
+    case = wl.mixed_1b_256()
+    layers = []
+    for l in range(cfg["layers"]):
+        W = {}
+        for j, name in enumerate(wl.TENSORS):
+            cols, rows = wl.tensor_shape(cfg, name)
+            host = case["weights"][name] if l == 0 else wl.synth.quant_matrix(
+                wl.MIX_1B[name], cols, rows, 4, 1 + 16 * l + j, wl.SIGMA[wl.MIX_1B[name]])
+            W[name] = torch.from_numpy(host).to("cuda")
+        layers.append(W)
+    x = torch.from_numpy(case["x"]).to("cuda")
+    q = torch.empty((ntok, dim), device="cuda")
+    k = torch.empty((ntok, kv), device="cuda")
+    v = torch.empty((ntok, kv), device="cuda")
+    o = torch.empty((ntok, dim), device="cuda")
+    gate = torch.empty((ntok, hidden), device="cuda")
+    up = torch.empty((ntok, hidden), device="cuda")
+    y = torch.empty((ntok, dim), device="cuda")
+    ws_qkv, n_qkv = _workspace(torch, qk, dim, dim + 2 * kv, ntok)
+    ws_o, n_o = _workspace(torch, qk, dim, dim, ntok)
+    ws_gu, n_gu = _workspace(torch, qk, dim, 2 * hidden, ntok)
+    ws_d, n_d = _workspace(torch, qk, hidden, dim, ntok)
+    L = qk.lib()
+    s = qk.stream_handle(stream)
+    mix = wl.MIX_1B
+
+    def T(name, W):
+        cols, rows = wl.tensor_shape(cfg, name)
+        return qk.Tensor((cols, rows), mix[name], W[name])
+
+    def step(i):
+        for W in layers:
+            arr = qk._matrices([(T("q", W), q), (T("k", W), k), (T("v", W), v)])
+            qk.check(L.qk_gemv_multi_batched_f32(arr, 3, x.data_ptr(), dim, dim, ntok, ws_qkv.data_ptr(), n_qkv, s),
+                     "qkv")
+            qk.check(L.qk_gemv_batched_f32(mix["o"], W["o"].data_ptr(), q.data_ptr(), dim, o.data_ptr(), dim, dim,
+                                           dim, ntok, ws_o.data_ptr(), n_o, s), "o")
+            arr = qk._matrices([(T("gate", W), gate), (T("up", W), up)])
+            qk.check(L.qk_gemv_multi_batched_f32(arr, 2, x.data_ptr(), dim, dim, ntok, ws_gu.data_ptr(), n_gu, s),
+                     "gate/up")
+            qk.check(L.qk_silu_mul_f32(gate.data_ptr(), up.data_ptr(), ntok * hidden, s), "silu")
+            qk.check(L.qk_gemv_batched_f32(mix["down"], W["down"].data_ptr(), gate.data_ptr(), hidden, y.data_ptr(),
+                                           dim, hidden, dim, ntok, ws_d.data_ptr(), n_d, s), "down")
+
+    wall, ms = time_launches(torch, step, steps, warmup, stream)
+    per_layer = sum(wl.tensor_shape(cfg, n)[0] * wl.tensor_shape(cfg, n)[1] for n in wl.TENSORS)
+    flops = 2.0 * ntok * per_layer * cfg["layers"]
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"tokens": ntok, "packing": "2 prefill chunks x 96 + 64 decodes", "ms_per_step": round(ms, 4),
+            "tokens_per_s": round(ntok / (ms * 1e-3), 1), "useful_TFLOPs": round(tflops, 1),
+            "mfma_util_of_fp16_dense_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "mfma_ops_per_useful_product": 2, "launches_per_step": 5 * cfg["layers"]}
+
+
+def bench_decode_1b(torch, qk, wl) -> dict:
+    """Random-init Llama-3.2-1B decode, one sequence: KV prefilled at 0..511,
+    16 prompt tokens at 512..527, then 64 greedy tokens, each step ending in
+    the 4-byte token download (FastRunner::forward, inferencer.cu:1424-1531).
+    Timed: the 64 greedy steps, wall clock."""
+    w = wl.LLAMA_1B_DECODE
+    cfg = w.cfg
+    W = wl.llama_weights(cfg, w.seed)
+    kc, vc = wl.llama_kv_prefill(cfg, w.seed, w.prefill_positions)
+    run = qk.Runner(cfg, W)
+    run.load_kv(kc, vc)
+    prompt = wl.llama_prompt(cfg, w.seed, w.prompt_tokens)
+    pos = w.prefill_positions
+    for i, tok in enumerate(prompt):
+        nxt = run.forward(int(tok), pos, i == len(prompt) - 1)
+        pos += 1
+    torch.cuda.synchronize()
+    start_pos = pos
+    t0 = time.perf_counter()
+    for _ in range(w.greedy_tokens):
+        nxt = run.forward(nxt, pos, True)
+        pos += 1
+    el = time.perf_counter() - t0
+    run.close()
+    kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
+    weights = sum(qk.tensor_bytes(wl.MIX_1B[n], *wl.tensor_shape(cfg, n)) for n in wl.TENSORS) * cfg["layers"] + \
+        qk.tensor_bytes(qk.Q6_K, cfg["dim"], cfg["vocab"])
+    kv_bytes = sum(cfg["layers"] * (p + 1) * kv_dim * 4 * 2 for p in range(start_pos, pos))
+    per_tok = el / w.greedy_tokens
+    gbps = (weights * w.greedy_tokens + kv_bytes) / el / 1e9
+    return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
+            "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
+            "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+            "launches_per_token": 11 * cfg["layers"] + 5}
 
 
 def reference_kernels(torch, args) -> int:
@@ -204,32 +376,14 @@ def main() -> int:
 
     if args.secondary:
         sec = {}
-        # Q4_K 2048x2048 (Llama-3.2-1B attn_q): launch-bound at this size.
-        w1, x1 = wl.gemv_q4k_2048()
-        w1d, x1d = torch.from_numpy(w1).to("cuda"), torch.from_numpy(x1).to("cuda")
-        y1 = torch.empty(2048, device="cuda")
-        t1 = qk.Tensor((2048, 2048), qk.Q4_K, w1d)
-        wall1, k1 = time_launches(torch, lambda i: qk.matvec(t1, x1d, y1, 2048, 2048, stream), 200, 20, stream)
-        b1 = qk.tensor_bytes(qk.Q4_K, 2048, 2048) + 2048 * 8
-        sec["gemv_q4k_2048x2048"] = {"kernel_us": round(k1 * 1e3, 2), "GBps_kernel": round(b1 / (k1 * 1e-3) / 1e9, 1)}
-        # Q4_K at scale: fused gate/up (2 x 8192 x 2048) over 16 layers' weights.
-        gu = []
-        for l in range(16):
-            wg = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 4, 0.02)
-            wu = wl.synth.quant_matrix(qk.Q4_K, 2048, 8192, 2, 100 + 16 * l + 5, 0.02)
-            gu.append((qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wg).to("cuda")),
-                       qk.Tensor((2048, 8192), qk.Q4_K, torch.from_numpy(wu).to("cuda"))))
-        g = torch.empty(8192, device="cuda")
-        u = torch.empty(8192, device="cuda")
-        xg = torch.from_numpy(wl.synth.normal_f32(2048, 2, 7)).to("cuda")
-        wall2, k2 = time_launches(
-            torch, lambda i: qk.gate_up(gu[i % 16][0], gu[i % 16][1], xg, g, u, 2048, 8192, stream), 320, 32, stream)
-        b2 = 2 * qk.tensor_bytes(qk.Q4_K, 2048, 8192) + 2048 * 4 + 2 * 8192 * 4
-        sec["gemv_q4k_gate_up_1b_2x8192x2048"] = {
-            "kernel_us": round(k2 * 1e3, 2), "GBps_kernel": round(b2 / (k2 * 1e-3) / 1e9, 1),
-            "frac_of_peak": round(b2 / (k2 * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        sec.update(bench_small_gemvs(torch, qk, wl, stream))
+        sec["ffn_3b_ragged_t32"] = bench_ffn_3b_ragged(torch, qk, wl, stream)
+        log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")
+        sec["mixed_1b_256"] = bench_mixed_1b_256(torch, qk, wl, stream)
+        log(f"[bench] mixed_1b_256: {json.dumps(sec['mixed_1b_256'])}")
+        sec["llama_1b_decode"] = bench_decode_1b(torch, qk, wl)
+        log(f"[bench] llama_1b_decode: {json.dumps(sec['llama_1b_decode'])}")
         result["secondary"] = sec
-        log(f"[bench] secondary: {json.dumps(sec)}")
 
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")

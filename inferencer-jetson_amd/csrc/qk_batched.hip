@@ -462,10 +462,17 @@ __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
     const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
     const float *part = p.partials + slot * p.splits * 4096 + wave * 1024 + lane;
     const int tbase = tile * kTokTile + 4 * kh;
+    // Every load is issued before the first add: the kernel is latency-bound.
+    float v[kMaxSplit][16];
+    #pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp)
+        #pragma unroll
+        for (int k = 0; k < 16; ++k) v[sp][k] = sp < p.splits ? part[sp * 4096 + k * 64] : 0.f;
     #pragma unroll
     for (int k = 0; k < 16; ++k) {
-        float s = 0.f;
-        for (int sp = 0; sp < p.splits; ++sp) s += part[sp * 4096 + k * 64];
+        float s = v[0][k];
+        #pragma unroll
+        for (int sp = 1; sp < kMaxSplit; ++sp) s += v[sp][k];
         const int t = tbase + 8 * (k >> 2) + (k & 3);
         if (row < M.rows && t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = s;
     }

@@ -42,8 +42,9 @@ int block_bytes(int type);
 // Validates a Q4_K / Q6_K weight operand shape; returns QK_OK or a status.
 int check_weights(const char *where, int type, const void *w, int cols, int rows);
 
-// Dynamic LDS of the attention kernel for positions 0..pos.
-size_t attention_lds_bytes(int pos, int head_dim);
+// Dynamic LDS of the attention kernel for positions 0..pos and `group`
+// query heads per KV head.
+size_t attention_lds_bytes(int pos, int head_dim, int group);
 
 // Per-device properties, cached once per device (thread-safe).
 struct DeviceInfo {

@@ -75,7 +75,7 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         if (!L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down || !L.attn_norm || !L.ffn_norm)
             return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_create: layer " + std::to_string(l) + " is incomplete");
     }
-    if (qk::attention_lds_bytes(c.context - 1, head_dim) > 150 * 1024)
+    if (c.heads / c.kv_heads > 8 || qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
         return qk::fail(QK_ERR_LIMIT, "qk_llama_create: context beyond the attention kernel's LDS budget");
 
     qk_llama *m = new qk_llama();

@@ -44,12 +44,37 @@ __device__ __forceinline__ float block_max256(float v, float *scratch) {
 }
 
 // rmsnorm_cuda (inferencer.cu:821-834): one 256-thread block per token.
+// Rows whose length is a multiple of 4 (and 16-byte aligned) read x as
+// float4 with every load of a thread in flight at once; the kernel is
+// latency-bound at decode sizes, so the loads must not wait on each other.
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const float *weight, float *out, int n,
-                                                      float eps) {
+                                                      float eps, int vec4) {
     __shared__ float scratch[4];
     const float *xt = x + static_cast<int64_t>(blockIdx.x) * n;
     float *ot = out + static_cast<int64_t>(blockIdx.x) * n;
     float ss = 0.f;
+    if (vec4) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xt);
+        const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+        float4 *o4 = reinterpret_cast<float4 *>(ot);
+        const int n4 = n >> 2;
+        #pragma unroll 4
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const float4 v = x4[i];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
+        }
+        ss = block_sum256(ss, scratch);
+        const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+        #pragma unroll 4
+        for (int i = threadIdx.x; i < n4; i += 256) {
+            const float4 v = x4[i], w = w4[i];
+            o4[i] = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < n; i += 256) ss = fmaf(xt[i], xt[i], ss);
     ss = block_sum256(ss, scratch);
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
@@ -81,64 +106,176 @@ __global__ void rope_kv_kernel(float *q, const float *k, const float *v, const f
     }
 }
 
-// attention_cuda (inferencer.cu:981-1009): one 256-thread block per query
-// head.  Phase 1: thread t scores positions t, t+256, ... (each reads its
-// own contiguous key row), scores staged in LDS.  Phase 2: softmax
-// normalisation.  Phase 3: thread (i, grp) accumulates p_t * v_t[i] over
-// positions t = grp mod G, coalesced over i; the G partial vectors are
-// summed in LDS.
-__global__ __launch_bounds__(256) void attention_kernel(const float *q, const float *key_cache,
-                                                        const float *value_cache, float *out, int layer, int pos,
-                                                        int context, int heads, int kv_heads, int head_dim) {
-    extern __shared__ float smem[];
-    float *qs = smem;                      // head_dim
-    float *score = smem + head_dim;        // pos + 1
-    float *part = score + pos + 1;         // 256
-    __shared__ float scratch[4];
-    const int head = blockIdx.x;
-    const int group = heads / kv_heads;
-    const int kvh = head / group;
-    const int kv_dim = kv_heads * head_dim;
+// attention_cuda (inferencer.cu:981-1009), GQA, one query token.  One
+// 1024-thread workgroup per KV head serves the G = heads / kv_heads query
+// heads that share it, so every key and value row is read from memory once.
+// At decode sizes the kernel is latency-bound: each phase issues all of its
+// loads before it consumes them.
+//   1. scores: thread t takes positions t, t + 1024, ...; it loads the key
+//      row (16 float4 at a time) and dots it with the G query rows (LDS
+//      broadcast), scaled by 1/sqrt(head_dim); scores go to LDS.
+//   2. per-head maximum, exp, per-head sum (block reductions in LDS).
+//   3. values: wave w owns a contiguous run of positions, lane = dimension;
+//      the 16 partial vectors per head are added in wave order and divided
+//      by the sum (deterministic).
+constexpr int kAttnThreads = 1024;
+constexpr int kAttnWaves = kAttnThreads / 64;
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnMaxDimLanes = 4;   // head_dim <= 256: four dimensions per lane
+
+struct AttnLds {
+    float *qs;      // [G][head_dim]
+    float *score;   // [G][pos + 1]
+    float *part;    // [waves][G][head_dim]
+    float *red;     // [waves][G]
+};
+
+__device__ __forceinline__ AttnLds attn_lds(float *smem, int G, int head_dim, int pos) {
+    AttnLds l;
+    l.qs = smem;
+    l.score = l.qs + G * head_dim;
+    l.part = l.score + G * (pos + 1);
+    l.red = l.part + kAttnWaves * G * head_dim;
+    return l;
+}
+
+// Block-wide reduction of G per-thread values (max or sum); every thread
+// receives the G results in v.
+template <bool MAX>
+__device__ __forceinline__ void attn_block_reduce(float *v, int G, float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int g = 0; g < G; ++g) {
+        const float r = MAX ? wave_max(v[g]) : wave_sum(v[g]);
+        if (lane == 0) red[wave * G + g] = r;
+    }
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+        float r = red[g];
+        for (int w = 1; w < kAttnWaves; ++w) r = MAX ? fmaxf(r, red[w * G + g]) : r + red[w * G + g];
+        v[g] = r;
+    }
+    __syncthreads();
+}
+
+// q: the token's query rows of the G heads of KV head kvh (already rotated);
+// kc / vc: the layer's caches offset to this KV head; out: the G output rows.
+__device__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos, int G,
+                               int head_dim, int kv_dim, float *smem) {
+    const AttnLds L = attn_lds(smem, G, head_dim, pos);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = pos + 1;
     const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
-    const float *kc = key_cache + static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    const float *vc = value_cache + static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    for (int i = threadIdx.x; i < head_dim; i += 256) qs[i] = q[head * head_dim + i];
+    for (int i = tid; i < G * head_dim; i += kAttnThreads) L.qs[i] = q[i];
     __syncthreads();
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t <= pos; t += 256) {
-        const float *kr = kc + static_cast<int64_t>(t) * kv_dim;
-        float dot = 0.f;
-        for (int i = 0; i < head_dim; i += 4) {
-            float4 kv4 = *reinterpret_cast<const float4 *>(kr + i);
-            dot = fmaf(qs[i], kv4.x, dot);
-            dot = fmaf(qs[i + 1], kv4.y, dot);
-            dot = fmaf(qs[i + 2], kv4.z, dot);
-            dot = fmaf(qs[i + 3], kv4.w, dot);
+
+    float m[kAttnMaxGroup];
+    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
+    for (int t = tid; t < n; t += kAttnThreads) {
+        const float4 *kr = reinterpret_cast<const float4 *>(kc + static_cast<int64_t>(t) * kv_dim);
+        float dot[kAttnMaxGroup];
+        for (int g = 0; g < G; ++g) dot[g] = 0.f;
+        for (int c = 0; c < head_dim; c += 64) {
+            float4 k4[16];
+            const int nc = min(16, (head_dim - c) >> 2);
+            #pragma unroll
+            for (int j = 0; j < 16; ++j)
+                if (j < nc) k4[j] = kr[(c >> 2) + j];
+            for (int g = 0; g < G; ++g) {
+                const float *qg = L.qs + g * head_dim + c;
+                float a = dot[g];
+                #pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    if (j < nc) {
+                        a = fmaf(qg[4 * j], k4[j].x, a);
+                        a = fmaf(qg[4 * j + 1], k4[j].y, a);
+                        a = fmaf(qg[4 * j + 2], k4[j].z, a);
+                        a = fmaf(qg[4 * j + 3], k4[j].w, a);
+                    }
+                dot[g] = a;
+            }
         }
-        dot *= inv;
-        score[t] = dot;
-        mx = fmaxf(mx, dot);
+        for (int g = 0; g < G; ++g) {
+            const float sc = dot[g] * inv;
+            L.score[g * n + t] = sc;
+            m[g] = fmaxf(m[g], sc);
+        }
     }
-    mx = block_max256(mx, scratch);
-    float den = 0.f;
-    for (int t = threadIdx.x; t <= pos; t += 256) {
-        float e = expf(score[t] - mx);
-        score[t] = e;
-        den += e;
+    attn_block_reduce<true>(m, G, L.red);   // its barriers also publish score[]
+
+    float den[kAttnMaxGroup];
+    for (int g = 0; g < G; ++g) den[g] = 0.f;
+    for (int t = tid; t < n; t += kAttnThreads)
+        for (int g = 0; g < G; ++g) {
+            const float e = expf(L.score[g * n + t] - m[g]);
+            L.score[g * n + t] = e;
+            den[g] += e;
+        }
+    attn_block_reduce<false>(den, G, L.red);
+
+    const int per = (n + kAttnWaves - 1) / kAttnWaves;
+    const int t0 = wave * per, t1 = min(n, t0 + per);
+    const int dims = (head_dim + 63) >> 6;   // dimensions per lane
+    float acc[kAttnMaxGroup][kAttnMaxDimLanes];
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = 0.f;
+    int t = t0;
+    for (; t + 4 <= t1; t += 4) {
+        float v[4][kAttnMaxDimLanes];
+        #pragma unroll
+        for (int u = 0; u < 4; ++u)
+            #pragma unroll
+            for (int j = 0; j < kAttnMaxDimLanes; ++j) {
+                const int d = lane + 64 * j;
+                v[u][j] = (j < dims && d < head_dim) ? vc[static_cast<int64_t>(t + u) * kv_dim + d] : 0.f;
+            }
+        for (int g = 0; g < G; ++g)
+            #pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float pr = L.score[g * n + t + u];
+                #pragma unroll
+                for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = fmaf(pr, v[u][j], acc[g][j]);
+            }
     }
-    den = block_sum256(den, scratch);   // its barriers also publish score[]
-    const int groups = 256 / head_dim;  // head_dim divides 256 (checked on the host)
-    const int i = threadIdx.x % head_dim, grp = threadIdx.x / head_dim;
-    float acc = 0.f;
-    if (grp < groups)
-        for (int t = grp; t <= pos; t += groups) acc = fmaf(score[t], vc[static_cast<int64_t>(t) * kv_dim + i], acc);
-    part[threadIdx.x] = acc;
+    for (; t < t1; ++t) {
+        float v[kAttnMaxDimLanes];
+        #pragma unroll
+        for (int j = 0; j < kAttnMaxDimLanes; ++j) {
+            const int d = lane + 64 * j;
+            v[j] = (j < dims && d < head_dim) ? vc[static_cast<int64_t>(t) * kv_dim + d] : 0.f;
+        }
+        for (int g = 0; g < G; ++g) {
+            const float pr = L.score[g * n + t];
+            #pragma unroll
+            for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = fmaf(pr, v[j], acc[g][j]);
+        }
+    }
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int j = 0; j < kAttnMaxDimLanes; ++j) {
+            const int d = lane + 64 * j;
+            if (j < dims && d < head_dim) L.part[(wave * G + g) * head_dim + d] = acc[g][j];
+        }
     __syncthreads();
-    if (threadIdx.x < head_dim) {
+    for (int i = tid; i < G * head_dim; i += kAttnThreads) {
+        const int g = i / head_dim;
         float s = 0.f;
-        for (int g = 0; g < groups; ++g) s += part[g * head_dim + threadIdx.x];
-        out[head * head_dim + threadIdx.x] = s / den;
+        for (int w = 0; w < kAttnWaves; ++w) s += L.part[w * G * head_dim + i];
+        out[i] = s / den[g];
     }
+}
+
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *q, const float *key_cache,
+                                                                 const float *value_cache, float *out, int layer,
+                                                                 int pos, int context, int heads, int kv_heads,
+                                                                 int head_dim) {
+    extern __shared__ float smem[];
+    const int kvh = blockIdx.x;
+    const int G = heads / kv_heads;
+    const int kv_dim = kv_heads * head_dim;
+    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
+    attend_kv_head(q + kvh * G * head_dim, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos, G,
+                   head_dim, kv_dim, smem);
 }
 
 __global__ void add_kernel(float *x, const float *y, int n) {
@@ -218,8 +355,8 @@ inline hipStream_t S(qk_stream s) { return static_cast<hipStream_t>(s); }
 
 }  // namespace
 
-size_t attention_lds_bytes(int pos, int head_dim) {
-    return (static_cast<size_t>(head_dim) + pos + 1 + 256) * sizeof(float);
+size_t attention_lds_bytes(int pos, int head_dim, int group) {
+    return static_cast<size_t>(group) * (head_dim + (pos + 1) + kAttnWaves * head_dim + kAttnWaves) * sizeof(float);
 }
 
 }  // namespace qk
@@ -230,7 +367,8 @@ int qk_rmsnorm_f32(const float *x, const float *weight, float *out, int n, int n
     if (!x || !weight || !out || n < 1 || n_tokens < 0)
         return qk::fail(QK_ERR_INVALID_ARG, "qk_rmsnorm_f32: null pointer or bad size");
     if (n_tokens == 0) return qk::ok();
-    hipLaunchKernelGGL(qk::rmsnorm_kernel, dim3(n_tokens), dim3(256), 0, qk::S(stream), x, weight, out, n, eps);
+    const int vec4 = n % 4 == 0 && qk::aligned(x, 16) && qk::aligned(weight, 16) && qk::aligned(out, 16);
+    hipLaunchKernelGGL(qk::rmsnorm_kernel, dim3(n_tokens), dim3(256), 0, qk::S(stream), x, weight, out, n, eps, vec4);
     return qk::launch_status("qk_rmsnorm_f32 launch");
 }
 
@@ -256,12 +394,14 @@ int qk_attention_f32(const float *q, const float *key_cache, const float *value_
         return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_f32: bad head layout or position outside context");
     if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: head_dim must be a multiple of 4 dividing 256");
+    if (heads / kv_heads > qk::kAttnMaxGroup)
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: more than 8 query heads per KV head");
     if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16))
         return qk::fail(QK_ERR_ALIGN, "qk_attention_f32: caches must be 16-byte aligned");
-    const size_t lds = qk::attention_lds_bytes(pos, head_dim);
+    const size_t lds = qk::attention_lds_bytes(pos, head_dim, heads / kv_heads);
     if (lds > 150 * 1024) return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: position beyond the LDS score buffer");
-    hipLaunchKernelGGL(qk::attention_kernel, dim3(heads), dim3(256), lds, qk::S(stream), q, key_cache, value_cache, out,
-                       layer, pos, context, heads, kv_heads, head_dim);
+    hipLaunchKernelGGL(qk::attention_kernel, dim3(kv_heads), dim3(qk::kAttnThreads), lds, qk::S(stream), q, key_cache,
+                       value_cache, out, layer, pos, context, heads, kv_heads, head_dim);
     return qk::launch_status("qk_attention_f32 launch");
 }
 

@@ -135,12 +135,14 @@ class BatchDescriptor:
         return int(self.seq_id.size)
 
 
-def ffn_3b_ragged(seed: int = 3, n_tokens: int = 32):
-    """3B FFN on n_tokens decode tokens of distinct sequences."""
+def ffn_3b_ragged(seed: int = 3, n_tokens: int = 32, copy: int = 0):
+    """3B FFN on n_tokens decode tokens of distinct sequences; copy > 0 gives
+    further weight sets (streams 16*copy + 1..3) for cache rotation in timing."""
     cfg = LLAMA_3B
-    gate = synth.quant_matrix(Q4_K, cfg["dim"], cfg["hidden"], seed, 1, SIGMA[Q4_K])
-    up = synth.quant_matrix(Q4_K, cfg["dim"], cfg["hidden"], seed, 2, SIGMA[Q4_K])
-    down = synth.quant_matrix(Q6_K, cfg["hidden"], cfg["dim"], seed, 3, SIGMA[Q6_K])
+    base = 16 * copy
+    gate = synth.quant_matrix(Q4_K, cfg["dim"], cfg["hidden"], seed, base + 1, SIGMA[Q4_K])
+    up = synth.quant_matrix(Q4_K, cfg["dim"], cfg["hidden"], seed, base + 2, SIGMA[Q4_K])
+    down = synth.quant_matrix(Q6_K, cfg["hidden"], cfg["dim"], seed, base + 3, SIGMA[Q6_K])
     x = synth.normal_f32(n_tokens * cfg["dim"], seed, 4).reshape(n_tokens, cfg["dim"])
     ctx = synth.uniform_i32(n_tokens, seed, 5, 64, 2048)
     desc = BatchDescriptor(seq_id=np.arange(n_tokens, dtype=np.int32), pos=(ctx - 1).astype(np.int32),

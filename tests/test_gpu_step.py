@@ -8,9 +8,10 @@ from conftest import rel_l2, to_dev
 pytestmark = pytest.mark.gpu
 
 
-def test_rmsnorm(qk, torch_gpu, oracle, synth):
+@pytest.mark.parametrize("n", [3072, 2048, 1001])
+def test_rmsnorm(qk, torch_gpu, oracle, synth, n):
     t = torch_gpu
-    n, ntok = 3072, 3
+    ntok = 3
     x = synth.normal_f32(n * ntok, 91, 1).reshape(ntok, n) * np.float32(50.0)
     w = synth.normal_f32(n, 91, 2)
     out = t.empty((ntok, n), device="cuda")
@@ -48,7 +49,8 @@ def test_rope_kv_write(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim):
     assert float(kc.abs().sum()) == 0.0 and float(vc.abs().sum()) == 0.0
 
 
-@pytest.mark.parametrize("heads,kv_heads,head_dim,pos", [(32, 8, 64, 591), (24, 8, 128, 100), (4, 4, 64, 0)])
+@pytest.mark.parametrize("heads,kv_heads,head_dim,pos", [(32, 8, 64, 591), (24, 8, 128, 100), (4, 4, 64, 0),
+                                                          (32, 8, 64, 1023), (8, 1, 32, 300), (4, 2, 256, 77)])
 def test_attention(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim, pos):
     t = torch_gpu
     ctx, layer, layers = 1024, 2, 3
