@@ -24,15 +24,17 @@
 //   pack_activations  once per (block, 32-token tile): x -> the record of
 //                     MFMA A operands (fp16 hi / lo, sub-block sums, scales)
 //                     in the caller's workspace.
-//   batch_mfma        a workgroup (4 waves) owns 128 weight rows x one token
-//                     tile x a run of blocks.  Per block it copies the record
-//                     into LDS (double-buffered: the next record and the next
-//                     block's weight bytes load while this block computes) and
-//                     each wave decodes the raw bytes of its 32 rows into MFMA
-//                     B operands in registers (lane l: row l%32, block half
-//                     l/32).  When one row group's blocks are split over
-//                     several workgroups (to put enough waves on the chip),
-//                     each writes its partial sums to the workspace;
+//   batch_gemm        a workgroup (4 waves) owns 256 weight rows (two 32-row
+//                     tiles per wave) x one or two token tiles x a run of
+//                     blocks.  Per block it copies the token tiles' records
+//                     into LDS with direct global->LDS loads (double-buffered:
+//                     the next block's records and weight bytes load while
+//                     this block computes); each wave decodes the raw bytes of
+//                     its rows into MFMA B operands in registers (lane l: row
+//                     l%32, block half l/32), and every decoded operand feeds
+//                     every token tile.  When one row group's blocks are split
+//                     over several workgroups (to put enough waves on the
+//                     chip), each writes its partial sums to the workspace;
 //   reduce_splits     adds them in split order, so results are deterministic.
 #include "qk_internal.h"
 
@@ -52,9 +54,10 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaMinTokens = 8;
 constexpr int kTokTile = 32;            // tokens per MFMA tile (the A rows)
-constexpr int kGroupRows = 128;         // weight rows per workgroup (4 waves x 32)
-constexpr int kMaxSplit = 4;            // workgroups splitting one row group's blocks
-constexpr int kTargetGroups = 512;      // two workgroups per CU
+constexpr int kRowTiles = 2;            // 32-row tiles per wave
+constexpr int kGroupRows = 128 * kRowTiles;   // weight rows per workgroup (4 waves)
+constexpr int kPartialFloats = 4 * kRowTiles * 16 * 64;   // one workgroup's partial sums per token tile
+constexpr int kMaxSplit = 8;            // workgroups splitting one row group's blocks
 
 // LDS tile of one block's activations for one 32-token tile, in MFMA A
 // operand order:
@@ -83,7 +86,7 @@ struct BatchMatrix {
     int type;
     int row_bytes;
     int ldy;
-    int group_begin;   // first 128-row group of this matrix in the launch
+    int group_begin;   // first row group (kGroupRows rows) of this matrix in the launch
 };
 
 struct BatchParams {
@@ -96,7 +99,7 @@ struct BatchParams {
     int tiles;
     int splits;             // workgroups sharing one row group's blocks
     int blocks_per_split;
-    float *partials;        // [group][tile][split][4096] when splits > 1
+    float *partials;        // [group][tile][split][kPartialFloats] when splits > 1
     const uint8_t *records; // packed activations, [tile][block][kTileBytes]
 };
 
@@ -278,119 +281,171 @@ __device__ __forceinline__ _Float16 s8_to_h(uint32_t v) {
     return static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(v & 0xFFu)));
 }
 
-// acc += this block's contribution (32 tokens x the lane's row).
+// Scale / bias operands of step j of block half hf for one row tile: the
+// Q4_K sub-block scales (code offset 0) or the Q6_K int8 scales (code - 32).
 template <int TYPE>
-__device__ __forceinline__ void block_mfma(const RawBlock &r, int type, const uint8_t *tile_lds, int kh, int col,
-                                           float16v &acc) {
-    const float4 *fr = reinterpret_cast<const float4 *>(tile_lds + 2 * kTileA + 2 * kTileM) + kh * 4;
-    float f[16];
-    #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 u = fr[i];
-        f[4 * i] = u.x;
-        f[4 * i + 1] = u.y;
-        f[4 * i + 2] = u.z;
-        f[4 * i + 3] = u.w;
-    }
-    float d, dmin = 0.f;
-    uint32_t sc4 = 0, mn4 = 0;
+__device__ __forceinline__ void step_scales(const RawBlock &r, int type, uint32_t sc4, int hf, int j, half2v &sa2,
+                                            half2v &ba2, half2v &sb2, half2v &bb2) {
+    _Float16 sa, sb, off;
     if (is_q4<TYPE>(type)) {
-        d = f16_bits_to_f32(r.hdr.x & 0xFFFFu);
-        dmin = f16_bits_to_f32(r.hdr.x >> 16);
-        q4k_scale_min4(r.hdr, kh, sc4, mn4);
+        sa = u8_to_h(sc4 >> (16 * hf));
+        sb = u8_to_h(sc4 >> (16 * hf + 8));
+        off = static_cast<_Float16>(-1024.f);
     } else {
-        d = f16_bits_to_f32(r.hdr.z);
+        // scales[kh*8 + 4*hf + 2*half + j/4]
+        const uint32_t sw = hf ? r.hdr.y : r.hdr.x;
+        sa = s8_to_h(sw >> (8 * (j >> 2)));
+        sb = s8_to_h(sw >> (8 * (j >> 2) + 16));
+        off = static_cast<_Float16>(-1056.f);   // code - 32
     }
-    const half8 *ahp = reinterpret_cast<const half8 *>(tile_lds) + kh * 32 + col;
-    const half8 *alp = reinterpret_cast<const half8 *>(tile_lds + kTileA) + kh * 32 + col;
-    float16v t;
+    sa2 = half2v{sa, sa};
+    sb2 = half2v{sb, sb};
+    ba2 = half2v{static_cast<_Float16>(off * sa), static_cast<_Float16>(off * sa)};
+    bb2 = half2v{static_cast<_Float16>(off * sb), static_cast<_Float16>(off * sb)};
+}
+
+// acc[r][t] += this block's contribution: RT row tiles (32 weight rows each,
+// lane l -> row l%32, block half l/32) x TT token tiles (32 tokens each).
+// Each decoded weight operand feeds TT token tiles; each activation operand
+// read from LDS feeds RT row tiles.
+template <int TYPE, int RT, int TT>
+__device__ __forceinline__ void block_mma(const RawBlock (&r)[RT], int type, const uint8_t *buf_lds, int kh, int col,
+                                          float16v (&acc)[RT][TT]) {
+    float d[RT], dmin[RT];
+    uint32_t sc4[RT], mn4[RT];
     #pragma unroll
-    for (int k = 0; k < 16; ++k) t[k] = 0.f;
+    for (int i = 0; i < RT; ++i) {
+        dmin[i] = 0.f;
+        sc4[i] = mn4[i] = 0;
+        if (is_q4<TYPE>(type)) {
+            d[i] = f16_bits_to_f32(r[i].hdr.x & 0xFFFFu);
+            dmin[i] = f16_bits_to_f32(r[i].hdr.x >> 16);
+            q4k_scale_min4(r[i].hdr, kh, sc4[i], mn4[i]);
+        } else {
+            d[i] = f16_bits_to_f32(r[i].hdr.z);
+        }
+    }
+    float16v t[RT][TT];
+    #pragma unroll
+    for (int i = 0; i < RT; ++i)
+        #pragma unroll
+        for (int u = 0; u < TT; ++u)
+            #pragma unroll
+            for (int k = 0; k < 16; ++k) t[i][u][k] = 0.f;
+    // Activation operands are read from LDS one step ahead of their use.
+    half8 ah[TT], al[TT];
+    #pragma unroll
+    for (int u = 0; u < TT; ++u) {
+        const uint8_t *tile = buf_lds + u * kTileBytes;
+        ah[u] = reinterpret_cast<const half8 *>(tile)[kh * 32 + col];
+        al[u] = reinterpret_cast<const half8 *>(tile + kTileA)[kh * 32 + col];
+    }
     #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
         #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            _Float16 sa, sb, off;
-            if (is_q4<TYPE>(type)) {
-                sa = u8_to_h(sc4 >> (16 * hf));
-                sb = u8_to_h(sc4 >> (16 * hf + 8));
-                off = static_cast<_Float16>(-1024.f);
-            } else {
-                // scales[kh*8 + 4*hf + 2*half + j/4]
-                const uint32_t sw = hf ? r.hdr.y : r.hdr.x;
-                sa = s8_to_h(sw >> (8 * (j >> 2)));
-                sb = s8_to_h(sw >> (8 * (j >> 2) + 16));
-                off = static_cast<_Float16>(-1056.f);   // code - 32
-            }
-            const half2v sa2 = {sa, sa}, sb2 = {sb, sb};
-            const half2v ba2 = {static_cast<_Float16>(off * sa), static_cast<_Float16>(off * sa)};
-            const half2v bb2 = {static_cast<_Float16>(off * sb), static_cast<_Float16>(off * sb)};
-            const half8 bw = decode_b<TYPE>(r, type, hf, j, sa2, ba2, sb2, bb2);
             const int st = hf * 8 + j;
-            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(ahp[st * 64], bw, t, 0, 0, 0);
-            t = __builtin_amdgcn_mfma_f32_32x32x16_f16(alp[st * 64], bw, t, 0, 0, 0);
+            half8 ahn[TT], aln[TT];
+            #pragma unroll
+            for (int u = 0; u < TT; ++u) {
+                const uint8_t *tile = buf_lds + u * kTileBytes;
+                const int sn = st < 15 ? st + 1 : st;
+                ahn[u] = reinterpret_cast<const half8 *>(tile)[sn * 64 + kh * 32 + col];
+                aln[u] = reinterpret_cast<const half8 *>(tile + kTileA)[sn * 64 + kh * 32 + col];
+            }
+            #pragma unroll
+            for (int i = 0; i < RT; ++i) {
+                half2v sa2, ba2, sb2, bb2;
+                step_scales<TYPE>(r[i], type, sc4[i], hf, j, sa2, ba2, sb2, bb2);
+                const half8 bw = decode_b<TYPE>(r[i], type, hf, j, sa2, ba2, sb2, bb2);
+                #pragma unroll
+                for (int u = 0; u < TT; ++u) {
+                    t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[u], bw, t[i][u], 0, 0, 0);
+                    t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[u], bw, t[i][u], 0, 0, 0);
+                }
+            }
+            #pragma unroll
+            for (int u = 0; u < TT; ++u) {
+                ah[u] = ahn[u];
+                al[u] = aln[u];
+            }
         }
     }
     #pragma unroll
-    for (int k = 0; k < 16; ++k) acc[k] = fmaf(d * f[k], t[k], acc[k]);
-    if (is_q4<TYPE>(type)) {
-        const half4 mh = reinterpret_cast<const half4 *>(tile_lds + 2 * kTileA)[kh * 32 + col];
-        const half4 ml = reinterpret_cast<const half4 *>(tile_lds + 2 * kTileA + kTileM)[kh * 32 + col];
-        half4 bm;
+    for (int u = 0; u < TT; ++u) {
+        const uint8_t *tile = buf_lds + u * kTileBytes;
+        const float4 *fr = reinterpret_cast<const float4 *>(tile + 2 * kTileA + 2 * kTileM) + kh * 4;
+        float f[16];
         #pragma unroll
-        for (int e = 0; e < 4; ++e) bm[e] = u8_to_h(mn4 >> (8 * e));
-        float16v tm;
+        for (int q = 0; q < 4; ++q) {
+            const float4 v = fr[q];
+            f[4 * q] = v.x;
+            f[4 * q + 1] = v.y;
+            f[4 * q + 2] = v.z;
+            f[4 * q + 3] = v.w;
+        }
         #pragma unroll
-        for (int k = 0; k < 16; ++k) tm[k] = 0.f;
-        tm = __builtin_amdgcn_mfma_f32_32x32x8f16(mh, bm, tm, 0, 0, 0);
-        tm = __builtin_amdgcn_mfma_f32_32x32x8f16(ml, bm, tm, 0, 0, 0);
-        #pragma unroll
-        for (int k = 0; k < 16; ++k) acc[k] = fmaf(-64.f * dmin * f[k], tm[k], acc[k]);
+        for (int i = 0; i < RT; ++i)
+            #pragma unroll
+            for (int k = 0; k < 16; ++k) acc[i][u][k] = fmaf(d[i] * f[k], t[i][u][k], acc[i][u][k]);
+        if (is_q4<TYPE>(type)) {
+            const half4 mh = reinterpret_cast<const half4 *>(tile + 2 * kTileA)[kh * 32 + col];
+            const half4 ml = reinterpret_cast<const half4 *>(tile + 2 * kTileA + kTileM)[kh * 32 + col];
+            #pragma unroll
+            for (int i = 0; i < RT; ++i) {
+                half4 bm;
+                #pragma unroll
+                for (int e = 0; e < 4; ++e) bm[e] = u8_to_h(mn4[i] >> (8 * e));
+                float16v tm;
+                #pragma unroll
+                for (int k = 0; k < 16; ++k) tm[k] = 0.f;
+                tm = __builtin_amdgcn_mfma_f32_32x32x8f16(mh, bm, tm, 0, 0, 0);
+                tm = __builtin_amdgcn_mfma_f32_32x32x8f16(ml, bm, tm, 0, 0, 0);
+                #pragma unroll
+                for (int k = 0; k < 16; ++k) acc[i][u][k] = fmaf(-64.f * dmin[i] * f[k], tm[k], acc[i][u][k]);
+            }
+        }
     }
 }
 
 // ---------------------------------------------------------------- GEMM --
 //
-// Workgroup = 4 waves = 128 weight rows (32 per wave, lane l -> row l%32,
-// block half l/32) x one 32-token tile x a run of blocks.  Per block the
-// workgroup stages the activations once in LDS (double-buffered) and each
-// wave decodes its rows' raw block bytes into MFMA B operands; the next
-// block's activations and weight bytes are loaded while this one computes.
+// Workgroup = 4 waves x kRowTiles row tiles = 256 weight rows, x TT token
+// tiles of 32 tokens, x a run of blocks.  Per block the workgroup copies the
+// TT activation records into LDS with direct global->LDS loads (no register
+// round trip), double-buffered: block b+1's records and weight bytes are in
+// flight while block b computes.  Wave w owns rows (i*4 + w)*32 .. +31 of
+// the group for row tile i.
 
-// Copy of one packed record into LDS in 16-byte chunks: the 2048 chunks of
-// the fp16 operands, eight per thread, then the 72 chunks of sums and
-// scales (every thread loads one, clamped; the first 72 store theirs).
-constexpr int kChunks = kTileBytes / 16;
-constexpr int kMainChunks = 2 * kTileA / 16;
-constexpr int kTailChunks = kChunks - kMainChunks;
-static_assert(kMainChunks == 8 * 256 && kTailChunks <= 256, "record copy layout");
+constexpr int kChunks = kTileBytes / 16;       // 16-byte chunks per record
+static_assert(kChunks > 8 * 256 && kChunks <= 9 * 256, "record copy layout");
 
-struct RecordStage {
-    uint4 v[8];
-    uint4 tail;
-};
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) const void global_void_t;
 
-__device__ __forceinline__ void record_load(const uint8_t *rec, RecordStage &s) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(rec);
+// Wave-cooperative copy of one record into LDS: chunk c of the record goes
+// to LDS byte 16*c; wave w issues chunks i*256 + w*64 + lane.
+__device__ __forceinline__ void record_dma(const uint8_t *rec, uint8_t *tile_lds, int wave, int lane) {
     #pragma unroll
-    for (int i = 0; i < 8; ++i) s.v[i] = src[i * 256 + threadIdx.x];
-    s.tail = src[kMainChunks + min(static_cast<int>(threadIdx.x), kTailChunks - 1)];
+    for (int i = 0; i < 9; ++i) {
+        const int c0 = i * 256 + wave * 64;   // wave-uniform
+        if (c0 + lane < kChunks)
+            __builtin_amdgcn_global_load_lds((global_void_t *)(rec + static_cast<size_t>(c0 + lane) * 16),
+                                             (lds_void_t *)(tile_lds + c0 * 16), 16, 0, 0);
+    }
 }
 
-__device__ __forceinline__ void record_store(const RecordStage &s, uint8_t *tile_lds) {
-    uint4 *dst = reinterpret_cast<uint4 *>(tile_lds);
-    #pragma unroll
-    for (int i = 0; i < 8; ++i) dst[i * 256 + threadIdx.x] = s.v[i];
-    if (threadIdx.x < kTailChunks) dst[kMainChunks + threadIdx.x] = s.tail;
-}
+__device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-template <int TYPE>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void batch_mfma(BatchParams p) {
+template <int TYPE, int TT>
+__global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int RT = kRowTiles;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kh = lane >> 5, col = lane & 31;
-    const int split = blockIdx.x % p.splits, group = blockIdx.x / p.splits, tile = blockIdx.y;
+    const int split = blockIdx.x % p.splits, group = blockIdx.x / p.splits;
+    const int tile0 = blockIdx.y * TT;
 
     int m = 0;
     #pragma unroll
@@ -399,58 +454,92 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const BatchMatrix &M = p.mat[m];
     const int type = TYPE ? TYPE : M.type;
     const int bpb = is_q4<TYPE>(type) ? 144 : 210;
-    const int row = (group - M.group_begin) * kGroupRows + wave * 32 + col;
-    const uint8_t *wrow = M.w + static_cast<size_t>(min(row, M.rows - 1)) * M.row_bytes;
-    const uint8_t *recs = p.records + static_cast<size_t>(tile) * p.nb * kTileBytes;
+    const uint8_t *wrow[RT];
+    int row[RT];
+    #pragma unroll
+    for (int i = 0; i < RT; ++i) {
+        row[i] = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
+        wrow[i] = M.w + static_cast<size_t>(min(row[i], M.rows - 1)) * M.row_bytes;
+    }
+    // Token tiles past the end read the last tile's records (in bounds) and store nothing.
+    const uint8_t *recs[TT];
+    #pragma unroll
+    for (int u = 0; u < TT; ++u)
+        recs[u] = p.records + static_cast<size_t>(min(tile0 + u, p.tiles - 1)) * p.nb * kTileBytes;
 
     const int b0 = split * p.blocks_per_split;
     const int b1 = min(p.nb, b0 + p.blocks_per_split);
-    RecordStage rs;
-    record_load(recs + static_cast<size_t>(b0) * kTileBytes, rs);
-    RawBlock cur = load_block<TYPE>(wrow + b0 * bpb, type, kh);
-    record_store(rs, lds);
+    #pragma unroll
+    for (int u = 0; u < TT; ++u) record_dma(recs[u] + static_cast<size_t>(b0) * kTileBytes, lds + u * kTileBytes, wave, lane);
+    RawBlock cur[RT];
+    #pragma unroll
+    for (int i = 0; i < RT; ++i) cur[i] = load_block<TYPE>(wrow[i] + b0 * bpb, type, kh);
+    wait_loads();
     __syncthreads();
 
-    float16v acc;
+    float16v acc[RT][TT];
     #pragma unroll
-    for (int k = 0; k < 16; ++k) acc[k] = 0.f;
+    for (int i = 0; i < RT; ++i)
+        #pragma unroll
+        for (int u = 0; u < TT; ++u)
+            #pragma unroll
+            for (int k = 0; k < 16; ++k) acc[i][u][k] = 0.f;
     for (int b = b0; b < b1; ++b) {
         const int buf = (b - b0) & 1;
-        // The last iteration reloads its own block (unconditional, in bounds).
+        // The last iteration reloads its own weight bytes (unconditional, in bounds).
         const int bn = min(b + 1, b1 - 1);
-        record_load(recs + static_cast<size_t>(bn) * kTileBytes, rs);
-        const RawBlock nxt = load_block<TYPE>(wrow + bn * bpb, type, kh);
-        block_mfma<TYPE>(cur, type, lds + buf * kTileBytes, kh, col, acc);
-        record_store(rs, lds + (buf ^ 1) * kTileBytes);
-        cur = nxt;
+        if (b + 1 < b1) {
+            #pragma unroll
+            for (int u = 0; u < TT; ++u)
+                record_dma(recs[u] + static_cast<size_t>(bn) * kTileBytes, lds + ((buf ^ 1) * TT + u) * kTileBytes, wave,
+                           lane);
+        }
+        RawBlock nxt[RT];
+        #pragma unroll
+        for (int i = 0; i < RT; ++i) nxt[i] = load_block<TYPE>(wrow[i] + bn * bpb, type, kh);
+        block_mma<TYPE, RT, TT>(cur, type, lds + buf * TT * kTileBytes, kh, col, acc);
+        #pragma unroll
+        for (int i = 0; i < RT; ++i) cur[i] = nxt[i];
+        wait_loads();
         __syncthreads();
     }
 
-    // Accumulator register k holds token 8*(k/4) + 4*kh + k%4 of the tile.
-    const int tbase = tile * kTokTile + 4 * kh;
+    // Accumulator register k holds token 8*(k/4) + 4*kh + k%4 of its tile.
     if (p.splits == 1) {
-        if (row < M.rows) {
+        #pragma unroll
+        for (int u = 0; u < TT; ++u) {
+            const int tbase = (tile0 + u) * kTokTile + 4 * kh;
             #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int t = tbase + 8 * (k >> 2) + (k & 3);
-                if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = acc[k];
+            for (int i = 0; i < RT; ++i) {
+                if (row[i] >= M.rows) continue;
+                #pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int t = tbase + 8 * (k >> 2) + (k & 3);
+                    if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row[i]] = acc[i][u][k];
+                }
             }
         }
         return;
     }
-
-    // Split blocks: the partial sums go to the workspace in accumulator
-    // order; reduce_splits adds them.
-    const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
-    float *mine = p.partials + (slot * p.splits + split) * 4096 + wave * 1024 + lane;
+    // Split blocks: partial sums to the workspace in accumulator order,
+    // [group][token tile][split][wave][row tile][k][lane]; reduce_splits adds them.
     #pragma unroll
-    for (int k = 0; k < 16; ++k) mine[k * 64] = acc[k];
+    for (int u = 0; u < TT; ++u) {
+        if (tile0 + u >= p.tiles) break;
+        const size_t slot = static_cast<size_t>(group) * p.tiles + tile0 + u;
+        float *mine = p.partials + (slot * p.splits + split) * kPartialFloats + wave * (RT * 1024) + lane;
+        #pragma unroll
+        for (int i = 0; i < RT; ++i)
+            #pragma unroll
+            for (int k = 0; k < 16; ++k) mine[i * 1024 + k * 64] = acc[i][u][k];
+    }
 }
 
 // y = the sum of a row group's split partials, in split order (deterministic).
-// One workgroup per (row group, tile); thread (wave, lane) owns the 16
-// outputs the same thread of batch_mfma produced.
+// One workgroup per (row group, token tile); thread (wave, lane) owns the
+// outputs the same thread of batch_gemm produced.
 __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
+    constexpr int RT = kRowTiles;
     const int group = blockIdx.x, tile = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int kh = lane >> 5, col = lane & 31;
@@ -458,23 +547,35 @@ __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
     #pragma unroll
     for (int i = 1; i < QK_MAX_FUSED; ++i) m += (i < p.n_mats && group >= p.mat[i].group_begin) ? 1 : 0;
     const BatchMatrix &M = p.mat[m];
-    const int row = (group - M.group_begin) * kGroupRows + wave * 32 + col;
     const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
-    const float *part = p.partials + slot * p.splits * 4096 + wave * 1024 + lane;
+    const float *part = p.partials + slot * p.splits * kPartialFloats + wave * (RT * 1024) + lane;
     const int tbase = tile * kTokTile + 4 * kh;
-    // Every load is issued before the first add: the kernel is latency-bound.
-    float v[kMaxSplit][16];
     #pragma unroll
-    for (int sp = 0; sp < kMaxSplit; ++sp)
+    for (int i = 0; i < RT; ++i) {
+        const int row = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
+        // Every load of a split run is issued before the first add: the kernel is latency-bound.
+        float s[16];
         #pragma unroll
-        for (int k = 0; k < 16; ++k) v[sp][k] = sp < p.splits ? part[sp * 4096 + k * 64] : 0.f;
-    #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        float s = v[0][k];
+        for (int k = 0; k < 16; ++k) s[k] = part[i * 1024 + k * 64];
+        for (int sp0 = 1; sp0 < p.splits; sp0 += 4) {
+            float v[4][16];
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                #pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    v[q][k] = sp0 + q < p.splits ? part[(sp0 + q) * kPartialFloats + i * 1024 + k * 64] : 0.f;
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                #pragma unroll
+                for (int k = 0; k < 16; ++k)
+                    if (sp0 + q < p.splits) s[k] += v[q][k];
+        }
+        if (row >= M.rows) continue;
         #pragma unroll
-        for (int sp = 1; sp < kMaxSplit; ++sp) s += v[sp][k];
-        const int t = tbase + 8 * (k >> 2) + (k & 3);
-        if (row < M.rows && t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = s;
+        for (int k = 0; k < 16; ++k) {
+            const int t = tbase + 8 * (k >> 2) + (k & 3);
+            if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = s[k];
+        }
     }
 }
 
@@ -488,11 +589,18 @@ int check_batched(const char *where, const float *x, int ldx, int cols, int n_to
 
 int tile_count(int n_tokens) { return (n_tokens + kTokTile - 1) / kTokTile; }
 
-// Workgroups sharing a row group's blocks: enough that about kTargetGroups
-// workgroups run, at most kMaxSplit, at least two blocks each.
-void split_plan(int64_t rows_total, int nb, int tiles, int &splits, int &per_split) {
-    const int64_t groups = std::max<int64_t>(1, (rows_total + kGroupRows - 1) / kGroupRows);
-    const int64_t want = (kTargetGroups + groups * tiles - 1) / (groups * tiles);
+// Token tiles per workgroup: two once there are two tiles (each decoded
+// weight operand then feeds 64 tokens), else one.
+int token_tiles_per_group(int tiles) { return tiles >= 2 ? 2 : 1; }
+
+// Workgroups sharing a row group's blocks: enough that about two workgroups
+// per CU (one with two token tiles, whose LDS fills a CU) are in flight, at
+// most kMaxSplit, at least two blocks each.
+void split_plan(int64_t groups, int nb, int tiles, int &splits, int &per_split) {
+    const int tt = token_tiles_per_group(tiles);
+    const int64_t target = static_cast<int64_t>(device_info().cus) * (tt == 1 ? 2 : 1);
+    const int64_t have = std::max<int64_t>(1, groups * ((tiles + tt - 1) / tt));
+    const int64_t want = (target + have - 1) / have;
     int s = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want, 1), std::min(kMaxSplit, std::max(1, nb / 2))));
     per_split = (nb + s - 1) / s;
     splits = (nb + per_split - 1) / per_split;
@@ -502,23 +610,65 @@ size_t records_bytes(int cols, int n_tokens) {
     return static_cast<size_t>(tile_count(n_tokens)) * (cols / 256) * kTileBytes;
 }
 
-// Workspace: packed activation records, then (when blocks are split) one
-// counter per (row group, tile) and the partial sums.
-size_t workspace_bytes(int cols, int64_t rows_total, int n_tokens) {
-    if (cols <= 0 || cols % 256 || rows_total <= 0 || n_tokens < kMfmaMinTokens) return 0;
+int64_t group_count(const int *rows, int n) {
+    int64_t g = 0;
+    for (int i = 0; i < n; ++i) g += (rows[i] + kGroupRows - 1) / kGroupRows;
+    return g;
+}
+
+// Workspace: packed activation records, then (when blocks are split) the
+// partial sums of every (row group, token tile, split).
+size_t workspace_bytes(int cols, const int *rows, int n_mats, int n_tokens) {
+    if (cols <= 0 || cols % 256 || n_mats < 1 || n_tokens < kMfmaMinTokens) return 0;
     const int tiles = tile_count(n_tokens);
     size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
+    const int64_t groups = group_count(rows, n_mats);
+    if (groups < 1) return 0;
     int splits, per_split;
-    split_plan(rows_total, cols / 256, tiles, splits, per_split);
+    split_plan(groups, cols / 256, tiles, splits, per_split);
     if (splits == 1) return bytes;
-    const int64_t groups = (rows_total + kGroupRows - 1) / kGroupRows + QK_MAX_FUSED - 1;
-    return bytes + static_cast<size_t>(groups) * tiles * splits * 4096 * sizeof(float);
+    return bytes + static_cast<size_t>(groups) * tiles * splits * kPartialFloats * sizeof(float);
+}
+
+// Workspace bound for the public query, which knows only the total row
+// count: the group count of any split of `rows_total` rows over at most
+// QK_MAX_FUSED matrices is at most rows_total/kGroupRows + QK_MAX_FUSED.
+size_t workspace_bound(int cols, int rows_total, int n_tokens) {
+    if (rows_total <= 0) return 0;
+    const int tiles = tile_count(n_tokens);
+    if (cols <= 0 || cols % 256 || n_tokens < kMfmaMinTokens) return 0;
+    size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
+    const int64_t gmin = (rows_total + kGroupRows - 1) / kGroupRows;
+    const int64_t gmax = rows_total / kGroupRows + QK_MAX_FUSED;
+    size_t best = 0;
+    for (int64_t g : {gmin, gmax}) {
+        int splits, per_split;
+        split_plan(g, cols / 256, tiles, splits, per_split);
+        if (splits > 1) best = std::max(best, static_cast<size_t>(g) * tiles * splits * kPartialFloats * sizeof(float));
+    }
+    // Between gmin and gmax the split count only falls as groups grow, and the
+    // partial bytes are groups * splits: bounded by gmax * splits(gmin).
+    int s_min, ps;
+    split_plan(gmin, cols / 256, tiles, s_min, ps);
+    if (s_min > 1) best = std::max(best, static_cast<size_t>(gmax) * tiles * s_min * kPartialFloats * sizeof(float));
+    return bytes + best;
+}
+
+template <int TT>
+void launch_gemm(int type, const dim3 &grid, size_t lds, hipStream_t stream, const BatchParams &p) {
+    if (type == QK_TYPE_Q4_K)
+        hipLaunchKernelGGL((batch_gemm<QK_TYPE_Q4_K, TT>), grid, dim3(256), lds, stream, p);
+    else if (type == QK_TYPE_Q6_K)
+        hipLaunchKernelGGL((batch_gemm<QK_TYPE_Q6_K, TT>), grid, dim3(256), lds, stream, p);
+    else
+        hipLaunchKernelGGL((batch_gemm<0, TT>), grid, dim3(256), lds, stream, p);
 }
 
 int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *x, int ldx, int cols, int n_tokens,
                 void *workspace, size_t workspace_size, hipStream_t stream, const char *where) {
     const int nb = cols / 256;
     const int tiles = tile_count(n_tokens);
+    const int tt = token_tiles_per_group(tiles);
     if (tiles > 65535) return fail(QK_ERR_LIMIT, std::string(where) + ": too many tokens in one launch");
     BatchParams p{};
     p.n_mats = n_mats;
@@ -527,8 +677,9 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     p.n_tokens = n_tokens;
     p.nb = nb;
     p.tiles = tiles;
-    int64_t groups = 0, rows_total = 0;
+    int64_t groups = 0;
     int type = mats[0].type;
+    int rows[QK_MAX_FUSED];
     for (int i = 0; i < n_mats; ++i) {
         BatchMatrix &M = p.mat[i];
         M.w = static_cast<const uint8_t *>(mats[i].w);
@@ -539,14 +690,14 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         M.ldy = ldy[i];
         M.group_begin = static_cast<int>(groups);
         groups += (M.rows + kGroupRows - 1) / kGroupRows;
-        rows_total += M.rows;
+        rows[i] = M.rows;
         if (static_cast<int64_t>(M.rows) * M.row_bytes > (int64_t(1) << 40))
             return fail(QK_ERR_LIMIT, std::string(where) + ": matrix too large");
         if (M.type != type) type = 0;
     }
-    split_plan(rows_total, nb, tiles, p.splits, p.blocks_per_split);
+    split_plan(groups, nb, tiles, p.splits, p.blocks_per_split);
     if (groups * p.splits > (1 << 30)) return fail(QK_ERR_LIMIT, std::string(where) + ": too many rows");
-    const size_t need = workspace_bytes(cols, rows_total, n_tokens);
+    const size_t need = workspace_bytes(cols, rows, n_mats, n_tokens);
     if (!workspace || workspace_size < need)
         return fail(QK_ERR_INVALID_ARG, std::string(where) + ": workspace smaller than " + std::to_string(need) +
                                             " bytes (qk_gemv_batched_workspace_bytes)");
@@ -555,14 +706,12 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     p.records = ws;
     if (p.splits > 1) p.partials = reinterpret_cast<float *>(ws + (records_bytes(cols, n_tokens) + 255) / 256 * 256);
     hipLaunchKernelGGL(pack_activations, dim3(nb, tiles), dim3(256), 0, stream, p, ws);
-    const dim3 grid(static_cast<unsigned>(groups * p.splits), tiles), block(256);
-    const size_t lds = 2 * kTileBytes;
-    if (type == QK_TYPE_Q4_K)
-        hipLaunchKernelGGL(batch_mfma<QK_TYPE_Q4_K>, grid, block, lds, stream, p);
-    else if (type == QK_TYPE_Q6_K)
-        hipLaunchKernelGGL(batch_mfma<QK_TYPE_Q6_K>, grid, block, lds, stream, p);
+    const dim3 grid(static_cast<unsigned>(groups * p.splits), (tiles + tt - 1) / tt);
+    const size_t lds = 2 * static_cast<size_t>(tt) * kTileBytes;
+    if (tt == 2)
+        launch_gemm<2>(type, grid, lds, stream, p);
     else
-        hipLaunchKernelGGL(batch_mfma<0>, grid, block, lds, stream, p);
+        launch_gemm<1>(type, grid, lds, stream, p);
     if (p.splits > 1)
         hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups), tiles), dim3(256), 0, stream, p);
     return launch_status(where);
@@ -574,7 +723,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
 extern "C" {
 
 size_t qk_gemv_batched_workspace_bytes(int cols, int rows, int n_tokens) {
-    return qk::workspace_bytes(cols, rows, n_tokens);
+    return qk::workspace_bound(cols, rows, n_tokens);
 }
 
 int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float *y, int ldy, int cols, int rows,

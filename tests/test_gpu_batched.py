@@ -106,7 +106,7 @@ def _fused(qk, t, mats, x, cols, ntok):
     return [y.cpu().numpy() for y in outs]
 
 
-@pytest.mark.parametrize("ntok", [8, 40])
+@pytest.mark.parametrize("ntok", [8, 40, 256])
 def test_mfma_fused_qkv_mixed_types(qk, torch_gpu, oracle, workloads, ntok):
     """Llama-3.2-1B QKV: Q4_K q/k, Q6_K v in one launch (mixed-type kernel)."""
     dim, kv = 2048, 512
@@ -121,7 +121,8 @@ def test_mfma_fused_qkv_mixed_types(qk, torch_gpu, oracle, workloads, ntok):
 
 
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
-@pytest.mark.parametrize("cols,rows,ntok", [(8192, 300, 8), (3072, 130, 64), (256, 64, 9)])
+@pytest.mark.parametrize("cols,rows,ntok", [(8192, 300, 8), (3072, 130, 64), (256, 64, 9), (2048, 700, 256),
+                                             (8192, 300, 100), (3072, 520, 32)])
 def test_mfma_shapes(qk, torch_gpu, oracle, workloads, qtype, cols, rows, ntok):
     w, x = workloads.gemv_case(qtype, cols, rows, seed=93 + ntok, n_tokens=ntok)
     y = run_batched(qk, torch_gpu, qtype, w, x, cols, rows)
@@ -175,9 +176,11 @@ def test_mfma_needs_workspace(qk, torch_gpu, workloads):
     cols, rows, ntok = 2048, 64, 8
     w, x = workloads.gemv_case(Q4_K, cols, rows, seed=100, n_tokens=ntok)
     need = qk.batch_workspace_bytes(cols, rows, ntok)
-    assert need > 0          # 64 rows x 8 blocks: the blocks split over several workgroups
+    records = 8 * 33920            # one 32-token tile of packed activations per 256 columns
+    assert need > records          # 64 rows x 8 blocks: the blocks split over several workgroups
     ws = t.empty(need, dtype=t.uint8, device="cuda")
     y = t.empty((ntok, rows), device="cuda")
     with pytest.raises(qk.QKError) as e:
-        qk.batch_matvec(qk.Tensor((cols, rows), Q4_K, to_dev(t, w)), to_dev(t, x), y, cols, rows, ntok, ws, need - 16)
+        qk.batch_matvec(qk.Tensor((cols, rows), Q4_K, to_dev(t, w)), to_dev(t, x), y, cols, rows, ntok, ws,
+                        records - 16)
     assert e.value.status == qk.QK_ERR_INVALID_ARG
