@@ -26,8 +26,7 @@
 //   Lanes of one row form aligned groups of gcd(P,64) lanes reduced with xor
 //   shuffles.  When C > 1 the group sums of a tile meet in LDS and lane t of
 //   the first wave adds row t's C sums in a fixed order (deterministic).
-//   The grid (at most two workgroups per CU for single-wave tiles, else the
-//   resident capacity) walks tiles grid-stride; a tile's loads are issued
+//   The grid (at most two workgroups per CU) walks tiles grid-stride; a tile's loads are issued
 //   before the previous tile's arithmetic, and the first two tiles' loads
 //   before the activation staging.
 //   blockIdx.y selects the token when several tokens share the weights.
@@ -68,6 +67,11 @@ struct GemvParams {
     int chunks;           // C
     int group_lanes;      // gcd(P, 64)
     int total_tiles;
+    // Decode-step fusions of the FP32 path (all off when zero):
+    const float *norm_w;  // stage RMSNorm(x) * norm_w instead of x
+    float norm_eps;
+    const float *up;      // stage x / (1 + exp(-x)) * up instead of x
+    int accumulate;       // y += W x instead of y = W x
 };
 
 struct Raw {
@@ -144,8 +148,7 @@ struct XGroup {
 };
 static_assert(sizeof(XGroup) == 64, "XGroup is one 64-byte LDS record");
 
-__device__ __forceinline__ XGroup make_group(const float *x16) {
-    float v[16];
+__device__ __forceinline__ void load16f(const float *x16, float *v) {
     #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const float4 q = *reinterpret_cast<const float4 *>(x16 + 4 * k);
@@ -154,6 +157,17 @@ __device__ __forceinline__ XGroup make_group(const float *x16) {
         v[4 * k + 2] = q.z;
         v[4 * k + 3] = q.w;
     }
+}
+
+__device__ __forceinline__ XGroup make_group_regs(const float *v);
+
+__device__ __forceinline__ XGroup make_group(const float *x16) {
+    float v[16];
+    load16f(x16, v);
+    return make_group_regs(v);
+}
+
+__device__ __forceinline__ XGroup make_group_regs(const float *v) {
     float m = 0.f, s = 0.f;
     #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -214,13 +228,56 @@ struct F32Policy {
         float X[4];
     };
 
-    // LDS bytes of the prepared activations of one token.
-    __host__ __device__ static size_t lds_bytes(int cols) { return static_cast<size_t>(cols / 16) * sizeof(XGroup); }
+    // LDS bytes of the prepared activations of one token, plus 64 bytes of
+    // reduction scratch for the fused RMSNorm.
+    __host__ __device__ static size_t lds_bytes(int cols) {
+        return static_cast<size_t>(cols / 16) * sizeof(XGroup) + 64;
+    }
 
     // Cooperative: the block writes every 16-column group of its token.
+    // With norm_w the staged values are x * (1/sqrt(mean(x^2) + eps)) * w,
+    // the arithmetic of rmsnorm_cuda (inferencer.cu:821-834); with up they
+    // are x / (1 + exp(-x)) * up, that of silu_cuda (inferencer.cu:1053-1056).
     __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
         const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
-        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) lds[gi] = make_group(x + gi * 16);
+        float scale = 1.f;
+        if (p.norm_w) {
+            float *scratch = reinterpret_cast<float *>(lds + cols / 16);
+            const float4 *x4 = reinterpret_cast<const float4 *>(x);
+            float ss = 0.f;
+            #pragma unroll 4
+            for (int i = threadIdx.x; i < cols / 4; i += blockDim.x) {
+                const float4 v = x4[i];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            #pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            ss = 0.f;
+            for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) ss += scratch[w];
+            scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
+        }
+        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) {
+            float v[16];
+            load16f(x + gi * 16, v);
+            if (p.norm_w) {
+                float w[16];
+                load16f(p.norm_w + gi * 16, w);
+                #pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = v[i] * scale * w[i];
+            }
+            if (p.up) {
+                float u[16];
+                load16f(p.up + static_cast<int64_t>(token) * p.ldx + gi * 16, u);
+                #pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = v[i] / (1.f + expf(-v[i])) * u[i];
+            }
+            lds[gi] = make_group_regs(v);
+        }
     }
 
     __device__ static void set_part(Lane &L, int part, const XGroup &gr) {
@@ -481,11 +538,11 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     int k = 0;
     while (true) {
         float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(a.t.type, a.r, L, g, h));
-        if (piece == 0 && a.t.valid) a.t.y[a.t.row] = v;
+        if (piece == 0 && a.t.valid) a.t.y[a.t.row] = p.accumulate ? a.t.y[a.t.row] + v : v;
         a = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
         if (++k == n_iter) break;
         v = group_sum<GROUP>(piece_dot<Policy, TYPE>(b.t.type, b.r, L, g, h));
-        if (piece == 0 && b.t.valid) b.t.y[b.t.row] = v;
+        if (piece == 0 && b.t.valid) b.t.y[b.t.row] = p.accumulate ? b.t.y[b.t.row] + v : v;
         b = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
         if (++k == n_iter) break;
     }
@@ -508,7 +565,7 @@ __device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, c
         if (rowref.valid) {
             float sum = 0.f;
             for (int c = 0; c < p.chunks; ++c) sum += buf[lane * p.chunks + c];
-            rowref.y[rowref.row] = sum;
+            rowref.y[rowref.row] = p.accumulate ? rowref.y[rowref.row] + sum : sum;
         }
     }
 }
@@ -570,7 +627,7 @@ __global__ __launch_bounds__(256) void gemv_long(GemvParams p) {
         }
         acc = group_sum<64>(acc);
         const TileRef t = locate(p, tile, 0, 0, token);
-        if (lane == 0 && t.valid) t.y[t.row] = acc;
+        if (lane == 0 && t.valid) t.y[t.row] = p.accumulate ? t.y[t.row] + acc : acc;
     }
 }
 
@@ -630,7 +687,11 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int block = wgroups * p.chunks * 64;
         const size_t lds = x_lds + static_cast<size_t>(wgroups) * 2 * p.tile_rows * p.chunks * sizeof(float);
         const void *k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP>);
-        const int cap = std::max(1, resident_blocks(k, block, lds) / n_tokens);
+        // Every block stages the whole activation row; two blocks per CU keep
+        // that staging small next to the weights (down projection 2048 x 8192:
+        // 512 blocks instead of the resident 1024).
+        const int cap = std::max(1, std::min(resident_blocks(k, block, lds), kWaveBlocksPerCu * device_info().cus) /
+                                        n_tokens);
         const int grid = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
         hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
     }
@@ -702,6 +763,26 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
     p.x = x;
     p.ldx = ldx;
     return launch<F32Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "qk_gemv_f32 launch");
+}
+
+bool gemv_fusable(int cols) {
+    if (cols <= 0 || cols % 256) return false;
+    const int pieces = cols / 64;
+    const int chunks = pieces / gcd_int(pieces, 64);
+    return chunks <= kMaxChunks && F32Policy::lds_bytes(cols) + 4096 <= kMaxLds;
+}
+
+int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int cols, const GemvFusion &f,
+                      hipStream_t stream) {
+    if (!gemv_fusable(cols)) return fail(QK_ERR_LIMIT, "fused GEMV: rows too long to stage the activations");
+    GemvParams p{};
+    p.x = x;
+    p.ldx = cols;
+    p.norm_w = f.norm_w;
+    p.norm_eps = f.norm_eps;
+    p.up = f.up;
+    p.accumulate = f.accumulate;
+    return launch<F32Policy>(p, mats, n_mats, cols, 1, nullptr, stream, "fused GEMV launch");
 }
 
 }  // namespace qk

@@ -44,7 +44,45 @@ int check_weights(const char *where, int type, const void *w, int cols, int rows
 
 // Dynamic LDS of the attention kernel for positions 0..pos and `group`
 // query heads per KV head.
-size_t attention_lds_bytes(int pos, int head_dim, int group);
+__host__ __device__ size_t attention_lds_bytes(int pos, int head_dim, int group);
+
+// Decode-step fusions of the FP32 GEMV (driver-internal, not in the C ABI):
+// the activations are staged as RMSNorm(x) * norm_w (rmsnorm_cuda) or as
+// x / (1 + exp(-x)) * up (silu_cuda), and the epilogue adds W x into y (the
+// residual add_cuda) instead of overwriting it.
+struct GemvFusion {
+    const float *norm_w = nullptr;
+    float norm_eps = 0.f;
+    const float *up = nullptr;
+    int accumulate = 0;
+};
+// Whether a row of cols columns can stage its activations for the fusions.
+bool gemv_fusable(int cols);
+// One token, arguments already validated.
+int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int cols, const GemvFusion &f,
+                      hipStream_t stream);
+// Whether the attention kernels serve `group` query heads per KV head and
+// head_dim (group in {1, 2, 3, 4, 6, 8}; head_dim a multiple of 4 dividing 256).
+bool attention_supported(int group, int head_dim);
+// RoPE of q and k at pos, the KV-cache write, then GQA attention of one
+// token (rope_cache_cuda + attention_cuda, inferencer.cu:930-1009) in one
+// launch; q, k, v are the unrotated projections.
+int launch_rope_attention(const float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                          float *key_cache, float *value_cache, float *out, int layer, int pos, int context,
+                          int heads, int kv_heads, int head_dim, hipStream_t stream);
+
+// The same with the positions split into chunks of 64 over several
+// workgroups per KV head (the decode driver's form).  workspace holds
+// attention_workspace_bytes(...) bytes, zeroed once before the first call
+// (its per-head tickets return to zero at the end of every call); calls that
+// share a workspace must not overlap.
+size_t attention_workspace_bytes(int kv_heads, int group, int head_dim, int context);
+// head_dim 64, 128 or 256 and at most 64 KV heads.
+bool chunked_attention_supported(int kv_heads, int group, int head_dim);
+int launch_rope_attention_chunked(const float *q, const float *k, const float *v, const float *cosine,
+                                  const float *sine, float *key_cache, float *value_cache, float *out, void *workspace,
+                                  int layer, int pos, int context, int heads, int kv_heads, int head_dim,
+                                  hipStream_t stream);
 
 // Per-device properties, cached once per device (thread-safe).
 struct DeviceInfo {

@@ -2,8 +2,10 @@
 //
 // The counterpart of FastGPU / FastRunner (inferencer.cu:1101-1150,
 // 1182-1532): buffers, KV cache and RoPE tables are allocated once in
-// qk_llama_create; qk_llama_forward issues one step in the order of
-// FastRunner::forward (inferencer.cu:1424-1531).  The step is generalised
+// qk_llama_create; qk_llama_forward issues one step with the arithmetic of
+// FastRunner::forward (inferencer.cu:1424-1531) in five launches per layer:
+// the RMSNorms, SiLU * up and residual adds are fused into the GEMVs around
+// them, RoPE and the KV write into the attention kernel.  The step is generalised
 // past the reference's Llama-3.2-3B hard-coding (inferencer.cu:1215-1217):
 // any head_dim dividing 256, GQA group and layer count.
 //
@@ -26,6 +28,7 @@ struct qk_llama {
     float *attn = nullptr, *tmp = nullptr, *gate = nullptr, *up = nullptr, *logits = nullptr;
     float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
     void *argmax_ws = nullptr;
+    void *attn_ws = nullptr;   // chunked attention partials and tickets (zeroed once)
     int32_t *d_next = nullptr, *d_token = nullptr;
     int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
     int last_next = -1;
@@ -42,7 +45,7 @@ int dev_alloc(T **p, size_t count, const char *what) {
 
 void release(qk_llama *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
-                    m->value_cache, m->cosine, m->sine, m->argmax_ws, m->d_next, m->d_token};
+                    m->value_cache, m->cosine, m->sine, m->argmax_ws, m->attn_ws, m->d_next, m->d_token};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
@@ -63,6 +66,13 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         c.kv_heads < 1 || c.dim % c.heads || c.heads % c.kv_heads || c.vocab < 1 || c.context < 1)
         return qk::fail(QK_ERR_SHAPE, "qk_llama_create: unsupported model shape");
     const int head_dim = c.dim / c.heads;
+    if (!qk::gemv_fusable(c.dim) || !qk::gemv_fusable(c.hidden))
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_create: dim or hidden too long to stage the activations of a step");
+    if (!qk::aligned(w->output_norm, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_llama_create: norm weights must be 16-byte aligned");
+    for (int l = 0; l < c.layers; ++l)
+        if (!qk::aligned(w->layers[l].attn_norm, 16) || !qk::aligned(w->layers[l].ffn_norm, 16))
+            return qk::fail(QK_ERR_ALIGN, "qk_llama_create: norm weights must be 16-byte aligned");
     if (head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_llama_create: head_dim must be a multiple of 4 dividing 256");
     if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
@@ -75,7 +85,8 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         if (!L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down || !L.attn_norm || !L.ffn_norm)
             return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_create: layer " + std::to_string(l) + " is incomplete");
     }
-    if (c.heads / c.kv_heads > 8 || qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
+    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim) ||
+        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
         return qk::fail(QK_ERR_LIMIT, "qk_llama_create: context beyond the attention kernel's LDS budget");
 
     qk_llama *m = new qk_llama();
@@ -103,6 +114,20 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token"))) {
         release(m);
         return st;
+    }
+    const int group = c.heads / c.kv_heads;
+    const size_t attn_ws = qk::chunked_attention_supported(c.kv_heads, group, head_dim)
+                               ? qk::attention_workspace_bytes(c.kv_heads, group, head_dim, c.context)
+                               : 0;
+    if (attn_ws) {
+        if ((st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), attn_ws, "attention workspace"))) {
+            release(m);
+            return st;
+        }
+        if (hipMemset(m->attn_ws, 0, attn_ws) != hipSuccess) {
+            release(m);
+            return qk::fail(QK_ERR_DEVICE, "qk_llama_create: cannot clear the attention workspace");
+        }
     }
     if (hipHostMalloc(reinterpret_cast<void **>(&m->h_token), 2 * sizeof(int32_t), hipHostMallocDefault) !=
         hipSuccess) {
@@ -167,34 +192,44 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     }
     m->last_next = -1;
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
+    // Five launches per layer: RMSNorm is staged inside the QKV / gate-up
+    // GEMVs, SiLU * up inside the down GEMV, the residual adds are their
+    // epilogues, and RoPE + the KV write open the attention kernel.
+    qk::GemvFusion attn_in, ffn_in, residual, down_in;
+    attn_in.norm_eps = ffn_in.norm_eps = c.eps;
+    residual.accumulate = down_in.accumulate = 1;
+    down_in.up = m->up;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
-        if ((st = qk_rmsnorm_f32(m->x, L.attn_norm, m->xn, dim, 1, c.eps, s))) return st;
+        attn_in.norm_w = L.attn_norm;
+        ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = qk_gemv_multi_f32(qkv, 3, m->xn, dim, s))) return st;
-        if ((st = qk_rope_kv_write(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l, pos,
-                                   c.context, c.heads, c.kv_heads, hd, s)))
-            return st;
-        if ((st = qk_attention_f32(m->q, m->key_cache, m->value_cache, m->attn, l, pos, c.context, c.heads,
-                                   c.kv_heads, hd, s)))
-            return st;
-        if ((st = qk_gemv_f32(L.o_type, L.o, m->attn, m->tmp, dim, dim, s))) return st;
-        if ((st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
-        if ((st = qk_rmsnorm_f32(m->x, L.ffn_norm, m->xn, dim, 1, c.eps, s))) return st;
+        if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, attn_in, s))) return st;
+        if (m->attn_ws)
+            st = qk::launch_rope_attention_chunked(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache,
+                                                   m->attn, m->attn_ws, l, pos, c.context, c.heads, c.kv_heads, hd, s);
+        else
+            st = qk::launch_rope_attention(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, m->attn,
+                                           l, pos, c.context, c.heads, c.kv_heads, hd, s);
+        if (st) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->x};
+        if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, residual, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = qk_gemv_multi_f32(gu, 2, m->xn, dim, s))) return st;
-        if ((st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s))) return st;
-        if ((st = qk_gemv_f32(L.down_type, L.down, m->gate, m->tmp, c.hidden, dim, s))) return st;
-        if ((st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
+        if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, ffn_in, s))) return st;
+        const qk_matrix down{L.down_type, dim, L.down, m->x};
+        if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, down_in, s))) return st;
     }
     if (!need_logits) {
         if (next_token) *next_token = -1;
         return qk::ok();
     }
-    if ((st = qk_rmsnorm_f32(m->x, m->w.output_norm, m->xn, dim, 1, c.eps, s))) return st;
+    qk::GemvFusion out_in;
+    out_in.norm_w = m->w.output_norm;
+    out_in.norm_eps = c.eps;
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
-    if ((st = qk_gemv_f32(out_type, out_w, m->xn, m->logits, dim, c.vocab, s))) return st;
+    const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+    if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, out_in, s))) return st;
     if ((st = qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s))) return st;
     if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)

@@ -10,6 +10,13 @@
 #include <cmath>
 
 namespace qk {
+
+// Query rows, scores of positions 0..pos, the 8 waves' partial outputs and
+// their reduction slots, for `group` query heads.
+__host__ __device__ size_t attention_lds_bytes(int pos, int head_dim, int group) {
+    return static_cast<size_t>(group) * (head_dim + (pos + 1) + 8 * head_dim + 8) * sizeof(float);
+}
+
 namespace {
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -107,21 +114,21 @@ __global__ void rope_kv_kernel(float *q, const float *k, const float *v, const f
 }
 
 // attention_cuda (inferencer.cu:981-1009), GQA, one query token.  One
-// 1024-thread workgroup per KV head serves the G = heads / kv_heads query
+// 512-thread workgroup per KV head serves the G = heads / kv_heads query
 // heads that share it, so every key and value row is read from memory once.
 // At decode sizes the kernel is latency-bound: each phase issues all of its
 // loads before it consumes them.
-//   1. scores: thread t takes positions t, t + 1024, ...; it loads the key
+//   1. scores: thread t takes positions t, t + 512, ...; it loads the key
 //      row (16 float4 at a time) and dots it with the G query rows (LDS
 //      broadcast), scaled by 1/sqrt(head_dim); scores go to LDS.
 //   2. per-head maximum, exp, per-head sum (block reductions in LDS).
-//   3. values: wave w owns a contiguous run of positions, lane = dimension;
-//      the 16 partial vectors per head are added in wave order and divided
-//      by the sum (deterministic).
-constexpr int kAttnThreads = 1024;
+//   3. values: wave w owns a contiguous run of positions, lane = dimension,
+//      rows loaded 16 positions at a time; the 8 partial vectors per head
+//      are added in wave order and divided by the sum (deterministic).
+constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
-constexpr int kAttnMaxGroup = 8;
-constexpr int kAttnMaxDimLanes = 4;   // head_dim <= 256: four dimensions per lane
+static_assert(kAttnWaves == 8, "attention_lds_bytes sizes 8 waves");
+constexpr int kAttnBatch = 16;        // value rows loaded together
 
 struct AttnLds {
     float *qs;      // [G][head_dim]
@@ -141,14 +148,16 @@ __device__ __forceinline__ AttnLds attn_lds(float *smem, int G, int head_dim, in
 
 // Block-wide reduction of G per-thread values (max or sum); every thread
 // receives the G results in v.
-template <bool MAX>
-__device__ __forceinline__ void attn_block_reduce(float *v, int G, float *red) {
+template <bool MAX, int G>
+__device__ __forceinline__ void attn_block_reduce(float *v, float *red) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    #pragma unroll
     for (int g = 0; g < G; ++g) {
         const float r = MAX ? wave_max(v[g]) : wave_sum(v[g]);
         if (lane == 0) red[wave * G + g] = r;
     }
     __syncthreads();
+    #pragma unroll
     for (int g = 0; g < G; ++g) {
         float r = red[g];
         for (int w = 1; w < kAttnWaves; ++w) r = MAX ? fmaxf(r, red[w * G + g]) : r + red[w * G + g];
@@ -159,8 +168,11 @@ __device__ __forceinline__ void attn_block_reduce(float *v, int G, float *red) {
 
 // q: the token's query rows of the G heads of KV head kvh (already rotated);
 // kc / vc: the layer's caches offset to this KV head; out: the G output rows.
-__device__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos, int G,
-                               int head_dim, int kv_dim, float *smem) {
+// G query heads per KV head and DL = ceil(head_dim / 64) dimensions per lane
+// are compile-time, so every per-head array stays in registers.
+template <int G, int DL>
+__device__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos, int head_dim,
+                               int kv_dim, float *smem) {
     const AttnLds L = attn_lds(smem, G, head_dim, pos);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n = pos + 1;
@@ -168,11 +180,13 @@ __device__ void attend_kv_head(const float *q, const float *kc, const float *vc,
     for (int i = tid; i < G * head_dim; i += kAttnThreads) L.qs[i] = q[i];
     __syncthreads();
 
-    float m[kAttnMaxGroup];
+    float m[G];
+    #pragma unroll
     for (int g = 0; g < G; ++g) m[g] = -INFINITY;
     for (int t = tid; t < n; t += kAttnThreads) {
         const float4 *kr = reinterpret_cast<const float4 *>(kc + static_cast<int64_t>(t) * kv_dim);
-        float dot[kAttnMaxGroup];
+        float dot[G];
+        #pragma unroll
         for (int g = 0; g < G; ++g) dot[g] = 0.f;
         for (int c = 0; c < head_dim; c += 64) {
             float4 k4[16];
@@ -180,8 +194,13 @@ __device__ void attend_kv_head(const float *q, const float *kc, const float *vc,
             #pragma unroll
             for (int j = 0; j < 16; ++j)
                 if (j < nc) k4[j] = kr[(c >> 2) + j];
+            // The query rows are re-read from LDS (broadcast) for every key
+            // row: an opaque offset keeps them out of registers.
+            int qoff = c;
+            asm volatile("" : "+v"(qoff));
+            #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float *qg = L.qs + g * head_dim + c;
+                const float *qg = L.qs + g * head_dim + qoff;
                 float a = dot[g];
                 #pragma unroll
                 for (int j = 0; j < 16; ++j)
@@ -194,67 +213,62 @@ __device__ void attend_kv_head(const float *q, const float *kc, const float *vc,
                 dot[g] = a;
             }
         }
+        #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float sc = dot[g] * inv;
             L.score[g * n + t] = sc;
             m[g] = fmaxf(m[g], sc);
         }
     }
-    attn_block_reduce<true>(m, G, L.red);   // its barriers also publish score[]
+    attn_block_reduce<true, G>(m, L.red);   // its barriers also publish score[]
 
-    float den[kAttnMaxGroup];
+    float den[G];
+    #pragma unroll
     for (int g = 0; g < G; ++g) den[g] = 0.f;
     for (int t = tid; t < n; t += kAttnThreads)
+        #pragma unroll
         for (int g = 0; g < G; ++g) {
             const float e = expf(L.score[g * n + t] - m[g]);
             L.score[g * n + t] = e;
             den[g] += e;
         }
-    attn_block_reduce<false>(den, G, L.red);
+    attn_block_reduce<false, G>(den, L.red);
 
     const int per = (n + kAttnWaves - 1) / kAttnWaves;
     const int t0 = wave * per, t1 = min(n, t0 + per);
-    const int dims = (head_dim + 63) >> 6;   // dimensions per lane
-    float acc[kAttnMaxGroup][kAttnMaxDimLanes];
+        float acc[G][DL];
+    #pragma unroll
     for (int g = 0; g < G; ++g)
         #pragma unroll
-        for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = 0.f;
-    int t = t0;
-    for (; t + 4 <= t1; t += 4) {
-        float v[4][kAttnMaxDimLanes];
+        for (int j = 0; j < DL; ++j) acc[g][j] = 0.f;
+    // Value rows in batches of 16 positions, every load of a batch issued
+    // before the first multiply-add.
+    for (int tb = t0; tb < t1; tb += kAttnBatch) {
+        float v[kAttnBatch][DL];
         #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int u = 0; u < kAttnBatch; ++u)
             #pragma unroll
-            for (int j = 0; j < kAttnMaxDimLanes; ++j) {
+            for (int j = 0; j < DL; ++j) {
                 const int d = lane + 64 * j;
-                v[u][j] = (j < dims && d < head_dim) ? vc[static_cast<int64_t>(t + u) * kv_dim + d] : 0.f;
+                v[u][j] = (tb + u < t1 && d < head_dim)
+                              ? vc[static_cast<int64_t>(tb + u) * kv_dim + d]
+                              : 0.f;
             }
+        #pragma unroll
         for (int g = 0; g < G; ++g)
             #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const float pr = L.score[g * n + t + u];
+            for (int u = 0; u < kAttnBatch; ++u) {
+                const float pr = tb + u < t1 ? L.score[g * n + tb + u] : 0.f;
                 #pragma unroll
-                for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = fmaf(pr, v[u][j], acc[g][j]);
+                for (int j = 0; j < DL; ++j) acc[g][j] = fmaf(pr, v[u][j], acc[g][j]);
             }
     }
-    for (; t < t1; ++t) {
-        float v[kAttnMaxDimLanes];
-        #pragma unroll
-        for (int j = 0; j < kAttnMaxDimLanes; ++j) {
-            const int d = lane + 64 * j;
-            v[j] = (j < dims && d < head_dim) ? vc[static_cast<int64_t>(t) * kv_dim + d] : 0.f;
-        }
-        for (int g = 0; g < G; ++g) {
-            const float pr = L.score[g * n + t];
-            #pragma unroll
-            for (int j = 0; j < kAttnMaxDimLanes; ++j) acc[g][j] = fmaf(pr, v[j], acc[g][j]);
-        }
-    }
+    #pragma unroll
     for (int g = 0; g < G; ++g)
         #pragma unroll
-        for (int j = 0; j < kAttnMaxDimLanes; ++j) {
+        for (int j = 0; j < DL; ++j) {
             const int d = lane + 64 * j;
-            if (j < dims && d < head_dim) L.part[(wave * G + g) * head_dim + d] = acc[g][j];
+            if (d < head_dim) L.part[(wave * G + g) * head_dim + d] = acc[g][j];
         }
     __syncthreads();
     for (int i = tid; i < G * head_dim; i += kAttnThreads) {
@@ -265,17 +279,243 @@ __device__ void attend_kv_head(const float *q, const float *kc, const float *vc,
     }
 }
 
+template <int G, int DL>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *q, const float *key_cache,
                                                                  const float *value_cache, float *out, int layer,
-                                                                 int pos, int context, int heads, int kv_heads,
-                                                                 int head_dim) {
+                                                                 int pos, int context, int kv_heads, int head_dim) {
     extern __shared__ float smem[];
     const int kvh = blockIdx.x;
-    const int G = heads / kv_heads;
     const int kv_dim = kv_heads * head_dim;
     const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    attend_kv_head(q + kvh * G * head_dim, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos, G,
-                   head_dim, kv_dim, smem);
+    attend_kv_head<G, DL>(q + kvh * G * head_dim, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos,
+                          head_dim, kv_dim, smem);
+}
+
+// Decode-step form: RoPE of the G query rows and of key head kvh at pos,
+// the key / value write into the caches at pos (rope_cache_cuda,
+// inferencer.cu:930-951), then attend_kv_head.  The rotated query rows live
+// in LDS after the attention's own buffers.  The cache row of pos is written
+// by this workgroup only (heads occupy disjoint 256-byte runs of a row) and
+// read back after a fence and a barrier.
+template <int G, int DL>
+__global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(
+    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
+    float *value_cache, float *out, int layer, int pos, int context, int kv_heads, int head_dim) {
+    extern __shared__ float smem[];
+    const int kvh = blockIdx.x, tid = threadIdx.x;
+    const int kv_dim = kv_heads * head_dim, half = head_dim / 2;
+    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
+    float *qrot = smem + attention_lds_bytes(pos, head_dim, G) / sizeof(float);
+    const float *cs = cosine + static_cast<int64_t>(pos) * half;
+    const float *sn = sine + static_cast<int64_t>(pos) * half;
+    for (int i = tid; i < G * half; i += kAttnThreads) {
+        const int f = i % half;
+        const int o = kvh * G * head_dim + 2 * i;   // pair i of this KV head's query rows
+        const float c = cs[f], si = sn[f];
+        const float q0 = q[o], q1 = q[o + 1];
+        qrot[2 * i] = q0 * c - q1 * si;
+        qrot[2 * i + 1] = q0 * si + q1 * c;
+    }
+    for (int f = tid; f < half; f += kAttnThreads) {
+        const float c = cs[f], si = sn[f];
+        const int o = kvh * head_dim + 2 * f;
+        const int64_t row = base + static_cast<int64_t>(pos) * kv_dim + 2 * f;
+        const float k0 = k[o], k1 = k[o + 1];
+        key_cache[row] = k0 * c - k1 * si;
+        key_cache[row + 1] = k0 * si + k1 * c;
+        value_cache[row] = v[o];
+        value_cache[row + 1] = v[o + 1];
+    }
+    __threadfence();
+    __syncthreads();
+    attend_kv_head<G, DL>(qrot, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos, head_dim, kv_dim,
+                          smem);
+}
+
+// ------------------------------------------------ chunked decode attention --
+//
+// The decode driver's attention: RoPE + KV write + GQA attention with the
+// positions split into chunks of kChunkPos, one 256-thread workgroup per
+// (KV head, chunk), so a step at a few hundred positions spreads over tens
+// of CUs instead of one per KV head.  Each workgroup rotates the G query
+// rows itself; the workgroup of the last chunk (the one holding pos) also
+// rotates the new key and writes key / value row pos of the caches, which
+// only it reads.  A chunk leaves (max, sum of exp, unnormalised output) per
+// head in the workspace; the last workgroup of a KV head to finish (an
+// atomic ticket per head, reset by that workgroup) merges the chunks in
+// chunk order -- the online-softmax merge of attention_cuda's running max
+// (inferencer.cu:991-1007) done across chunks.
+constexpr int kChunkPos = 64;
+constexpr int kChunkThreads = 256;
+
+template <int G, int DL>
+__global__ __launch_bounds__(kChunkThreads) void rope_attention_chunked_kernel(
+    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
+    float *value_cache, float *out, float *partials, int *tickets, int layer, int pos, int context, int kv_heads,
+    int head_dim) {
+    // head_dim == 64 * DL (checked on the host).
+    __shared__ float qs[G * 64 * DL];
+    __shared__ float score[G][kChunkPos];
+    __shared__ float part[4][G * 64 * DL];
+    __shared__ float red[4][G];
+    __shared__ int last;
+    const int kvh = blockIdx.x, chunk = blockIdx.y, nchunks = gridDim.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kv_dim = kv_heads * head_dim, half = head_dim / 2;
+    const int n = pos + 1;
+    const int c0 = chunk * kChunkPos, c1 = min(n, c0 + kChunkPos);
+    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
+    const float *kc = key_cache + base, *vc = value_cache + base;
+    const float *cs = cosine + static_cast<int64_t>(pos) * half;
+    const float *sn = sine + static_cast<int64_t>(pos) * half;
+
+    for (int i = tid; i < G * half; i += kChunkThreads) {
+        const int f = i % half;
+        const int o = kvh * G * head_dim + 2 * i;
+        const float c = cs[f], si = sn[f];
+        const float q0 = q[o], q1 = q[o + 1];
+        qs[2 * i] = q0 * c - q1 * si;
+        qs[2 * i + 1] = q0 * si + q1 * c;
+    }
+    if (chunk == nchunks - 1) {
+        for (int f = tid; f < half; f += kChunkThreads) {
+            const float c = cs[f], si = sn[f];
+            const int o = kvh * head_dim + 2 * f;
+            const int64_t row = base + static_cast<int64_t>(pos) * kv_dim + 2 * f;
+            const float k0 = k[o], k1 = k[o + 1];
+            key_cache[row] = k0 * c - k1 * si;
+            key_cache[row + 1] = k0 * si + k1 * c;
+            value_cache[row] = v[o];
+            value_cache[row + 1] = v[o + 1];
+        }
+        __threadfence();
+    }
+    __syncthreads();
+
+    // 1. Scores: four lanes per position, each a quarter of head_dim.
+    const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
+    const int quarter = head_dim / 4;          // 16 * DL columns
+    const int pl = wave * 16 + (lane >> 2);    // position within the chunk
+    const int qd = lane & 3;
+    const int t = c0 + pl;
+    float dot[G];
+    #pragma unroll
+    for (int g = 0; g < G; ++g) dot[g] = 0.f;
+    if (t < c1) {
+        const float4 *kr = reinterpret_cast<const float4 *>(kc + static_cast<int64_t>(t) * kv_dim + qd * quarter);
+        float4 k4[4 * DL];
+        #pragma unroll
+        for (int j = 0; j < 4 * DL; ++j) k4[j] = kr[j];
+        #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float *qg = qs + g * head_dim + qd * quarter;
+            float a = 0.f;
+            #pragma unroll
+            for (int j = 0; j < 4 * DL; ++j) {
+                a = fmaf(qg[4 * j], k4[j].x, a);
+                a = fmaf(qg[4 * j + 1], k4[j].y, a);
+                a = fmaf(qg[4 * j + 2], k4[j].z, a);
+                a = fmaf(qg[4 * j + 3], k4[j].w, a);
+            }
+            dot[g] = a;
+        }
+    }
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+        dot[g] += __shfl_xor(dot[g], 1);
+        dot[g] += __shfl_xor(dot[g], 2);
+    }
+    float m[G];
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float sc = dot[g] * inv;
+        if (qd == 0) score[g][pl] = t < c1 ? sc : -INFINITY;
+        m[g] = t < c1 ? sc : -INFINITY;
+        m[g] = wave_max(m[g]);
+        if (lane == 0) red[wave][g] = m[g];
+    }
+    __syncthreads();
+    #pragma unroll
+    for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
+    __syncthreads();
+
+    // 2. exp and the chunk's sum per head.
+    float l[G];
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float e = 0.f;
+        if (tid < kChunkPos) {
+            e = c0 + tid < c1 ? expf(score[g][tid] - m[g]) : 0.f;
+            score[g][tid] = e;
+        }
+        l[g] = wave_sum(e);   // wave 0 holds every position
+    }
+    __syncthreads();
+
+    // 3. Values: wave w takes positions w*16 .. +15 of the chunk, lane = dimension.
+    float acc[G][DL];
+    #pragma unroll
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int j = 0; j < DL; ++j) acc[g][j] = 0.f;
+    {
+        float vv[16][DL];
+        #pragma unroll
+        for (int u = 0; u < 16; ++u)
+            #pragma unroll
+            for (int j = 0; j < DL; ++j) {
+                const int tt = c0 + wave * 16 + u, d = lane + 64 * j;
+                vv[u][j] = (tt < c1 && d < head_dim) ? vc[static_cast<int64_t>(tt) * kv_dim + d] : 0.f;
+            }
+        #pragma unroll
+        for (int g = 0; g < G; ++g)
+            #pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float pr = score[g][wave * 16 + u];
+                #pragma unroll
+                for (int j = 0; j < DL; ++j) acc[g][j] = fmaf(pr, vv[u][j], acc[g][j]);
+            }
+    }
+    #pragma unroll
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int j = 0; j < DL; ++j) {
+            const int d = lane + 64 * j;
+            if (d < head_dim) part[wave][g * head_dim + d] = acc[g][j];
+        }
+    __syncthreads();
+
+    // The chunk's partial: [G] max, [G] sum, [G][head_dim] output.
+    const int stride = G * (head_dim + 2);
+    float *mine = partials + (static_cast<size_t>(kvh) * nchunks + chunk) * stride;
+    #pragma unroll
+    for (int g = 0; g < G; ++g)
+        if (tid == g) {
+            mine[g] = m[g];
+            mine[G + g] = l[g];
+        }
+    for (int i = tid; i < G * head_dim; i += kChunkThreads)
+        mine[2 * G + i] = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(tickets + kvh, 1) == nchunks - 1;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const float *all = partials + static_cast<size_t>(kvh) * nchunks * stride;
+    for (int i = tid; i < G * head_dim; i += kChunkThreads) {
+        const int g = i / head_dim;
+        float mx = -INFINITY;
+        for (int c = 0; c < nchunks; ++c) mx = fmaxf(mx, all[c * stride + g]);
+        float num = 0.f, den = 0.f;
+        for (int c = 0; c < nchunks; ++c) {
+            const float w = expf(all[c * stride + g] - mx);
+            den = fmaf(w, all[c * stride + G + g], den);
+            num = fmaf(w, all[c * stride + 2 * G + i], num);
+        }
+        out[kvh * G * head_dim + i] = num / den;
+    }
+    if (tid == 0) atomicExch(tickets + kvh, 0);
 }
 
 __global__ void add_kernel(float *x, const float *y, int n) {
@@ -351,12 +591,91 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
     }
 }
 
+// Kernel instance for G query heads per KV head and head_dim: G in
+// {1, 2, 3, 4, 6, 8}, head_dim <= 256.  NULL when unsupported.
+template <template <int, int> class K>
+const void *attention_instance(int G, int head_dim) {
+    const int dl = (head_dim + 63) / 64;
+#define QK_ATTN_CASE(g)                                        \
+    case g:                                                    \
+        return dl == 1   ? K<g, 1>::fn()                       \
+               : dl == 2 ? K<g, 2>::fn()                       \
+               : dl <= 4 ? K<g, 4>::fn()                       \
+                         : nullptr;
+    switch (G) {
+        QK_ATTN_CASE(1)
+        QK_ATTN_CASE(2)
+        QK_ATTN_CASE(3)
+        QK_ATTN_CASE(4)
+        QK_ATTN_CASE(6)
+        QK_ATTN_CASE(8)
+        default: return nullptr;
+    }
+#undef QK_ATTN_CASE
+}
+
+template <int G, int DL>
+struct PlainAttention {
+    static const void *fn() { return reinterpret_cast<const void *>(attention_kernel<G, DL>); }
+};
+template <int G, int DL>
+struct ChunkedAttention {
+    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_chunked_kernel<G, DL>); }
+};
+template <int G, int DL>
+struct RopeAttention {
+    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_kernel<G, DL>); }
+};
+
 inline hipStream_t S(qk_stream s) { return static_cast<hipStream_t>(s); }
 
 }  // namespace
 
-size_t attention_lds_bytes(int pos, int head_dim, int group) {
-    return static_cast<size_t>(group) * (head_dim + (pos + 1) + kAttnWaves * head_dim + kAttnWaves) * sizeof(float);
+size_t attention_workspace_bytes(int kv_heads, int group, int head_dim, int context) {
+    const size_t chunks = (static_cast<size_t>(context) + kChunkPos - 1) / kChunkPos;
+    return (static_cast<size_t>(kv_heads) * chunks * group * (head_dim + 2)) * sizeof(float) +
+           static_cast<size_t>(kv_heads) * sizeof(int) + 256;
+}
+
+int launch_rope_attention_chunked(const float *q, const float *k, const float *v, const float *cosine,
+                                  const float *sine, float *key_cache, float *value_cache, float *out, void *workspace,
+                                  int layer, int pos, int context, int heads, int kv_heads, int head_dim,
+                                  hipStream_t stream) {
+    const int G = heads / kv_heads;
+    const void *fn = head_dim % 64 == 0 && kv_heads <= 64 ? attention_instance<ChunkedAttention>(G, head_dim) : nullptr;
+    if (!fn) return fail(QK_ERR_LIMIT, "chunked attention: unsupported head layout");
+    const int nchunks = (pos + kChunkPos) / kChunkPos;
+    int *tickets = static_cast<int *>(workspace);
+    float *partials = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + 256);
+    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &partials, &tickets, &layer, &pos,
+                    &context, &kv_heads, &head_dim};
+    if (hipLaunchKernel(fn, dim3(kv_heads, nchunks), dim3(kChunkThreads), args, 0, stream) != hipSuccess)
+        return launch_status("chunked attention launch");
+    return launch_status("chunked attention launch");
+}
+
+bool chunked_attention_supported(int kv_heads, int group, int head_dim) {
+    return head_dim % 64 == 0 && head_dim <= 256 && kv_heads <= 64 &&
+           attention_instance<ChunkedAttention>(group, head_dim) != nullptr;
+}
+
+bool attention_supported(int group, int head_dim) {
+    return head_dim >= 4 && head_dim % 4 == 0 && 256 % head_dim == 0 &&
+           attention_instance<PlainAttention>(group, head_dim) != nullptr;
+}
+
+int launch_rope_attention(const float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                          float *key_cache, float *value_cache, float *out, int layer, int pos, int context,
+                          int heads, int kv_heads, int head_dim, hipStream_t stream) {
+    const int G = heads / kv_heads;
+    const void *fn = attention_instance<RopeAttention>(G, head_dim);
+    if (!fn) return fail(QK_ERR_LIMIT, "rope + attention: unsupported query heads per KV head or head_dim");
+    const size_t lds = attention_lds_bytes(pos, head_dim, G) + static_cast<size_t>(G) * head_dim * sizeof(float);
+    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &layer, &pos, &context, &kv_heads,
+                    &head_dim};
+    if (hipLaunchKernel(fn, dim3(kv_heads), dim3(kAttnThreads), args, lds, stream) != hipSuccess)
+        return launch_status("rope + attention launch");
+    return launch_status("rope + attention launch");
 }
 
 }  // namespace qk
@@ -394,14 +713,15 @@ int qk_attention_f32(const float *q, const float *key_cache, const float *value_
         return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_f32: bad head layout or position outside context");
     if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: head_dim must be a multiple of 4 dividing 256");
-    if (heads / kv_heads > qk::kAttnMaxGroup)
-        return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: more than 8 query heads per KV head");
+    const void *fn = qk::attention_instance<qk::PlainAttention>(heads / kv_heads, head_dim);
+    if (!fn) return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
     if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16))
         return qk::fail(QK_ERR_ALIGN, "qk_attention_f32: caches must be 16-byte aligned");
     const size_t lds = qk::attention_lds_bytes(pos, head_dim, heads / kv_heads);
     if (lds > 150 * 1024) return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: position beyond the LDS score buffer");
-    hipLaunchKernelGGL(qk::attention_kernel, dim3(kv_heads), dim3(qk::kAttnThreads), lds, qk::S(stream), q, key_cache,
-                       value_cache, out, layer, pos, context, heads, kv_heads, head_dim);
+    void *args[] = {&q, &key_cache, &value_cache, &out, &layer, &pos, &context, &kv_heads, &head_dim};
+    if (hipLaunchKernel(fn, dim3(kv_heads), dim3(qk::kAttnThreads), args, lds, qk::S(stream)) != hipSuccess)
+        return qk::launch_status("qk_attention_f32 launch");
     return qk::launch_status("qk_attention_f32 launch");
 }
 
