@@ -270,8 +270,60 @@ def bench_decode_1b(torch, qk, wl) -> dict:
     return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
             "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            "launches_per_token": 11 * cfg["layers"] + 5}
+            "launches_per_token": 5 * cfg["layers"] + 4}
 
+
+def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
+    """Random-init Llama-3.2-1B decode step for 32 ragged sequences at once:
+    sequence s decodes at position ctx_s - 1 with ctx_s ~ U[64, 2048] (the
+    ragged descriptor of the 3B FFN workload, seed 3), its KV rows packed in
+    one cache and filled with N(0,1) on the device.  Timed: `steps` steps,
+    each ending in the 32 greedy tokens' download; positions advance."""
+    import ctypes
+    cfg = dict(wl.LLAMA_1B, context=2048 + steps + warmup)
+    W = wl.llama_weights(cfg, 2)
+    desc = wl.ffn_3b_ragged()["desc"]
+    n = desc.n_tokens
+    cap = desc.ctx_len.astype(int) + steps + warmup
+    kv_row = [int(x) for x in (wl.np.concatenate([[0], wl.np.cumsum(cap[:-1])]))]
+    rows = int(cap.sum())
+    runner = qk.BatchRunner(cfg, W, max_tokens=n, cache_rows=rows)
+    kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
+    kp, vp = runner.kv_cache()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    for dst in (kp, vp):
+        per_layer = rows * kv_dim
+        for l in range(cfg["layers"]):
+            blk = torch.randn(per_layer, device="cuda", generator=g)
+            if hip.hipMemcpy(dst + l * per_layer * 4, blk.data_ptr(), per_layer * 4, 3) != 0:
+                raise RuntimeError("device copy failed")
+            del blk
+    torch.cuda.synchronize()
+    tokens = [int(x) for x in wl.synth.uniform_i32(n, 3, 6, 0, cfg["vocab"] - 1)]
+    pos = [int(c) - 1 for c in desc.ctx_len]
+    for _ in range(warmup):
+        tokens = runner.forward(tokens, pos, kv_row, True)
+        pos = [p + 1 for p in pos]
+    torch.cuda.synchronize()
+    kv_read = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tokens = runner.forward(tokens, pos, kv_row, True)
+        kv_read += sum(cfg["layers"] * (p + 1) * kv_dim * 4 * 2 for p in pos)
+        pos = [p + 1 for p in pos]
+    el = time.perf_counter() - t0
+    runner.close()
+    weights = sum(qk.tensor_bytes(wl.MIX_1B[t], *wl.tensor_shape(cfg, t)) for t in wl.TENSORS) * cfg["layers"] + \
+        qk.tensor_bytes(qk.Q6_K, cfg["dim"], cfg["vocab"])
+    moved = weights * steps + kv_read
+    ms = el / steps * 1e3
+    return {"sequences": n, "ms_per_step": round(ms, 4), "tokens_per_s": round(n * steps / el, 1),
+            "weight_bytes_per_step": weights, "kv_bytes_per_step": int(kv_read / steps),
+            "GBps": round(moved / el / 1e9, 1), "frac_of_peak": round(moved / el / 1e9 / HBM_PEAK_GBPS, 4),
+            "context": "ctx ~ U[64, 2048] per sequence (seed 3)"}
 
 def reference_kernels(torch, args) -> int:
     """Plain copy / streaming read of 256 MiB buffers (4 rotating sources)."""
@@ -383,6 +435,8 @@ def main() -> int:
         log(f"[bench] mixed_1b_256: {json.dumps(sec['mixed_1b_256'])}")
         sec["llama_1b_decode"] = bench_decode_1b(torch, qk, wl)
         log(f"[bench] llama_1b_decode: {json.dumps(sec['llama_1b_decode'])}")
+        sec["llama_1b_batch_decode_32"] = bench_batch_decode_1b(torch, qk, wl)
+        log(f"[bench] llama_1b_batch_decode_32: {json.dumps(sec['llama_1b_batch_decode_32'])}")
         result["secondary"] = sec
 
     if not args.no_cpu_baseline:

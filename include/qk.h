@@ -179,6 +179,48 @@ int qk_silu_mul_f32(float *gate, const float *up, int n, qk_stream stream);
 size_t qk_argmax_workspace_bytes(int n);
 int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_stream stream);
 
+/* ----------------------------------------------- ragged decode batches -- */
+
+/* One token of a ragged decode batch: the position of the token in its
+   sequence and the first row of that sequence in the packed KV caches
+   ([layer][cache_rows][kv_dim]; a sequence owns rows kv_row .. kv_row +
+   capacity - 1).  The nearest reference code serves one sequence at
+   contiguous positions (start_pos + token, inferencer.cu:956-959,
+   1012-1016); this descriptor lets every token of a batch belong to a
+   different sequence. */
+typedef struct qk_batch_token {
+    int32_t pos;
+    int32_t seq;       /* sequence id; informational */
+    int64_t kv_row;
+} qk_batch_token;
+
+/* RoPE of token t's q (heads*head_dim at q + t*heads*head_dim, in place) and
+   k at its own position, k and v written to row kv_row + pos of `layer`.
+   desc is a device array of n_tokens entries; tokens outside the cache
+   (pos >= context or kv_row + pos >= cache_rows) are skipped.  Replaces
+   rope_cache_batch_cuda (inferencer.cu:953-979). */
+int qk_rope_kv_write_batched(float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                             float *key_cache, float *value_cache, int layer, int64_t cache_rows,
+                             const qk_batch_token *desc, int n_tokens, int context, int heads, int kv_heads,
+                             int head_dim, qk_stream stream);
+
+/* GQA attention of every token of a ragged batch over rows kv_row ..
+   kv_row + pos of its sequence; out is [n_tokens][heads*head_dim].  max_pos
+   bounds every pos (it sizes the score buffer); a token beyond it or beyond
+   the cache gets NaN outputs.  Replaces attention_batch_cuda
+   (inferencer.cu:1011-1041). */
+int qk_attention_batched_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,
+                             int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos, int heads,
+                             int kv_heads, int head_dim, qk_stream stream);
+
+/* Greedy token of each of `rows` rows of n values (row r at v + r*ldv), the
+   lowest index among equal maxima; out is a device array of rows ints.
+   workspace holds qk_argmax_rows_workspace_bytes(n, rows) bytes.  The
+   per-token form of argmax_blocks_cuda + argmax_final_cuda. */
+size_t qk_argmax_rows_workspace_bytes(int n, int rows);
+int qk_argmax_rows_f32(const float *v, int n, int64_t ldv, int rows, int32_t *out, void *workspace,
+                       qk_stream stream);
+
 /* ---------------------------------------------------- decode-step driver -- */
 
 /* Llama configuration (the llama.* GGUF keys read at inferencer.cu:1205-1214). */
@@ -220,6 +262,31 @@ int qk_llama_logits(qk_llama *m, const float **logits);
    stream like the reference's 4-byte copy, inferencer.cu:1529); otherwise
    the step stays asynchronous and *next_token is -1. */
 int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next_token);
+
+/* ------------------------------------------- batched decode-step driver -- */
+
+/* A decode step for a ragged batch: up to max_tokens tokens, each from its
+   own sequence, with packed KV caches of cache_rows rows per layer
+   ([layer][cache_rows][kv_dim], fp32).  The multi-sequence counterpart of
+   FastRunner::prefill's batched path (inferencer.cu:1279-1423), which serves
+   one sequence; every projection runs through qk_gemv_multi_batched_f32 /
+   qk_gemv_batched_f32 (matrix cores from 8 tokens on).  Buffers, caches and
+   workspaces are allocated once at create; weights stay the caller's. */
+typedef struct qk_llama_batch qk_llama_batch;
+
+int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens,
+                          int64_t cache_rows, qk_stream stream, qk_llama_batch **out);
+int qk_llama_batch_destroy(qk_llama_batch *m);
+/* Device pointers to the fp32 caches, [layer][cache_rows][kv_dim]. */
+int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_cache);
+/* Device pointer to the fp32 logits of the last step with need_logits,
+   [n_tokens][vocab]. */
+int qk_llama_batch_logits(qk_llama_batch *m, const float **logits);
+/* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  With
+   need_logits, next_tokens[t] (host) receives each token's greedy successor
+   and the call synchronises the stream; otherwise it stays asynchronous. */
+int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
+                           int need_logits, int32_t *next_tokens);
 
 #ifdef __cplusplus
 }

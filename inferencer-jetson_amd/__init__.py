@@ -49,6 +49,11 @@ class qk_matrix(ctypes.Structure):
                 ("w", ctypes.c_void_p), ("y", ctypes.c_void_p)]
 
 
+class qk_batch_token(ctypes.Structure):
+    """One token of a ragged decode batch (include/qk.h)."""
+    _fields_ = [("pos", ctypes.c_int32), ("seq", ctypes.c_int32), ("kv_row", ctypes.c_int64)]
+
+
 class qk_llama_config(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab", "context")] + \
                [("eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
@@ -95,6 +100,18 @@ SIGNATURES = {
     "qk_llama_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_forward": (_i, [_vp, _i, _i, _i, ctypes.POINTER(ctypes.c_int)]),
+    "qk_rope_kv_write_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i,
+                                      _vp]),
+    "qk_attention_batched_f32": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i, _vp]),
+    "qk_argmax_rows_workspace_bytes": (ctypes.c_size_t, [_i, _i]),
+    "qk_argmax_rows_f32": (_i, [_vp, _i, ctypes.c_int64, _i, _vp, _vp, _vp]),
+    "qk_llama_batch_create": (_i, [ctypes.POINTER(qk_llama_config), ctypes.POINTER(qk_llama_weights), _i,
+                                   ctypes.c_int64, _vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_batch_destroy": (_i, [_vp]),
+    "qk_llama_batch_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
+                                    ctypes.POINTER(ctypes.c_int32)]),
 }
 
 _LIB = None
@@ -259,6 +276,35 @@ def matvec_i8(t: Tensor, xq, xscale, out, cols: int, rows: int, n_tokens: int = 
                            n_tokens, stream_handle(stream)), "INT8 matrix launch")
 
 
+def _upload_weights(owner, cfg: dict, weights: dict):
+    """Device copies of workloads.llama_weights-style host arrays, kept alive
+    by owner._dev; returns (qk_llama_config, qk_llama_weights)."""
+    import numpy as np
+    import torch
+    owner._dev = []
+
+    def up(a):
+        t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+        owner._dev.append(t)
+        return t.data_ptr()
+
+    layers = (qk_llama_layer * cfg["layers"])()
+    for i, L in enumerate(weights["layers"]):
+        for name in ("q", "k", "v", "o", "gate", "up", "down"):
+            setattr(layers[i], name + "_type", L[name + "_type"])
+            setattr(layers[i], name, up(L[name]))
+        layers[i].attn_norm = up(L["attn_norm"])
+        layers[i].ffn_norm = up(L["ffn_norm"])
+    owner._layers = layers
+    out = weights.get("output")
+    w = qk_llama_weights(embd_type=weights["embd_type"], token_embd=up(weights["token_embd"]),
+                         output_type=weights.get("output_type", 0), output=up(out) if out is not None else None,
+                         output_norm=up(weights["output_norm"]), layers=layers)
+    c = qk_llama_config(**{k: cfg[k] for k in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab",
+                                                "context")}, eps=cfg["eps"], rope_theta=cfg["rope_theta"])
+    return c, w
+
+
 class Runner:
     """FastRunner (inferencer.cu:1182-1532) over the C ABI's decode driver.
 
@@ -266,30 +312,8 @@ class Runner:
     they are copied to device memory owned by this object."""
 
     def __init__(self, cfg: dict, weights: dict, stream=None):
-        import numpy as np
-        import torch
         self.cfg = cfg
-        self._dev = []
-
-        def up(a):
-            t = torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
-            self._dev.append(t)
-            return t.data_ptr()
-
-        layers = (qk_llama_layer * cfg["layers"])()
-        for i, L in enumerate(weights["layers"]):
-            for name in ("q", "k", "v", "o", "gate", "up", "down"):
-                setattr(layers[i], name + "_type", L[name + "_type"])
-                setattr(layers[i], name, up(L[name]))
-            layers[i].attn_norm = up(L["attn_norm"])
-            layers[i].ffn_norm = up(L["ffn_norm"])
-        self._layers = layers
-        out = weights.get("output")
-        w = qk_llama_weights(embd_type=weights["embd_type"], token_embd=up(weights["token_embd"]),
-                             output_type=weights.get("output_type", 0), output=up(out) if out is not None else None,
-                             output_norm=up(weights["output_norm"]), layers=layers)
-        c = qk_llama_config(**{k: cfg[k] for k in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab",
-                                                    "context")}, eps=cfg["eps"], rope_theta=cfg["rope_theta"])
+        c, w = _upload_weights(self, cfg, weights)
         h = ctypes.c_void_p()
         check(lib().qk_llama_create(ctypes.byref(c), ctypes.byref(w), stream_handle(stream), ctypes.byref(h)),
               "FastRunner")
@@ -316,6 +340,59 @@ class Runner:
         nxt = ctypes.c_int(-1)
         check(lib().qk_llama_forward(self.handle, token, pos, int(need_logits), ctypes.byref(nxt)), "forward")
         return nxt.value
+
+
+class BatchRunner:
+    """Ragged decode batches over the C ABI's batched driver
+    (qk_llama_batch_*): every token of a step belongs to its own sequence,
+    whose KV rows start at desc.kv_row in caches of cache_rows rows per
+    layer."""
+
+    def __init__(self, cfg: dict, weights: dict, max_tokens: int, cache_rows: int, stream=None):
+        self.cfg = cfg
+        self.cache_rows = cache_rows
+        c, w = _upload_weights(self, cfg, weights)
+        h = ctypes.c_void_p()
+        check(lib().qk_llama_batch_create(ctypes.byref(c), ctypes.byref(w), max_tokens, cache_rows,
+                                          stream_handle(stream), ctypes.byref(h)), "batched runner")
+        self.handle = h
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().qk_llama_batch_destroy(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def kv_cache(self) -> tuple[int, int]:
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        check(lib().qk_llama_batch_kv_cache(self.handle, ctypes.byref(k), ctypes.byref(v)), "kv_cache")
+        return k.value, v.value
+
+    def forward(self, tokens, pos, kv_row, need_logits: bool = True, seq=None):
+        """tokens, pos, kv_row: per-token sequences; returns the greedy next
+        tokens (list) or None."""
+        n = len(tokens)
+        tok = (ctypes.c_int32 * n)(*[int(t) for t in tokens])
+        desc = (qk_batch_token * n)()
+        for i in range(n):
+            desc[i].pos, desc[i].kv_row = int(pos[i]), int(kv_row[i])
+            desc[i].seq = int(seq[i]) if seq is not None else i
+        nxt = (ctypes.c_int32 * n)()
+        check(lib().qk_llama_batch_forward(self.handle, tok, desc, n, int(need_logits), nxt), "batched forward")
+        return list(nxt) if need_logits else None
+
+    def logits(self, n_tokens: int):
+        import numpy as np
+        p = ctypes.c_void_p()
+        check(lib().qk_llama_batch_logits(self.handle, ctypes.byref(p)), "logits")
+        return copy_to_host(p.value, n_tokens * self.cfg["vocab"], np.float32).reshape(n_tokens, self.cfg["vocab"])
+
+    def load_kv(self, key_cache, value_cache) -> None:
+        """Copy fp32 caches laid out [layer][cache_rows][kv_dim]."""
+        k, v = self.kv_cache()
+        copy_to_device(k, key_cache)
+        copy_to_device(v, value_cache)
 
 
 _HIP = None

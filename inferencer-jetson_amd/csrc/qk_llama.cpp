@@ -15,6 +15,7 @@
 // inferencer.cu:1529) and nothing host->device.
 #include "qk_internal.h"
 
+#include <algorithm>
 #include <cmath>
 #include <vector>
 
@@ -236,6 +237,220 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");
     m->last_next = m->h_token[1];
     if (next_token) *next_token = m->last_next;
+    return qk::ok();
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------- ragged batches --
+
+struct qk_llama_batch {
+    qk_llama_config cfg{};
+    qk_llama_weights w{};
+    std::vector<qk_llama_layer> layers;
+    hipStream_t stream = nullptr;
+    int head_dim = 0, kv_dim = 0, max_tokens = 0;
+    int64_t cache_rows = 0;
+    float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *tmp = nullptr;
+    float *gate = nullptr, *up = nullptr, *logits = nullptr;
+    float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
+    void *gemm_ws = nullptr, *argmax_ws = nullptr;
+    size_t gemm_ws_bytes = 0;
+    int32_t *d_tokens = nullptr, *d_next = nullptr;
+    qk_batch_token *d_desc = nullptr;
+    uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, results
+};
+
+namespace {
+
+void release_batch(qk_llama_batch *m) {
+    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
+                    m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->d_tokens, m->d_next, m->d_desc};
+    for (void *b : bufs)
+        if (b) (void)hipFree(b);
+    if (m->h_stage) (void)hipHostFree(m->h_stage);
+    delete m;
+}
+
+size_t stage_bytes(int max_tokens) {
+    return static_cast<size_t>(max_tokens) * (2 * sizeof(int32_t) + sizeof(qk_batch_token));
+}
+
+}  // namespace
+
+extern "C" {
+
+int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens, int64_t cache_rows,
+                          qk_stream stream, qk_llama_batch **out) {
+    if (!cfg || !w || !out || !w->layers || !w->token_embd || !w->output_norm)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_create: null argument");
+    const qk_llama_config &c = *cfg;
+    if (c.dim < 256 || c.dim % 256 || c.hidden % 256 || c.hidden < 256 || c.layers < 1 || c.heads < 1 ||
+        c.kv_heads < 1 || c.dim % c.heads || c.heads % c.kv_heads || c.vocab < 1 || c.context < 1)
+        return qk::fail(QK_ERR_SHAPE, "qk_llama_batch_create: unsupported model shape");
+    if (max_tokens < 1 || max_tokens > 4096 || cache_rows < 1)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_create: max_tokens must be 1..4096 and cache_rows >= 1");
+    const int head_dim = c.dim / c.heads;
+    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim) ||
+        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: head layout or context beyond the attention kernel");
+    if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
+        return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: embedding and output must be Q4_K or Q6_K");
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = w->layers[l];
+        if (!quant_type(L.q_type) || !quant_type(L.k_type) || !quant_type(L.v_type) || !quant_type(L.o_type) ||
+            !quant_type(L.gate_type) || !quant_type(L.up_type) || !quant_type(L.down_type))
+            return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: layer " + std::to_string(l) + " has a non-K-quant tensor");
+        if (!L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down || !L.attn_norm || !L.ffn_norm)
+            return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_create: layer " + std::to_string(l) + " is incomplete");
+    }
+    qk_llama_batch *m = new qk_llama_batch();
+    m->cfg = c;
+    m->w = *w;
+    m->layers.assign(w->layers, w->layers + c.layers);
+    m->w.layers = m->layers.data();
+    m->stream = static_cast<hipStream_t>(stream);
+    m->head_dim = head_dim;
+    m->kv_dim = head_dim * c.kv_heads;
+    m->max_tokens = max_tokens;
+    m->cache_rows = cache_rows;
+    const size_t T = static_cast<size_t>(max_tokens);
+    const size_t cache = static_cast<size_t>(c.layers) * cache_rows * m->kv_dim;
+    const int half = head_dim / 2;
+    size_t ws = 0;
+    const int kv = m->kv_dim;
+    const int shapes[][2] = {{c.dim, c.dim + 2 * kv}, {c.dim, c.dim}, {c.dim, 2 * c.hidden}, {c.hidden, c.dim},
+                             {c.dim, c.vocab}};
+    for (const auto &sh : shapes) ws = std::max(ws, qk_gemv_batched_workspace_bytes(sh[0], sh[1], max_tokens));
+    m->gemm_ws_bytes = ws;
+    int st = QK_OK;
+    if ((st = dev_alloc(&m->x, T * c.dim, "residual")) || (st = dev_alloc(&m->xn, T * c.dim, "normalized state")) ||
+        (st = dev_alloc(&m->q, T * c.dim, "query")) || (st = dev_alloc(&m->k, T * kv, "key")) ||
+        (st = dev_alloc(&m->v, T * kv, "value")) || (st = dev_alloc(&m->attn, T * c.dim, "attention")) ||
+        (st = dev_alloc(&m->tmp, T * c.dim, "residual update")) || (st = dev_alloc(&m->gate, T * c.hidden, "gate")) ||
+        (st = dev_alloc(&m->up, T * c.hidden, "up projection")) ||
+        (st = dev_alloc(&m->logits, T * c.vocab, "logits")) || (st = dev_alloc(&m->key_cache, cache, "key cache")) ||
+        (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
+        (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
+        (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
+        (ws && (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->gemm_ws), ws, "matrix workspace"))) ||
+        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
+                        "argmax workspace")) ||
+        (st = dev_alloc(&m->d_tokens, T, "input tokens")) || (st = dev_alloc(&m->d_next, T, "next tokens")) ||
+        (st = dev_alloc(&m->d_desc, T, "batch descriptor"))) {
+        release_batch(m);
+        return st;
+    }
+    if (hipHostMalloc(reinterpret_cast<void **>(&m->h_stage), stage_bytes(max_tokens), hipHostMallocDefault) !=
+        hipSuccess) {
+        release_batch(m);
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_create: cannot allocate pinned staging");
+    }
+    std::vector<float> cosines(static_cast<size_t>(c.context) * half), sines(cosines.size()), freq(half);
+    for (int i = 0; i < half; ++i) freq[i] = std::pow(c.rope_theta, -2.f * static_cast<float>(i) / head_dim);
+    for (int pos = 0; pos < c.context; ++pos)
+        for (int i = 0; i < half; ++i) {
+            const float angle = static_cast<float>(pos) * freq[i];
+            cosines[static_cast<size_t>(pos) * half + i] = std::cos(angle);
+            sines[static_cast<size_t>(pos) * half + i] = std::sin(angle);
+        }
+    if (hipMemcpy(m->cosine, cosines.data(), cosines.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(m->sine, sines.data(), sines.size() * sizeof(float), hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemset(m->key_cache, 0, cache * sizeof(float)) != hipSuccess ||
+        hipMemset(m->value_cache, 0, cache * sizeof(float)) != hipSuccess) {
+        release_batch(m);
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_create: table upload failed");
+    }
+    *out = m;
+    return qk::ok();
+}
+
+int qk_llama_batch_destroy(qk_llama_batch *m) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_destroy: null handle");
+    (void)hipStreamSynchronize(m->stream);
+    release_batch(m);
+    return qk::ok();
+}
+
+int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_cache) {
+    if (!m || !key_cache || !value_cache)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_kv_cache: null argument");
+    *key_cache = m->key_cache;
+    *value_cache = m->value_cache;
+    return qk::ok();
+}
+
+int qk_llama_batch_logits(qk_llama_batch *m, const float **logits) {
+    if (!m || !logits) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_logits: null argument");
+    *logits = m->logits;
+    return qk::ok();
+}
+
+int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
+                           int need_logits, int32_t *next_tokens) {
+    if (!m || !tokens || !desc || (need_logits && !next_tokens))
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: null argument");
+    const qk_llama_config &c = m->cfg;
+    if (n_tokens < 1 || n_tokens > m->max_tokens)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token count outside 1..max_tokens");
+    int max_pos = 0;
+    for (int t = 0; t < n_tokens; ++t) {
+        const qk_batch_token &d = desc[t];
+        if (tokens[t] < 0 || tokens[t] >= c.vocab || d.pos < 0 || d.pos >= c.context || d.kv_row < 0 ||
+            d.kv_row + d.pos >= m->cache_rows)
+            return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token " + std::to_string(t) +
+                                                    " outside the vocabulary, the context or the cache");
+        max_pos = std::max(max_pos, d.pos);
+    }
+    hipStream_t s = m->stream;
+    const int T = n_tokens, dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
+    int32_t *h_tokens = reinterpret_cast<int32_t *>(m->h_stage);
+    int32_t *h_next = h_tokens + m->max_tokens;
+    qk_batch_token *h_desc = reinterpret_cast<qk_batch_token *>(h_next + m->max_tokens);
+    // The pinned staging is reused: the previous step's copies must be done.
+    if (hipStreamSynchronize(s) != hipSuccess) return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: stream error");
+    std::copy(tokens, tokens + T, h_tokens);
+    std::copy(desc, desc + T, h_desc);
+    if (hipMemcpyAsync(m->d_tokens, h_tokens, T * sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess ||
+        hipMemcpyAsync(m->d_desc, h_desc, T * sizeof(qk_batch_token), hipMemcpyHostToDevice, s) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: batch upload failed");
+    int st;
+    void *ws = m->gemm_ws;
+    const size_t wsb = m->gemm_ws_bytes;
+    if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, m->d_tokens, T, m->x, dim, c.vocab, s))) return st;
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        if ((st = qk_rmsnorm_f32(m->x, L.attn_norm, m->xn, dim, T, c.eps, s))) return st;
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = qk_gemv_multi_batched_f32(qkv, 3, m->xn, dim, dim, T, ws, wsb, s))) return st;
+        if ((st = qk_rope_kv_write_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
+                                           m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
+            return st;
+        if ((st = qk_attention_batched_f32(m->q, m->key_cache, m->value_cache, m->attn, l, m->cache_rows, m->d_desc, T,
+                                           max_pos, c.heads, c.kv_heads, hd, s)))
+            return st;
+        if ((st = qk_gemv_batched_f32(L.o_type, L.o, m->attn, dim, m->tmp, dim, dim, dim, T, ws, wsb, s))) return st;
+        if ((st = qk_add_f32(m->x, m->tmp, T * dim, s))) return st;
+        if ((st = qk_rmsnorm_f32(m->x, L.ffn_norm, m->xn, dim, T, c.eps, s))) return st;
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+        if ((st = qk_gemv_multi_batched_f32(gu, 2, m->xn, dim, dim, T, ws, wsb, s))) return st;
+        if ((st = qk_silu_mul_f32(m->gate, m->up, T * c.hidden, s))) return st;
+        if ((st = qk_gemv_batched_f32(L.down_type, L.down, m->gate, c.hidden, m->tmp, dim, c.hidden, dim, T, ws, wsb,
+                                      s)))
+            return st;
+        if ((st = qk_add_f32(m->x, m->tmp, T * dim, s))) return st;
+    }
+    if (!need_logits) return qk::ok();
+    if ((st = qk_rmsnorm_f32(m->x, m->w.output_norm, m->xn, dim, T, c.eps, s))) return st;
+    const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
+    const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
+    if ((st = qk_gemv_batched_f32(out_type, out_w, m->xn, dim, m->logits, c.vocab, dim, c.vocab, T, ws, wsb, s)))
+        return st;
+    if ((st = qk_argmax_rows_f32(m->logits, c.vocab, c.vocab, T, m->d_next, m->argmax_ws, s))) return st;
+    if (hipMemcpyAsync(h_next, m->d_next, T * sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: next token download failed");
+    std::copy(h_next, h_next + T, next_tokens);
     return qk::ok();
 }
 

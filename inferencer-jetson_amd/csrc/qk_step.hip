@@ -518,6 +518,69 @@ __global__ __launch_bounds__(kChunkThreads) void rope_attention_chunked_kernel(
     if (tid == 0) atomicExch(tickets + kvh, 0);
 }
 
+// ------------------------------------------------- ragged decode batches --
+//
+// Token t of a batch attends to its own sequence: rows kv_row .. kv_row + pos
+// of layer `layer` in caches laid out [layer][cache_rows][kv_dim] (each
+// sequence owns a contiguous run of rows).  The reference's batched kernels
+// (rope_cache_batch_cuda, attention_batch_cuda, inferencer.cu:953-1041) serve
+// one sequence at contiguous positions; the descriptor generalises them to
+// a ragged batch.  A token whose descriptor falls outside the cache is not
+// written and its attention output is NaN.
+
+__device__ __forceinline__ bool token_ok(const qk_batch_token &d, int64_t cache_rows, int max_pos) {
+    return d.pos >= 0 && d.pos <= max_pos && d.kv_row >= 0 && d.kv_row + d.pos < cache_rows;
+}
+
+__global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v, const float *cosine,
+                                       const float *sine, float *key_cache, float *value_cache, int layer,
+                                       int64_t cache_rows, const qk_batch_token *desc, int context, int q_pairs,
+                                       int kv_pairs, int half_head) {
+    const int t = blockIdx.y;
+    const int pair = blockIdx.x * blockDim.x + threadIdx.x;
+    if (pair >= q_pairs) return;
+    const qk_batch_token d = desc[t];
+    if (!token_ok(d, cache_rows, context - 1)) return;
+    const int f = pair % half_head;
+    const float c = cosine[static_cast<int64_t>(d.pos) * half_head + f];
+    const float s = sine[static_cast<int64_t>(d.pos) * half_head + f];
+    const int i = pair * 2;
+    float *qt = q + static_cast<int64_t>(t) * q_pairs * 2;
+    const float q0 = qt[i], q1 = qt[i + 1];
+    qt[i] = q0 * c - q1 * s;
+    qt[i + 1] = q0 * s + q1 * c;
+    if (pair < kv_pairs) {
+        const int kv_dim = kv_pairs * 2;
+        const float *kt = k + static_cast<int64_t>(t) * kv_dim, *vt = v + static_cast<int64_t>(t) * kv_dim;
+        const int64_t o = (static_cast<int64_t>(layer) * cache_rows + d.kv_row + d.pos) * kv_dim + i;
+        const float k0 = kt[i], k1 = kt[i + 1];
+        key_cache[o] = k0 * c - k1 * s;
+        key_cache[o + 1] = k0 * s + k1 * c;
+        value_cache[o] = vt[i];
+        value_cache[o + 1] = vt[i + 1];
+    }
+}
+
+template <int G, int DL>
+__global__ __launch_bounds__(kAttnThreads) void attention_batched_kernel(const float *q, const float *key_cache,
+                                                                         const float *value_cache, float *out,
+                                                                         int layer, int64_t cache_rows,
+                                                                         const qk_batch_token *desc, int max_pos,
+                                                                         int kv_heads, int head_dim) {
+    extern __shared__ float smem[];
+    const int kvh = blockIdx.x, t = blockIdx.y;
+    const int kv_dim = kv_heads * head_dim, heads = kv_heads * G;
+    const qk_batch_token d = desc[t];
+    float *o = out + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
+    if (!token_ok(d, cache_rows, max_pos)) {
+        for (int i = threadIdx.x; i < G * head_dim; i += kAttnThreads) o[i] = __builtin_nanf("");
+        return;
+    }
+    const int64_t base = (static_cast<int64_t>(layer) * cache_rows + d.kv_row) * kv_dim + kvh * head_dim;
+    attend_kv_head<G, DL>(q + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim, key_cache + base,
+                          value_cache + base, o, d.pos, head_dim, kv_dim, smem);
+}
+
 __global__ void add_kernel(float *x, const float *y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += y[i];
@@ -543,7 +606,11 @@ __device__ __forceinline__ void arg_better(float &bv, int &bi, float v, int i) {
 
 constexpr int kArgmaxBlock = 1024;
 
-__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int n, float *pv, int *pi) {
+// Row blockIdx.y of v (stride ldv) -> partials pv / pi + row * gridDim.x.
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int n, int64_t ldv, float *pv, int *pi) {
+    v += static_cast<int64_t>(blockIdx.y) * ldv;
+    pv += static_cast<int64_t>(blockIdx.y) * gridDim.x;
+    pi += static_cast<int64_t>(blockIdx.y) * gridDim.x;
     __shared__ float sv[4];
     __shared__ int si[4];
     float bv = -INFINITY;
@@ -569,7 +636,11 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
     }
 }
 
+// One block per row: the row's parts partials -> out[row].
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int *pi, int parts, int32_t *out) {
+    pv += static_cast<int64_t>(blockIdx.x) * parts;
+    pi += static_cast<int64_t>(blockIdx.x) * parts;
+    out += blockIdx.x;
     __shared__ float sv[4];
     __shared__ int si[4];
     float bv = -INFINITY;
@@ -617,6 +688,10 @@ const void *attention_instance(int G, int head_dim) {
 template <int G, int DL>
 struct PlainAttention {
     static const void *fn() { return reinterpret_cast<const void *>(attention_kernel<G, DL>); }
+};
+template <int G, int DL>
+struct BatchedAttention {
+    static const void *fn() { return reinterpret_cast<const void *>(attention_batched_kernel<G, DL>); }
 };
 template <int G, int DL>
 struct ChunkedAttention {
@@ -739,10 +814,72 @@ int qk_silu_mul_f32(float *gate, const float *up, int n, qk_stream stream) {
     return qk::launch_status("qk_silu_mul_f32 launch");
 }
 
+int qk_rope_kv_write_batched(float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                             float *key_cache, float *value_cache, int layer, int64_t cache_rows,
+                             const qk_batch_token *desc, int n_tokens, int context, int heads, int kv_heads,
+                             int head_dim, qk_stream stream) {
+    if (!q || !k || !v || !cosine || !sine || !key_cache || !value_cache || (!desc && n_tokens > 0) || n_tokens < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_rope_kv_write_batched: null pointer or negative count");
+    if (head_dim < 2 || head_dim % 2 || heads < 1 || kv_heads < 1 || heads % kv_heads || layer < 0 ||
+        cache_rows < 1 || context < 1)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_rope_kv_write_batched: bad head layout or cache shape");
+    if (n_tokens == 0) return qk::ok();
+    if (n_tokens > 65535) return qk::fail(QK_ERR_LIMIT, "qk_rope_kv_write_batched: too many tokens in one launch");
+    const int q_pairs = heads * head_dim / 2, kv_pairs = kv_heads * head_dim / 2;
+    hipLaunchKernelGGL(qk::rope_kv_batched_kernel, dim3((q_pairs + 255) / 256, n_tokens), dim3(256), 0, qk::S(stream),
+                       q, k, v, cosine, sine, key_cache, value_cache, layer, cache_rows, desc, context, q_pairs,
+                       kv_pairs, head_dim / 2);
+    return qk::launch_status("qk_rope_kv_write_batched launch");
+}
+
+int qk_attention_batched_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,
+                             int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos, int heads,
+                             int kv_heads, int head_dim, qk_stream stream) {
+    if (!q || !key_cache || !value_cache || !out || (!desc && n_tokens > 0) || n_tokens < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_batched_f32: null pointer or negative count");
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads || layer < 0 || cache_rows < 1 || max_pos < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_batched_f32: bad head layout or cache shape");
+    if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: head_dim must be a multiple of 4 dividing 256");
+    const void *fn = qk::attention_instance<qk::BatchedAttention>(heads / kv_heads, head_dim);
+    if (!fn)
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
+    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_attention_batched_f32: caches must be 16-byte aligned");
+    const size_t lds = qk::attention_lds_bytes(max_pos, head_dim, heads / kv_heads);
+    if (lds > 150 * 1024) return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: max_pos beyond the LDS score buffer");
+    if (n_tokens == 0) return qk::ok();
+    if (n_tokens > 65535) return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: too many tokens in one launch");
+    void *args[] = {&q, &key_cache, &value_cache, &out, &layer, &cache_rows, &desc, &max_pos, &kv_heads, &head_dim};
+    if (hipLaunchKernel(fn, dim3(kv_heads, n_tokens), dim3(qk::kAttnThreads), args, lds, qk::S(stream)) != hipSuccess)
+        return qk::launch_status("qk_attention_batched_f32 launch");
+    return qk::launch_status("qk_attention_batched_f32 launch");
+}
+
 size_t qk_argmax_workspace_bytes(int n) {
     if (n < 1) return 0;
     const size_t parts = (static_cast<size_t>(n) + qk::kArgmaxBlock - 1) / qk::kArgmaxBlock;
     return parts * (sizeof(float) + sizeof(int));
+}
+
+size_t qk_argmax_rows_workspace_bytes(int n, int rows) {
+    if (rows < 1) return 0;
+    return qk_argmax_workspace_bytes(n) * static_cast<size_t>(rows);
+}
+
+int qk_argmax_rows_f32(const float *v, int n, int64_t ldv, int rows, int32_t *out, void *workspace,
+                       qk_stream stream) {
+    if (!v || !out || !workspace || n < 1 || rows < 0 || ldv < n)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_argmax_rows_f32: null pointer, empty row or bad stride");
+    if (!qk::aligned(workspace, 4)) return qk::fail(QK_ERR_ALIGN, "qk_argmax_rows_f32: workspace must be 4-byte aligned");
+    if (rows == 0) return qk::ok();
+    if (rows > 65535) return qk::fail(QK_ERR_LIMIT, "qk_argmax_rows_f32: too many rows in one launch");
+    const int parts = (n + qk::kArgmaxBlock - 1) / qk::kArgmaxBlock;
+    float *pv = static_cast<float *>(workspace);
+    int *pi = reinterpret_cast<int *>(pv + static_cast<size_t>(parts) * rows);
+    hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts, rows), dim3(256), 0, qk::S(stream), v, n, ldv, pv, pi);
+    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(rows), dim3(256), 0, qk::S(stream), pv, pi, parts, out);
+    return qk::launch_status("qk_argmax_rows_f32 launch");
 }
 
 int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_stream stream) {
@@ -752,7 +889,7 @@ int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_strea
     const int parts = (n + qk::kArgmaxBlock - 1) / qk::kArgmaxBlock;
     float *pv = static_cast<float *>(workspace);
     int *pi = reinterpret_cast<int *>(pv + parts);
-    hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts), dim3(256), 0, qk::S(stream), v, n, pv, pi);
+    hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts), dim3(256), 0, qk::S(stream), v, n, int64_t(n), pv, pi);
     hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(1), dim3(256), 0, qk::S(stream), pv, pi, parts, out);
     return qk::launch_status("qk_argmax_f32 launch");
 }

@@ -1,0 +1,160 @@
+"""Ragged decode batches on the GPU: the batched RoPE / KV write and
+attention kernels per token against the oracle's fp64 restatements
+(rope_cache_batch_cuda, attention_batch_cuda, inferencer.cu:953-1041,
+generalised to one sequence per token), the per-row argmax, and the batched
+decode step (qk_llama_batch_forward) against one fp64 oracle model per
+sequence: identical greedy tokens, logits within rel-L2 1e-4 on the small
+model (teacher-forced on the oracle's tokens, with the top-2 margin printed
+per token like --compare-prefill, inferencer.cu:1814-1825)."""
+import numpy as np
+import pytest
+
+from conftest import rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(dim=512, layers=2, heads=8, kv_heads=2, hidden=1024, vocab=1000, context=64, eps=1e-5,
+             rope_theta=10000.0)
+
+
+def _desc(qk, t, pos, kv_row):
+    arr = np.zeros(len(pos), dtype=[("pos", "<i4"), ("seq", "<i4"), ("kv_row", "<i8")])
+    arr["pos"], arr["seq"], arr["kv_row"] = pos, np.arange(len(pos)), kv_row
+    return t.from_numpy(arr.view(np.uint8).copy()).to("cuda")
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(32, 8, 64), (24, 8, 128)])
+def test_batched_rope_and_attention(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim):
+    t = torch_gpu
+    layers, layer, ctx = 2, 1, 300
+    pos = np.array([0, 5, 77, 150, 299, 31, 200], dtype=np.int64)
+    n = len(pos)
+    kv_row = np.arange(n, dtype=np.int64) * ctx           # sequence s owns rows s*ctx .. s*ctx + ctx - 1
+    rows = n * ctx
+    kv = kv_heads * head_dim
+    cos, sin = oracle.rope_tables(ctx, head_dim, 500000.0)
+    kc = synth.normal_f32(layers * rows * kv, 60, 1).reshape(layers, rows, kv)
+    vc = synth.normal_f32(layers * rows * kv, 60, 2).reshape(layers, rows, kv)
+    q = synth.normal_f32(n * heads * head_dim, 60, 3).reshape(n, heads * head_dim)
+    k = synth.normal_f32(n * kv, 60, 4).reshape(n, kv)
+    v = synth.normal_f32(n * kv, 60, 5).reshape(n, kv)
+    qd, kd, vd, cd, sd = (to_dev(t, a) for a in (q, k, v, cos, sin))
+    kcd, vcd = to_dev(t, kc), to_dev(t, vc)
+    dd = _desc(qk, t, pos, kv_row)
+    out = t.empty((n, heads * head_dim), device="cuda")
+    L = qk.lib()
+    qk.check(L.qk_rope_kv_write_batched(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), cd.data_ptr(), sd.data_ptr(),
+                                        kcd.data_ptr(), vcd.data_ptr(), layer, rows, dd.data_ptr(), n, ctx, heads,
+                                        kv_heads, head_dim, None), "rope batched")
+    qk.check(L.qk_attention_batched_f32(qd.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), out.data_ptr(), layer, rows,
+                                        dd.data_ptr(), n, int(pos.max()), heads, kv_heads, head_dim, None),
+             "attention batched")
+    t.cuda.synchronize()
+    got_k = kcd.cpu().numpy()
+    got = out.cpu().numpy()
+    for i in range(n):
+        qr = oracle.rope(q[i], cos, sin, int(pos[i]), head_dim)
+        kr = oracle.rope(k[i], cos, sin, int(pos[i]), head_dim)
+        r0 = int(kv_row[i])
+        assert np.max(np.abs(got_k[layer, r0 + pos[i]] - kr)) < 1e-5
+        kseq = kc[layer, r0:r0 + ctx].copy()
+        vseq = vc[layer, r0:r0 + ctx].copy()
+        kseq[pos[i]], vseq[pos[i]] = kr, v[i]
+        want = oracle.attention(qr, kseq[: pos[i] + 1], vseq[: pos[i] + 1], int(pos[i]), heads, kv_heads, head_dim)
+        assert rel_l2(got[i], want) < 1e-5, i
+    # other layers untouched
+    assert np.array_equal(got_k[0], kc[0])
+
+
+def test_batched_attention_rejects_out_of_range_tokens(qk, torch_gpu, synth):
+    """A descriptor beyond max_pos or the cache yields NaN outputs, never an
+    out-of-bounds read."""
+    t = torch_gpu
+    heads, kv_heads, hd, rows = 4, 2, 64, 100
+    kv = kv_heads * hd
+    kcd = t.zeros((1, rows, kv), device="cuda")
+    vcd = t.zeros((1, rows, kv), device="cuda")
+    q = t.ones((3, heads * hd), device="cuda")
+    dd = _desc(qk, t, np.array([10, 60, 5]), np.array([0, 50, 98]))   # ok; beyond max_pos; beyond the cache
+    out = t.zeros((3, heads * hd), device="cuda")
+    qk.check(qk.lib().qk_attention_batched_f32(q.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), out.data_ptr(), 0, rows,
+                                               dd.data_ptr(), 3, 40, heads, kv_heads, hd, None), "attention")
+    t.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.all(np.isfinite(o[0])) and np.all(np.isnan(o[1])) and np.all(np.isnan(o[2]))
+
+
+def test_argmax_rows(qk, torch_gpu, oracle, synth):
+    t = torch_gpu
+    rows, n, ld = 5, 128256, 128300
+    v = synth.normal_f32(rows * ld, 61, 1).reshape(rows, ld)
+    v[1, [3, 90000]] = 40.0                # tie: lowest index wins
+    v[2, n:] = 1e9                         # beyond n: ignored
+    vd = to_dev(t, v)
+    ws = t.empty(qk.lib().qk_argmax_rows_workspace_bytes(n, rows), dtype=t.uint8, device="cuda")
+    out = t.full((rows,), -1, dtype=t.int32, device="cuda")
+    qk.check(qk.lib().qk_argmax_rows_f32(vd.data_ptr(), n, ld, rows, out.data_ptr(), ws.data_ptr(), None), "argmax rows")
+    t.cuda.synchronize()
+    assert out.cpu().tolist() == [oracle.argmax(v[r, :n]) for r in range(rows)]
+
+
+def batch_case(wl, synth, cfg, seed, positions):
+    """Per-sequence caches [layer][context][kv_dim] (N(0,1) below pos, zero
+    above) and the packed [layer][S*context][kv_dim] caches of the batch."""
+    S, ctx = len(positions), cfg["context"]
+    kv = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
+    seqs = []
+    for s, p in enumerate(positions):
+        kc = np.zeros((cfg["layers"], ctx, kv), dtype=np.float32)
+        vc = np.zeros_like(kc)
+        kc[:, :p] = synth.normal_f32(cfg["layers"] * p * kv, seed, 10 + 2 * s).reshape(cfg["layers"], p, kv)
+        vc[:, :p] = synth.normal_f32(cfg["layers"] * p * kv, seed, 11 + 2 * s).reshape(cfg["layers"], p, kv)
+        seqs.append((kc, vc))
+    packed_k = np.concatenate([k for k, _ in seqs], axis=1)
+    packed_v = np.concatenate([v for _, v in seqs], axis=1)
+    return seqs, packed_k, packed_v
+
+
+def run_batch_decode(qk, oracle, wl, synth, cfg, seed, positions, steps, logits_tol):
+    W = wl.llama_weights(cfg, seed)
+    S, ctx = len(positions), cfg["context"]
+    seqs, pk, pv = batch_case(wl, synth, cfg, seed, positions)
+    br = qk.BatchRunner(cfg, W, max_tokens=S, cache_rows=S * ctx)
+    br.load_kv(pk, pv)
+    orcs = []
+    for s, p in enumerate(positions):
+        om = oracle.Llama(cfg, W)
+        om.load_cache(seqs[s][0], seqs[s][1], p)
+        orcs.append(om)
+    tokens = [int(x) for x in synth.uniform_i32(S, seed, 30, 0, cfg["vocab"] - 1)]
+    pos = list(positions)
+    kv_row = [s * ctx for s in range(S)]
+    for step in range(steps):
+        got = br.forward(tokens, pos, kv_row, True)
+        lg = br.logits(S)
+        want = []
+        for s in range(S):
+            o, ref = orcs[s].forward(tokens[s], pos[s], True)
+            top = np.sort(ref)[-2:]
+            err = rel_l2(lg[s], ref)
+            print(f"step {step} seq {s} pos {pos[s]}: gpu {got[s]} ref {o} top2 margin {top[1] - top[0]:.4f} "
+                  f"logits rel-L2 {err:.2e}", flush=True)
+            assert err < logits_tol
+            want.append(o)
+        assert got == want
+        tokens = want                      # teacher-forced on the oracle's tokens
+        pos = [p + 1 for p in pos]
+    br.close()
+
+
+@pytest.mark.parametrize("positions", [[3, 10, 21, 33, 58], [3, 10, 21, 33, 40, 47, 52, 58]])
+def test_small_llama_ragged_batch(qk, torch_gpu, oracle, workloads, synth, positions):
+    """5 tokens (GEMV path) and 8 tokens (matrix-core path), one per sequence."""
+    run_batch_decode(qk, oracle, workloads, synth, SMALL, seed=12, positions=positions, steps=4, logits_tol=1e-4)
+
+
+def test_llama_1b_ragged_batch(qk, torch_gpu, oracle, workloads, synth):
+    """Random-init Llama-3.2-1B, 8 sequences at ragged positions 64..599."""
+    cfg = dict(workloads.LLAMA_1B, context=640)
+    positions = [64, 599, 130, 257, 401, 88, 512, 333]
+    run_batch_decode(qk, oracle, workloads, synth, cfg, seed=2, positions=positions, steps=2, logits_tol=1e-2)
