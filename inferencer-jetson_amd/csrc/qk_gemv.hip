@@ -228,56 +228,15 @@ struct F32Policy {
         float X[4];
     };
 
-    // LDS bytes of the prepared activations of one token, plus 64 bytes of
-    // reduction scratch for the fused RMSNorm.
-    __host__ __device__ static size_t lds_bytes(int cols) {
-        return static_cast<size_t>(cols / 16) * sizeof(XGroup) + 64;
-    }
+    static constexpr bool kFused = false;
+
+    // LDS bytes of the prepared activations of one token.
+    __host__ __device__ static size_t lds_bytes(int cols) { return static_cast<size_t>(cols / 16) * sizeof(XGroup); }
 
     // Cooperative: the block writes every 16-column group of its token.
-    // With norm_w the staged values are x * (1/sqrt(mean(x^2) + eps)) * w,
-    // the arithmetic of rmsnorm_cuda (inferencer.cu:821-834); with up they
-    // are x / (1 + exp(-x)) * up, that of silu_cuda (inferencer.cu:1053-1056).
     __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
         const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
-        float scale = 1.f;
-        if (p.norm_w) {
-            float *scratch = reinterpret_cast<float *>(lds + cols / 16);
-            const float4 *x4 = reinterpret_cast<const float4 *>(x);
-            float ss = 0.f;
-            #pragma unroll 4
-            for (int i = threadIdx.x; i < cols / 4; i += blockDim.x) {
-                const float4 v = x4[i];
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-            }
-            #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-            if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = ss;
-            __syncthreads();
-            ss = 0.f;
-            for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) ss += scratch[w];
-            scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
-        }
-        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) {
-            float v[16];
-            load16f(x + gi * 16, v);
-            if (p.norm_w) {
-                float w[16];
-                load16f(p.norm_w + gi * 16, w);
-                #pragma unroll
-                for (int i = 0; i < 16; ++i) v[i] = v[i] * scale * w[i];
-            }
-            if (p.up) {
-                float u[16];
-                load16f(p.up + static_cast<int64_t>(token) * p.ldx + gi * 16, u);
-                #pragma unroll
-                for (int i = 0; i < 16; ++i) v[i] = v[i] / (1.f + expf(-v[i])) * u[i];
-            }
-            lds[gi] = make_group_regs(v);
-        }
+        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) lds[gi] = make_group(x + gi * 16);
     }
 
     __device__ static void set_part(Lane &L, int part, const XGroup &gr) {
@@ -346,10 +305,71 @@ struct F32Policy {
     }
 };
 
+// The decode driver's fused staging: RMSNorm or SiLU * up applied while the
+// activations are staged, and the residual add in the epilogue.  A policy
+// of its own so the plain kernels carry none of it.
+struct F32FusedPolicy : F32Policy {
+    static constexpr bool kFused = true;
+
+    // LDS bytes of the prepared activations of one token, plus 64 bytes of
+    // reduction scratch for the fused RMSNorm.
+    __host__ __device__ static size_t lds_bytes(int cols) {
+        return static_cast<size_t>(cols / 16) * sizeof(XGroup) + 64;
+    }
+
+    // Cooperative: the block writes every 16-column group of its token.
+    // With norm_w the staged values are x * (1/sqrt(mean(x^2) + eps)) * w,
+    // the arithmetic of rmsnorm_cuda (inferencer.cu:821-834); with up they
+    // are x / (1 + exp(-x)) * up, that of silu_cuda (inferencer.cu:1053-1056).
+    __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
+        const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
+        float scale = 1.f;
+        if (p.norm_w) {
+            float *scratch = reinterpret_cast<float *>(lds + cols / 16);
+            const float4 *x4 = reinterpret_cast<const float4 *>(x);
+            float ss = 0.f;
+            #pragma unroll 4
+            for (int i = threadIdx.x; i < cols / 4; i += blockDim.x) {
+                const float4 v = x4[i];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            #pragma unroll
+            for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+            if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            ss = 0.f;
+            for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) ss += scratch[w];
+            scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
+        }
+        for (int gi = threadIdx.x; gi < cols / 16; gi += blockDim.x) {
+            float v[16];
+            load16f(x + gi * 16, v);
+            if (p.norm_w) {
+                float w[16];
+                load16f(p.norm_w + gi * 16, w);
+                #pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = v[i] * scale * w[i];
+            }
+            if (p.up) {
+                float u[16];
+                load16f(p.up + static_cast<int64_t>(token) * p.ldx + gi * 16, u);
+                #pragma unroll
+                for (int i = 0; i < 16; ++i) v[i] = v[i] / (1.f + expf(-v[i])) * u[i];
+            }
+            lds[gi] = make_group_regs(v);
+        }
+    }
+
+};
+
 // ------------------------------------------------------------ INT8 path --
 
 struct I8Policy {
     static constexpr bool kPrepLds = false;
+    static constexpr bool kFused = false;
     __host__ __device__ static size_t lds_bytes(int) { return 0; }
     __device__ static void prep(const GemvParams &, int, int, XGroup *) {}
 
@@ -466,6 +486,15 @@ __device__ __forceinline__ float piece_dot(int type, const Raw &r, const typenam
     return is_q4k<TYPE>(type) ? Policy::q4k(r, L, g) : Policy::q6k(r, L, h);
 }
 
+// Output store: overwrite, or (fused policy with accumulate) add into y.
+template <class Policy>
+__device__ __forceinline__ void store_y(const GemvParams &p, float *y, float v) {
+    if constexpr (Policy::kFused) {
+        if (p.accumulate) v += *y;
+    }
+    *y = v;
+}
+
 __device__ __forceinline__ float dpp_add(float v, int ctrl_id) {
     int moved;
     const int bits = __builtin_bit_cast(int, v);
@@ -538,11 +567,11 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     int k = 0;
     while (true) {
         float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(a.t.type, a.r, L, g, h));
-        if (piece == 0 && a.t.valid) a.t.y[a.t.row] = p.accumulate ? a.t.y[a.t.row] + v : v;
+        if (piece == 0 && a.t.valid) store_y<Policy>(p, a.t.y + a.t.row, v);
         a = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
         if (++k == n_iter) break;
         v = group_sum<GROUP>(piece_dot<Policy, TYPE>(b.t.type, b.r, L, g, h));
-        if (piece == 0 && b.t.valid) b.t.y[b.t.row] = p.accumulate ? b.t.y[b.t.row] + v : v;
+        if (piece == 0 && b.t.valid) store_y<Policy>(p, b.t.y + b.t.row, v);
         b = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
         if (++k == n_iter) break;
     }
@@ -565,7 +594,7 @@ __device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, c
         if (rowref.valid) {
             float sum = 0.f;
             for (int c = 0; c < p.chunks; ++c) sum += buf[lane * p.chunks + c];
-            rowref.y[rowref.row] = p.accumulate ? rowref.y[rowref.row] + sum : sum;
+            store_y<Policy>(p, rowref.y + rowref.row, sum);
         }
     }
 }
@@ -627,7 +656,7 @@ __global__ __launch_bounds__(256) void gemv_long(GemvParams p) {
         }
         acc = group_sum<64>(acc);
         const TileRef t = locate(p, tile, 0, 0, token);
-        if (lane == 0 && t.valid) t.y[t.row] = p.accumulate ? t.y[t.row] + acc : acc;
+        if (lane == 0 && t.valid) store_y<Policy>(p, t.y + t.row, acc);
     }
 }
 
@@ -769,7 +798,7 @@ bool gemv_fusable(int cols) {
     if (cols <= 0 || cols % 256) return false;
     const int pieces = cols / 64;
     const int chunks = pieces / gcd_int(pieces, 64);
-    return chunks <= kMaxChunks && F32Policy::lds_bytes(cols) + 4096 <= kMaxLds;
+    return chunks <= kMaxChunks && F32FusedPolicy::lds_bytes(cols) + 4096 <= kMaxLds;
 }
 
 int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int cols, const GemvFusion &f,
@@ -782,7 +811,7 @@ int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int col
     p.norm_eps = f.norm_eps;
     p.up = f.up;
     p.accumulate = f.accumulate;
-    return launch<F32Policy>(p, mats, n_mats, cols, 1, nullptr, stream, "fused GEMV launch");
+    return launch<F32FusedPolicy>(p, mats, n_mats, cols, 1, nullptr, stream, "fused GEMV launch");
 }
 
 }  // namespace qk
