@@ -158,6 +158,34 @@ __device__ __forceinline__ float q6k_value(const uint8_t *block, int i) {
     return d * static_cast<float>(sc) * static_cast<float>(q);
 }
 
+// Lane-group sums within a wave (DPP row operations, then cross-row
+// shuffles).
+__device__ __forceinline__ float dpp_add(float v, int ctrl_id) {
+    int moved;
+    const int bits = __builtin_bit_cast(int, v);
+    switch (ctrl_id) {
+        case 0: moved = __builtin_amdgcn_update_dpp(0, bits, 0xB1, 0xF, 0xF, true); break;   // quad_perm 1,0,3,2
+        case 1: moved = __builtin_amdgcn_update_dpp(0, bits, 0x4E, 0xF, 0xF, true); break;   // quad_perm 2,3,0,1
+        case 2: moved = __builtin_amdgcn_update_dpp(0, bits, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
+        default: moved = __builtin_amdgcn_update_dpp(0, bits, 0x140, 0xF, 0xF, true); break; // row_mirror
+    }
+    return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum over aligned groups of GROUP lanes; every lane of a group receives
+// the group's total.  DPP covers groups up to a 16-lane row; wider groups
+// finish with cross-row shuffles.
+template <int GROUP>
+__device__ __forceinline__ float group_sum(float v) {
+    if (GROUP >= 2) v = dpp_add(v, 0);
+    if (GROUP >= 4) v = dpp_add(v, 1);
+    if (GROUP >= 8) v = dpp_add(v, 2);
+    if (GROUP >= 16) v = dpp_add(v, 3);
+    if (GROUP >= 32) v += __shfl_xor(v, 16);
+    if (GROUP >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
 // 6-bit scale / min of Q4_K sub-blocks 4g + part (q4_scale_min,
 // inferencer.cu:489-497), one per byte.
 __device__ __forceinline__ void q4k_scale_min4(const uint4 &hdr, int g, uint32_t &sc, uint32_t &mn) {

@@ -116,19 +116,17 @@ __global__ void rope_kv_kernel(float *q, const float *k, const float *v, const f
 // attention_cuda (inferencer.cu:981-1009), GQA, one query token.  One
 // 512-thread workgroup per KV head serves the G = heads / kv_heads query
 // heads that share it, so every key and value row is read from memory once.
-// At decode sizes the kernel is latency-bound: each phase issues all of its
-// loads before it consumes them.
-//   1. scores: thread t takes positions t, t + 512, ...; it loads the key
-//      row (16 float4 at a time) and dots it with the G query rows (LDS
-//      broadcast), scaled by 1/sqrt(head_dim); scores go to LDS.
+//   1. scores: 16 lanes per key row, each row dotted with the G query rows
+//      (held in registers), 16-lane DPP sums, scaled by 1/sqrt(head_dim);
+//      scores go to LDS.
 //   2. per-head maximum, exp, per-head sum (block reductions in LDS).
-//   3. values: wave w owns a contiguous run of positions, lane = dimension,
-//      rows loaded 16 positions at a time; the 8 partial vectors per head
-//      are added in wave order and divided by the sum (deterministic).
+//   3. values: wave w owns a contiguous run of positions, 16 lanes per row;
+//      the 8 partial vectors per head are added in wave order and divided by
+//      the sum (deterministic).
+// Each phase keeps several steps of loads in flight before it consumes them.
 constexpr int kAttnThreads = 512;
 constexpr int kAttnWaves = kAttnThreads / 64;
 static_assert(kAttnWaves == 8, "attention_lds_bytes sizes 8 waves");
-constexpr int kAttnBatch = 16;        // value rows loaded together
 
 struct AttnLds {
     float *qs;      // [G][head_dim]
@@ -166,62 +164,81 @@ __device__ __forceinline__ void attn_block_reduce(float *v, float *red) {
     __syncthreads();
 }
 
+__device__ __forceinline__ float4 ld_row4(__amdgpu_buffer_rsrc_t r, int lane_off, int row_off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, row_off, 0));
+}
+
+__device__ __forceinline__ float dot4(const float4 &a, const float4 &b, float acc) {
+    acc = fmaf(a.x, b.x, acc);
+    acc = fmaf(a.y, b.y, acc);
+    acc = fmaf(a.z, b.z, acc);
+    return fmaf(a.w, b.w, acc);
+}
+
 // q: the token's query rows of the G heads of KV head kvh (already rotated);
-// kc / vc: the layer's caches offset to this KV head; out: the G output rows.
-// G query heads per KV head and DL = ceil(head_dim / 64) dimensions per lane
-// are compile-time, so every per-head array stays in registers.
+// kc / vc: the layer's caches offset to this KV head's first row; out: the G
+// output rows.  G query heads per KV head and DL = ceil(head_dim / 64) are
+// compile-time, so every per-head array stays in registers.
+//
+// Memory access: 16 lanes share a cache row (lane sub reads dimensions
+// 64c + 4*sub .. +3 of chunk c as one float4), so one load instruction of a
+// wave covers four whole rows.  Rows are read through buffer resources that
+// span exactly the rows a phase may read: a row past the range reads as zero.
 template <int G, int DL>
-__device__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos, int head_dim,
-                               int kv_dim, float *smem) {
+__device__ __forceinline__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos,
+                                               int head_dim, int kv_dim, float *smem) {
     const AttnLds L = attn_lds(smem, G, head_dim, pos);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane & 15, rq = lane >> 4;
+    const bool act = 4 * sub < head_dim;         // head_dim < 64 leaves lanes idle
     const int n = pos + 1;
+    const int row_bytes = kv_dim * 4;
+    const int lane_off = (rq * kv_dim + 4 * min(sub, max(head_dim / 4 - 1, 0))) * 4;
+    constexpr int U = (16 / DL) / (G > 4 ? 2 : 1);   // 4-row steps in flight per wave
     const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
     for (int i = tid; i < G * head_dim; i += kAttnThreads) L.qs[i] = q[i];
     __syncthreads();
+    float4 qv[G][DL];
+    #pragma unroll
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int c = 0; c < DL; ++c)
+            qv[g][c] = act ? *reinterpret_cast<const float4 *>(L.qs + g * head_dim + 64 * c + 4 * sub)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
 
+    // 1. Scores.  Step u of wave w covers rows it0 + (u*waves + w)*4 + rq.
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kc), 0, n * row_bytes, 0x00020000);
     float m[G];
     #pragma unroll
     for (int g = 0; g < G; ++g) m[g] = -INFINITY;
-    for (int t = tid; t < n; t += kAttnThreads) {
-        const float4 *kr = reinterpret_cast<const float4 *>(kc + static_cast<int64_t>(t) * kv_dim);
-        float dot[G];
+    for (int it0 = 0; it0 < n; it0 += kAttnWaves * 4 * U) {
+        float4 k4[U][DL];
         #pragma unroll
-        for (int g = 0; g < G; ++g) dot[g] = 0.f;
-        for (int c = 0; c < head_dim; c += 64) {
-            float4 k4[16];
-            const int nc = min(16, (head_dim - c) >> 2);
+        for (int u = 0; u < U; ++u)
             #pragma unroll
-            for (int j = 0; j < 16; ++j)
-                if (j < nc) k4[j] = kr[(c >> 2) + j];
-            // The query rows are re-read from LDS (broadcast) for every key
-            // row: an opaque offset keeps them out of registers.
-            int qoff = c;
-            asm volatile("" : "+v"(qoff));
+            for (int c = 0; c < DL; ++c)
+                k4[u][c] = ld_row4(krs, lane_off + 256 * c, (it0 + (u * kAttnWaves + wave) * 4) * row_bytes);
+        #pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = it0 + (u * kAttnWaves + wave) * 4 + rq;
             #pragma unroll
             for (int g = 0; g < G; ++g) {
-                const float *qg = L.qs + g * head_dim + qoff;
-                float a = dot[g];
+                float a = 0.f;
                 #pragma unroll
-                for (int j = 0; j < 16; ++j)
-                    if (j < nc) {
-                        a = fmaf(qg[4 * j], k4[j].x, a);
-                        a = fmaf(qg[4 * j + 1], k4[j].y, a);
-                        a = fmaf(qg[4 * j + 2], k4[j].z, a);
-                        a = fmaf(qg[4 * j + 3], k4[j].w, a);
-                    }
-                dot[g] = a;
+                for (int c = 0; c < DL; ++c) a = dot4(qv[g][c], k4[u][c], a);
+                const float sc = group_sum<16>(a) * inv;
+                if (t < n) {
+                    if (sub == 0) L.score[g * n + t] = sc;
+                    m[g] = fmaxf(m[g], sc);
+                }
             }
-        }
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float sc = dot[g] * inv;
-            L.score[g * n + t] = sc;
-            m[g] = fmaxf(m[g], sc);
         }
     }
     attn_block_reduce<true, G>(m, L.red);   // its barriers also publish score[]
 
+    // 2. exp and the per-head sums.
     float den[G];
     #pragma unroll
     for (int g = 0; g < G; ++g) den[g] = 0.f;
@@ -234,41 +251,53 @@ __device__ void attend_kv_head(const float *q, const float *kc, const float *vc,
         }
     attn_block_reduce<false, G>(den, L.red);
 
+    // 3. Values: wave w owns rows t0 .. t1-1, four per step (row t0 + 4s + rq).
     const int per = (n + kAttnWaves - 1) / kAttnWaves;
-    const int t0 = wave * per, t1 = min(n, t0 + per);
-        float acc[G][DL];
+    const int t0 = min(n, wave * per), t1 = min(n, t0 + per);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(vc + static_cast<int64_t>(t0) * kv_dim), 0, (t1 - t0) * row_bytes, 0x00020000);
+    float4 acc[G][DL];
     #pragma unroll
     for (int g = 0; g < G; ++g)
         #pragma unroll
-        for (int j = 0; j < DL; ++j) acc[g][j] = 0.f;
-    // Value rows in batches of 16 positions, every load of a batch issued
-    // before the first multiply-add.
-    for (int tb = t0; tb < t1; tb += kAttnBatch) {
-        float v[kAttnBatch][DL];
+        for (int c = 0; c < DL; ++c) acc[g][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = 0; s0 < t1 - t0; s0 += 4 * U) {
+        float4 v4[U][DL];
         #pragma unroll
-        for (int u = 0; u < kAttnBatch; ++u)
+        for (int u = 0; u < U; ++u)
             #pragma unroll
-            for (int j = 0; j < DL; ++j) {
-                const int d = lane + 64 * j;
-                v[u][j] = (tb + u < t1 && d < head_dim)
-                              ? vc[static_cast<int64_t>(tb + u) * kv_dim + d]
-                              : 0.f;
-            }
+            for (int c = 0; c < DL; ++c) v4[u][c] = ld_row4(vrs, lane_off + 256 * c, (s0 + 4 * u) * row_bytes);
         #pragma unroll
-        for (int g = 0; g < G; ++g)
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + s0 + 4 * u + rq;
             #pragma unroll
-            for (int u = 0; u < kAttnBatch; ++u) {
-                const float pr = tb + u < t1 ? L.score[g * n + tb + u] : 0.f;
+            for (int g = 0; g < G; ++g) {
+                const float pr = t < t1 ? L.score[g * n + t] : 0.f;
                 #pragma unroll
-                for (int j = 0; j < DL; ++j) acc[g][j] = fmaf(pr, v[u][j], acc[g][j]);
+                for (int c = 0; c < DL; ++c) {
+                    acc[g][c].x = fmaf(pr, v4[u][c].x, acc[g][c].x);
+                    acc[g][c].y = fmaf(pr, v4[u][c].y, acc[g][c].y);
+                    acc[g][c].z = fmaf(pr, v4[u][c].z, acc[g][c].z);
+                    acc[g][c].w = fmaf(pr, v4[u][c].w, acc[g][c].w);
+                }
             }
+        }
     }
+    // The four row groups of the wave meet in lanes 0..15.
     #pragma unroll
     for (int g = 0; g < G; ++g)
         #pragma unroll
-        for (int j = 0; j < DL; ++j) {
-            const int d = lane + 64 * j;
-            if (d < head_dim) L.part[(wave * G + g) * head_dim + d] = acc[g][j];
+        for (int c = 0; c < DL; ++c) {
+            float4 &a = acc[g][c];
+            a.x += __shfl_xor(a.x, 16);
+            a.y += __shfl_xor(a.y, 16);
+            a.z += __shfl_xor(a.z, 16);
+            a.w += __shfl_xor(a.w, 16);
+            a.x += __shfl_xor(a.x, 32);
+            a.y += __shfl_xor(a.y, 32);
+            a.z += __shfl_xor(a.z, 32);
+            a.w += __shfl_xor(a.w, 32);
+            if (rq == 0 && act) *reinterpret_cast<float4 *>(L.part + (wave * G + g) * head_dim + 64 * c + 4 * sub) = a;
         }
     __syncthreads();
     for (int i = tid; i < G * head_dim; i += kAttnThreads) {
