@@ -21,7 +21,7 @@
 // the activation scale are applied in fp32 when the block is done.
 //
 // Three kernels:
-//   pack_activations  once per (block, 32-token tile): x -> the record of
+//   pack_activations  once per (block, 8 tokens): x -> the record of
 //                     MFMA A operands (fp16 hi / lo, sub-block sums, scales)
 //                     in the caller's workspace.
 //   batch_gemm        a workgroup (4 waves) owns 256 weight rows (two 32-row
@@ -35,7 +35,8 @@
 //                     every token tile.  When one row group's blocks are split
 //                     over several workgroups (to put enough waves on the
 //                     chip), each writes its partial sums to the workspace;
-//   reduce_splits     adds them in split order, so results are deterministic.
+//   reduce_splits     adds them in split order, so results are deterministic,
+//                     and applies the call's epilogue.
 #include "qk_internal.h"
 
 #include <algorithm>
@@ -101,6 +102,11 @@ struct BatchParams {
     int blocks_per_split;
     float *partials;        // [group][tile][split][kPartialFloats] when splits > 1
     const uint8_t *records; // packed activations, [tile][block][kTileBytes]
+    // Decode-driver fusions (zero: plain x, overwrite y):
+    const float *norm_w;    // stage RMSNorm(x) * norm_w
+    float norm_eps;
+    const float *up;        // stage x / (1 + exp(-x)) * up (up has x's layout)
+    int accumulate;         // y += W x
 };
 
 // ---------------------------------------------------- activation staging --
@@ -112,11 +118,37 @@ struct XStage {
     float v[32];
 };
 
-__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, XStage &s) {
-    const int tl = threadIdx.x >> 3, q = threadIdx.x & 7;
+// With norm_w, the token's RMSNorm scale 1/sqrt(mean(x^2) + eps) over all
+// cols (eight lanes per token, rmsnorm_cuda's arithmetic, inferencer.cu:
+// 821-834) multiplies x and the gain is applied; with up, x / (1 + exp(-x))
+// * up (silu_cuda, inferencer.cu:1053-1056).
+__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, int tl, int q, XStage &s) {
     const int t = tile * kTokTile + tl;
+    const int cols = p.nb * 256;
+    float scale = 1.f;
+    if (p.norm_w) {
+        float ss = 0.f;
+        if (t < p.n_tokens) {
+            // Sixteen float4 per lane in flight at a time: the row is long and
+            // only nb x tiles workgroups share the work.
+            const float4 *row = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx);
+            #pragma unroll 16
+            for (int i = q; i < cols / 4; i += 8) {
+                const float4 v = row[i];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+        }
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
+    }
     if (t < p.n_tokens) {
-        const float4 *src = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32);
+        const int64_t at = static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32;
+        const float4 *src = reinterpret_cast<const float4 *>(p.x + at);
         #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const float4 u = src[i];
@@ -124,6 +156,29 @@ __device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b
             s.v[4 * i + 1] = u.y;
             s.v[4 * i + 2] = u.z;
             s.v[4 * i + 3] = u.w;
+        }
+        if (p.norm_w) {
+            const float4 *w4 = reinterpret_cast<const float4 *>(p.norm_w + b * 256 + q * 32);
+            #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 w = w4[i];
+                s.v[4 * i] = s.v[4 * i] * scale * w.x;
+                s.v[4 * i + 1] = s.v[4 * i + 1] * scale * w.y;
+                s.v[4 * i + 2] = s.v[4 * i + 2] * scale * w.z;
+                s.v[4 * i + 3] = s.v[4 * i + 3] * scale * w.w;
+            }
+        }
+        if (p.up) {
+            const float4 *u4 = reinterpret_cast<const float4 *>(p.up + at);
+            #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float4 u = u4[i];
+                const float g0 = s.v[4 * i], g1 = s.v[4 * i + 1], g2 = s.v[4 * i + 2], g3 = s.v[4 * i + 3];
+                s.v[4 * i] = g0 / (1.f + expf(-g0)) * u.x;
+                s.v[4 * i + 1] = g1 / (1.f + expf(-g1)) * u.y;
+                s.v[4 * i + 2] = g2 / (1.f + expf(-g2)) * u.z;
+                s.v[4 * i + 3] = g3 / (1.f + expf(-g3)) * u.w;
+            }
         }
     } else {
         #pragma unroll
@@ -134,8 +189,7 @@ __device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b
 // x' = x * 2^shift with the block maximum of the token in [2^14, 2^15)
 // (shift capped at 140 so 2^-shift stays a nonzero fp32), split into fp16
 // hi + lo; a non-finite activation makes the token's scale NaN.
-__device__ __forceinline__ void stage_store(const XStage &s, uint8_t *tile) {
-    const int tl = threadIdx.x >> 3, q = threadIdx.x & 7;
+__device__ __forceinline__ void stage_store(const XStage &s, int tl, int q, uint8_t *tile) {
     float m = 0.f;
     bool bad = false;
     #pragma unroll
@@ -194,13 +248,19 @@ __device__ __forceinline__ void stage_store(const XStage &s, uint8_t *tile) {
     }
 }
 
-// One workgroup per (block, 32-token tile): the tile's activations of the
-// block, packed once into the workspace record the GEMM copies into LDS.
-__global__ __launch_bounds__(256) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
-    const int b = blockIdx.x, tile = blockIdx.y;
+// One 64-thread workgroup per (block, eight tokens of a 32-token tile): the
+// tokens' activations of the block, packed into the workspace record the
+// GEMM copies into LDS.  Thread (token tl, sub-block q); the eight lanes of a
+// token meet in shuffles.
+constexpr int kPackTokens = 8;
+__global__ __launch_bounds__(64) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
+    const int b = blockIdx.x;
+    const int tile = blockIdx.y / (kTokTile / kPackTokens);
+    const int tl = (blockIdx.y % (kTokTile / kPackTokens)) * kPackTokens + (threadIdx.x >> 3);
+    const int q = threadIdx.x & 7;
     XStage xs;
-    stage_load(p, tile, b, xs);
-    stage_store(xs, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
+    stage_load(p, tile, b, tl, q, xs);
+    stage_store(xs, tl, q, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
 }
 
 // ------------------------------------------------------- weight operands --
@@ -408,6 +468,12 @@ __device__ __forceinline__ void block_mma(const RawBlock (&r)[RT], int type, con
     }
 }
 
+// Output store: overwrite, or add into y (the driver's residual add).
+__device__ __forceinline__ void store_out(const BatchParams &p, float *y, float v) {
+    if (p.accumulate) v += *y;
+    *y = v;
+}
+
 // ---------------------------------------------------------------- GEMM --
 //
 // Workgroup = 4 waves x kRowTiles row tiles = 256 weight rows, x TT token
@@ -515,14 +581,16 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
                 #pragma unroll
                 for (int k = 0; k < 16; ++k) {
                     const int t = tbase + 8 * (k >> 2) + (k & 3);
-                    if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row[i]] = acc[i][u][k];
+                    if (t < p.n_tokens) store_out(p, M.y + static_cast<int64_t>(t) * M.ldy + row[i], acc[i][u][k]);
                 }
             }
         }
         return;
     }
     // Split blocks: partial sums to the workspace in accumulator order,
-    // [group][token tile][split][wave][row tile][k][lane]; reduce_splits adds them.
+    // [group][token tile][split][wave][row tile][k][lane]; reduce_splits adds
+    // them.  (A last-workgroup reduction inside this kernel would need a
+    // device-scope fence per workgroup, measured slower than the extra launch.)
     #pragma unroll
     for (int u = 0; u < TT; ++u) {
         if (tile0 + u >= p.tiles) break;
@@ -535,47 +603,56 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     }
 }
 
-// y = the sum of a row group's split partials, in split order (deterministic).
-// One workgroup per (row group, token tile); thread (wave, lane) owns the
-// outputs the same thread of batch_gemm produced.
-__global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
+// y = the sum of a row group's split partials, in split order (deterministic),
+// stored with the call's epilogue (overwrite or add).  One 64-thread
+// workgroup per (row group, GEMM wave, row tile, token tile): lane l owns the
+// outputs lane l of that GEMM wave produced for that row tile.
+__global__ __launch_bounds__(64) void reduce_splits(BatchParams p) {
     constexpr int RT = kRowTiles;
-    const int group = blockIdx.x, tile = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int group = blockIdx.x / (4 * RT), sub = blockIdx.x % (4 * RT);
+    const int wave = sub % 4, i = sub / 4, tile = blockIdx.y;
+    const int lane = threadIdx.x;
     const int kh = lane >> 5, col = lane & 31;
     int m = 0;
     #pragma unroll
-    for (int i = 1; i < QK_MAX_FUSED; ++i) m += (i < p.n_mats && group >= p.mat[i].group_begin) ? 1 : 0;
+    for (int j = 1; j < QK_MAX_FUSED; ++j) m += (j < p.n_mats && group >= p.mat[j].group_begin) ? 1 : 0;
     const BatchMatrix &M = p.mat[m];
     const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
-    const float *part = p.partials + slot * p.splits * kPartialFloats + wave * (RT * 1024) + lane;
+    const float *part = p.partials + slot * p.splits * kPartialFloats + wave * (RT * 1024) + i * 1024 + lane;
     const int tbase = tile * kTokTile + 4 * kh;
+    const int row = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
+    // Every load of a split run is issued before the first add: the kernel is latency-bound.
+    float sum[16];
     #pragma unroll
-    for (int i = 0; i < RT; ++i) {
-        const int row = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
-        // Every load of a split run is issued before the first add: the kernel is latency-bound.
-        float s[16];
+    for (int k = 0; k < 16; ++k) sum[k] = part[k * 64];
+    for (int sp0 = 1; sp0 < p.splits; sp0 += 4) {
+        float v[4][16];
         #pragma unroll
-        for (int k = 0; k < 16; ++k) s[k] = part[i * 1024 + k * 64];
-        for (int sp0 = 1; sp0 < p.splits; sp0 += 4) {
-            float v[4][16];
+        for (int q = 0; q < 4; ++q)
             #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                #pragma unroll
-                for (int k = 0; k < 16; ++k)
-                    v[q][k] = sp0 + q < p.splits ? part[(sp0 + q) * kPartialFloats + i * 1024 + k * 64] : 0.f;
+            for (int k = 0; k < 16; ++k) v[q][k] = sp0 + q < p.splits ? part[(sp0 + q) * kPartialFloats + k * 64] : 0.f;
+        #pragma unroll
+        for (int q = 0; q < 4; ++q)
             #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                #pragma unroll
-                for (int k = 0; k < 16; ++k)
-                    if (sp0 + q < p.splits) s[k] += v[q][k];
-        }
-        if (row >= M.rows) continue;
+            for (int k = 0; k < 16; ++k)
+                if (sp0 + q < p.splits) sum[k] += v[q][k];
+    }
+    if (row >= M.rows) return;
+    if (p.accumulate) {
+        // The residual values, all loaded before the first store.
+        float yv[16];
         #pragma unroll
         for (int k = 0; k < 16; ++k) {
             const int t = tbase + 8 * (k >> 2) + (k & 3);
-            if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = s[k];
+            yv[k] = t < p.n_tokens ? M.y[static_cast<int64_t>(t) * M.ldy + row] : 0.f;
         }
+        #pragma unroll
+        for (int k = 0; k < 16; ++k) sum[k] = yv[k] + sum[k];
+    }
+    #pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int t = tbase + 8 * (k >> 2) + (k & 3);
+        if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = sum[k];
     }
 }
 
@@ -665,7 +742,8 @@ void launch_gemm(int type, const dim3 &grid, size_t lds, hipStream_t stream, con
 }
 
 int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *x, int ldx, int cols, int n_tokens,
-                void *workspace, size_t workspace_size, hipStream_t stream, const char *where) {
+                void *workspace, size_t workspace_size, hipStream_t stream, const char *where,
+                const GemvFusion *fusion = nullptr) {
     const int nb = cols / 256;
     const int tiles = tile_count(n_tokens);
     const int tt = token_tiles_per_group(tiles);
@@ -703,21 +781,40 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
                                             " bytes (qk_gemv_batched_workspace_bytes)");
     if (!aligned(workspace, 256)) return fail(QK_ERR_ALIGN, std::string(where) + ": workspace not 256-byte aligned");
     uint8_t *ws = static_cast<uint8_t *>(workspace);
+    const int tgroups = (tiles + tt - 1) / tt;
     p.records = ws;
     if (p.splits > 1) p.partials = reinterpret_cast<float *>(ws + (records_bytes(cols, n_tokens) + 255) / 256 * 256);
-    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles), dim3(256), 0, stream, p, ws);
-    const dim3 grid(static_cast<unsigned>(groups * p.splits), (tiles + tt - 1) / tt);
+    if (fusion) {
+        p.norm_w = fusion->norm_w;
+        p.norm_eps = fusion->norm_eps;
+        p.up = fusion->up;
+        p.accumulate = fusion->accumulate;
+    }
+    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(64), 0, stream, p, ws);
+    const dim3 grid(static_cast<unsigned>(groups * p.splits), tgroups);
     const size_t lds = 2 * static_cast<size_t>(tt) * kTileBytes;
     if (tt == 2)
         launch_gemm<2>(type, grid, lds, stream, p);
     else
         launch_gemm<1>(type, grid, lds, stream, p);
     if (p.splits > 1)
-        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups), tiles), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups * 4 * kRowTiles), tiles), dim3(64), 0, stream,
+                           p);
     return launch_status(where);
 }
 
 }  // namespace
+
+int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
+                         const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream) {
+    int ldy[QK_MAX_FUSED];
+    for (int m = 0; m < n_mats; ++m) ldy[m] = mats[m].rows;
+    if (n_tokens >= kMfmaMinTokens)
+        return launch_mfma(mats, n_mats, ldy, x, ldx, cols, n_tokens, workspace, workspace_size, stream,
+                           "fused batched GEMM", &f);
+    return launch_gemv_fused(mats, n_mats, x, ldx, cols, n_tokens, ldy, f, stream);
+}
+
 }  // namespace qk
 
 extern "C" {

@@ -775,17 +775,17 @@ bool gemv_fusable(int cols) {
     return chunks <= kMaxChunks && F32FusedPolicy::lds_bytes(cols) + 4096 <= kMaxLds;
 }
 
-int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int cols, const GemvFusion &f,
-                      hipStream_t stream) {
+int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
+                      const int *ldy, const GemvFusion &f, hipStream_t stream) {
     if (!gemv_fusable(cols)) return fail(QK_ERR_LIMIT, "fused GEMV: rows too long to stage the activations");
     GemvParams p{};
     p.x = x;
-    p.ldx = cols;
+    p.ldx = ldx;
     p.norm_w = f.norm_w;
     p.norm_eps = f.norm_eps;
     p.up = f.up;
     p.accumulate = f.accumulate;
-    return launch<F32FusedPolicy>(p, mats, n_mats, cols, 1, nullptr, stream, "fused GEMV launch");
+    return launch<F32FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "fused GEMV launch");
 }
 
 }  // namespace qk

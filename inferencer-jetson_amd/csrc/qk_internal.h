@@ -58,9 +58,16 @@ struct GemvFusion {
 };
 // Whether a row of cols columns can stage its activations for the fusions.
 bool gemv_fusable(int cols);
-// One token, arguments already validated.
-int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int cols, const GemvFusion &f,
-                      hipStream_t stream);
+// n_tokens tokens (x + t*ldx; y + t*ldy[m], NULL: rows), arguments already
+// validated.
+int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
+                      const int *ldy, const GemvFusion &f, hipStream_t stream);
+// The same for a batch of n_tokens tokens, token-major (ldy = rows): the
+// matrix-core GEMM from 8 tokens on (staging fused into its pack kernel, the
+// residual add into its epilogue), the fused GEMV below.  workspace as for
+// qk_gemv_multi_batched_f32.
+int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
+                         const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream);
 // Whether the attention kernels serve `group` query heads per KV head and
 // head_dim (group in {1, 2, 3, 4, 6, 8}; head_dim a multiple of 4 dividing 256).
 bool attention_supported(int group, int head_dim);
@@ -83,6 +90,13 @@ int launch_rope_attention_chunked(const float *q, const float *k, const float *v
                                   const float *sine, float *key_cache, float *value_cache, float *out, void *workspace,
                                   int layer, int pos, int context, int heads, int kv_heads, int head_dim,
                                   hipStream_t stream);
+
+// Ragged-batch form of launch_rope_attention: token t at desc[t] (device),
+// q / k / v token-major; max_pos bounds every position.
+int launch_rope_attention_batched(const float *q, const float *k, const float *v, const float *cosine,
+                                  const float *sine, float *key_cache, float *value_cache, float *out, int layer,
+                                  int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos,
+                                  int heads, int kv_heads, int head_dim, hipStream_t stream);
 
 // Per-device properties, cached once per device (thread-safe).
 struct DeviceInfo {

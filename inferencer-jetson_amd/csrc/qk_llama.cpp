@@ -205,7 +205,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         attn_in.norm_w = L.attn_norm;
         ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, attn_in, s))) return st;
+        if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, dim, 1, nullptr, attn_in, s))) return st;
         if (m->attn_ws)
             st = qk::launch_rope_attention_chunked(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache,
                                                    m->attn, m->attn_ws, l, pos, c.context, c.heads, c.kv_heads, hd, s);
@@ -214,11 +214,11 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
                                            l, pos, c.context, c.heads, c.kv_heads, hd, s);
         if (st) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
-        if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, residual, s))) return st;
+        if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, dim, 1, nullptr, residual, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, ffn_in, s))) return st;
+        if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, dim, 1, nullptr, ffn_in, s))) return st;
         const qk_matrix down{L.down_type, dim, L.down, m->x};
-        if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, down_in, s))) return st;
+        if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, c.hidden, 1, nullptr, down_in, s))) return st;
     }
     if (!need_logits) {
         if (next_token) *next_token = -1;
@@ -230,7 +230,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
-    if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, out_in, s))) return st;
+    if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, dim, 1, nullptr, out_in, s))) return st;
     if ((st = qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s))) return st;
     if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
@@ -292,10 +292,17 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_create: max_tokens must be 1..4096 and cache_rows >= 1");
     const int head_dim = c.dim / c.heads;
     if (!qk::attention_supported(c.heads / c.kv_heads, head_dim) ||
-        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
+        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) + 4 * c.dim / c.kv_heads > 150 * 1024)
         return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: head layout or context beyond the attention kernel");
     if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
         return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: embedding and output must be Q4_K or Q6_K");
+    if (!qk::gemv_fusable(c.dim) || !qk::gemv_fusable(c.hidden))
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: dim or hidden too long to stage the activations");
+    if (!qk::aligned(w->output_norm, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_llama_batch_create: norm weights must be 16-byte aligned");
+    for (int l = 0; l < c.layers; ++l)
+        if (!qk::aligned(w->layers[l].attn_norm, 16) || !qk::aligned(w->layers[l].ffn_norm, 16))
+            return qk::fail(QK_ERR_ALIGN, "qk_llama_batch_create: norm weights must be 16-byte aligned");
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = w->layers[l];
         if (!quant_type(L.q_type) || !quant_type(L.k_type) || !quant_type(L.v_type) || !quant_type(L.o_type) ||
@@ -418,34 +425,38 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
     void *ws = m->gemm_ws;
     const size_t wsb = m->gemm_ws_bytes;
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, m->d_tokens, T, m->x, dim, c.vocab, s))) return st;
+    // Per layer: fused QKV (RMSNorm staged), RoPE + KV write + attention,
+    // o (+ residual), fused gate/up (RMSNorm staged), down (SiLU * up staged,
+    // + residual).
+    qk::GemvFusion attn_in, ffn_in, residual, down_in;
+    attn_in.norm_eps = ffn_in.norm_eps = c.eps;
+    residual.accumulate = down_in.accumulate = 1;
+    down_in.up = m->up;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
-        if ((st = qk_rmsnorm_f32(m->x, L.attn_norm, m->xn, dim, T, c.eps, s))) return st;
+        attn_in.norm_w = L.attn_norm;
+        ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = qk_gemv_multi_batched_f32(qkv, 3, m->xn, dim, dim, T, ws, wsb, s))) return st;
-        if ((st = qk_rope_kv_write_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
-                                           m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
+        if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, attn_in, ws, wsb, s))) return st;
+        if ((st = qk::launch_rope_attention_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache,
+                                                    m->attn, l, m->cache_rows, m->d_desc, T, max_pos, c.heads,
+                                                    c.kv_heads, hd, s)))
             return st;
-        if ((st = qk_attention_batched_f32(m->q, m->key_cache, m->value_cache, m->attn, l, m->cache_rows, m->d_desc, T,
-                                           max_pos, c.heads, c.kv_heads, hd, s)))
-            return st;
-        if ((st = qk_gemv_batched_f32(L.o_type, L.o, m->attn, dim, m->tmp, dim, dim, dim, T, ws, wsb, s))) return st;
-        if ((st = qk_add_f32(m->x, m->tmp, T * dim, s))) return st;
-        if ((st = qk_rmsnorm_f32(m->x, L.ffn_norm, m->xn, dim, T, c.eps, s))) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->x};
+        if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, residual, ws, wsb, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = qk_gemv_multi_batched_f32(gu, 2, m->xn, dim, dim, T, ws, wsb, s))) return st;
-        if ((st = qk_silu_mul_f32(m->gate, m->up, T * c.hidden, s))) return st;
-        if ((st = qk_gemv_batched_f32(L.down_type, L.down, m->gate, c.hidden, m->tmp, dim, c.hidden, dim, T, ws, wsb,
-                                      s)))
-            return st;
-        if ((st = qk_add_f32(m->x, m->tmp, T * dim, s))) return st;
+        if ((st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, ffn_in, ws, wsb, s))) return st;
+        const qk_matrix down{L.down_type, dim, L.down, m->x};
+        if ((st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s))) return st;
     }
     if (!need_logits) return qk::ok();
-    if ((st = qk_rmsnorm_f32(m->x, m->w.output_norm, m->xn, dim, T, c.eps, s))) return st;
+    qk::GemvFusion out_in;
+    out_in.norm_w = m->w.output_norm;
+    out_in.norm_eps = c.eps;
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
-    if ((st = qk_gemv_batched_f32(out_type, out_w, m->xn, dim, m->logits, c.vocab, dim, c.vocab, T, ws, wsb, s)))
-        return st;
+    const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+    if ((st = qk::launch_batched_fused(&head, 1, m->x, dim, dim, T, out_in, ws, wsb, s))) return st;
     if ((st = qk_argmax_rows_f32(m->logits, c.vocab, c.vocab, T, m->d_next, m->argmax_ws, s))) return st;
     if (hipMemcpyAsync(h_next, m->d_next, T * sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)

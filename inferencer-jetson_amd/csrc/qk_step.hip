@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *q,
 // inferencer.cu:930-951), then attend_kv_head.  The rotated query rows live
 // in LDS after the attention's own buffers.  The cache row of pos is written
 // by this workgroup only (heads occupy disjoint 256-byte runs of a row) and
-// read back after a fence and a barrier.
+// read back after a barrier.
 template <int G, int DL>
 __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(
     const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
@@ -355,8 +355,7 @@ __global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(
         value_cache[row] = v[o];
         value_cache[row + 1] = v[o + 1];
     }
-    __threadfence();
-    __syncthreads();
+    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
     attend_kv_head<G, DL>(qrot, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos, head_dim, kv_dim,
                           smem);
 }
@@ -417,9 +416,8 @@ __global__ __launch_bounds__(kChunkThreads) void rope_attention_chunked_kernel(
             value_cache[row] = v[o];
             value_cache[row + 1] = v[o + 1];
         }
-        __threadfence();
     }
-    __syncthreads();
+    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
 
     // 1. Scores: four lanes per position, each a quarter of head_dim.
     const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
@@ -610,6 +608,51 @@ __global__ __launch_bounds__(kAttnThreads) void attention_batched_kernel(const f
                           value_cache + base, o, d.pos, head_dim, kv_dim, smem);
 }
 
+// Decode-driver form for ragged batches: RoPE of token t's G query rows and
+// of its key head kvh at its own position, the key / value write into row
+// kv_row + pos (written and read back by this workgroup only, ordered by
+// the barrier), then attend_kv_head over the token's own rows.
+template <int G, int DL>
+__global__ __launch_bounds__(kAttnThreads) void rope_attention_batched_kernel(
+    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
+    float *value_cache, float *out, int layer, int64_t cache_rows, const qk_batch_token *desc, int max_pos,
+    int kv_heads, int head_dim) {
+    extern __shared__ float smem[];
+    const int kvh = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int kv_dim = kv_heads * head_dim, heads = kv_heads * G, half = head_dim / 2;
+    const qk_batch_token d = desc[t];
+    float *o = out + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
+    if (!token_ok(d, cache_rows, max_pos)) {
+        for (int i = tid; i < G * head_dim; i += kAttnThreads) o[i] = __builtin_nanf("");
+        return;
+    }
+    const int64_t base = (static_cast<int64_t>(layer) * cache_rows + d.kv_row) * kv_dim + kvh * head_dim;
+    float *qrot = smem + attention_lds_bytes(max_pos, head_dim, G) / sizeof(float);
+    const float *cs = cosine + static_cast<int64_t>(d.pos) * half;
+    const float *sn = sine + static_cast<int64_t>(d.pos) * half;
+    const float *qt = q + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
+    for (int i = tid; i < G * half; i += kAttnThreads) {
+        const int f = i % half;
+        const float c = cs[f], si = sn[f];
+        const float q0 = qt[2 * i], q1 = qt[2 * i + 1];
+        qrot[2 * i] = q0 * c - q1 * si;
+        qrot[2 * i + 1] = q0 * si + q1 * c;
+    }
+    const float *kt = k + static_cast<int64_t>(t) * kv_dim + kvh * head_dim;
+    const float *vt = v + static_cast<int64_t>(t) * kv_dim + kvh * head_dim;
+    for (int f = tid; f < half; f += kAttnThreads) {
+        const float c = cs[f], si = sn[f];
+        const int64_t row = base + static_cast<int64_t>(d.pos) * kv_dim + 2 * f;
+        const float k0 = kt[2 * f], k1 = kt[2 * f + 1];
+        key_cache[row] = k0 * c - k1 * si;
+        key_cache[row + 1] = k0 * si + k1 * c;
+        value_cache[row] = vt[2 * f];
+        value_cache[row + 1] = vt[2 * f + 1];
+    }
+    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
+    attend_kv_head<G, DL>(qrot, key_cache + base, value_cache + base, o, d.pos, head_dim, kv_dim, smem);
+}
+
 __global__ void add_kernel(float *x, const float *y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += y[i];
@@ -723,6 +766,10 @@ struct BatchedAttention {
     static const void *fn() { return reinterpret_cast<const void *>(attention_batched_kernel<G, DL>); }
 };
 template <int G, int DL>
+struct RopeBatchedAttention {
+    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_batched_kernel<G, DL>); }
+};
+template <int G, int DL>
 struct ChunkedAttention {
     static const void *fn() { return reinterpret_cast<const void *>(rope_attention_chunked_kernel<G, DL>); }
 };
@@ -756,6 +803,22 @@ int launch_rope_attention_chunked(const float *q, const float *k, const float *v
     if (hipLaunchKernel(fn, dim3(kv_heads, nchunks), dim3(kChunkThreads), args, 0, stream) != hipSuccess)
         return launch_status("chunked attention launch");
     return launch_status("chunked attention launch");
+}
+
+int launch_rope_attention_batched(const float *q, const float *k, const float *v, const float *cosine,
+                                  const float *sine, float *key_cache, float *value_cache, float *out, int layer,
+                                  int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos,
+                                  int heads, int kv_heads, int head_dim, hipStream_t stream) {
+    const int G = heads / kv_heads;
+    const void *fn = attention_instance<RopeBatchedAttention>(G, head_dim);
+    if (!fn) return fail(QK_ERR_LIMIT, "batched rope + attention: unsupported head layout");
+    if (n_tokens > 65535) return fail(QK_ERR_LIMIT, "batched rope + attention: too many tokens in one launch");
+    const size_t lds = attention_lds_bytes(max_pos, head_dim, G) + static_cast<size_t>(G) * head_dim * sizeof(float);
+    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &layer, &cache_rows, &desc, &max_pos,
+                    &kv_heads, &head_dim};
+    if (hipLaunchKernel(fn, dim3(kv_heads, n_tokens), dim3(kAttnThreads), args, lds, stream) != hipSuccess)
+        return launch_status("batched rope + attention launch");
+    return launch_status("batched rope + attention launch");
 }
 
 bool chunked_attention_supported(int kv_heads, int group, int head_dim) {
