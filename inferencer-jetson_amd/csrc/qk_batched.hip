@@ -58,7 +58,7 @@ constexpr int kTokTile = 32;            // tokens per MFMA tile (the A rows)
 constexpr int kRowTiles = 2;            // 32-row tiles per wave
 constexpr int kGroupRows = 128 * kRowTiles;   // weight rows per workgroup (4 waves)
 constexpr int kPartialFloats = 4 * kRowTiles * 16 * 64;   // one workgroup's partial sums per token tile
-constexpr int kMaxSplit = 8;            // workgroups splitting one row group's blocks
+constexpr int kMaxSplit = 16;           // workgroups splitting one row group's blocks
 
 // LDS tile of one block's activations for one 32-token tile, in MFMA A
 // operand order:
@@ -672,13 +672,13 @@ int token_tiles_per_group(int tiles) { return tiles >= 2 ? 2 : 1; }
 
 // Workgroups sharing a row group's blocks: enough that about two workgroups
 // per CU (one with two token tiles, whose LDS fills a CU) are in flight, at
-// most kMaxSplit, at least two blocks each.
+// most kMaxSplit, at least one block each.
 void split_plan(int64_t groups, int nb, int tiles, int &splits, int &per_split) {
     const int tt = token_tiles_per_group(tiles);
     const int64_t target = static_cast<int64_t>(device_info().cus) * (tt == 1 ? 2 : 1);
     const int64_t have = std::max<int64_t>(1, groups * ((tiles + tt - 1) / tt));
     const int64_t want = (target + have - 1) / have;
-    int s = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want, 1), std::min(kMaxSplit, std::max(1, nb / 2))));
+    int s = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want, 1), std::min(kMaxSplit, nb)));
     per_split = (nb + s - 1) / s;
     splits = (nb + per_split - 1) / per_split;
 }
