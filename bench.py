@@ -365,10 +365,12 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
-    ap.add_argument("--only", choices=["gemv", "copy", "stream"], default="gemv",
+    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "decode", "batch_decode"],
+                    default="gemv",
                     help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
                          "(a plain 256 MiB copy calibrates FETCH_SIZE / WRITE_SIZE; a streaming read gives "
-                         "the practical read ceiling)")
+                         "the practical read ceiling); ffn / mixed / decode / batch_decode: run one secondary "
+                         "workload alone (for profiling) and print its result")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -381,8 +383,16 @@ def main() -> int:
     import inferencer_jetson_amd.workloads as wl
 
     torch.cuda.set_device(0)
-    if args.only != "gemv":
+    if args.only in ("copy", "stream"):
         return reference_kernels(torch, args)
+    if args.only != "gemv":
+        stream = torch.cuda.current_stream()
+        run = {"ffn": lambda: bench_ffn_3b_ragged(torch, qk, wl, stream),
+               "mixed": lambda: bench_mixed_1b_256(torch, qk, wl, stream),
+               "decode": lambda: bench_decode_1b(torch, qk, wl),
+               "batch_decode": lambda: bench_batch_decode_1b(torch, qk, wl)}[args.only]
+        print(json.dumps({args.only: run()}), flush=True)
+        return 0
     stream = torch.cuda.current_stream()
     cols, rows = 2048, 128256
     log(f"[bench] building {args.copies} LM-head copies ({rows}x{cols} Q6_K)")
