@@ -161,8 +161,9 @@ int qk_rope_kv_write(float *q, const float *k, const float *v, const float *cosi
                      const float *sine, float *key_cache, float *value_cache, int layer, int pos,
                      int context, int heads, int kv_heads, int head_dim, qk_stream stream);
 
-/* GQA attention of one query token over cache positions 0..pos of a layer.
-   Replaces attention_cuda (inferencer.cu:981-1009), generalised head_dim. */
+/* GQA attention of one query token over cache positions 0..pos of a layer
+   (caches and out 16-byte aligned).  Replaces attention_cuda
+   (inferencer.cu:981-1009), generalised head_dim. */
 int qk_attention_f32(const float *q, const float *key_cache, const float *value_cache,
                      float *out, int layer, int pos, int context, int heads, int kv_heads,
                      int head_dim, qk_stream stream);
@@ -205,13 +206,30 @@ int qk_rope_kv_write_batched(float *q, const float *k, const float *v, const flo
                              int head_dim, qk_stream stream);
 
 /* GQA attention of every token of a ragged batch over rows kv_row ..
-   kv_row + pos of its sequence; out is [n_tokens][heads*head_dim].  max_pos
-   bounds every pos (it sizes the score buffer); a token beyond it or beyond
-   the cache gets NaN outputs.  Replaces attention_batch_cuda
+   kv_row + pos of its sequence; out is [n_tokens][heads*head_dim] (16-byte
+   aligned, like the caches).  max_pos bounds every pos; a token beyond it or
+   beyond the cache gets NaN outputs.  Replaces attention_batch_cuda
    (inferencer.cu:1011-1041). */
 int qk_attention_batched_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,
                              int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos, int heads,
                              int kv_heads, int head_dim, qk_stream stream);
+
+/* qk_attention_batched_f32 with every token's rows spread over several
+   workgroups: rows 0..pos of a token are cut into splits of split_rows rows
+   (0: chosen from the batch), each split leaves a partial (max, sum of exp,
+   output) in workspace and a second kernel merges them in split order.  A
+   token whose rows fit one split is written directly.  workspace holds
+   qk_attention_split_workspace_bytes(n_tokens, ..., max_pos) bytes for the
+   chosen split; with less (or none) the call takes fewer, longer splits.
+   Calls sharing a workspace must not overlap.  No reference counterpart:
+   attention_cuda (inferencer.cu:981-1009) runs one block per head over the
+   whole context, which one CU reads at a few tens of GB/s. */
+size_t qk_attention_split_workspace_bytes(int n_tokens, int heads, int kv_heads, int head_dim, int max_pos,
+                                          int split_rows);
+int qk_attention_split_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,
+                           int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos, int heads,
+                           int kv_heads, int head_dim, int split_rows, void *workspace, size_t workspace_size,
+                           qk_stream stream);
 
 /* Greedy token of each of `rows` rows of n values (row r at v + r*ldv), the
    lowest index among equal maxima; out is a device array of rows ints.

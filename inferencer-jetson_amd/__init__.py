@@ -103,6 +103,9 @@ SIGNATURES = {
     "qk_rope_kv_write_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i,
                                       _vp]),
     "qk_attention_batched_f32": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i, _vp]),
+    "qk_attention_split_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i, _i, _i]),
+    "qk_attention_split_f32": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i, _i, _vp,
+                                    ctypes.c_size_t, _vp]),
     "qk_argmax_rows_workspace_bytes": (ctypes.c_size_t, [_i, _i]),
     "qk_argmax_rows_f32": (_i, [_vp, _i, ctypes.c_int64, _i, _vp, _vp, _vp]),
     "qk_llama_batch_create": (_i, [ctypes.POINTER(qk_llama_config), ctypes.POINTER(qk_llama_weights), _i,

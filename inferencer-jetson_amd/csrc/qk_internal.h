@@ -42,10 +42,6 @@ int block_bytes(int type);
 // Validates a Q4_K / Q6_K weight operand shape; returns QK_OK or a status.
 int check_weights(const char *where, int type, const void *w, int cols, int rows);
 
-// Dynamic LDS of the attention kernel for positions 0..pos and `group`
-// query heads per KV head.
-__host__ __device__ size_t attention_lds_bytes(int pos, int head_dim, int group);
-
 // Decode-step fusions of the FP32 GEMV (driver-internal, not in the C ABI):
 // the activations are staged as RMSNorm(x) * norm_w (rmsnorm_cuda) or as
 // x / (1 + exp(-x)) * up (silu_cuda), and the epilogue adds W x into y (the
@@ -68,35 +64,39 @@ int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx
 // qk_gemv_multi_batched_f32.
 int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                          const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream);
-// Whether the attention kernels serve `group` query heads per KV head and
+// Whether the attention kernel serves `group` query heads per KV head and
 // head_dim (group in {1, 2, 3, 4, 6, 8}; head_dim a multiple of 4 dividing 256).
 bool attention_supported(int group, int head_dim);
-// RoPE of q and k at pos, the KV-cache write, then GQA attention of one
-// token (rope_cache_cuda + attention_cuda, inferencer.cu:930-1009) in one
-// launch; q, k, v are the unrotated projections.
-int launch_rope_attention(const float *q, const float *k, const float *v, const float *cosine, const float *sine,
-                          float *key_cache, float *value_cache, float *out, int layer, int pos, int context,
-                          int heads, int kv_heads, int head_dim, hipStream_t stream);
 
-// The same with the positions split into chunks of 64 over several
-// workgroups per KV head (the decode driver's form).  workspace holds
-// attention_workspace_bytes(...) bytes, zeroed once before the first call
-// (its per-head tickets return to zero at the end of every call); calls that
-// share a workspace must not overlap.
-size_t attention_workspace_bytes(int kv_heads, int group, int head_dim, int context);
-// head_dim 64, 128 or 256 and at most 64 KV heads.
-bool chunked_attention_supported(int kv_heads, int group, int head_dim);
-int launch_rope_attention_chunked(const float *q, const float *k, const float *v, const float *cosine,
-                                  const float *sine, float *key_cache, float *value_cache, float *out, void *workspace,
-                                  int layer, int pos, int context, int heads, int kv_heads, int head_dim,
-                                  hipStream_t stream);
-
-// Ragged-batch form of launch_rope_attention: token t at desc[t] (device),
-// q / k / v token-major; max_pos bounds every position.
-int launch_rope_attention_batched(const float *q, const float *k, const float *v, const float *cosine,
-                                  const float *sine, float *key_cache, float *value_cache, float *out, int layer,
-                                  int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos,
-                                  int heads, int kv_heads, int head_dim, hipStream_t stream);
+// Split-row attention (GQA, one or many tokens): the rows 0..pos of every
+// (token, KV head) are cut into splits of split_rows rows, one 256-thread
+// workgroup each, so a token's cache read spreads over many CUs.  With k set
+// it also rotates q and k at pos and writes the key / value row (the
+// workgroup holding row pos writes it and takes it from LDS, so no other
+// workgroup reads it); with k NULL q is already rotated and the caches hold
+// row pos.  Every token of one call must own its cache rows.
+struct SplitAttention {
+    const float *q;                  // [n_tokens][heads * head_dim]
+    const float *k, *v;              // [n_tokens][kv_heads * head_dim] or NULL
+    const float *cosine, *sine;      // [context][head_dim / 2] (with k)
+    float *key_cache, *value_cache;  // [layers][cache_rows][kv_heads * head_dim]
+    float *out;                      // [n_tokens][heads * head_dim]
+    const qk_batch_token *desc;      // device, n_tokens entries; NULL: one token at pos, kv_row 0
+    int64_t cache_rows;
+    int64_t rows_hint;               // sum over tokens of pos + 1 (0: n_tokens * (max_pos + 1))
+    int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
+};
+// Rows per split for head_rows (token, KV head) rows in all, the longest
+// token max_rows rows (the split policy).
+int split_attention_rows(int64_t head_rows, int max_rows);
+// Workspace of launch_split_attention (the split partials) for n_tokens
+// tokens of at most max_rows rows (at most 64 MiB; 0 when one split always
+// serves).  A call with less workspace takes fewer, longer splits, one with
+// none a single split.  Calls sharing a workspace must not overlap.
+size_t split_attention_workspace_bytes(int n_tokens, int heads, int kv_heads, int head_dim, int max_rows);
+// split_rows <= 0 takes the policy's value.  Arguments validated by the caller.
+int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
+                           hipStream_t stream);
 
 // Per-device properties, cached once per device (thread-safe).
 struct DeviceInfo {

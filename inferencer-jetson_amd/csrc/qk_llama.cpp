@@ -29,7 +29,8 @@ struct qk_llama {
     float *attn = nullptr, *tmp = nullptr, *gate = nullptr, *up = nullptr, *logits = nullptr;
     float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
     void *argmax_ws = nullptr;
-    void *attn_ws = nullptr;   // chunked attention partials and tickets (zeroed once)
+    void *attn_ws = nullptr;   // split-attention partials
+    size_t attn_ws_bytes = 0;
     int32_t *d_next = nullptr, *d_token = nullptr;
     int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
     int last_next = -1;
@@ -86,9 +87,8 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         if (!L.q || !L.k || !L.v || !L.o || !L.gate || !L.up || !L.down || !L.attn_norm || !L.ffn_norm)
             return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_create: layer " + std::to_string(l) + " is incomplete");
     }
-    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim) ||
-        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) > 150 * 1024)
-        return qk::fail(QK_ERR_LIMIT, "qk_llama_create: context beyond the attention kernel's LDS budget");
+    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim))
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_create: head layout outside the attention kernel");
 
     qk_llama *m = new qk_llama();
     m->cfg = c;
@@ -116,19 +116,11 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         release(m);
         return st;
     }
-    const int group = c.heads / c.kv_heads;
-    const size_t attn_ws = qk::chunked_attention_supported(c.kv_heads, group, head_dim)
-                               ? qk::attention_workspace_bytes(c.kv_heads, group, head_dim, c.context)
-                               : 0;
-    if (attn_ws) {
-        if ((st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), attn_ws, "attention workspace"))) {
-            release(m);
-            return st;
-        }
-        if (hipMemset(m->attn_ws, 0, attn_ws) != hipSuccess) {
-            release(m);
-            return qk::fail(QK_ERR_DEVICE, "qk_llama_create: cannot clear the attention workspace");
-        }
+    m->attn_ws_bytes = qk::split_attention_workspace_bytes(1, c.heads, c.kv_heads, head_dim, c.context);
+    if (m->attn_ws_bytes &&
+        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) {
+        release(m);
+        return st;
     }
     if (hipHostMalloc(reinterpret_cast<void **>(&m->h_token), 2 * sizeof(int32_t), hipHostMallocDefault) !=
         hipSuccess) {
@@ -200,19 +192,30 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     attn_in.norm_eps = ffn_in.norm_eps = c.eps;
     residual.accumulate = down_in.accumulate = 1;
     down_in.up = m->up;
+    qk::SplitAttention attn{};
+    attn.q = m->q;
+    attn.k = m->k;
+    attn.v = m->v;
+    attn.cosine = m->cosine;
+    attn.sine = m->sine;
+    attn.key_cache = m->key_cache;
+    attn.value_cache = m->value_cache;
+    attn.out = m->attn;
+    attn.cache_rows = c.context;
+    attn.rows_hint = pos + 1;
+    attn.pos = attn.max_pos = pos;
+    attn.n_tokens = 1;
+    attn.heads = c.heads;
+    attn.kv_heads = c.kv_heads;
+    attn.head_dim = hd;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
         ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
         if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, dim, 1, nullptr, attn_in, s))) return st;
-        if (m->attn_ws)
-            st = qk::launch_rope_attention_chunked(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache,
-                                                   m->attn, m->attn_ws, l, pos, c.context, c.heads, c.kv_heads, hd, s);
-        else
-            st = qk::launch_rope_attention(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, m->attn,
-                                           l, pos, c.context, c.heads, c.kv_heads, hd, s);
-        if (st) return st;
+        attn.layer = l;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, dim, 1, nullptr, residual, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
@@ -254,8 +257,8 @@ struct qk_llama_batch {
     float *x = nullptr, *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *tmp = nullptr;
     float *gate = nullptr, *up = nullptr, *logits = nullptr;
     float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
-    void *gemm_ws = nullptr, *argmax_ws = nullptr;
-    size_t gemm_ws_bytes = 0;
+    void *gemm_ws = nullptr, *argmax_ws = nullptr, *attn_ws = nullptr;
+    size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
     int32_t *d_tokens = nullptr, *d_next = nullptr;
     qk_batch_token *d_desc = nullptr;
     uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, results
@@ -265,7 +268,8 @@ namespace {
 
 void release_batch(qk_llama_batch *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
-                    m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->d_tokens, m->d_next, m->d_desc};
+                    m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->attn_ws, m->d_tokens, m->d_next,
+                    m->d_desc};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
@@ -291,9 +295,8 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     if (max_tokens < 1 || max_tokens > 4096 || cache_rows < 1)
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_create: max_tokens must be 1..4096 and cache_rows >= 1");
     const int head_dim = c.dim / c.heads;
-    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim) ||
-        qk::attention_lds_bytes(c.context - 1, head_dim, c.heads / c.kv_heads) + 4 * c.dim / c.kv_heads > 150 * 1024)
-        return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: head layout or context beyond the attention kernel");
+    if (!qk::attention_supported(c.heads / c.kv_heads, head_dim))
+        return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: head layout outside the attention kernel");
     if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
         return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: embedding and output must be Q4_K or Q6_K");
     if (!qk::gemv_fusable(c.dim) || !qk::gemv_fusable(c.hidden))
@@ -330,6 +333,7 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
                              {c.dim, c.vocab}};
     for (const auto &sh : shapes) ws = std::max(ws, qk_gemv_batched_workspace_bytes(sh[0], sh[1], max_tokens));
     m->gemm_ws_bytes = ws;
+    m->attn_ws_bytes = qk::split_attention_workspace_bytes(max_tokens, c.heads, c.kv_heads, head_dim, c.context);
     int st = QK_OK;
     if ((st = dev_alloc(&m->x, T * c.dim, "residual")) || (st = dev_alloc(&m->xn, T * c.dim, "normalized state")) ||
         (st = dev_alloc(&m->q, T * c.dim, "query")) || (st = dev_alloc(&m->k, T * kv, "key")) ||
@@ -341,6 +345,8 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
         (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
         (ws && (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->gemm_ws), ws, "matrix workspace"))) ||
+        (m->attn_ws_bytes &&
+         (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) ||
         (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
                         "argmax workspace")) ||
         (st = dev_alloc(&m->d_tokens, T, "input tokens")) || (st = dev_alloc(&m->d_next, T, "next tokens")) ||
@@ -401,6 +407,7 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
     if (n_tokens < 1 || n_tokens > m->max_tokens)
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token count outside 1..max_tokens");
     int max_pos = 0;
+    int64_t rows = 0;
     for (int t = 0; t < n_tokens; ++t) {
         const qk_batch_token &d = desc[t];
         if (tokens[t] < 0 || tokens[t] >= c.vocab || d.pos < 0 || d.pos >= c.context || d.kv_row < 0 ||
@@ -408,6 +415,7 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
             return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token " + std::to_string(t) +
                                                     " outside the vocabulary, the context or the cache");
         max_pos = std::max(max_pos, d.pos);
+        rows += d.pos + 1;
     }
     hipStream_t s = m->stream;
     const int T = n_tokens, dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
@@ -432,16 +440,31 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
     attn_in.norm_eps = ffn_in.norm_eps = c.eps;
     residual.accumulate = down_in.accumulate = 1;
     down_in.up = m->up;
+    qk::SplitAttention attn{};
+    attn.q = m->q;
+    attn.k = m->k;
+    attn.v = m->v;
+    attn.cosine = m->cosine;
+    attn.sine = m->sine;
+    attn.key_cache = m->key_cache;
+    attn.value_cache = m->value_cache;
+    attn.out = m->attn;
+    attn.desc = m->d_desc;
+    attn.cache_rows = m->cache_rows;
+    attn.rows_hint = rows;
+    attn.max_pos = max_pos;
+    attn.n_tokens = T;
+    attn.heads = c.heads;
+    attn.kv_heads = c.kv_heads;
+    attn.head_dim = hd;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
         ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
         if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, attn_in, ws, wsb, s))) return st;
-        if ((st = qk::launch_rope_attention_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache,
-                                                    m->attn, l, m->cache_rows, m->d_desc, T, max_pos, c.heads,
-                                                    c.kv_heads, hd, s)))
-            return st;
+        attn.layer = l;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, residual, ws, wsb, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};

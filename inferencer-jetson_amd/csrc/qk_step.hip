@@ -7,15 +7,10 @@
 // head_dim, and written for wave64.
 #include "qk_internal.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace qk {
-
-// Query rows, scores of positions 0..pos, the 8 waves' partial outputs and
-// their reduction slots, for `group` query heads.
-__host__ __device__ size_t attention_lds_bytes(int pos, int head_dim, int group) {
-    return static_cast<size_t>(group) * (head_dim + (pos + 1) + 8 * head_dim + 8) * sizeof(float);
-}
 
 namespace {
 
@@ -124,46 +119,6 @@ __global__ void rope_kv_kernel(float *q, const float *k, const float *v, const f
 //      the 8 partial vectors per head are added in wave order and divided by
 //      the sum (deterministic).
 // Each phase keeps several steps of loads in flight before it consumes them.
-constexpr int kAttnThreads = 512;
-constexpr int kAttnWaves = kAttnThreads / 64;
-static_assert(kAttnWaves == 8, "attention_lds_bytes sizes 8 waves");
-
-struct AttnLds {
-    float *qs;      // [G][head_dim]
-    float *score;   // [G][pos + 1]
-    float *part;    // [waves][G][head_dim]
-    float *red;     // [waves][G]
-};
-
-__device__ __forceinline__ AttnLds attn_lds(float *smem, int G, int head_dim, int pos) {
-    AttnLds l;
-    l.qs = smem;
-    l.score = l.qs + G * head_dim;
-    l.part = l.score + G * (pos + 1);
-    l.red = l.part + kAttnWaves * G * head_dim;
-    return l;
-}
-
-// Block-wide reduction of G per-thread values (max or sum); every thread
-// receives the G results in v.
-template <bool MAX, int G>
-__device__ __forceinline__ void attn_block_reduce(float *v, float *red) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float r = MAX ? wave_max(v[g]) : wave_sum(v[g]);
-        if (lane == 0) red[wave * G + g] = r;
-    }
-    __syncthreads();
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float r = red[g];
-        for (int w = 1; w < kAttnWaves; ++w) r = MAX ? fmaxf(r, red[w * G + g]) : r + red[w * G + g];
-        v[g] = r;
-    }
-    __syncthreads();
-}
-
 __device__ __forceinline__ float4 ld_row4(__amdgpu_buffer_rsrc_t r, int lane_off, int row_off) {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, lane_off, row_off, 0));
 }
@@ -173,376 +128,6 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b, float ac
     acc = fmaf(a.y, b.y, acc);
     acc = fmaf(a.z, b.z, acc);
     return fmaf(a.w, b.w, acc);
-}
-
-// q: the token's query rows of the G heads of KV head kvh (already rotated);
-// kc / vc: the layer's caches offset to this KV head's first row; out: the G
-// output rows.  G query heads per KV head and DL = ceil(head_dim / 64) are
-// compile-time, so every per-head array stays in registers.
-//
-// Memory access: 16 lanes share a cache row (lane sub reads dimensions
-// 64c + 4*sub .. +3 of chunk c as one float4), so one load instruction of a
-// wave covers four whole rows.  Rows are read through buffer resources that
-// span exactly the rows a phase may read: a row past the range reads as zero.
-template <int G, int DL>
-__device__ __forceinline__ void attend_kv_head(const float *q, const float *kc, const float *vc, float *out, int pos,
-                                               int head_dim, int kv_dim, float *smem) {
-    const AttnLds L = attn_lds(smem, G, head_dim, pos);
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = lane & 15, rq = lane >> 4;
-    const bool act = 4 * sub < head_dim;         // head_dim < 64 leaves lanes idle
-    const int n = pos + 1;
-    const int row_bytes = kv_dim * 4;
-    const int lane_off = (rq * kv_dim + 4 * min(sub, max(head_dim / 4 - 1, 0))) * 4;
-    constexpr int U = (16 / DL) / (G > 4 ? 2 : 1);   // 4-row steps in flight per wave
-    const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
-    for (int i = tid; i < G * head_dim; i += kAttnThreads) L.qs[i] = q[i];
-    __syncthreads();
-    float4 qv[G][DL];
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        #pragma unroll
-        for (int c = 0; c < DL; ++c)
-            qv[g][c] = act ? *reinterpret_cast<const float4 *>(L.qs + g * head_dim + 64 * c + 4 * sub)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-
-    // 1. Scores.  Step u of wave w covers rows it0 + (u*waves + w)*4 + rq.
-    const __amdgpu_buffer_rsrc_t krs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kc), 0, n * row_bytes, 0x00020000);
-    float m[G];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) m[g] = -INFINITY;
-    for (int it0 = 0; it0 < n; it0 += kAttnWaves * 4 * U) {
-        float4 k4[U][DL];
-        #pragma unroll
-        for (int u = 0; u < U; ++u)
-            #pragma unroll
-            for (int c = 0; c < DL; ++c)
-                k4[u][c] = ld_row4(krs, lane_off + 256 * c, (it0 + (u * kAttnWaves + wave) * 4) * row_bytes);
-        #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = it0 + (u * kAttnWaves + wave) * 4 + rq;
-            #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float a = 0.f;
-                #pragma unroll
-                for (int c = 0; c < DL; ++c) a = dot4(qv[g][c], k4[u][c], a);
-                const float sc = group_sum<16>(a) * inv;
-                if (t < n) {
-                    if (sub == 0) L.score[g * n + t] = sc;
-                    m[g] = fmaxf(m[g], sc);
-                }
-            }
-        }
-    }
-    attn_block_reduce<true, G>(m, L.red);   // its barriers also publish score[]
-
-    // 2. exp and the per-head sums.
-    float den[G];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) den[g] = 0.f;
-    for (int t = tid; t < n; t += kAttnThreads)
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float e = expf(L.score[g * n + t] - m[g]);
-            L.score[g * n + t] = e;
-            den[g] += e;
-        }
-    attn_block_reduce<false, G>(den, L.red);
-
-    // 3. Values: wave w owns rows t0 .. t1-1, four per step (row t0 + 4s + rq).
-    const int per = (n + kAttnWaves - 1) / kAttnWaves;
-    const int t0 = min(n, wave * per), t1 = min(n, t0 + per);
-    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(vc + static_cast<int64_t>(t0) * kv_dim), 0, (t1 - t0) * row_bytes, 0x00020000);
-    float4 acc[G][DL];
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        #pragma unroll
-        for (int c = 0; c < DL; ++c) acc[g][c] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = 0; s0 < t1 - t0; s0 += 4 * U) {
-        float4 v4[U][DL];
-        #pragma unroll
-        for (int u = 0; u < U; ++u)
-            #pragma unroll
-            for (int c = 0; c < DL; ++c) v4[u][c] = ld_row4(vrs, lane_off + 256 * c, (s0 + 4 * u) * row_bytes);
-        #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + s0 + 4 * u + rq;
-            #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float pr = t < t1 ? L.score[g * n + t] : 0.f;
-                #pragma unroll
-                for (int c = 0; c < DL; ++c) {
-                    acc[g][c].x = fmaf(pr, v4[u][c].x, acc[g][c].x);
-                    acc[g][c].y = fmaf(pr, v4[u][c].y, acc[g][c].y);
-                    acc[g][c].z = fmaf(pr, v4[u][c].z, acc[g][c].z);
-                    acc[g][c].w = fmaf(pr, v4[u][c].w, acc[g][c].w);
-                }
-            }
-        }
-    }
-    // The four row groups of the wave meet in lanes 0..15.
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        #pragma unroll
-        for (int c = 0; c < DL; ++c) {
-            float4 &a = acc[g][c];
-            a.x += __shfl_xor(a.x, 16);
-            a.y += __shfl_xor(a.y, 16);
-            a.z += __shfl_xor(a.z, 16);
-            a.w += __shfl_xor(a.w, 16);
-            a.x += __shfl_xor(a.x, 32);
-            a.y += __shfl_xor(a.y, 32);
-            a.z += __shfl_xor(a.z, 32);
-            a.w += __shfl_xor(a.w, 32);
-            if (rq == 0 && act) *reinterpret_cast<float4 *>(L.part + (wave * G + g) * head_dim + 64 * c + 4 * sub) = a;
-        }
-    __syncthreads();
-    for (int i = tid; i < G * head_dim; i += kAttnThreads) {
-        const int g = i / head_dim;
-        float s = 0.f;
-        for (int w = 0; w < kAttnWaves; ++w) s += L.part[w * G * head_dim + i];
-        out[i] = s / den[g];
-    }
-}
-
-template <int G, int DL>
-__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float *q, const float *key_cache,
-                                                                 const float *value_cache, float *out, int layer,
-                                                                 int pos, int context, int kv_heads, int head_dim) {
-    extern __shared__ float smem[];
-    const int kvh = blockIdx.x;
-    const int kv_dim = kv_heads * head_dim;
-    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    attend_kv_head<G, DL>(q + kvh * G * head_dim, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos,
-                          head_dim, kv_dim, smem);
-}
-
-// Decode-step form: RoPE of the G query rows and of key head kvh at pos,
-// the key / value write into the caches at pos (rope_cache_cuda,
-// inferencer.cu:930-951), then attend_kv_head.  The rotated query rows live
-// in LDS after the attention's own buffers.  The cache row of pos is written
-// by this workgroup only (heads occupy disjoint 256-byte runs of a row) and
-// read back after a barrier.
-template <int G, int DL>
-__global__ __launch_bounds__(kAttnThreads) void rope_attention_kernel(
-    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
-    float *value_cache, float *out, int layer, int pos, int context, int kv_heads, int head_dim) {
-    extern __shared__ float smem[];
-    const int kvh = blockIdx.x, tid = threadIdx.x;
-    const int kv_dim = kv_heads * head_dim, half = head_dim / 2;
-    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    float *qrot = smem + attention_lds_bytes(pos, head_dim, G) / sizeof(float);
-    const float *cs = cosine + static_cast<int64_t>(pos) * half;
-    const float *sn = sine + static_cast<int64_t>(pos) * half;
-    for (int i = tid; i < G * half; i += kAttnThreads) {
-        const int f = i % half;
-        const int o = kvh * G * head_dim + 2 * i;   // pair i of this KV head's query rows
-        const float c = cs[f], si = sn[f];
-        const float q0 = q[o], q1 = q[o + 1];
-        qrot[2 * i] = q0 * c - q1 * si;
-        qrot[2 * i + 1] = q0 * si + q1 * c;
-    }
-    for (int f = tid; f < half; f += kAttnThreads) {
-        const float c = cs[f], si = sn[f];
-        const int o = kvh * head_dim + 2 * f;
-        const int64_t row = base + static_cast<int64_t>(pos) * kv_dim + 2 * f;
-        const float k0 = k[o], k1 = k[o + 1];
-        key_cache[row] = k0 * c - k1 * si;
-        key_cache[row + 1] = k0 * si + k1 * c;
-        value_cache[row] = v[o];
-        value_cache[row + 1] = v[o + 1];
-    }
-    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
-    attend_kv_head<G, DL>(qrot, key_cache + base, value_cache + base, out + kvh * G * head_dim, pos, head_dim, kv_dim,
-                          smem);
-}
-
-// ------------------------------------------------ chunked decode attention --
-//
-// The decode driver's attention: RoPE + KV write + GQA attention with the
-// positions split into chunks of kChunkPos, one 256-thread workgroup per
-// (KV head, chunk), so a step at a few hundred positions spreads over tens
-// of CUs instead of one per KV head.  Each workgroup rotates the G query
-// rows itself; the workgroup of the last chunk (the one holding pos) also
-// rotates the new key and writes key / value row pos of the caches, which
-// only it reads.  A chunk leaves (max, sum of exp, unnormalised output) per
-// head in the workspace; the last workgroup of a KV head to finish (an
-// atomic ticket per head, reset by that workgroup) merges the chunks in
-// chunk order -- the online-softmax merge of attention_cuda's running max
-// (inferencer.cu:991-1007) done across chunks.
-constexpr int kChunkPos = 64;
-constexpr int kChunkThreads = 256;
-
-template <int G, int DL>
-__global__ __launch_bounds__(kChunkThreads) void rope_attention_chunked_kernel(
-    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
-    float *value_cache, float *out, float *partials, int *tickets, int layer, int pos, int context, int kv_heads,
-    int head_dim) {
-    // head_dim == 64 * DL (checked on the host).
-    __shared__ float qs[G * 64 * DL];
-    __shared__ float score[G][kChunkPos];
-    __shared__ float part[4][G * 64 * DL];
-    __shared__ float red[4][G];
-    __shared__ int last;
-    const int kvh = blockIdx.x, chunk = blockIdx.y, nchunks = gridDim.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int kv_dim = kv_heads * head_dim, half = head_dim / 2;
-    const int n = pos + 1;
-    const int c0 = chunk * kChunkPos, c1 = min(n, c0 + kChunkPos);
-    const int64_t base = static_cast<int64_t>(layer) * context * kv_dim + kvh * head_dim;
-    const float *kc = key_cache + base, *vc = value_cache + base;
-    const float *cs = cosine + static_cast<int64_t>(pos) * half;
-    const float *sn = sine + static_cast<int64_t>(pos) * half;
-
-    for (int i = tid; i < G * half; i += kChunkThreads) {
-        const int f = i % half;
-        const int o = kvh * G * head_dim + 2 * i;
-        const float c = cs[f], si = sn[f];
-        const float q0 = q[o], q1 = q[o + 1];
-        qs[2 * i] = q0 * c - q1 * si;
-        qs[2 * i + 1] = q0 * si + q1 * c;
-    }
-    if (chunk == nchunks - 1) {
-        for (int f = tid; f < half; f += kChunkThreads) {
-            const float c = cs[f], si = sn[f];
-            const int o = kvh * head_dim + 2 * f;
-            const int64_t row = base + static_cast<int64_t>(pos) * kv_dim + 2 * f;
-            const float k0 = k[o], k1 = k[o + 1];
-            key_cache[row] = k0 * c - k1 * si;
-            key_cache[row + 1] = k0 * si + k1 * c;
-            value_cache[row] = v[o];
-            value_cache[row + 1] = v[o + 1];
-        }
-    }
-    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
-
-    // 1. Scores: four lanes per position, each a quarter of head_dim.
-    const float inv = 1.0f / sqrtf(static_cast<float>(head_dim));
-    const int quarter = head_dim / 4;          // 16 * DL columns
-    const int pl = wave * 16 + (lane >> 2);    // position within the chunk
-    const int qd = lane & 3;
-    const int t = c0 + pl;
-    float dot[G];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) dot[g] = 0.f;
-    if (t < c1) {
-        const float4 *kr = reinterpret_cast<const float4 *>(kc + static_cast<int64_t>(t) * kv_dim + qd * quarter);
-        float4 k4[4 * DL];
-        #pragma unroll
-        for (int j = 0; j < 4 * DL; ++j) k4[j] = kr[j];
-        #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            const float *qg = qs + g * head_dim + qd * quarter;
-            float a = 0.f;
-            #pragma unroll
-            for (int j = 0; j < 4 * DL; ++j) {
-                a = fmaf(qg[4 * j], k4[j].x, a);
-                a = fmaf(qg[4 * j + 1], k4[j].y, a);
-                a = fmaf(qg[4 * j + 2], k4[j].z, a);
-                a = fmaf(qg[4 * j + 3], k4[j].w, a);
-            }
-            dot[g] = a;
-        }
-    }
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        dot[g] += __shfl_xor(dot[g], 1);
-        dot[g] += __shfl_xor(dot[g], 2);
-    }
-    float m[G];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        const float sc = dot[g] * inv;
-        if (qd == 0) score[g][pl] = t < c1 ? sc : -INFINITY;
-        m[g] = t < c1 ? sc : -INFINITY;
-        m[g] = wave_max(m[g]);
-        if (lane == 0) red[wave][g] = m[g];
-    }
-    __syncthreads();
-    #pragma unroll
-    for (int g = 0; g < G; ++g) m[g] = fmaxf(fmaxf(red[0][g], red[1][g]), fmaxf(red[2][g], red[3][g]));
-    __syncthreads();
-
-    // 2. exp and the chunk's sum per head.
-    float l[G];
-    #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float e = 0.f;
-        if (tid < kChunkPos) {
-            e = c0 + tid < c1 ? expf(score[g][tid] - m[g]) : 0.f;
-            score[g][tid] = e;
-        }
-        l[g] = wave_sum(e);   // wave 0 holds every position
-    }
-    __syncthreads();
-
-    // 3. Values: wave w takes positions w*16 .. +15 of the chunk, lane = dimension.
-    float acc[G][DL];
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        #pragma unroll
-        for (int j = 0; j < DL; ++j) acc[g][j] = 0.f;
-    {
-        float vv[16][DL];
-        #pragma unroll
-        for (int u = 0; u < 16; ++u)
-            #pragma unroll
-            for (int j = 0; j < DL; ++j) {
-                const int tt = c0 + wave * 16 + u, d = lane + 64 * j;
-                vv[u][j] = (tt < c1 && d < head_dim) ? vc[static_cast<int64_t>(tt) * kv_dim + d] : 0.f;
-            }
-        #pragma unroll
-        for (int g = 0; g < G; ++g)
-            #pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                const float pr = score[g][wave * 16 + u];
-                #pragma unroll
-                for (int j = 0; j < DL; ++j) acc[g][j] = fmaf(pr, vv[u][j], acc[g][j]);
-            }
-    }
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        #pragma unroll
-        for (int j = 0; j < DL; ++j) {
-            const int d = lane + 64 * j;
-            if (d < head_dim) part[wave][g * head_dim + d] = acc[g][j];
-        }
-    __syncthreads();
-
-    // The chunk's partial: [G] max, [G] sum, [G][head_dim] output.
-    const int stride = G * (head_dim + 2);
-    float *mine = partials + (static_cast<size_t>(kvh) * nchunks + chunk) * stride;
-    #pragma unroll
-    for (int g = 0; g < G; ++g)
-        if (tid == g) {
-            mine[g] = m[g];
-            mine[G + g] = l[g];
-        }
-    for (int i = tid; i < G * head_dim; i += kChunkThreads)
-        mine[2 * G + i] = (part[0][i] + part[1][i]) + (part[2][i] + part[3][i]);
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) last = atomicAdd(tickets + kvh, 1) == nchunks - 1;
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const float *all = partials + static_cast<size_t>(kvh) * nchunks * stride;
-    for (int i = tid; i < G * head_dim; i += kChunkThreads) {
-        const int g = i / head_dim;
-        float mx = -INFINITY;
-        for (int c = 0; c < nchunks; ++c) mx = fmaxf(mx, all[c * stride + g]);
-        float num = 0.f, den = 0.f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float w = expf(all[c * stride + g] - mx);
-            den = fmaf(w, all[c * stride + G + g], den);
-            num = fmaf(w, all[c * stride + 2 * G + i], num);
-        }
-        out[kvh * G * head_dim + i] = num / den;
-    }
-    if (tid == 0) atomicExch(tickets + kvh, 0);
 }
 
 // ------------------------------------------------- ragged decode batches --
@@ -588,69 +173,351 @@ __global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v,
     }
 }
 
-template <int G, int DL>
-__global__ __launch_bounds__(kAttnThreads) void attention_batched_kernel(const float *q, const float *key_cache,
-                                                                         const float *value_cache, float *out,
-                                                                         int layer, int64_t cache_rows,
-                                                                         const qk_batch_token *desc, int max_pos,
-                                                                         int kv_heads, int head_dim) {
-    extern __shared__ float smem[];
-    const int kvh = blockIdx.x, t = blockIdx.y;
-    const int kv_dim = kv_heads * head_dim, heads = kv_heads * G;
-    const qk_batch_token d = desc[t];
-    float *o = out + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
-    if (!token_ok(d, cache_rows, max_pos)) {
-        for (int i = threadIdx.x; i < G * head_dim; i += kAttnThreads) o[i] = __builtin_nanf("");
-        return;
-    }
-    const int64_t base = (static_cast<int64_t>(layer) * cache_rows + d.kv_row) * kv_dim + kvh * head_dim;
-    attend_kv_head<G, DL>(q + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim, key_cache + base,
-                          value_cache + base, o, d.pos, head_dim, kv_dim, smem);
+// ------------------------------------------------- split-row attention --
+//
+// One 256-thread workgroup per (KV head, token, split of split_rows rows).
+// A CU on its own reads a few tens of GB/s, so a token's rows are spread
+// over many CUs.  L lanes share a cache row (8, or 16 when G * head_dim >
+// 512 to bound the registers), lane `sub` holding dimensions 4L*j + 4*sub
+// .. +3 for j < NF, so one load instruction of a wave covers 64 / L rows.
+// Every K / V load of the first round is issued before the query rows are
+// read (the cache latency overlaps the RoPE); later rounds are issued while
+// the previous one is consumed.  Lane group rq keeps its own running (max,
+// sum of exp, unnormalised output) over the rows it sees -- the online
+// softmax of attention_cuda (inferencer.cu:991-1007), in base-2 units -- and
+// the groups and the waves meet by the same merge.  A token with one split
+// writes its output directly; otherwise each split leaves a partial and a
+// second kernel merges them in split order.  (A merge by the last workgroup
+// to finish needs a device-scope release per workgroup, an L2 write-back
+// that costs about a microsecond each and serialises per XCD.)
+constexpr int kSplitThreads = 256;
+constexpr int kSplitWaves = kSplitThreads / 64;
+constexpr int kMaxSplits = 64;        // splits per token at most
+constexpr int kMinSplitRows = 64;     // rows per split at least
+constexpr int kSplitTarget = 128;     // workgroups a call aims at
+constexpr size_t kMaxSplitWorkspace = size_t(64) << 20;
+
+struct SplitAttnKernelArgs {
+    SplitAttention a;
+    float *partials;   // [n_tokens * kv_heads][splits][split_header(G) + G * head_dim]
+    int split_rows;
+    int splits;        // most splits of any token (the partials' stride)
+};
+
+// A split partial: max [G], sum of exp [G], padded to 16 bytes, then the
+// unnormalised output rows [G][head_dim].
+__host__ __device__ constexpr int split_header(int G) { return (2 * G + 3) & ~3; }
+
+// Register plan of an instance: NU steps of 64/L rows per wave per round,
+// K / V buffers (8 * NU * NF VGPRs) within what the query and output rows
+// (8 * G * NF) leave of about 200.
+template <int G, int NF>
+constexpr int split_steps() {
+    constexpr int cap = NF >= 8 ? 1 : 8 / NF;
+    constexpr int fit = (200 - 8 * G * NF) / (8 * NF + 4 * G);
+    return fit < 1 ? 1 : fit < cap ? fit : cap;
 }
 
-// Decode-driver form for ragged batches: RoPE of token t's G query rows and
-// of its key head kvh at its own position, the key / value write into row
-// kv_row + pos (written and read back by this workgroup only, ordered by
-// the barrier), then attend_kv_head over the token's own rows.
-template <int G, int DL>
-__global__ __launch_bounds__(kAttnThreads) void rope_attention_batched_kernel(
-    const float *q, const float *k, const float *v, const float *cosine, const float *sine, float *key_cache,
-    float *value_cache, float *out, int layer, int64_t cache_rows, const qk_batch_token *desc, int max_pos,
-    int kv_heads, int head_dim) {
-    extern __shared__ float smem[];
-    const int kvh = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int kv_dim = kv_heads * head_dim, heads = kv_heads * G, half = head_dim / 2;
-    const qk_batch_token d = desc[t];
-    float *o = out + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
-    if (!token_ok(d, cache_rows, max_pos)) {
-        for (int i = tid; i < G * head_dim; i += kAttnThreads) o[i] = __builtin_nanf("");
+__device__ __forceinline__ float4 scale4(const float4 &a, float f) {
+    return make_float4(a.x * f, a.y * f, a.z * f, a.w * f);
+}
+
+__device__ __forceinline__ void fma4(float p, const float4 &v, float4 &acc) {
+    acc.x = fmaf(p, v.x, acc.x);
+    acc.y = fmaf(p, v.y, acc.y);
+    acc.z = fmaf(p, v.z, acc.z);
+    acc.w = fmaf(p, v.w, acc.w);
+}
+
+// Scores (base-2 units, -inf outside the split) of NU rows, one per lane
+// group, against the G query rows.
+template <int G, int NF, int L, int NU>
+__device__ __forceinline__ void score_rows(const float4 (&qv)[G][NF], const float4 (&kk)[NU][NF], const bool (&ok)[NU],
+                                           float scale, float (&s)[NU][G]) {
+    #pragma unroll
+    for (int u = 0; u < NU; ++u)
+        #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float a = 0.f;
+            #pragma unroll
+            for (int j = 0; j < NF; ++j) a = dot4(qv[g][j], kk[u][j], a);
+            const float sc = group_sum<L>(a) * scale;
+            s[u][g] = ok[u] ? sc : -INFINITY;
+        }
+}
+
+// Online-softmax update of a lane group's state with NU scored rows.
+template <int G, int NF, int NU>
+__device__ __forceinline__ void absorb_rows(const float (&s)[NU][G], const float4 (&vv)[NU][NF], float (&m)[G],
+                                            float (&l)[G], float4 (&acc)[G][NF]) {
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mb = s[0][g];
+        #pragma unroll
+        for (int u = 1; u < NU; ++u) mb = fmaxf(mb, s[u][g]);
+        const float mn = fmaxf(m[g], mb);
+        const float ref = mn == -INFINITY ? 0.f : mn;   // no row yet: the state stays zero
+        const float f = __builtin_amdgcn_exp2f(m[g] - ref);
+        l[g] *= f;
+        #pragma unroll
+        for (int j = 0; j < NF; ++j) acc[g][j] = scale4(acc[g][j], f);
+        #pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const float p = __builtin_amdgcn_exp2f(s[u][g] - ref);
+            l[g] += p;
+            #pragma unroll
+            for (int j = 0; j < NF; ++j) fma4(p, vv[u][j], acc[g][j]);
+        }
+        m[g] = mn;
+    }
+}
+
+// Merge of two (max, sum) states: the scale factors of each side.
+__device__ __forceinline__ void merge_scales(float &m, float &l, float mo, float lo, float &f, float &fo) {
+    const float mn = fmaxf(m, mo);
+    const float ref = mn == -INFINITY ? 0.f : mn;
+    f = __builtin_amdgcn_exp2f(m - ref);
+    fo = __builtin_amdgcn_exp2f(mo - ref);
+    l = l * f + lo * fo;
+    m = mn;
+}
+
+template <int G, int NF, int L>
+__global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAttnKernelArgs ka) {
+    constexpr int NU = split_steps<G, NF>();
+    constexpr int R = 64 / L;          // rows per load instruction
+    constexpr int HD = 4 * NF * L;     // dimensions a lane group covers (>= head_dim)
+    constexpr int kRound = NU * kSplitWaves * R;
+    __shared__ float4 qs[G * HD / 4];
+    __shared__ float4 knew[HD / 4], vnew[HD / 4];
+    __shared__ float4 part[kSplitWaves][G * HD / 4];
+    __shared__ float wm[kSplitWaves][G], wl[kSplitWaves][G];
+    const SplitAttention &a = ka.a;
+    const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int sub = lane % L, rq = lane / L;
+    const int hd = a.head_dim, hv = hd / 4, kv_dim = a.kv_heads * hd, half = hd / 2;
+    const qk_batch_token d = a.desc ? a.desc[b] : qk_batch_token{a.pos, 0, 0};
+    float *o = a.out + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
+    if (!token_ok(d, a.cache_rows, a.max_pos)) {
+        if (split == 0)
+            for (int i = tid; i < G * hd; i += kSplitThreads) o[i] = __builtin_nanf("");
         return;
     }
-    const int64_t base = (static_cast<int64_t>(layer) * cache_rows + d.kv_row) * kv_dim + kvh * head_dim;
-    float *qrot = smem + attention_lds_bytes(max_pos, head_dim, G) / sizeof(float);
-    const float *cs = cosine + static_cast<int64_t>(d.pos) * half;
-    const float *sn = sine + static_cast<int64_t>(d.pos) * half;
-    const float *qt = q + static_cast<int64_t>(t) * heads * head_dim + kvh * G * head_dim;
-    for (int i = tid; i < G * half; i += kAttnThreads) {
-        const int f = i % half;
-        const float c = cs[f], si = sn[f];
-        const float q0 = qt[2 * i], q1 = qt[2 * i + 1];
-        qrot[2 * i] = q0 * c - q1 * si;
-        qrot[2 * i + 1] = q0 * si + q1 * c;
+    const int n = d.pos + 1;
+    const int r0 = split * ka.split_rows;
+    if (r0 >= n) return;
+    const int r1 = min(n, r0 + ka.split_rows);
+    const int nsplit = (n + ka.split_rows - 1) / ka.split_rows;
+    const bool fresh = a.k != nullptr && r1 == n;   // this split holds row pos and writes it
+    const int rows = (fresh ? r1 - 1 : r1) - r0;    // rows read from the caches
+    const int64_t head0 = (static_cast<int64_t>(a.layer) * a.cache_rows + d.kv_row) * kv_dim + kvh * hd;
+    const int64_t first = head0 + static_cast<int64_t>(r0) * kv_dim;
+    const int row_bytes = kv_dim * 4;
+    const bool act = sub < hv;   // head_dim < 4L leaves lanes idle
+    const int lane_off = (rq * kv_dim + 4 * min(sub, hv - 1)) * 4;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(a.key_cache + first, 0, rows * row_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs =
+        __builtin_amdgcn_make_buffer_rsrc(a.value_cache + first, 0, rows * row_bytes, 0x00020000);
+
+    // Step u of wave w in the round at rb covers rows rb + (u * waves + w) * R
+    // + rq of the split; rows past `rows` read as zero.
+    float4 kk[NU][NF], vv[NU][NF];
+    #pragma unroll
+    for (int u = 0; u < NU; ++u)
+        #pragma unroll
+        for (int j = 0; j < NF; ++j)
+            kk[u][j] = ld_row4(krs, lane_off + 16 * L * j, (u * kSplitWaves + wave) * R * row_bytes);
+    #pragma unroll
+    for (int u = 0; u < NU; ++u)
+        #pragma unroll
+        for (int j = 0; j < NF; ++j)
+            vv[u][j] = ld_row4(vrs, lane_off + 16 * L * j, (u * kSplitWaves + wave) * R * row_bytes);
+
+    // Query rows (rotated here when k is given) and the fresh key / value row.
+    const float *qt = a.q + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
+    float *qsf = reinterpret_cast<float *>(qs);
+    if (a.k) {
+        const float *cs = a.cosine + static_cast<int64_t>(d.pos) * half;
+        const float *sn = a.sine + static_cast<int64_t>(d.pos) * half;
+        for (int i = tid; i < G * half; i += kSplitThreads) {
+            const int g = i / half, f = i - g * half;
+            const float c = cs[f], si = sn[f];
+            const float q0 = qt[g * hd + 2 * f], q1 = qt[g * hd + 2 * f + 1];
+            qsf[g * HD + 2 * f] = q0 * c - q1 * si;
+            qsf[g * HD + 2 * f + 1] = q0 * si + q1 * c;
+        }
+        if (fresh) {
+            const float *kt = a.k + static_cast<int64_t>(b) * kv_dim + kvh * hd;
+            const float *vt = a.v + static_cast<int64_t>(b) * kv_dim + kvh * hd;
+            float *kn = reinterpret_cast<float *>(knew), *vn = reinterpret_cast<float *>(vnew);
+            const int64_t row = head0 + static_cast<int64_t>(d.pos) * kv_dim;
+            for (int f = tid; f < half; f += kSplitThreads) {
+                const float c = cs[f], si = sn[f];
+                const float k0 = kt[2 * f], k1 = kt[2 * f + 1];
+                const float kr0 = k0 * c - k1 * si, kr1 = k0 * si + k1 * c;
+                const float v0 = vt[2 * f], v1 = vt[2 * f + 1];
+                kn[2 * f] = kr0;
+                kn[2 * f + 1] = kr1;
+                vn[2 * f] = v0;
+                vn[2 * f + 1] = v1;
+                a.key_cache[row + 2 * f] = kr0;
+                a.key_cache[row + 2 * f + 1] = kr1;
+                a.value_cache[row + 2 * f] = v0;
+                a.value_cache[row + 2 * f + 1] = v1;
+            }
+        }
+    } else {
+        for (int i = tid; i < G * hd; i += kSplitThreads) {
+            const int g = i / hd;
+            qsf[g * HD + i - g * hd] = qt[i];
+        }
     }
-    const float *kt = k + static_cast<int64_t>(t) * kv_dim + kvh * head_dim;
-    const float *vt = v + static_cast<int64_t>(t) * kv_dim + kvh * head_dim;
-    for (int f = tid; f < half; f += kAttnThreads) {
-        const float c = cs[f], si = sn[f];
-        const int64_t row = base + static_cast<int64_t>(d.pos) * kv_dim + 2 * f;
-        const float k0 = kt[2 * f], k1 = kt[2 * f + 1];
-        key_cache[row] = k0 * c - k1 * si;
-        key_cache[row + 1] = k0 * si + k1 * c;
-        value_cache[row] = vt[2 * f];
-        value_cache[row + 1] = vt[2 * f + 1];
+    __syncthreads();
+    float4 qv[G][NF];
+    #pragma unroll
+    for (int g = 0; g < G; ++g)
+        #pragma unroll
+        for (int j = 0; j < NF; ++j)
+            qv[g][j] = act ? qs[g * HD / 4 + L * j + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+
+    // Scores in base-2 units: exp(x) = exp2(x * log2(e)).
+    const float scale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));
+    float m[G], l[G];
+    float4 acc[G][NF];
+    #pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -INFINITY;
+        l[g] = 0.f;
+        #pragma unroll
+        for (int j = 0; j < NF; ++j) acc[g][j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    __syncthreads();   // workgroup-scope release / acquire: this workgroup reads the row back
-    attend_kv_head<G, DL>(qrot, key_cache + base, value_cache + base, o, d.pos, head_dim, kv_dim, smem);
+    for (int rb = 0; rb < rows; rb += kRound) {
+        bool ok[NU];
+        #pragma unroll
+        for (int u = 0; u < NU; ++u) ok[u] = rb + (u * kSplitWaves + wave) * R + rq < rows;
+        float s[NU][G];
+        score_rows<G, NF, L, NU>(qv, kk, ok, scale, s);
+        // The next round's keys load while this round's values are consumed.
+        // Unconditional: past the split they read as zero without memory
+        // traffic, and a branch here would make the compiler wait for every
+        // load in flight before the values.
+        #pragma unroll
+        for (int u = 0; u < NU; ++u)
+            #pragma unroll
+            for (int j = 0; j < NF; ++j)
+                kk[u][j] = ld_row4(krs, lane_off + 16 * L * j, (rb + kRound + (u * kSplitWaves + wave) * R) * row_bytes);
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the value work
+        absorb_rows<G, NF, NU>(s, vv, m, l, acc);
+        #pragma unroll
+        for (int u = 0; u < NU; ++u)
+            #pragma unroll
+            for (int j = 0; j < NF; ++j)
+                vv[u][j] = ld_row4(vrs, lane_off + 16 * L * j, (rb + kRound + (u * kSplitWaves + wave) * R) * row_bytes);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (fresh && wave == kSplitWaves - 1) {   // row pos, from LDS, in lane group 0
+        float4 k1[1][NF], v1[1][NF];
+        #pragma unroll
+        for (int j = 0; j < NF; ++j) {
+            k1[0][j] = act ? knew[L * j + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+            v1[0][j] = act ? vnew[L * j + sub] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const bool ok1[1] = {rq == 0};
+        float s1[1][G];
+        score_rows<G, NF, L, 1>(qv, k1, ok1, scale, s1);
+        absorb_rows<G, NF, 1>(s1, v1, m, l, acc);
+    }
+
+    // The wave's lane groups meet in every lane, then the waves in LDS.
+    #pragma unroll
+    for (int off = L; off < 64; off *= 2)
+        #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float f, fo;
+            merge_scales(m[g], l[g], __shfl_xor(m[g], off), __shfl_xor(l[g], off), f, fo);
+            #pragma unroll
+            for (int j = 0; j < NF; ++j) {
+                float4 &x = acc[g][j];
+                x.x = x.x * f + __shfl_xor(x.x, off) * fo;
+                x.y = x.y * f + __shfl_xor(x.y, off) * fo;
+                x.z = x.z * f + __shfl_xor(x.z, off) * fo;
+                x.w = x.w * f + __shfl_xor(x.w, off) * fo;
+            }
+        }
+    if (rq == 0 && act)
+        #pragma unroll
+        for (int g = 0; g < G; ++g)
+            #pragma unroll
+            for (int j = 0; j < NF; ++j) part[wave][g * HD / 4 + L * j + sub] = acc[g][j];
+    if (lane == 0)
+        #pragma unroll
+        for (int g = 0; g < G; ++g) {
+            wm[wave][g] = m[g];
+            wl[wave][g] = l[g];
+        }
+    __syncthreads();
+
+    constexpr int kHdr = split_header(G);
+    const int pstride = kHdr + G * hd;
+    float *mine = ka.partials + ((static_cast<int64_t>(b) * a.kv_heads + kvh) * ka.splits + split) * pstride;
+    for (int i = tid; i < G * hv; i += kSplitThreads) {
+        const int g = i / hv, e = i - g * hv;
+        float mw = wm[0][g], lw = wl[0][g];
+        float4 x = part[0][g * HD / 4 + e];
+        #pragma unroll
+        for (int w = 1; w < kSplitWaves; ++w) {
+            float f, fo;
+            merge_scales(mw, lw, wm[w][g], wl[w][g], f, fo);
+            const float4 y = part[w][g * HD / 4 + e];
+            x.x = x.x * f + y.x * fo;
+            x.y = x.y * f + y.y * fo;
+            x.z = x.z * f + y.z * fo;
+            x.w = x.w * f + y.w * fo;
+        }
+        if (nsplit == 1) {
+            *reinterpret_cast<float4 *>(o + g * hd + 4 * e) = scale4(x, 1.0f / lw);
+        } else {
+            if (e == 0) {
+                mine[g] = mw;
+                mine[G + g] = lw;
+            }
+            *reinterpret_cast<float4 *>(mine + kHdr + g * hd + 4 * e) = x;
+        }
+    }
+}
+
+// The splits of (token, KV head) with more than one: the partials merged in
+// split order.
+template <int G>
+__global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka) {
+    const SplitAttention &a = ka.a;
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const qk_batch_token d = a.desc ? a.desc[b] : qk_batch_token{a.pos, 0, 0};
+    if (!token_ok(d, a.cache_rows, a.max_pos)) return;
+    const int nsplit = (d.pos + ka.split_rows) / ka.split_rows;
+    if (nsplit == 1) return;
+    const int hd = a.head_dim;
+    constexpr int kHdr = split_header(G);
+    const int pstride = kHdr + G * hd;
+    const float *all = ka.partials + (static_cast<int64_t>(b) * a.kv_heads + kvh) * ka.splits * pstride;
+    float *o = a.out + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
+    for (int i = threadIdx.x; i < G * hd; i += 256) {
+        const int g = i / hd;
+        float mx = -INFINITY;
+        #pragma unroll 8
+        for (int p = 0; p < nsplit; ++p) mx = fmaxf(mx, all[p * pstride + g]);
+        float num = 0.f, den = 0.f;
+        #pragma unroll 8
+        for (int p = 0; p < nsplit; ++p) {
+            const float w = __builtin_amdgcn_exp2f(all[p * pstride + g] - mx);
+            den = fmaf(w, all[p * pstride + G + g], den);
+            num = fmaf(w, all[p * pstride + kHdr + i], num);
+        }
+        o[i] = num / den;
+    }
 }
 
 __global__ void add_kernel(float *x, const float *y, int n) {
@@ -734,116 +601,122 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
     }
 }
 
-// Kernel instance for G query heads per KV head and head_dim: G in
-// {1, 2, 3, 4, 6, 8}, head_dim <= 256.  NULL when unsupported.
-template <template <int, int> class K>
-const void *attention_instance(int G, int head_dim) {
-    const int dl = (head_dim + 63) / 64;
-#define QK_ATTN_CASE(g)                                        \
-    case g:                                                    \
-        return dl == 1   ? K<g, 1>::fn()                       \
-               : dl == 2 ? K<g, 2>::fn()                       \
-               : dl <= 4 ? K<g, 4>::fn()                       \
-                         : nullptr;
-    switch (G) {
-        QK_ATTN_CASE(1)
-        QK_ATTN_CASE(2)
-        QK_ATTN_CASE(3)
-        QK_ATTN_CASE(4)
-        QK_ATTN_CASE(6)
-        QK_ATTN_CASE(8)
-        default: return nullptr;
-    }
-#undef QK_ATTN_CASE
+// Split-attention instance for G and head_dim: 8 lanes per cache row when
+// G * head_dim <= 512, else 16; NF float4 per lane.  NULL when unsupported.
+template <int G, int NF, int L>
+const void *split_fn() {
+    return reinterpret_cast<const void *>(split_attention_kernel<G, NF, L>);
 }
 
-template <int G, int DL>
-struct PlainAttention {
-    static const void *fn() { return reinterpret_cast<const void *>(attention_kernel<G, DL>); }
-};
-template <int G, int DL>
-struct BatchedAttention {
-    static const void *fn() { return reinterpret_cast<const void *>(attention_batched_kernel<G, DL>); }
-};
-template <int G, int DL>
-struct RopeBatchedAttention {
-    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_batched_kernel<G, DL>); }
-};
-template <int G, int DL>
-struct ChunkedAttention {
-    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_chunked_kernel<G, DL>); }
-};
-template <int G, int DL>
-struct RopeAttention {
-    static const void *fn() { return reinterpret_cast<const void *>(rope_attention_kernel<G, DL>); }
-};
+template <int G>
+const void *split_for(int head_dim) {
+    if (G * head_dim <= 512) {
+        if (head_dim <= 32) return split_fn<G, 1, 8>();
+        if (head_dim == 64) return split_fn<G, 2, 8>();
+        if constexpr (G <= 4)
+            if (head_dim == 128) return split_fn<G, 4, 8>();
+        if constexpr (G <= 2)
+            if (head_dim == 256) return split_fn<G, 8, 8>();
+        return nullptr;
+    }
+    if constexpr (G >= 6)
+        if (head_dim == 128) return split_fn<G, 2, 16>();
+    if constexpr (G >= 3)
+        if (head_dim == 256) return split_fn<G, 4, 16>();
+    return nullptr;
+}
+
+const void *split_instance(int G, int head_dim) {
+    if (head_dim < 4 || head_dim % 4 || 256 % head_dim) return nullptr;
+    switch (G) {
+        case 1: return split_for<1>(head_dim);
+        case 2: return split_for<2>(head_dim);
+        case 3: return split_for<3>(head_dim);
+        case 4: return split_for<4>(head_dim);
+        case 6: return split_for<6>(head_dim);
+        case 8: return split_for<8>(head_dim);
+        default: return nullptr;
+    }
+}
+
+const void *split_merge_instance(int G) {
+    switch (G) {
+        case 1: return reinterpret_cast<const void *>(split_merge_kernel<1>);
+        case 2: return reinterpret_cast<const void *>(split_merge_kernel<2>);
+        case 3: return reinterpret_cast<const void *>(split_merge_kernel<3>);
+        case 4: return reinterpret_cast<const void *>(split_merge_kernel<4>);
+        case 6: return reinterpret_cast<const void *>(split_merge_kernel<6>);
+        case 8: return reinterpret_cast<const void *>(split_merge_kernel<8>);
+        default: return nullptr;
+    }
+}
 
 inline hipStream_t S(qk_stream s) { return static_cast<hipStream_t>(s); }
 
 }  // namespace
 
-size_t attention_workspace_bytes(int kv_heads, int group, int head_dim, int context) {
-    const size_t chunks = (static_cast<size_t>(context) + kChunkPos - 1) / kChunkPos;
-    return (static_cast<size_t>(kv_heads) * chunks * group * (head_dim + 2)) * sizeof(float) +
-           static_cast<size_t>(kv_heads) * sizeof(int) + 256;
+int split_attention_rows(int64_t head_rows, int max_rows) {
+    // About kSplitTarget workgroups over the call's (token, KV head) rows, at
+    // least kMinSplitRows rows a split, at most kMaxSplits splits a token.
+    int64_t rows = (head_rows + kSplitTarget - 1) / kSplitTarget;
+    rows = std::max<int64_t>(rows, (static_cast<int64_t>(max_rows) + kMaxSplits - 1) / kMaxSplits);
+    rows = std::max<int64_t>(kMinSplitRows, (rows + 15) / 16 * 16);
+    return static_cast<int>(std::min<int64_t>(rows, std::max(max_rows, 1)));
 }
 
-int launch_rope_attention_chunked(const float *q, const float *k, const float *v, const float *cosine,
-                                  const float *sine, float *key_cache, float *value_cache, float *out, void *workspace,
-                                  int layer, int pos, int context, int heads, int kv_heads, int head_dim,
-                                  hipStream_t stream) {
+size_t split_attention_workspace_bytes(int n_tokens, int heads, int kv_heads, int head_dim, int max_rows) {
+    if (n_tokens < 1 || kv_heads < 1 || heads < kv_heads || max_rows <= kMinSplitRows) return 0;
     const int G = heads / kv_heads;
-    const void *fn = head_dim % 64 == 0 && kv_heads <= 64 ? attention_instance<ChunkedAttention>(G, head_dim) : nullptr;
-    if (!fn) return fail(QK_ERR_LIMIT, "chunked attention: unsupported head layout");
-    const int nchunks = (pos + kChunkPos) / kChunkPos;
-    int *tickets = static_cast<int *>(workspace);
-    float *partials = reinterpret_cast<float *>(static_cast<uint8_t *>(workspace) + 256);
-    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &partials, &tickets, &layer, &pos,
-                    &context, &kv_heads, &head_dim};
-    if (hipLaunchKernel(fn, dim3(kv_heads, nchunks), dim3(kChunkThreads), args, 0, stream) != hipSuccess)
-        return launch_status("chunked attention launch");
-    return launch_status("chunked attention launch");
+    const size_t splits = std::min<size_t>(kMaxSplits, (static_cast<size_t>(max_rows) + kMinSplitRows - 1) / kMinSplitRows);
+    const size_t part = static_cast<size_t>(split_header(G) + G * head_dim) * sizeof(float);
+    return std::min<size_t>(kMaxSplitWorkspace, static_cast<size_t>(n_tokens) * kv_heads * splits * part);
 }
 
-int launch_rope_attention_batched(const float *q, const float *k, const float *v, const float *cosine,
-                                  const float *sine, float *key_cache, float *value_cache, float *out, int layer,
-                                  int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos,
-                                  int heads, int kv_heads, int head_dim, hipStream_t stream) {
-    const int G = heads / kv_heads;
-    const void *fn = attention_instance<RopeBatchedAttention>(G, head_dim);
-    if (!fn) return fail(QK_ERR_LIMIT, "batched rope + attention: unsupported head layout");
-    if (n_tokens > 65535) return fail(QK_ERR_LIMIT, "batched rope + attention: too many tokens in one launch");
-    const size_t lds = attention_lds_bytes(max_pos, head_dim, G) + static_cast<size_t>(G) * head_dim * sizeof(float);
-    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &layer, &cache_rows, &desc, &max_pos,
-                    &kv_heads, &head_dim};
-    if (hipLaunchKernel(fn, dim3(kv_heads, n_tokens), dim3(kAttnThreads), args, lds, stream) != hipSuccess)
-        return launch_status("batched rope + attention launch");
-    return launch_status("batched rope + attention launch");
+int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
+                           hipStream_t stream) {
+    const int G = a.heads / a.kv_heads;
+    const void *fn = split_instance(G, a.head_dim);
+    if (!fn) return fail(QK_ERR_LIMIT, "split attention: unsupported head layout");
+    if (a.n_tokens > 65535) return fail(QK_ERR_LIMIT, "split attention: too many tokens in one launch");
+    const int max_rows = a.max_pos + 1;
+    if (split_rows <= 0) {
+        const int64_t rows = a.rows_hint > 0 ? a.rows_hint : static_cast<int64_t>(a.n_tokens) * max_rows;
+        split_rows = split_attention_rows(rows * a.kv_heads, max_rows);
+    }
+    split_rows = std::min(split_rows, max_rows);
+    int nsplit = (max_rows + split_rows - 1) / split_rows;
+    if (nsplit > 1) {
+        // Fewer, longer splits when the workspace is short; one without it.
+        const size_t per = static_cast<size_t>(a.n_tokens) * a.kv_heads *
+                           static_cast<size_t>(split_header(G) + G * a.head_dim) * sizeof(float);
+        const int64_t fit = workspace ? static_cast<int64_t>(workspace_size / per) : 0;
+        if (fit < 2)
+            split_rows = max_rows;
+        else if (nsplit > fit)
+            split_rows = static_cast<int>((max_rows + fit - 1) / fit);
+        nsplit = (max_rows + split_rows - 1) / split_rows;
+    }
+    // Row offsets of a split (plus one round of prefetch past it) stay below 2 GiB.
+    if ((static_cast<int64_t>(split_rows) + 512) * a.kv_heads * a.head_dim * static_cast<int64_t>(sizeof(float)) >=
+        (1ll << 31))
+        return fail(QK_ERR_LIMIT, "split attention: a split spans 2 GiB of cache rows");
+    SplitAttnKernelArgs ka;
+    ka.a = a;
+    ka.partials = nsplit > 1 ? static_cast<float *>(workspace) : nullptr;
+    ka.split_rows = split_rows;
+    ka.splits = nsplit;
+    void *args[] = {&ka};
+    if (hipLaunchKernel(fn, dim3(a.kv_heads, a.n_tokens, nsplit), dim3(kSplitThreads), args, 0, stream) != hipSuccess)
+        return launch_status("split attention launch");
+    if (nsplit > 1) {
+        const void *merge = split_merge_instance(G);
+        if (hipLaunchKernel(merge, dim3(a.kv_heads, a.n_tokens), dim3(256), args, 0, stream) != hipSuccess)
+            return launch_status("split attention merge launch");
+    }
+    return launch_status("split attention launch");
 }
 
-bool chunked_attention_supported(int kv_heads, int group, int head_dim) {
-    return head_dim % 64 == 0 && head_dim <= 256 && kv_heads <= 64 &&
-           attention_instance<ChunkedAttention>(group, head_dim) != nullptr;
-}
-
-bool attention_supported(int group, int head_dim) {
-    return head_dim >= 4 && head_dim % 4 == 0 && 256 % head_dim == 0 &&
-           attention_instance<PlainAttention>(group, head_dim) != nullptr;
-}
-
-int launch_rope_attention(const float *q, const float *k, const float *v, const float *cosine, const float *sine,
-                          float *key_cache, float *value_cache, float *out, int layer, int pos, int context,
-                          int heads, int kv_heads, int head_dim, hipStream_t stream) {
-    const int G = heads / kv_heads;
-    const void *fn = attention_instance<RopeAttention>(G, head_dim);
-    if (!fn) return fail(QK_ERR_LIMIT, "rope + attention: unsupported query heads per KV head or head_dim");
-    const size_t lds = attention_lds_bytes(pos, head_dim, G) + static_cast<size_t>(G) * head_dim * sizeof(float);
-    void *args[] = {&q, &k, &v, &cosine, &sine, &key_cache, &value_cache, &out, &layer, &pos, &context, &kv_heads,
-                    &head_dim};
-    if (hipLaunchKernel(fn, dim3(kv_heads), dim3(kAttnThreads), args, lds, stream) != hipSuccess)
-        return launch_status("rope + attention launch");
-    return launch_status("rope + attention launch");
-}
+bool attention_supported(int group, int head_dim) { return split_instance(group, head_dim) != nullptr; }
 
 }  // namespace qk
 
@@ -880,16 +753,23 @@ int qk_attention_f32(const float *q, const float *key_cache, const float *value_
         return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_f32: bad head layout or position outside context");
     if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: head_dim must be a multiple of 4 dividing 256");
-    const void *fn = qk::attention_instance<qk::PlainAttention>(heads / kv_heads, head_dim);
-    if (!fn) return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
-    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16))
-        return qk::fail(QK_ERR_ALIGN, "qk_attention_f32: caches must be 16-byte aligned");
-    const size_t lds = qk::attention_lds_bytes(pos, head_dim, heads / kv_heads);
-    if (lds > 150 * 1024) return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: position beyond the LDS score buffer");
-    void *args[] = {&q, &key_cache, &value_cache, &out, &layer, &pos, &context, &kv_heads, &head_dim};
-    if (hipLaunchKernel(fn, dim3(kv_heads), dim3(qk::kAttnThreads), args, lds, qk::S(stream)) != hipSuccess)
-        return qk::launch_status("qk_attention_f32 launch");
-    return qk::launch_status("qk_attention_f32 launch");
+    if (!qk::attention_supported(heads / kv_heads, head_dim))
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
+    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16) || !qk::aligned(out, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_attention_f32: caches and out must be 16-byte aligned");
+    qk::SplitAttention a{};
+    a.q = q;
+    a.key_cache = const_cast<float *>(key_cache);
+    a.value_cache = const_cast<float *>(value_cache);
+    a.out = out;
+    a.cache_rows = context;
+    a.layer = layer;
+    a.pos = a.max_pos = pos;
+    a.n_tokens = 1;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    return qk::launch_split_attention(a, 0, nullptr, 0, qk::S(stream));
 }
 
 int qk_add_f32(float *x, const float *y, int n, qk_stream stream) {
@@ -933,19 +813,67 @@ int qk_attention_batched_f32(const float *q, const float *key_cache, const float
         return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_batched_f32: bad head layout or cache shape");
     if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: head_dim must be a multiple of 4 dividing 256");
-    const void *fn = qk::attention_instance<qk::BatchedAttention>(heads / kv_heads, head_dim);
-    if (!fn)
+    if (!qk::attention_supported(heads / kv_heads, head_dim))
         return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
-    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16))
-        return qk::fail(QK_ERR_ALIGN, "qk_attention_batched_f32: caches must be 16-byte aligned");
-    const size_t lds = qk::attention_lds_bytes(max_pos, head_dim, heads / kv_heads);
-    if (lds > 150 * 1024) return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: max_pos beyond the LDS score buffer");
+    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16) || !qk::aligned(out, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_attention_batched_f32: caches and out must be 16-byte aligned");
     if (n_tokens == 0) return qk::ok();
-    if (n_tokens > 65535) return qk::fail(QK_ERR_LIMIT, "qk_attention_batched_f32: too many tokens in one launch");
-    void *args[] = {&q, &key_cache, &value_cache, &out, &layer, &cache_rows, &desc, &max_pos, &kv_heads, &head_dim};
-    if (hipLaunchKernel(fn, dim3(kv_heads, n_tokens), dim3(qk::kAttnThreads), args, lds, qk::S(stream)) != hipSuccess)
-        return qk::launch_status("qk_attention_batched_f32 launch");
-    return qk::launch_status("qk_attention_batched_f32 launch");
+    qk::SplitAttention a{};
+    a.q = q;
+    a.key_cache = const_cast<float *>(key_cache);
+    a.value_cache = const_cast<float *>(value_cache);
+    a.out = out;
+    a.desc = desc;
+    a.cache_rows = cache_rows;
+    a.layer = layer;
+    a.max_pos = max_pos;
+    a.n_tokens = n_tokens;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    return qk::launch_split_attention(a, 0, nullptr, 0, qk::S(stream));
+}
+
+size_t qk_attention_split_workspace_bytes(int n_tokens, int heads, int kv_heads, int head_dim, int max_pos,
+                                          int split_rows) {
+    if (n_tokens < 1 || heads < 1 || kv_heads < 1 || heads % kv_heads || head_dim < 4 || max_pos < 0) return 0;
+    if (split_rows <= 0) return qk::split_attention_workspace_bytes(n_tokens, heads, kv_heads, head_dim, max_pos + 1);
+    const size_t splits = (static_cast<size_t>(max_pos) + split_rows) / split_rows;
+    if (splits < 2) return 0;
+    const int G = heads / kv_heads;
+    return static_cast<size_t>(n_tokens) * kv_heads * splits * (qk::split_header(G) + G * head_dim) * sizeof(float);
+}
+
+int qk_attention_split_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,
+                           int64_t cache_rows, const qk_batch_token *desc, int n_tokens, int max_pos, int heads,
+                           int kv_heads, int head_dim, int split_rows, void *workspace, size_t workspace_size,
+                           qk_stream stream) {
+    if (!q || !key_cache || !value_cache || !out || (!desc && n_tokens > 0) || n_tokens < 0 || split_rows < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_split_f32: null pointer or negative count");
+    if (heads < 1 || kv_heads < 1 || heads % kv_heads || layer < 0 || cache_rows < 1 || max_pos < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_attention_split_f32: bad head layout or cache shape");
+    if (head_dim < 4 || head_dim % 4 || 256 % head_dim)
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_split_f32: head_dim must be a multiple of 4 dividing 256");
+    if (!qk::attention_supported(heads / kv_heads, head_dim))
+        return qk::fail(QK_ERR_LIMIT, "qk_attention_split_f32: query heads per KV head must be 1, 2, 3, 4, 6 or 8");
+    if (!qk::aligned(key_cache, 16) || !qk::aligned(value_cache, 16) || !qk::aligned(out, 16) ||
+        !qk::aligned(workspace, 16))
+        return qk::fail(QK_ERR_ALIGN, "qk_attention_split_f32: caches, out and workspace must be 16-byte aligned");
+    if (n_tokens == 0) return qk::ok();
+    qk::SplitAttention a{};
+    a.q = q;
+    a.key_cache = const_cast<float *>(key_cache);
+    a.value_cache = const_cast<float *>(value_cache);
+    a.out = out;
+    a.desc = desc;
+    a.cache_rows = cache_rows;
+    a.layer = layer;
+    a.max_pos = max_pos;
+    a.n_tokens = n_tokens;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    return qk::launch_split_attention(a, split_rows, workspace, workspace_size, qk::S(stream));
 }
 
 size_t qk_argmax_workspace_bytes(int n) {

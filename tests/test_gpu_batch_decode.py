@@ -84,6 +84,98 @@ def test_batched_attention_rejects_out_of_range_tokens(qk, torch_gpu, synth):
     assert np.all(np.isfinite(o[0])) and np.all(np.isnan(o[1])) and np.all(np.isnan(o[2]))
 
 
+def _split_case(qk, t, oracle, synth, heads, kv_heads, head_dim, pos, seed):
+    """Caches with each token's sequence at its own rows, rotated queries, and
+    the oracle's attention per token."""
+    layers, layer = 2, 1
+    n = len(pos)
+    ctx = int(pos.max()) + 1
+    kv_row = np.arange(n, dtype=np.int64) * ctx
+    rows = n * ctx
+    kv = kv_heads * head_dim
+    kc = synth.normal_f32(layers * rows * kv, seed, 1).reshape(layers, rows, kv)
+    vc = synth.normal_f32(layers * rows * kv, seed, 2).reshape(layers, rows, kv)
+    q = synth.normal_f32(n * heads * head_dim, seed, 3).reshape(n, heads * head_dim)
+    want = [oracle.attention(q[i], kc[layer, kv_row[i]:kv_row[i] + pos[i] + 1],
+                             vc[layer, kv_row[i]:kv_row[i] + pos[i] + 1], int(pos[i]), heads, kv_heads, head_dim)
+            for i in range(n)]
+    dev = dict(q=to_dev(t, q), kc=to_dev(t, kc), vc=to_dev(t, vc), desc=_desc(qk, t, pos, kv_row),
+               out=t.empty((n, heads * head_dim), device="cuda"))
+    return dev, want, layer, rows
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(32, 8, 64), (24, 8, 128), (8, 1, 32), (4, 2, 256),
+                                                     (48, 8, 128), (16, 2, 256), (12, 3, 16)])
+@pytest.mark.parametrize("split_rows", [0, 7, 64])
+def test_split_attention(qk, torch_gpu, oracle, synth, heads, kv_heads, head_dim, split_rows):
+    """Rows spread over splits of 7 (ragged last splits, splits shorter than
+    one load round), 64 and the batch's own choice, partials merged by the
+    second kernel: the oracle's attention per token within rel-L2 1e-5."""
+    t = torch_gpu
+    pos = np.array([0, 6, 7, 63, 64, 130, 299, 1, 200], dtype=np.int64)
+    dev, want, layer, rows = _split_case(qk, t, oracle, synth, heads, kv_heads, head_dim, pos, 62)
+    L = qk.lib()
+    n, max_pos = len(pos), int(pos.max())
+    wsb = L.qk_attention_split_workspace_bytes(n, heads, kv_heads, head_dim, max_pos, split_rows)
+    if split_rows:
+        assert wsb == n * kv_heads * (max_pos // split_rows + 1) * \
+            ((2 * (heads // kv_heads) + 3) // 4 * 4 + heads // kv_heads * head_dim) * 4
+    ws = t.empty(max(wsb, 16), dtype=t.uint8, device="cuda")
+    qk.check(L.qk_attention_split_f32(dev["q"].data_ptr(), dev["kc"].data_ptr(), dev["vc"].data_ptr(),
+                                      dev["out"].data_ptr(), layer, rows, dev["desc"].data_ptr(), n, max_pos, heads,
+                                      kv_heads, head_dim, split_rows, ws.data_ptr(), wsb, None), "split attention")
+    t.cuda.synchronize()
+    got = dev["out"].cpu().numpy()
+    for i in range(n):
+        assert rel_l2(got[i], want[i]) < 1e-5, (i, int(pos[i]))
+
+
+@pytest.mark.parametrize("room", ["none", "short"])
+def test_split_attention_short_workspace(qk, torch_gpu, oracle, synth, room):
+    """With no workspace the call runs one split per token; with a workspace
+    shorter than the splits ask for, fewer and longer splits: the same
+    results either way."""
+    t = torch_gpu
+    heads, kv_heads, head_dim = 32, 8, 64
+    pos = np.array([500, 3, 257, 64], dtype=np.int64)
+    dev, want, layer, rows = _split_case(qk, t, oracle, synth, heads, kv_heads, head_dim, pos, 63)
+    L = qk.lib()
+    n, max_pos = len(pos), int(pos.max())
+    full = L.qk_attention_split_workspace_bytes(n, heads, kv_heads, head_dim, max_pos, 16)
+    wsb = 0 if room == "none" else full // 5
+    ws = t.empty(max(full, 16), dtype=t.uint8, device="cuda")
+    qk.check(L.qk_attention_split_f32(dev["q"].data_ptr(), dev["kc"].data_ptr(), dev["vc"].data_ptr(),
+                                      dev["out"].data_ptr(), layer, rows, dev["desc"].data_ptr(), n, max_pos, heads,
+                                      kv_heads, head_dim, 16, ws.data_ptr() if wsb else None, wsb, None),
+             "split attention")
+    t.cuda.synchronize()
+    got = dev["out"].cpu().numpy()
+    for i in range(n):
+        assert rel_l2(got[i], want[i]) < 1e-5, i
+
+
+def test_split_attention_rejects_out_of_range_tokens(qk, torch_gpu, synth):
+    """Descriptors beyond max_pos or the cache give NaN rows with several
+    splits too, and never read outside the cache."""
+    t = torch_gpu
+    heads, kv_heads, hd, rows = 4, 2, 64, 100
+    kv = kv_heads * hd
+    kcd = t.zeros((1, rows, kv), device="cuda")
+    vcd = t.zeros((1, rows, kv), device="cuda")
+    q = t.ones((3, heads * hd), device="cuda")
+    dd = _desc(qk, t, np.array([30, 60, 5]), np.array([0, 30, 98]))   # ok; beyond max_pos; beyond the cache
+    out = t.zeros((3, heads * hd), device="cuda")
+    L = qk.lib()
+    wsb = L.qk_attention_split_workspace_bytes(3, heads, kv_heads, hd, 40, 8)
+    ws = t.empty(wsb, dtype=t.uint8, device="cuda")
+    qk.check(L.qk_attention_split_f32(q.data_ptr(), kcd.data_ptr(), vcd.data_ptr(), out.data_ptr(), 0, rows,
+                                      dd.data_ptr(), 3, 40, heads, kv_heads, hd, 8, ws.data_ptr(), wsb, None),
+             "split attention")
+    t.cuda.synchronize()
+    o = out.cpu().numpy()
+    assert np.all(np.isfinite(o[0])) and np.all(np.isnan(o[1])) and np.all(np.isnan(o[2]))
+
+
 def test_argmax_rows(qk, torch_gpu, oracle, synth):
     t = torch_gpu
     rows, n, ld = 5, 128256, 128300
