@@ -270,7 +270,9 @@ def bench_decode_1b(torch, qk, wl) -> dict:
     return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
             "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            "launches_per_token": 5 * cfg["layers"] + 4}
+            # Per layer: QKV, attention + split merge, o, gate/up, down; then
+            # embedding, LM head and the two argmax stages.
+            "kernels_per_token": 6 * cfg["layers"] + 4}
 
 
 def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
