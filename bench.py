@@ -3,9 +3,12 @@
 
 A step is one pass of the hot path over one batch of synthetic input: one
 Q6_K GEMV over the tied LM head, 128256 x 2048 (215.5 MB of super-blocks),
-batch 1, fp32 activations.  Four weight copies of that matrix (862 MB) rotate
-from step to step so that the ~256 MB last-level cache cannot serve them;
-all inputs are resident in HBM before timing starts.
+batch 1, fp32 activations, weights in the split Q6_K layout that the model
+drivers repack them into at load time (qk_q6k_split: the same bytes, fields
+16-byte aligned); the GGUF-layout time is reported beside it.  Four weight
+copies of that matrix (862 MB) rotate from step to step so that the ~256 MB
+last-level cache cannot serve them; all inputs are resident in HBM before
+timing starts.
 
 value = algorithmic bytes per step (weights + x + y) * steps / wall time of
 the timed region (synchronize on both sides).  roofline.achieved divides the
@@ -361,8 +364,9 @@ def reference_kernels(torch, args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed launches first: the clocks settle over the first ~40 ms of a run")
     ap.add_argument("--copies", type=int, default=4, help="rotating weight copies (>= 2x the last-level cache)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -405,12 +409,17 @@ def main() -> int:
         copies.append(torch.from_numpy(w).to("cuda"))
     x = torch.from_numpy(x_host).to("cuda")
     y = torch.empty(rows, dtype=torch.float32, device="cuda")
-    tensors = [qk.Tensor((cols, rows), qk.Q6_K, wc) for wc in copies]
+    gguf = [qk.Tensor((cols, rows), qk.Q6_K, wc) for wc in copies]
+    # The layout the model drivers run: each copy repacked once by
+    # qk_q6k_split (same 210 bytes per block, every field 16-byte aligned).
+    tensors = [qk.split_q6k(t, stream) for t in gguf]
+    torch.cuda.synchronize()
 
     def launch(i):
         qk.matvec(tensors[i % len(tensors)], x, y, cols, rows, stream)
 
-    weight_bytes = qk.tensor_bytes(qk.Q6_K, cols, rows)
+    weight_bytes = qk.tensor_bytes(qk.Q6_K_SPLIT, cols, rows)
+    assert weight_bytes == qk.tensor_bytes(qk.Q6_K, cols, rows)   # 2048 columns: no row padding
     step_bytes = weight_bytes + cols * 4 + rows * 4
     log(f"[bench] timing {args.steps} steps after {args.warmup} warmup")
     wall, kern_ms = time_launches(torch, launch, args.steps, args.warmup, stream)
@@ -431,7 +440,7 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic (seeded random Q6_K super-blocks, x ~ N(0,1))",
         "config": {"workload": "lm_head_q6k: Q6_K GEMV 128256x2048 (tied LM head), batch 1, "
-                               f"{args.copies} rotating weight copies",
+                               f"{args.copies} rotating weight copies, split Q6_K layout",
                    "rows": rows, "cols": cols, "bytes_per_step": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic},
@@ -440,6 +449,12 @@ def main() -> int:
 
     if args.secondary:
         sec = {}
+        _, kg = time_launches(torch, lambda i: qk.matvec(gguf[i % len(gguf)], x, y, cols, rows, stream),
+                              200, 20, stream)
+        sec["lm_head_q6k_gguf_layout"] = {"kernel_us": round(kg * 1e3, 2),
+                                          "GBps_kernel": round(step_bytes / (kg * 1e-3) / 1e9, 1),
+                                          "frac_of_peak": round(step_bytes / (kg * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"[bench] lm_head_q6k_gguf_layout: {json.dumps(sec['lm_head_q6k_gguf_layout'])}")
         sec.update(bench_small_gemvs(torch, qk, wl, stream))
         sec["ffn_3b_ragged_t32"] = bench_ffn_3b_ragged(torch, qk, wl, stream)
         log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")

@@ -38,12 +38,20 @@ extern "C" {
 #define QK_TYPE_F16 1
 #define QK_TYPE_Q4_K 12
 #define QK_TYPE_Q6_K 14
+/* A Q6_K matrix in the split layout made by qk_q6k_split (no reference
+   counterpart): the same 210 bytes per super-block, each row of nb =
+   cols/256 blocks stored as four streams -- ql [nb][128], qh [nb][64],
+   scales [nb][16], d [nb] (fp16) -- and padded to a multiple of 16 bytes,
+   so every field a kernel reads is 16-byte aligned (in the GGUF layout a
+   Q6_K block is only 2-byte aligned at odd block indices).  Accepted
+   wherever Q6_K is. */
+#define QK_TYPE_Q6_K_SPLIT 114
 
 /* Status codes. */
 #define QK_OK 0
 #define QK_ERR_INVALID_ARG 1   /* null pointer, negative count, bad leading dimension */
 #define QK_ERR_SHAPE 2         /* cols not a positive multiple of 256, rows < 1 */
-#define QK_ERR_TYPE 3          /* storage type other than Q4_K / Q6_K */
+#define QK_ERR_TYPE 3          /* storage type other than Q4_K / Q6_K / Q6_K split */
 #define QK_ERR_ALIGN 4         /* base pointer or leading dimension misaligned */
 #define QK_ERR_DEVICE 5        /* HIP runtime error at launch */
 #define QK_ERR_LIMIT 6         /* size beyond what the kernels index */
@@ -58,7 +66,8 @@ const char *qk_status_string(int status);
 /* Detail of the last failing call on this host thread ("" if none). */
 const char *qk_last_error(void);
 /* Bytes per 256-value super-block (144 / 210; 0 for other types) and bytes of
-   a cols x rows tensor: the size rule of inferencer.cu:252-259. */
+   a cols x rows tensor: the size rule of inferencer.cu:252-259 (split Q6_K
+   rows rounded up to 16 bytes). */
 int qk_block_bytes(int type);
 int64_t qk_tensor_bytes(int type, int64_t cols, int64_t rows);
 
@@ -121,9 +130,15 @@ int qk_gemv_multi_batched_f32(const qk_matrix *mats, int n_mats, const float *x,
 int qk_dequant_rows(int type, const void *w, float *out, int cols, int row0, int nrows,
                     qk_stream stream);
 
+/* Copy a cols x rows Q6_K matrix (GGUF block bytes at src) into the split
+   layout of QK_TYPE_Q6_K_SPLIT at dst (qk_tensor_bytes(QK_TYPE_Q6_K_SPLIT,
+   cols, rows) bytes, 16-byte aligned, not overlapping src).  A load-time
+   step: the block bytes are moved, never decoded. */
+int qk_q6k_split(const void *src, void *dst, int cols, int rows, qk_stream stream);
+
 /* out[t*cols + c] = W[tokens[t]][c]; tokens is a device array of n_tokens
    ids in [0, vocab).  Replaces embedding_cuda / embedding_batch_cuda
-   (inferencer.cu:806-819); any Q4_K or Q6_K table. */
+   (inferencer.cu:806-819); any Q4_K, Q6_K or split Q6_K table. */
 int qk_embedding(int type, const void *w, const int32_t *tokens, int n_tokens, float *out,
                  int cols, int vocab, qk_stream stream);
 
@@ -266,8 +281,11 @@ typedef struct qk_llama_weights {
 typedef struct qk_llama qk_llama;
 
 /* Allocates the step buffers, KV cache and RoPE tables once (the FastGPU /
-   FastRunner constructors, inferencer.cu:1115-1142, 1196-1249).  The weights
-   stay owned by the caller. */
+   FastRunner constructors, inferencer.cu:1115-1142, 1196-1249).  Every Q6_K
+   tensor is copied once into the split layout (QK_TYPE_Q6_K_SPLIT, owned by
+   the handle, freed by destroy); create returns after those copies, so the
+   caller's Q6_K buffers may be released then.  Q4_K, split Q6_K and norm
+   tensors are read in place at every step and stay owned by the caller. */
 int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream,
                     qk_llama **out);
 int qk_llama_destroy(qk_llama *m);
@@ -289,7 +307,8 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
    FastRunner::prefill's batched path (inferencer.cu:1279-1423), which serves
    one sequence; every projection runs through qk_gemv_multi_batched_f32 /
    qk_gemv_batched_f32 (matrix cores from 8 tokens on).  Buffers, caches and
-   workspaces are allocated once at create; weights stay the caller's. */
+   workspaces are allocated once at create; weights are handled as by
+   qk_llama_create (Q6_K copied into the split layout, the rest read in place). */
 typedef struct qk_llama_batch qk_llama_batch;
 
 int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens,

@@ -23,8 +23,10 @@ _HERE = pathlib.Path(__file__).resolve().parent
 LIB_PATH = _HERE / "libqk.so"
 
 F32, F16, Q4_K, Q6_K = 0, 1, 12, 14
-BLOCK_BYTES = {Q4_K: 144, Q6_K: 210}
-STORAGE_NAMES = {F32: "FP32", F16: "FP16", Q4_K: "Q4_K", Q6_K: "Q6_K"}
+Q6_K_SPLIT = 114   # Q6_K in the split row layout of qk_q6k_split (16-byte aligned fields)
+BLOCK_BYTES = {Q4_K: 144, Q6_K: 210, Q6_K_SPLIT: 210}
+QUANT_TYPES = (Q4_K, Q6_K, Q6_K_SPLIT)
+STORAGE_NAMES = {F32: "FP32", F16: "FP16", Q4_K: "Q4_K", Q6_K: "Q6_K", Q6_K_SPLIT: "Q6_K (split)"}
 MAX_FUSED = 8
 
 QK_OK = 0
@@ -85,6 +87,7 @@ SIGNATURES = {
     "qk_gemv_multi_batched_f32": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
     "qk_dequant_rows": (_i, [_i, _vp, _vp, _i, _i, _i, _vp]),
     "qk_embedding": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _vp]),
+    "qk_q6k_split": (_i, [_vp, _vp, _i, _i, _vp]),
     "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
@@ -164,7 +167,10 @@ def tensor_bytes(qtype: int, cols: int, rows: int) -> int:
     """Bytes of a quantized tensor: the size rule of inferencer.cu:252-259."""
     if qtype not in BLOCK_BYTES or cols % 256 or cols <= 0 or rows < 0:
         raise QKError("tensor_bytes", QK_ERR_SHAPE, "Invalid quantized tensor shape")
-    return cols // 256 * BLOCK_BYTES[qtype] * rows
+    row = cols // 256 * BLOCK_BYTES[qtype]
+    if qtype == Q6_K_SPLIT:
+        row = (row + 15) // 16 * 16   # split rows start 16-byte aligned
+    return row * rows
 
 
 @dataclass
@@ -189,7 +195,7 @@ class Tensor:
 
 def matvec(t: Tensor, inp, out, expected_cols: int, expected_rows: int, stream=None) -> None:
     """FastGPU::matvec (inferencer.cu:1156-1171), FP32 mode: out = W inp."""
-    if t.cols() != expected_cols or t.rows() != expected_rows or t.type not in (Q4_K, Q6_K):
+    if t.cols() != expected_cols or t.rows() != expected_rows or t.type not in QUANT_TYPES:
         raise QKError("matvec", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
     check(lib().qk_gemv_f32(t.type, t.gpu, ptr(inp), ptr(out), expected_cols, expected_rows,
                             stream_handle(stream)), "quantized matrix launch")
@@ -215,7 +221,7 @@ def multi_matvec(pairs, inp, cols: int, stream=None) -> None:
 def qkv(wq: Tensor, wk: Tensor, wv: Tensor, x, q, k, v, dim: int, kv_dim: int, stream=None) -> None:
     """qkv_cuda (inferencer.cu:753-784), FP32 mode: Q4_K q/k, Q4_K or Q6_K v."""
     if (wq.rows(), wk.rows(), wv.rows()) != (dim, kv_dim, kv_dim) or wq.type != Q4_K or wk.type != Q4_K \
-            or wv.type not in (Q4_K, Q6_K):
+            or wv.type not in QUANT_TYPES:
         raise QKError("qkv", QK_ERR_SHAPE, "Unexpected QKV quantization")
     multi_matvec([(wq, q), (wk, k), (wv, v)], x, dim, stream)
 
@@ -236,7 +242,7 @@ def batch_matvec(t: Tensor, inp, out, cols: int, rows: int, count: int, workspac
                  workspace_bytes: int = 0, stream=None) -> None:
     """FastRunner::batch_matvec (inferencer.cu:1265-1278) with FP32 semantics:
     out[t*rows + r] = sum_c W[r][c] inp[t*cols + c] for t < count."""
-    if t.cols() != cols or t.rows() != rows or t.type not in (Q4_K, Q6_K):
+    if t.cols() != cols or t.rows() != rows or t.type not in QUANT_TYPES:
         raise QKError("batch_matvec", QK_ERR_SHAPE, "Unexpected batched matrix shape")
     check(lib().qk_gemv_batched_f32(t.type, t.gpu, ptr(inp), cols, ptr(out), rows, cols, rows, count,
                                     ptr(workspace), workspace_bytes, stream_handle(stream)),
@@ -249,6 +255,18 @@ def dequant_rows(t: Tensor, out, row0: int, nrows: int, stream=None) -> None:
         raise QKError("dequant_rows", QK_ERR_INVALID_ARG, "row range outside the tensor")
     check(lib().qk_dequant_rows(t.type, t.gpu, ptr(out), t.cols(), row0, nrows, stream_handle(stream)),
           "dequant launch")
+
+
+def split_q6k(t: Tensor, stream=None) -> Tensor:
+    """A copy of a Q6_K tensor in the split layout (qk_q6k_split): same block
+    bytes, every field 16-byte aligned."""
+    import torch
+
+    if t.type != Q6_K:
+        raise QKError("split_q6k", QK_ERR_TYPE, "split_q6k takes a Q6_K tensor")
+    dst = torch.empty(tensor_bytes(Q6_K_SPLIT, t.cols(), t.rows()), dtype=torch.uint8, device="cuda")
+    check(lib().qk_q6k_split(t.gpu, ptr(dst), t.cols(), t.rows(), stream_handle(stream)), "Q6_K split")
+    return Tensor((t.cols(), t.rows()), Q6_K_SPLIT, dst)
 
 
 def embedding(t: Tensor, tokens, out, n_tokens: int, stream=None) -> None:
@@ -270,7 +288,7 @@ def quantize(x, xq, xscale, cols: int, n_tokens: int = 1, ldx: int | None = None
 def matvec_i8(t: Tensor, xq, xscale, out, cols: int, rows: int, n_tokens: int = 1, ldxq: int | None = None,
               ldscale: int | None = None, ldy: int | None = None, stream=None) -> None:
     """gemv_q4_dp4a / gemv_q6_dp4a / gemv_batch_dp4a (inferencer.cu:558-569, 663-699)."""
-    if t.cols() != cols or t.rows() != rows or t.type not in (Q4_K, Q6_K):
+    if t.cols() != cols or t.rows() != rows or t.type not in QUANT_TYPES:
         raise QKError("matvec_i8", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
     ldxq = cols if ldxq is None else ldxq
     ldscale = cols // 32 if ldscale is None else ldscale

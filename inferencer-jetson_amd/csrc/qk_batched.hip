@@ -277,21 +277,26 @@ __device__ __forceinline__ bool is_q4(int type) {
     return TYPE == QK_TYPE_Q4_K || (TYPE == 0 && type == QK_TYPE_Q4_K);
 }
 
+// Block b of the row at `row` (nb blocks per row; Q6_K in the GGUF or the
+// split layout).
 template <int TYPE>
-__device__ __forceinline__ RawBlock load_block(const uint8_t *blk, int type, int kh) {
+__device__ __forceinline__ RawBlock load_block(const uint8_t *row, int b, int nb, int type, int kh) {
     RawBlock r;
     if (is_q4<TYPE>(type)) {
+        const uint8_t *blk = row + b * 144;
         r.hdr = load16(blk);
         #pragma unroll
         for (int i = 0; i < 4; ++i) r.q[i] = load16(blk + 16 + kh * 64 + 16 * i);
         r.h[0] = r.h[1] = make_uint4(0, 0, 0, 0);
     } else {
+        const bool split = TYPE == QK_TYPE_Q6_K_SPLIT || (TYPE == 0 && type == QK_TYPE_Q6_K_SPLIT);
+        const Q6Fields f = q6_fields(row, nb, b, split);
         #pragma unroll
-        for (int i = 0; i < 4; ++i) r.q[i] = load16(blk + kh * 64 + 16 * i);
-        r.h[0] = load16(blk + 128 + kh * 32);
-        r.h[1] = load16(blk + 128 + kh * 32 + 16);
-        const uint2 sc = load8(blk + 192 + kh * 8);
-        r.hdr = make_uint4(sc.x, sc.y, load2(blk + 208), 0);
+        for (int i = 0; i < 4; ++i) r.q[i] = load16(f.ql + kh * 64 + 16 * i);
+        r.h[0] = load16(f.qh + kh * 32);
+        r.h[1] = load16(f.qh + kh * 32 + 16);
+        const uint2 sc = load8(f.sc + kh * 8);
+        r.hdr = make_uint4(sc.x, sc.y, load2(f.d), 0);
     }
     return r;
 }
@@ -519,7 +524,6 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     m = __builtin_amdgcn_readfirstlane(m);
     const BatchMatrix &M = p.mat[m];
     const int type = TYPE ? TYPE : M.type;
-    const int bpb = is_q4<TYPE>(type) ? 144 : 210;
     const uint8_t *wrow[RT];
     int row[RT];
     #pragma unroll
@@ -539,7 +543,7 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     for (int u = 0; u < TT; ++u) record_dma(recs[u] + static_cast<size_t>(b0) * kTileBytes, lds + u * kTileBytes, wave, lane);
     RawBlock cur[RT];
     #pragma unroll
-    for (int i = 0; i < RT; ++i) cur[i] = load_block<TYPE>(wrow[i] + b0 * bpb, type, kh);
+    for (int i = 0; i < RT; ++i) cur[i] = load_block<TYPE>(wrow[i], b0, p.nb, type, kh);
     wait_loads();
     __syncthreads();
 
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
         }
         RawBlock nxt[RT];
         #pragma unroll
-        for (int i = 0; i < RT; ++i) nxt[i] = load_block<TYPE>(wrow[i] + bn * bpb, type, kh);
+        for (int i = 0; i < RT; ++i) nxt[i] = load_block<TYPE>(wrow[i], bn, p.nb, type, kh);
         block_mma<TYPE, RT, TT>(cur, type, lds + buf * TT * kTileBytes, kh, col, acc);
         #pragma unroll
         for (int i = 0; i < RT; ++i) cur[i] = nxt[i];
@@ -737,6 +741,8 @@ void launch_gemm(int type, const dim3 &grid, size_t lds, hipStream_t stream, con
         hipLaunchKernelGGL((batch_gemm<QK_TYPE_Q4_K, TT>), grid, dim3(256), lds, stream, p);
     else if (type == QK_TYPE_Q6_K)
         hipLaunchKernelGGL((batch_gemm<QK_TYPE_Q6_K, TT>), grid, dim3(256), lds, stream, p);
+    else if (type == QK_TYPE_Q6_K_SPLIT)
+        hipLaunchKernelGGL((batch_gemm<QK_TYPE_Q6_K_SPLIT, TT>), grid, dim3(256), lds, stream, p);
     else
         hipLaunchKernelGGL((batch_gemm<0, TT>), grid, dim3(256), lds, stream, p);
 }
@@ -764,7 +770,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         M.y = mats[i].y;
         M.rows = mats[i].rows;
         M.type = mats[i].type;
-        M.row_bytes = nb * block_bytes(M.type);
+        M.row_bytes = static_cast<int>(row_bytes(M.type, nb));
         M.ldy = ldy[i];
         M.group_begin = static_cast<int>(groups);
         groups += (M.rows + kGroupRows - 1) / kGroupRows;

@@ -10,16 +10,19 @@
 namespace qk {
 namespace {
 
+// Element i of block b of a row (any of the three layouts).
+__device__ __forceinline__ float block_value(const uint8_t *row, int type, int nb, int b, int i) {
+    if (type == QK_TYPE_Q4_K) return q4k_value(row + b * 144, i);
+    return q6k_value(q6_fields(row, nb, b, type == QK_TYPE_Q6_K_SPLIT), i);
+}
+
 __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *w, float *out, int type, int nb,
-                                                           int row0, int nrows) {
+                                                           int64_t row_bytes, int row0, int nrows) {
     const int i = threadIdx.x;
-    const int bpb = type == QK_TYPE_Q4_K ? 144 : 210;
     const int64_t total = static_cast<int64_t>(nrows) * nb;
     for (int64_t blk = blockIdx.x; blk < total; blk += gridDim.x) {
         const int64_t r = blk / nb, b = blk - r * nb;
-        const uint8_t *block = w + ((row0 + r) * nb + b) * bpb;
-        float v = type == QK_TYPE_Q4_K ? q4k_value(block, i) : q6k_value(block, i);
-        out[blk * 256 + i] = v;
+        out[blk * 256 + i] = block_value(w + (row0 + r) * row_bytes, type, nb, static_cast<int>(b), i);
     }
 }
 
@@ -27,9 +30,9 @@ __global__ __launch_bounds__(256) void dequant_rows_kernel(const uint8_t *w, flo
 // (inferencer.cu:1426-1427) happens here: an id outside [0, vocab) reads
 // nothing and yields a NaN row.
 __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t *w, const int32_t *tokens, float *out,
-                                                        int type, int nb, int n_tokens, int vocab) {
+                                                        int type, int nb, int64_t row_bytes, int n_tokens,
+                                                        int vocab) {
     const int i = threadIdx.x;
-    const int bpb = type == QK_TYPE_Q4_K ? 144 : 210;
     const int64_t total = static_cast<int64_t>(n_tokens) * nb;
     for (int64_t blk = blockIdx.x; blk < total; blk += gridDim.x) {
         const int64_t t = blk / nb, b = blk - t * nb;
@@ -38,8 +41,29 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t *w, const 
             out[blk * 256 + i] = __builtin_nanf("");
             continue;
         }
-        const uint8_t *block = w + (static_cast<int64_t>(token) * nb + b) * bpb;
-        out[blk * 256 + i] = type == QK_TYPE_Q4_K ? q4k_value(block, i) : q6k_value(block, i);
+        out[blk * 256 + i] = block_value(w + static_cast<int64_t>(token) * row_bytes, type, nb, static_cast<int>(b), i);
+    }
+}
+
+// GGUF Q6_K rows -> split rows: one 64-thread workgroup per block moves its
+// 105 two-byte units (the source block is only 2-byte aligned): units 0..63
+// are ql, 64..95 qh, 96..103 scales, 104 d.  The workgroup of a row's last
+// block also zeroes the row's padding.
+__global__ __launch_bounds__(64) void q6k_split_kernel(const uint8_t *src, uint8_t *dst, int nb, int64_t dst_row_bytes,
+                                                       int64_t nblocks) {
+    for (int64_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+        const int64_t r = blk / nb;
+        const int b = static_cast<int>(blk - r * nb);
+        const uint8_t *s = src + blk * 210;
+        uint8_t *row = dst + r * dst_row_bytes;
+        const Q6Fields f = q6_fields(row, nb, b, true);
+        for (int u = threadIdx.x; u < 105; u += 64) {
+            const uint16_t v = static_cast<uint16_t>(load2(s + 2 * u));
+            const uint8_t *o = u < 64 ? f.ql + 2 * u : u < 96 ? f.qh + 2 * (u - 64) : u < 104 ? f.sc + 2 * (u - 96) : f.d;
+            __builtin_memcpy(const_cast<uint8_t *>(o), &v, 2);
+        }
+        if (b == nb - 1)
+            for (int64_t i = static_cast<int64_t>(nb) * 210 + threadIdx.x; i < dst_row_bytes; i += 64) row[i] = 0;
     }
 }
 
@@ -61,8 +85,8 @@ int qk_dequant_rows(int type, const void *w, float *out, int cols, int row0, int
     if (nrows == 0) return qk::ok();
     const int nb = cols / 256;
     hipLaunchKernelGGL(qk::dequant_rows_kernel, dim3(qk::grid_for(static_cast<int64_t>(nrows) * nb)), dim3(256),
-                       0, static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(w), out, type, nb, row0,
-                       nrows);
+                       0, static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(w), out, type, nb,
+                       qk::row_bytes(type, nb), row0, nrows);
     return qk::launch_status("qk_dequant_rows launch");
 }
 
@@ -76,8 +100,26 @@ int qk_embedding(int type, const void *w, const int32_t *tokens, int n_tokens, f
     const int nb = cols / 256;
     hipLaunchKernelGGL(qk::embedding_kernel, dim3(qk::grid_for(static_cast<int64_t>(n_tokens) * nb)), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const uint8_t *>(w), tokens, out, type, nb,
-                       n_tokens, vocab);
+                       qk::row_bytes(type, nb), n_tokens, vocab);
     return qk::launch_status("qk_embedding launch");
+}
+
+int qk_q6k_split(const void *src, void *dst, int cols, int rows, qk_stream stream) {
+    int st = qk::check_weights("qk_q6k_split", QK_TYPE_Q6_K, src, cols, rows);
+    if (st) return st;
+    if (!dst) return qk::fail(QK_ERR_INVALID_ARG, "qk_q6k_split: null destination");
+    if (!qk::aligned(dst, 16)) return qk::fail(QK_ERR_ALIGN, "qk_q6k_split: destination not 16-byte aligned");
+    const int nb = cols / 256;
+    const int64_t src_bytes = static_cast<int64_t>(rows) * nb * 210;
+    const int64_t dst_row = qk::row_bytes(QK_TYPE_Q6_K_SPLIT, nb);
+    const uint8_t *s = static_cast<const uint8_t *>(src);
+    const uint8_t *d = static_cast<const uint8_t *>(dst);
+    if (d < s + src_bytes && s < d + dst_row * rows)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_q6k_split: source and destination overlap");
+    const int64_t nblocks = static_cast<int64_t>(rows) * nb;
+    hipLaunchKernelGGL(qk::q6k_split_kernel, dim3(qk::grid_for(nblocks)), dim3(64), 0, static_cast<hipStream_t>(stream),
+                       s, static_cast<uint8_t *>(dst), nb, dst_row, nblocks);
+    return qk::launch_status("qk_q6k_split launch");
 }
 
 }  // extern "C"

@@ -41,7 +41,21 @@ namespace qk {
 namespace {
 
 constexpr int kMaxChunks = 16;
+// Workgroups per CU of the grid-stride GEMV kernels.  Each workgroup stages
+// the activations once, so a launch with few tiles per wave runs fewer
+// workgroups; a long launch over 16-byte aligned weight fields runs more
+// waves to keep more loads in flight (measured on MI355X, 1 token):
+//   gemv_wave, 128256 x 2048 split Q6_K: 40.0 us at 2 / CU, 38.6 us at 4
+//     (the GGUF Q6_K layout, bound by its misaligned field loads, slows to
+//     41.3 us at 4); Q4_K gate/up 2 x 8192 x 2048: 9.6 us at 2, 10.2 at 4.
+//   gemv_split, split Q6_K 2048 x 8192: 9.6 us at 2 / CU, 8.6 at 1; Q4_K
+//     3072 x 3072: 6.6 / 6.1; Q4_K 8192 x 3072: 8.7 / 10.1; split Q6_K
+//     128256 x 3072: 73.5 / 111.
 constexpr int kWaveBlocksPerCu = 2;
+constexpr int kWaveBlocksPerCuLong = 4;
+constexpr int kWaveLongTiles = 16;      // tiles per wave at kWaveBlocksPerCu
+constexpr int kSplitBlocksPerCu = 2;
+constexpr int kSplitShortTiles = 3;     // tiles per wave-group at kSplitBlocksPerCu
 // Activations staged per workgroup plus the split kernels' reduction slots.
 constexpr size_t kMaxLds = 64 * 1024;
 
@@ -81,10 +95,11 @@ struct Raw {
 };
 
 struct TileRef {
-    const uint8_t *blk;
+    const uint8_t *blk;   // the lane's block (GGUF layouts) or its row (split Q6_K)
     float *y;
     int row;
     int type;
+    int b;                // block index within the row
     bool valid;
 };
 
@@ -98,8 +113,9 @@ __device__ __forceinline__ TileRef locate(const GemvParams &p, int tile, int rit
     t.valid = t.row < M.rows;
     const int row = t.valid ? t.row : M.rows - 1;   // keep loads in bounds
     t.type = M.type;
+    t.b = piece_block;
     t.y = M.y + static_cast<int64_t>(token) * M.ldy;
-    const int bpb = M.type == QK_TYPE_Q4_K ? 144 : 210;
+    const int bpb = M.type == QK_TYPE_Q4_K ? 144 : M.type == QK_TYPE_Q6_K ? 210 : 0;
     t.blk = M.w + static_cast<size_t>(row) * M.row_bytes + static_cast<size_t>(piece_block) * bpb;
     return t;
 }
@@ -463,9 +479,22 @@ __device__ __forceinline__ bool is_q4k(int type) {
 }
 
 template <int TYPE>
-__device__ __forceinline__ Raw fetch_typed(const TileRef &t, int g, int h) {
+__device__ __forceinline__ bool is_q6s(int type) {
+    return TYPE == QK_TYPE_Q6_K_SPLIT || (TYPE == 0 && type == QK_TYPE_Q6_K_SPLIT);
+}
+
+// nb: blocks per row (the split layout's stream offsets).
+template <int TYPE>
+__device__ __forceinline__ Raw fetch_typed(const TileRef &t, int g, int h, int nb) {
     Raw r;
-    if (is_q4k<TYPE>(t.type)) {
+    if (is_q6s<TYPE>(t.type)) {
+        const Q6Fields f = q6_fields(t.blk, nb, t.b, true);   // every field 16-byte aligned
+        r.a = load16(f.ql + g * 64 + h * 16);
+        r.b = load16(f.ql + 32 + g * 64 + h * 16);
+        r.c = load16(f.qh + g * 32 + h * 16);
+        r.s = load8(f.sc + g * 8);
+        r.d = load2(f.d);
+    } else if (is_q4k<TYPE>(t.type)) {
         r.a = load16(t.blk);                              // d, dmin, scales
         r.b = load16(t.blk + 16 + g * 64 + h * 16);      // parts 0 / 1
         r.c = load16(t.blk + 48 + g * 64 + h * 16);      // parts 2 / 3
@@ -505,7 +534,7 @@ template <int TYPE>
 __device__ __forceinline__ Slot prep(const GemvParams &p, int tile, int rit, int piece, int token, int g, int h) {
     Slot s;
     s.t = locate(p, tile, rit, piece >> 2, token);
-    s.r = fetch_typed<TYPE>(s.t, g, h);
+    s.r = fetch_typed<TYPE>(s.t, g, h, p.pieces >> 2);
     return s;
 }
 
@@ -625,7 +654,7 @@ __global__ __launch_bounds__(256) void gemv_long(GemvParams p) {
             typename Policy::Lane L;
             Policy::load_direct(L, p, token, piece);
             const TileRef t = locate(p, tile, 0, piece >> 2, token);
-            const Raw r = fetch_typed<0>(t, g, h);
+            const Raw r = fetch_typed<0>(t, g, h, p.pieces >> 2);
             acc += piece_dot<Policy, 0>(t.type, r, L, g, h);
         }
         acc = group_sum<64>(acc);
@@ -679,10 +708,12 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
     if (p.chunks == 1) {
         const int block = 256, waves = block / 64;
         const void *k = reinterpret_cast<const void *>(gemv_wave<Policy, TYPE, GROUP>);
-        // Two workgroups (8 waves) per CU stream faster than the resident
-        // maximum: measured 41.9 vs 43.0 us on the 128256 x 2048 Q6_K LM head.
-        const int cap = std::max(1, std::min(resident_blocks(k, block, x_lds), kWaveBlocksPerCu * device_info().cus) /
-                                        n_tokens);
+        const int cus = device_info().cus;
+        const bool aligned = TYPE == QK_TYPE_Q4_K || TYPE == QK_TYPE_Q6_K_SPLIT;
+        const bool long_launch =
+            static_cast<int64_t>(p.total_tiles) * n_tokens >= int64_t(kWaveLongTiles) * kWaveBlocksPerCu * waves * cus;
+        const int per_cu = aligned && long_launch ? kWaveBlocksPerCuLong : kWaveBlocksPerCu;
+        const int cap = std::max(1, std::min(resident_blocks(k, block, x_lds), per_cu * cus) / n_tokens);
         const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
         hipLaunchKernelGGL((gemv_wave<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
     } else {
@@ -690,11 +721,14 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int block = wgroups * p.chunks * 64;
         const size_t lds = x_lds + static_cast<size_t>(wgroups) * 2 * p.tile_rows * p.chunks * sizeof(float);
         const void *k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP>);
-        // Every block stages the whole activation row; two blocks per CU keep
-        // that staging small next to the weights (down projection 2048 x 8192:
-        // 512 blocks instead of the resident 1024).
-        const int cap = std::max(1, std::min(resident_blocks(k, block, lds), kWaveBlocksPerCu * device_info().cus) /
-                                        n_tokens);
+        // Every block stages the whole activation row: two blocks per CU (one
+        // when each wave-group would see fewer than kSplitShortTiles tiles)
+        // keep that staging small next to the weights.
+        const int cus = device_info().cus;
+        const bool short_launch = static_cast<int64_t>(p.total_tiles) * n_tokens <
+                                  int64_t(kSplitShortTiles) * kSplitBlocksPerCu * wgroups * cus;
+        const int per_cu = short_launch ? 1 : kSplitBlocksPerCu;
+        const int cap = std::max(1, std::min(resident_blocks(k, block, lds), per_cu * cus) / n_tokens);
         const int grid = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
         hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
     }
@@ -730,7 +764,7 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
         M.y = mats[m].y;
         M.rows = mats[m].rows;
         M.type = mats[m].type;
-        M.row_bytes = nb * block_bytes(M.type);
+        M.row_bytes = static_cast<int>(row_bytes(M.type, nb));
         M.ldy = ldy ? ldy[m] : M.rows;
         M.tile_begin = static_cast<int>(tiles);
         tiles += (M.rows + p.tile_rows - 1) / p.tile_rows;
@@ -750,6 +784,8 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
         launch_group<Policy, QK_TYPE_Q4_K>(p, n_tokens, stream);
     } else if (type == QK_TYPE_Q6_K) {
         launch_group<Policy, QK_TYPE_Q6_K>(p, n_tokens, stream);
+    } else if (type == QK_TYPE_Q6_K_SPLIT) {
+        launch_group<Policy, QK_TYPE_Q6_K_SPLIT>(p, n_tokens, stream);
     } else {
         launch_group<Policy, 0>(p, n_tokens, stream);
     }

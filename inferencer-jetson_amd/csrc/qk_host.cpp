@@ -29,14 +29,19 @@ int launch_status(const char *where) {
 }
 
 int block_bytes(int type) {
-    return type == QK_TYPE_Q4_K ? 144 : type == QK_TYPE_Q6_K ? 210 : 0;
+    return type == QK_TYPE_Q4_K ? 144 : type == QK_TYPE_Q6_K || type == QK_TYPE_Q6_K_SPLIT ? 210 : 0;
+}
+
+int64_t row_bytes(int type, int nb) {
+    const int64_t raw = static_cast<int64_t>(nb) * block_bytes(type);
+    return type == QK_TYPE_Q6_K_SPLIT ? (raw + 15) / 16 * 16 : raw;
 }
 
 int check_weights(const char *where, int type, const void *w, int cols, int rows) {
     // Mirrors FastGPU::matvec's checks (inferencer.cu:1157-1158) and the
     // quantized shape rule (inferencer.cu:254-256), plus the alignment the
     // GGUF data section guarantees (inferencer.cu:270-272).
-    if (type != QK_TYPE_Q4_K && type != QK_TYPE_Q6_K)
+    if (!block_bytes(type))
         return fail(QK_ERR_TYPE, std::string(where) + ": unsupported storage type " + std::to_string(type));
     if (cols <= 0 || cols % 256 != 0 || rows < 1)
         return fail(QK_ERR_SHAPE, std::string(where) + ": unexpected quantized matrix shape " +
@@ -90,8 +95,8 @@ int qk_block_bytes(int type) { return qk::block_bytes(type); }
 
 int64_t qk_tensor_bytes(int type, int64_t cols, int64_t rows) {
     int bpb = qk::block_bytes(type);
-    if (!bpb || cols <= 0 || cols % 256 || rows < 0) return -1;
-    return cols / 256 * bpb * rows;
+    if (!bpb || cols <= 0 || cols % 256 || rows < 0 || cols / 256 > (1 << 24)) return -1;
+    return qk::row_bytes(type, static_cast<int>(cols / 256)) * rows;
 }
 
 }  // extern "C"

@@ -39,6 +39,9 @@ int launch_status(const char *where);
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 int block_bytes(int type);
+// Bytes of one row of nb blocks: nb * 144 (Q4_K), nb * 210 (Q6_K), nb * 210
+// rounded up to 16 (split Q6_K, so every row starts 16-byte aligned).
+int64_t row_bytes(int type, int nb);
 // Validates a Q4_K / Q6_K weight operand shape; returns QK_OK or a status.
 int check_weights(const char *where, int type, const void *w, int cols, int rows);
 
@@ -161,15 +164,34 @@ __device__ __forceinline__ float q4k_value(const uint8_t *block, int i) {
     return d * static_cast<float>(sc) * static_cast<float>(q) - dmin * static_cast<float>(m);
 }
 
-__device__ __forceinline__ float q6k_value(const uint8_t *block, int i) {
+// The four fields of a Q6_K block: ql (128 B), qh (64 B), scales (16 B), d.
+struct Q6Fields {
+    const uint8_t *ql, *qh, *sc, *d;
+};
+
+// Block b of a row of nb blocks starting at `row`: contiguous in the GGUF
+// layout, or in the split layout (QK_TYPE_Q6_K_SPLIT) the row's ql [nb][128],
+// qh [nb][64], scales [nb][16] and d [nb] streams, every field 16-byte
+// aligned when the row is.
+__device__ __forceinline__ Q6Fields q6_fields(const uint8_t *row, int nb, int b, bool split) {
+    if (split) return {row + b * 128, row + nb * 128 + b * 64, row + nb * 192 + b * 16, row + nb * 208 + b * 2};
+    const uint8_t *blk = row + b * 210;
+    return {blk, blk + 128, blk + 192, blk + 208};
+}
+
+__device__ __forceinline__ float q6k_value(const Q6Fields &f, int i) {
     int group = i >> 7, p = i & 127, lane = p & 31, part = p >> 5;
-    int low = block[group * 64 + (part & 1) * 32 + lane];
+    int low = f.ql[group * 64 + (part & 1) * 32 + lane];
     low = part < 2 ? (low & 15) : (low >> 4);
-    int high = (block[128 + group * 32 + lane] >> (part * 2)) & 3;
+    int high = (f.qh[group * 32 + lane] >> (part * 2)) & 3;
     int q = (low | (high << 4)) - 32;
-    float d = f16_bits_to_f32(load2(block + 208));
-    int sc = static_cast<int8_t>(block[192 + group * 8 + part * 2 + (lane >> 4)]);
+    float d = f16_bits_to_f32(load2(f.d));
+    int sc = static_cast<int8_t>(f.sc[group * 8 + part * 2 + (lane >> 4)]);
     return d * static_cast<float>(sc) * static_cast<float>(q);
+}
+
+__device__ __forceinline__ float q6k_value(const uint8_t *block, int i) {
+    return q6k_value(Q6Fields{block, block + 128, block + 192, block + 208}, i);
 }
 
 // Lane-group sums within a wave (DPP row operations, then cross-row

@@ -34,6 +34,7 @@ struct qk_llama {
     int32_t *d_next = nullptr, *d_token = nullptr;
     int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
     int last_next = -1;
+    std::vector<void *> owned;    // split-layout copies of the Q6_K weights
 };
 
 namespace {
@@ -51,10 +52,46 @@ void release(qk_llama *m) {
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
+    for (void *b : m->owned) (void)hipFree(b);
     delete m;
 }
 
-bool quant_type(int t) { return t == QK_TYPE_Q4_K || t == QK_TYPE_Q6_K; }
+bool quant_type(int t) { return t == QK_TYPE_Q4_K || t == QK_TYPE_Q6_K || t == QK_TYPE_Q6_K_SPLIT; }
+
+// A Q6_K tensor in the GGUF layout is copied once into the split layout
+// (QK_TYPE_Q6_K_SPLIT: every field a kernel reads 16-byte aligned) and the
+// driver uses the copy; the caller keeps its weights.
+int split_tensor(std::vector<void *> &owned, int &type, const void *&w, int cols, int rows, hipStream_t s) {
+    if (type != QK_TYPE_Q6_K) return QK_OK;
+    void *dst = nullptr;
+    if (hipMalloc(&dst, static_cast<size_t>(qk_tensor_bytes(QK_TYPE_Q6_K_SPLIT, cols, rows))) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "cannot allocate a split-layout Q6_K copy");
+    owned.push_back(dst);
+    if (int st = qk_q6k_split(w, dst, cols, rows, s)) return st;
+    type = QK_TYPE_Q6_K_SPLIT;
+    w = dst;
+    return QK_OK;
+}
+
+int split_weights(std::vector<void *> &owned, qk_llama_weights &w, std::vector<qk_llama_layer> &layers,
+                  const qk_llama_config &c, int kv_dim, hipStream_t s) {
+    int st;
+    for (qk_llama_layer &L : layers)
+        if ((st = split_tensor(owned, L.q_type, L.q, c.dim, c.dim, s)) ||
+            (st = split_tensor(owned, L.k_type, L.k, c.dim, kv_dim, s)) ||
+            (st = split_tensor(owned, L.v_type, L.v, c.dim, kv_dim, s)) ||
+            (st = split_tensor(owned, L.o_type, L.o, c.dim, c.dim, s)) ||
+            (st = split_tensor(owned, L.gate_type, L.gate, c.dim, c.hidden, s)) ||
+            (st = split_tensor(owned, L.up_type, L.up, c.dim, c.hidden, s)) ||
+            (st = split_tensor(owned, L.down_type, L.down, c.hidden, c.dim, s)))
+            return st;
+    if ((st = split_tensor(owned, w.embd_type, w.token_embd, c.dim, c.vocab, s))) return st;
+    if (w.output && (st = split_tensor(owned, w.output_type, w.output, c.dim, c.vocab, s))) return st;
+    // The copies are complete before create returns: the caller may release
+    // its Q6_K buffers from then on.
+    if (hipStreamSynchronize(s) != hipSuccess) return qk::fail(QK_ERR_DEVICE, "Q6_K split copies failed");
+    return QK_OK;
+}
 
 }  // namespace
 
@@ -78,7 +115,7 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
     if (head_dim % 4 || 256 % head_dim)
         return qk::fail(QK_ERR_LIMIT, "qk_llama_create: head_dim must be a multiple of 4 dividing 256");
     if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
-        return qk::fail(QK_ERR_TYPE, "qk_llama_create: embedding and output must be Q4_K or Q6_K");
+        return qk::fail(QK_ERR_TYPE, "qk_llama_create: embedding and output must be Q4_K or Q6_K (either layout)");
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = w->layers[l];
         if (!quant_type(L.q_type) || !quant_type(L.k_type) || !quant_type(L.v_type) || !quant_type(L.o_type) ||
@@ -144,6 +181,11 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         release(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_create: table upload failed");
     }
+    if ((st = split_weights(m->owned, m->w, m->layers, c, m->kv_dim, m->stream))) {
+        release(m);
+        return st;
+    }
+    m->w.layers = m->layers.data();
     *out = m;
     return qk::ok();
 }
@@ -262,6 +304,7 @@ struct qk_llama_batch {
     int32_t *d_tokens = nullptr, *d_next = nullptr;
     qk_batch_token *d_desc = nullptr;
     uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, results
+    std::vector<void *> owned;    // split-layout copies of the Q6_K weights
 };
 
 namespace {
@@ -273,6 +316,7 @@ void release_batch(qk_llama_batch *m) {
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
+    for (void *b : m->owned) (void)hipFree(b);
     delete m;
 }
 
@@ -298,7 +342,7 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     if (!qk::attention_supported(c.heads / c.kv_heads, head_dim))
         return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: head layout outside the attention kernel");
     if (!quant_type(w->embd_type) || (w->output && !quant_type(w->output_type)))
-        return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: embedding and output must be Q4_K or Q6_K");
+        return qk::fail(QK_ERR_TYPE, "qk_llama_batch_create: embedding and output must be Q4_K or Q6_K (either layout)");
     if (!qk::gemv_fusable(c.dim) || !qk::gemv_fusable(c.hidden))
         return qk::fail(QK_ERR_LIMIT, "qk_llama_batch_create: dim or hidden too long to stage the activations");
     if (!qk::aligned(w->output_norm, 16))
@@ -374,6 +418,11 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         release_batch(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_create: table upload failed");
     }
+    if ((st = split_weights(m->owned, m->w, m->layers, c, m->kv_dim, m->stream))) {
+        release_batch(m);
+        return st;
+    }
+    m->w.layers = m->layers.data();
     *out = m;
     return qk::ok();
 }

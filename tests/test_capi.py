@@ -62,6 +62,17 @@ def test_tensor_bytes_match_reference_size_rule(qk, qtype, cols, rows, want):
     assert qk.tensor_bytes(qtype, cols, rows) == want
 
 
+@pytest.mark.parametrize("cols,rows", [(256, 1), (2048, 128256), (3072, 5), (8192, 3)])
+def test_split_tensor_bytes_pad_rows_to_16(qk, cols, rows):
+    """The split Q6_K layout keeps 210 bytes per block and rounds each row
+    up to a 16-byte multiple."""
+    lib = qk.lib()
+    want = (cols // 256 * 210 + 15) // 16 * 16 * rows
+    assert lib.qk_block_bytes(114) == 210
+    assert lib.qk_tensor_bytes(114, cols, rows) == want
+    assert qk.tensor_bytes(114, cols, rows) == want
+
+
 def test_block_bytes_rejects_other_types(qk):
     lib = qk.lib()
     assert lib.qk_block_bytes(0) == 0 and lib.qk_block_bytes(13) == 0
