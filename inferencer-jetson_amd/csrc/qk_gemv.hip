@@ -224,15 +224,21 @@ __device__ __forceinline__ XGroup make_group_regs(const float *v) {
 }
 
 // sum_i code_i * x_i of one part: codes are four dwords of byte codes 0..63.
+// The L1 and L0 dots share one integer accumulator: for 16 codes below 64
+// and limbs of at most 128 in magnitude, |256 * sum(c * L1) + sum(c * L0)|
+// < 257 * 16 * 63 * 128 < 2^25, so it is exact, and its conversion rounds
+// once, like fma(float(d1), 256, float(d0)).
 __device__ __forceinline__ float limb_dot(const uint32_t *codes, const int *limb, float scale) {
-    int d0 = 0, d1 = 0, d2 = 0;
+    int d01 = 0, d2 = 0;
     #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        d0 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[k], d0, false);
-        d1 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[4 + k], d1, false);
+        d01 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[4 + k], d01, false);
         d2 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[8 + k], d2, false);
     }
-    return fmaf(static_cast<float>(d2), 65536.f, fmaf(static_cast<float>(d1), 256.f, static_cast<float>(d0))) * scale;
+    d01 <<= 8;
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) d01 = __builtin_amdgcn_sdot4(static_cast<int>(codes[k]), limb[k], d01, false);
+    return fmaf(static_cast<float>(d2), 65536.f, static_cast<float>(d01)) * scale;
 }
 
 struct F32Policy {
