@@ -152,6 +152,20 @@ int qk_embedding(int type, const void *w, const int32_t *tokens, int n_tokens, f
 int qk_quantize_x32(const float *x, int ldx, int8_t *xq, int ldxq, float *xscale, int ldscale,
                     int cols, int n_tokens, qk_stream stream);
 
+/* RMSNorm and the per-32 quantization in one launch: out = x * 1/sqrt(
+   mean(x^2) + eps) * weight exactly as qk_rmsnorm_f32 (out may be NULL to
+   skip the fp32 copy), then xq / xscale of those values exactly as
+   qk_quantize_x32 -- bit-identical to the two calls in sequence.  Token t
+   reads x + t*ldx and writes out + t*ldout, xq + t*ldxq, xscale + t*ldscale.
+   cols % 32 == 0 (QK_ERR_SHAPE); x, weight and out 16-byte aligned with ldx,
+   ldout multiples of 4, xq 4-byte aligned with ldxq a multiple of 4
+   (QK_ERR_ALIGN).  Replaces rmsnorm_quantize_cuda and
+   rmsnorm_quantize_batch_cuda (inferencer.cu:839-889; the reference's batch
+   strides are 8192 and 256). */
+int qk_rmsnorm_quantize_x32(const float *x, int ldx, const float *weight, float *out, int ldout,
+                            int8_t *xq, int ldxq, float *xscale, int ldscale, int cols, int n_tokens,
+                            float eps, qk_stream stream);
+
 /* INT8-activation GEMV for n_tokens tokens (1 = decode): exact integer
    sub-block dots, fp32 combine.  Replaces gemv_q4_dp4a / gemv_q6_dp4a
    (inferencer.cu:558-569, 663-674) and gemv_batch_dp4a

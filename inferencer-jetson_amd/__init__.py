@@ -89,6 +89,7 @@ SIGNATURES = {
     "qk_embedding": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _vp]),
     "qk_q6k_split": (_i, [_vp, _vp, _i, _i, _vp]),
     "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "qk_rmsnorm_quantize_x32": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "qk_rope_kv_write": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
@@ -283,6 +284,20 @@ def quantize(x, xq, xscale, cols: int, n_tokens: int = 1, ldx: int | None = None
     ldscale = (cols + 31) // 32 if ldscale is None else ldscale
     check(lib().qk_quantize_x32(ptr(x), ldx, ptr(xq), ldxq, ptr(xscale), ldscale, cols, n_tokens,
                                 stream_handle(stream)), "activation quantization launch")
+
+
+def rmsnorm_quantize(x, weight, out, xq, xscale, cols: int, n_tokens: int = 1, eps: float = 1e-5,
+                     ldx: int | None = None, ldout: int | None = None, ldxq: int | None = None,
+                     ldscale: int | None = None, stream=None) -> None:
+    """rmsnorm_quantize_cuda / rmsnorm_quantize_batch_cuda (inferencer.cu:839-889): RMSNorm then the
+    per-32 quantization in one launch (out may be None)."""
+    ldx = cols if ldx is None else ldx
+    ldout = cols if ldout is None else ldout
+    ldxq = cols if ldxq is None else ldxq
+    ldscale = cols // 32 if ldscale is None else ldscale
+    check(lib().qk_rmsnorm_quantize_x32(ptr(x), ldx, ptr(weight), ptr(out), ldout, ptr(xq), ldxq, ptr(xscale),
+                                        ldscale, cols, n_tokens, eps, stream_handle(stream)),
+          "fused RMSNorm quantization launch")
 
 
 def matvec_i8(t: Tensor, xq, xscale, out, cols: int, rows: int, n_tokens: int = 1, ldxq: int | None = None,

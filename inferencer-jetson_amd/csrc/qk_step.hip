@@ -83,6 +83,57 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float *x, const floa
     for (int i = threadIdx.x; i < n; i += 256) ot[i] = xt[i] * scale * weight[i];
 }
 
+// rmsnorm_quantize_cuda / rmsnorm_quantize_batch_cuda (inferencer.cu:839-889):
+// one 256-thread block per token normalises the row exactly as rmsnorm_kernel's
+// float4 path (same sum-of-squares order, same scale) and quantizes it in the
+// same pass: a 32-value group is eight float4 of eight adjacent lanes, whose
+// amax meets in three xor shuffles; scale and rounding are those of
+// quantize_x32_kernel, so xq / xscale equal the two-launch result bit for bit.
+// The reference reduces the row once per 32-value block; here once per token.
+__global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float *x, int ldx, const float *weight,
+                                                               float *out, int ldout, int8_t *xq, int ldxq,
+                                                               float *xscale, int ldscale, int n, float eps) {
+    __shared__ float scratch[4];
+    const int64_t token = blockIdx.x;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + token * ldx);
+    const float4 *w4 = reinterpret_cast<const float4 *>(weight);
+    const int n4 = n >> 2;
+    float ss = 0.f;
+    #pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = x4[i];
+        ss = fmaf(v.x, v.x, ss);
+        ss = fmaf(v.y, v.y, ss);
+        ss = fmaf(v.z, v.z, ss);
+        ss = fmaf(v.w, v.w, ss);
+    }
+    ss = block_sum256(ss, scratch);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+    float4 *o4 = out ? reinterpret_cast<float4 *>(out + token * ldout) : nullptr;
+    uint32_t *q4 = reinterpret_cast<uint32_t *>(xq + token * ldxq);
+    float *st = xscale + token * ldscale;
+    // n4 is a multiple of 8, so the eight lanes of a group are all in range
+    // together and the shuffles never mix groups.
+    #pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += 256) {
+        const float4 v = x4[i], w = w4[i];
+        const float4 o = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+        if (o4) o4[i] = o;
+        float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        const float gs = amax > 0.f ? amax / 127.f : 1.f;
+        if ((i & 7) == 0) st[i >> 3] = gs;
+        auto q8 = [gs](float val) {
+            int q = static_cast<int>(rintf(val / gs));
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            return static_cast<uint32_t>(q) & 0xFFu;
+        };
+        q4[i] = q8(o.x) | (q8(o.y) << 8) | (q8(o.z) << 16) | (q8(o.w) << 24);
+    }
+}
+
 // rope_cache_cuda (inferencer.cu:930-951) for any head_dim: rotate adjacent
 // pairs of q in place; rotate k into the key cache and copy v.
 __global__ void rope_kv_kernel(float *q, const float *k, const float *v, const float *cosine, const float *sine,
@@ -729,6 +780,23 @@ int qk_rmsnorm_f32(const float *x, const float *weight, float *out, int n, int n
     const int vec4 = n % 4 == 0 && qk::aligned(x, 16) && qk::aligned(weight, 16) && qk::aligned(out, 16);
     hipLaunchKernelGGL(qk::rmsnorm_kernel, dim3(n_tokens), dim3(256), 0, qk::S(stream), x, weight, out, n, eps, vec4);
     return qk::launch_status("qk_rmsnorm_f32 launch");
+}
+
+int qk_rmsnorm_quantize_x32(const float *x, int ldx, const float *weight, float *out, int ldout, int8_t *xq,
+                            int ldxq, float *xscale, int ldscale, int cols, int n_tokens, float eps,
+                            qk_stream stream) {
+    if (!x || !weight || !xq || !xscale || cols < 1 || n_tokens < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_rmsnorm_quantize_x32: null pointer or bad size");
+    if (cols % 32) return qk::fail(QK_ERR_SHAPE, "qk_rmsnorm_quantize_x32: cols must be a multiple of 32");
+    if (n_tokens == 0) return qk::ok();
+    if (ldx < cols || ldxq < cols || ldscale < cols / 32 || (out && ldout < cols))
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_rmsnorm_quantize_x32: leading dimension smaller than the row");
+    if (!qk::aligned(x, 16) || !qk::aligned(weight, 16) || (out && !qk::aligned(out, 16)) || !qk::aligned(xq, 4) ||
+        ldx % 4 || (out && ldout % 4) || ldxq % 4)
+        return qk::fail(QK_ERR_ALIGN, "qk_rmsnorm_quantize_x32: x, weight, out need 16-byte rows, xq 4-byte rows");
+    hipLaunchKernelGGL(qk::rmsnorm_quantize_kernel, dim3(n_tokens), dim3(256), 0, qk::S(stream), x, ldx, weight, out,
+                       ldout, xq, ldxq, xscale, ldscale, cols, eps);
+    return qk::launch_status("qk_rmsnorm_quantize_x32 launch");
 }
 
 int qk_rope_kv_write(float *q, const float *k, const float *v, const float *cosine, const float *sine,

@@ -128,6 +128,20 @@ def test_int8_validation(qk):
     assert lib.qk_gemv_i8(12, w, None, 2048, xs, 64, y, 16, 2048, 16, 1, None) == qk.QK_ERR_INVALID_ARG
 
 
+def test_rmsnorm_quantize_validation(qk):
+    lib = qk.lib()
+    x, w, o, xq, xs = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    f = lib.qk_rmsnorm_quantize_x32
+    assert f(x, 2048, w, o, 2048, xq, 2048, xs, 64, 2048, 0, 1e-5, None) == qk.QK_OK        # no tokens
+    assert f(None, 2048, w, o, 2048, xq, 2048, xs, 64, 2048, 1, 1e-5, None) == qk.QK_ERR_INVALID_ARG
+    assert f(x, 2048, w, o, 2048, xq, 2048, xs, 64, 2040, 1, 1e-5, None) == qk.QK_ERR_SHAPE  # cols % 32
+    assert f(x, 2048, w, o, 2048, xq, 2048, xs, 63, 2048, 1, 1e-5, None) == qk.QK_ERR_INVALID_ARG
+    assert f(x + 4, 2048, w, o, 2048, xq, 2048, xs, 64, 2048, 1, 1e-5, None) == qk.QK_ERR_ALIGN
+    assert f(x, 2050, w, o, 2048, xq, 2048, xs, 64, 2048, 1, 1e-5, None) == qk.QK_ERR_ALIGN
+    assert f(x, 2048, w, o, 2048, xq + 2, 2048, xs, 64, 2048, 1, 1e-5, None) == qk.QK_ERR_ALIGN
+    assert f(x, 2048, w, o, 2048, xq, 2050, xs, 64, 2048, 1, 1e-5, None) == qk.QK_ERR_ALIGN
+
+
 def test_batched_workspace_sizes(qk):
     lib = qk.lib()
     assert lib.qk_gemv_batched_workspace_bytes(0, 64, 32) == 0
