@@ -55,6 +55,8 @@ extern "C" {
 #define QK_ERR_ALIGN 4         /* base pointer or leading dimension misaligned */
 #define QK_ERR_DEVICE 5        /* HIP runtime error at launch */
 #define QK_ERR_LIMIT 6         /* size beyond what the kernels index */
+#define QK_ERR_FORMAT 7        /* malformed or unsupported GGUF file */
+#define QK_ERR_IO 8            /* file cannot be opened or mapped */
 
 typedef void *qk_stream;
 
@@ -338,6 +340,64 @@ int qk_llama_batch_logits(qk_llama_batch *m, const float **logits);
    and the call synchronises the stream; otherwise it stays asynchronous. */
 int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
                            int need_logits, int32_t *next_tokens);
+
+/* --------------------------------------------------------------- GGUF -- */
+
+/* A GGUF v3 model file, mapped read-only (the reference's GGUF struct,
+   inferencer.cu:204-340).  Scalar metadata is kept as doubles, string values
+   as strings, tokenizer.ggml.tokens / merges as string arrays; other arrays
+   are skipped.  Tensors may be FP32 (0), FP16 (1), Q4_K (12) or Q6_K (14).
+   Stricter than the reference: every tensor's offset + bytes must lie inside
+   the data section (the reference checks offset < size, inferencer.cu:282),
+   offsets must be multiples of general.alignment, and names must be unique;
+   each violation is QK_ERR_FORMAT. */
+typedef struct qk_gguf qk_gguf;
+
+typedef struct qk_gguf_tensor {
+    const char *name;      /* valid until qk_gguf_close */
+    int type;              /* 0 FP32, 1 FP16, 12 Q4_K, 14 Q6_K */
+    int n_dims;            /* 1..4 */
+    int64_t dims[4];       /* dims[0] is contiguous (cols); unused dims are 1 */
+    uint64_t offset;       /* from the start of the data section */
+    uint64_t bytes;
+    const void *host;      /* inside the mapping */
+    const void *device;    /* after qk_gguf_upload, else NULL */
+} qk_gguf_tensor;
+
+/* QK_ERR_IO if the file cannot be opened or mapped, QK_ERR_FORMAT with the
+   reason in qk_last_error() if it is not a valid GGUF v3 file. */
+int qk_gguf_open(const char *path, qk_gguf **out);
+/* Unmaps the file and frees the device copy. */
+int qk_gguf_close(qk_gguf *g);
+/* A scalar metadata value (GGUF::param, inferencer.cu:290-294); missing keys
+   are QK_ERR_INVALID_ARG. */
+int qk_gguf_param(const qk_gguf *g, const char *key, double *value);
+/* A string metadata value, or NULL. */
+const char *qk_gguf_string(const qk_gguf *g, const char *key);
+int64_t qk_gguf_tensor_count(const qk_gguf *g);
+/* Tensors in file order. */
+int qk_gguf_tensor_at(const qk_gguf *g, int64_t index, qk_gguf_tensor *out);
+/* GGUF::tensor (inferencer.cu:317-321); missing names are QK_ERR_INVALID_ARG. */
+int qk_gguf_find_tensor(const qk_gguf *g, const char *name, qk_gguf_tensor *out);
+/* which = 0: tokenizer.ggml.tokens, 1: tokenizer.ggml.merges. */
+int64_t qk_gguf_token_count(const qk_gguf *g, int which);
+/* The bytes of entry i (not NUL-terminated; *length receives the size). */
+const char *qk_gguf_token(const qk_gguf *g, int which, int64_t i, int64_t *length);
+/* The mapped data section, its size and the alignment in effect. */
+int qk_gguf_data(const qk_gguf *g, const void **host, uint64_t *bytes, uint64_t *alignment);
+/* Copies the data section into one device buffer owned by the handle
+   (GGUF::upload, inferencer.cu:322-339: same free-memory margin) and sets
+   every tensor's device pointer.  Synchronises the stream. */
+int qk_gguf_upload(qk_gguf *g, qk_stream stream);
+/* The llama.* hyper-parameters and every tensor of a Llama model by its GGUF
+   name (FastRunner's constructor, inferencer.cu:1196-1214, any shape the
+   decode drivers support), ready for qk_llama_create: matrices Q4_K or Q6_K
+   with dims {cols, rows}, norms FP32 of dims {dim}; output.weight optional
+   (tied to token_embd.weight).  llama.vocab_size when present, else the
+   embedding's row count.  Requires qk_gguf_upload; layers receives
+   cfg.layers entries (at most max_layers); w->layers points at it. */
+int qk_gguf_llama(const qk_gguf *g, int context, qk_llama_config *cfg, qk_llama_weights *w,
+                  qk_llama_layer *layers, int max_layers);
 
 #ifdef __cplusplus
 }

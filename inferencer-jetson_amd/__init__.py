@@ -36,6 +36,8 @@ QK_ERR_TYPE = 3
 QK_ERR_ALIGN = 4
 QK_ERR_DEVICE = 5
 QK_ERR_LIMIT = 6
+QK_ERR_FORMAT = 7
+QK_ERR_IO = 8
 
 
 class QKError(RuntimeError):
@@ -71,6 +73,13 @@ class qk_llama_weights(ctypes.Structure):
     _fields_ = [("embd_type", ctypes.c_int), ("token_embd", ctypes.c_void_p), ("output_type", ctypes.c_int),
                 ("output", ctypes.c_void_p), ("output_norm", ctypes.c_void_p),
                 ("layers", ctypes.POINTER(qk_llama_layer))]
+
+
+class qk_gguf_tensor(ctypes.Structure):
+    """One tensor-table entry of a GGUF file (include/qk.h)."""
+    _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int), ("n_dims", ctypes.c_int),
+                ("dims", ctypes.c_int64 * 4), ("offset", ctypes.c_uint64), ("bytes", ctypes.c_uint64),
+                ("host", ctypes.c_void_p), ("device", ctypes.c_void_p)]
 
 
 _i, _vp, _f = ctypes.c_int, ctypes.c_void_p, ctypes.c_float
@@ -119,6 +128,20 @@ SIGNATURES = {
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
+    "qk_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_gguf_close": (_i, [_vp]),
+    "qk_gguf_param": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
+    "qk_gguf_string": (ctypes.c_char_p, [_vp, ctypes.c_char_p]),
+    "qk_gguf_tensor_count": (ctypes.c_int64, [_vp]),
+    "qk_gguf_tensor_at": (_i, [_vp, ctypes.c_int64, ctypes.POINTER(qk_gguf_tensor)]),
+    "qk_gguf_find_tensor": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(qk_gguf_tensor)]),
+    "qk_gguf_token_count": (ctypes.c_int64, [_vp, _i]),
+    "qk_gguf_token": (_vp, [_vp, _i, ctypes.c_int64, ctypes.POINTER(ctypes.c_int64)]),
+    "qk_gguf_data": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_uint64),
+                          ctypes.POINTER(ctypes.c_uint64)]),
+    "qk_gguf_upload": (_i, [_vp, _vp]),
+    "qk_gguf_llama": (_i, [_vp, _i, ctypes.POINTER(qk_llama_config), ctypes.POINTER(qk_llama_weights),
+                           ctypes.POINTER(qk_llama_layer), _i]),
 }
 
 _LIB = None
@@ -341,19 +364,115 @@ def _upload_weights(owner, cfg: dict, weights: dict):
     return c, w
 
 
+class GGUF:
+    """A GGUF v3 model file (the reference's GGUF struct, inferencer.cu:204-340)
+    through qk_gguf_*: parameters, string values, tokenizer arrays, the
+    tensor table, and the device copy made by upload()."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        check(lib().qk_gguf_open(str(path).encode(), ctypes.byref(h)), "GGUF")
+        self.handle = h
+        self.path = str(path)
+
+    def close(self):
+        if getattr(self, "handle", None):
+            lib().qk_gguf_close(self.handle)
+            self.handle = None
+
+    __del__ = close
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def param(self, key: str) -> float:
+        v = ctypes.c_double()
+        check(lib().qk_gguf_param(self.handle, key.encode(), ctypes.byref(v)), "GGUF parameter")
+        return v.value
+
+    def string(self, key: str):
+        v = lib().qk_gguf_string(self.handle, key.encode())
+        return None if v is None else v.decode("utf-8", "surrogateescape")
+
+    def tensors(self) -> list:
+        out = []
+        for i in range(lib().qk_gguf_tensor_count(self.handle)):
+            t = qk_gguf_tensor()
+            check(lib().qk_gguf_tensor_at(self.handle, i, ctypes.byref(t)), "GGUF tensor")
+            out.append(t)
+        return out
+
+    def tensor(self, name: str) -> qk_gguf_tensor:
+        t = qk_gguf_tensor()
+        check(lib().qk_gguf_find_tensor(self.handle, name.encode(), ctypes.byref(t)), "GGUF tensor")
+        return t
+
+    def host_bytes(self, name: str):
+        """A copy of a tensor's bytes from the mapping (numpy uint8)."""
+        import numpy as np
+        t = self.tensor(name)
+        return np.frombuffer(ctypes.string_at(t.host, t.bytes), dtype=np.uint8).copy()
+
+    def tokens(self, which: int = 0) -> list:
+        """tokenizer.ggml.tokens (0) or tokenizer.ggml.merges (1) as bytes."""
+        out = []
+        n = ctypes.c_int64()
+        for i in range(lib().qk_gguf_token_count(self.handle, which)):
+            p = lib().qk_gguf_token(self.handle, which, i, ctypes.byref(n))
+            out.append(ctypes.string_at(p, n.value) if n.value else b"")
+        return out
+
+    def data(self):
+        p, n, a = ctypes.c_void_p(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().qk_gguf_data(self.handle, ctypes.byref(p), ctypes.byref(n), ctypes.byref(a)), "GGUF data")
+        return p.value, n.value, a.value
+
+    def upload(self, stream=None) -> None:
+        check(lib().qk_gguf_upload(self.handle, stream_handle(stream)), "GGUF upload")
+
+    def llama(self, context: int):
+        """(qk_llama_config, qk_llama_weights, layer array) of the uploaded model."""
+        c, w = qk_llama_config(), qk_llama_weights()
+        n = int(self.param("llama.block_count"))
+        layers = (qk_llama_layer * max(n, 1))()
+        check(lib().qk_gguf_llama(self.handle, context, ctypes.byref(c), ctypes.byref(w), layers, n), "GGUF llama")
+        return c, w, layers
+
+
+def _config_dict(c: qk_llama_config) -> dict:
+    return {k: getattr(c, k) for k in ("dim", "layers", "heads", "kv_heads", "hidden", "vocab", "context", "eps",
+                                       "rope_theta")}
+
+
 class Runner:
     """FastRunner (inferencer.cu:1182-1532) over the C ABI's decode driver.
 
     weights is a dict of host numpy arrays (workloads.llama_weights layout);
-    they are copied to device memory owned by this object."""
+    they are copied to device memory owned by this object.  from_gguf builds
+    it from an uploaded GGUF file instead."""
 
     def __init__(self, cfg: dict, weights: dict, stream=None):
         self.cfg = cfg
         c, w = _upload_weights(self, cfg, weights)
+        self._create(c, w, stream)
+
+    def _create(self, c, w, stream):
         h = ctypes.c_void_p()
         check(lib().qk_llama_create(ctypes.byref(c), ctypes.byref(w), stream_handle(stream), ctypes.byref(h)),
               "FastRunner")
         self.handle = h
+
+    @classmethod
+    def from_gguf(cls, model: GGUF, context: int, stream=None) -> "Runner":
+        self = cls.__new__(cls)
+        c, w, self._layers = model.llama(context)
+        self._model = model
+        self.cfg = _config_dict(c)
+        self._create(c, w, stream)
+        return self
 
     def close(self):
         if getattr(self, "handle", None):
@@ -388,10 +507,24 @@ class BatchRunner:
         self.cfg = cfg
         self.cache_rows = cache_rows
         c, w = _upload_weights(self, cfg, weights)
+        self._create(c, w, max_tokens, cache_rows, stream)
+
+    def _create(self, c, w, max_tokens, cache_rows, stream):
         h = ctypes.c_void_p()
         check(lib().qk_llama_batch_create(ctypes.byref(c), ctypes.byref(w), max_tokens, cache_rows,
                                           stream_handle(stream), ctypes.byref(h)), "batched runner")
         self.handle = h
+
+    @classmethod
+    def from_gguf(cls, model: GGUF, context: int, max_tokens: int, cache_rows: int, stream=None) -> "BatchRunner":
+        """context bounds every token's position (the RoPE table length)."""
+        self = cls.__new__(cls)
+        c, w, self._layers = model.llama(context)
+        self._model = model
+        self.cfg = _config_dict(c)
+        self.cache_rows = cache_rows
+        self._create(c, w, max_tokens, cache_rows, stream)
+        return self
 
     def close(self):
         if getattr(self, "handle", None):

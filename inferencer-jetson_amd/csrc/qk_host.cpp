@@ -85,6 +85,8 @@ const char *qk_status_string(int status) {
         case QK_ERR_ALIGN: return "misaligned pointer or leading dimension";
         case QK_ERR_DEVICE: return "HIP device error";
         case QK_ERR_LIMIT: return "size beyond kernel limits";
+        case QK_ERR_FORMAT: return "malformed or unsupported GGUF file";
+        case QK_ERR_IO: return "file cannot be opened or mapped";
         default: return "unknown status";
     }
 }

@@ -114,7 +114,6 @@ __global__ __launch_bounds__(256) void rmsnorm_quantize_kernel(const float *x, i
     float *st = xscale + token * ldscale;
     // n4 is a multiple of 8, so the eight lanes of a group are all in range
     // together and the shuffles never mix groups.
-    #pragma unroll 4
     for (int i = threadIdx.x; i < n4; i += 256) {
         const float4 v = x4[i], w = w4[i];
         const float4 o = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
