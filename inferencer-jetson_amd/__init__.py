@@ -376,9 +376,10 @@ class GGUF:
         self.path = str(path)
 
     def close(self):
-        if getattr(self, "handle", None):
-            lib().qk_gguf_close(self.handle)
-            self.handle = None
+        # At interpreter exit the module's globals may already be gone.
+        if getattr(self, "handle", None) and _LIB is not None:
+            _LIB.qk_gguf_close(self.handle)
+        self.handle = None
 
     __del__ = close
 
@@ -475,9 +476,10 @@ class Runner:
         return self
 
     def close(self):
-        if getattr(self, "handle", None):
-            lib().qk_llama_destroy(self.handle)
-            self.handle = None
+        # At interpreter exit the module's globals may already be gone.
+        if getattr(self, "handle", None) and _LIB is not None:
+            _LIB.qk_llama_destroy(self.handle)
+        self.handle = None
 
     __del__ = close
 
@@ -527,9 +529,10 @@ class BatchRunner:
         return self
 
     def close(self):
-        if getattr(self, "handle", None):
-            lib().qk_llama_batch_destroy(self.handle)
-            self.handle = None
+        # At interpreter exit the module's globals may already be gone.
+        if getattr(self, "handle", None) and _LIB is not None:
+            _LIB.qk_llama_batch_destroy(self.handle)
+        self.handle = None
 
     __del__ = close
 

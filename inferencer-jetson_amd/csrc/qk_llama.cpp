@@ -33,6 +33,8 @@ struct qk_llama {
     size_t attn_ws_bytes = 0;
     int32_t *d_next = nullptr, *d_token = nullptr;
     int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
+    hipEvent_t upload_done = nullptr;   // the last token upload from h_token[0] has read it
+    bool upload_pending = false;
     int last_next = -1;
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
 };
@@ -52,6 +54,7 @@ void release(qk_llama *m) {
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
+    if (m->upload_done) (void)hipEventDestroy(m->upload_done);
     for (void *b : m->owned) (void)hipFree(b);
     delete m;
 }
@@ -160,7 +163,8 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         return st;
     }
     if (hipHostMalloc(reinterpret_cast<void **>(&m->h_token), 2 * sizeof(int32_t), hipHostMallocDefault) !=
-        hipSuccess) {
+            hipSuccess ||
+        hipEventCreateWithFlags(&m->upload_done, hipEventDisableTiming) != hipSuccess) {
         release(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_create: cannot allocate pinned staging");
     }
@@ -220,9 +224,15 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     int st;
     const int32_t *tok = m->d_next;
     if (token != m->last_next) {
+        // A step without logits returns before its work runs: the pinned slot
+        // is rewritten only once the previous upload has read it.
+        if (m->upload_pending && hipEventSynchronize(m->upload_done) != hipSuccess)
+            return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: stream error");
         m->h_token[0] = token;
-        if (hipMemcpyAsync(m->d_token, m->h_token, sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess)
+        if (hipMemcpyAsync(m->d_token, m->h_token, sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess ||
+            hipEventRecord(m->upload_done, s) != hipSuccess)
             return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: token upload failed");
+        m->upload_pending = true;
         tok = m->d_token;
     }
     m->last_next = -1;
@@ -280,6 +290,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");
+    m->upload_pending = false;   // the synchronisation retired every upload
     m->last_next = m->h_token[1];
     if (next_token) *next_token = m->last_next;
     return qk::ok();

@@ -69,3 +69,26 @@ def test_llama_1b_decode_64_greedy_tokens(qk, torch_gpu, oracle, workloads):
         assert err < 1e-2
     assert len(tg) == w.greedy_tokens
     assert tg == tr
+
+
+def test_prompt_steps_queued_behind_busy_stream(qk, torch_gpu, workloads):
+    """Steps without logits return before their work runs.  With the stream
+    held busy, eight such steps with different tokens are all queued before
+    the first executes; each must still embed its own token (the host's
+    staging slot is not reused before its upload has read it).  Logits must
+    equal a run that synchronises after every step."""
+    t = torch_gpu
+    W = workloads.llama_weights(SMALL, 5)
+    prompt = [5, 17, 999, 3, 250, 600, 42, 7]
+    r1, r2 = qk.Runner(SMALL, W), qk.Runner(SMALL, W)
+    busy = t.ones(2 ** 27, device="cuda")
+    t.cuda.synchronize()
+    for _ in range(30):
+        busy.mul_(1.0001)                  # a few ms of queued work on the default stream
+    for i, tok in enumerate(prompt):
+        r1.forward(tok, i, i == len(prompt) - 1)
+    for i, tok in enumerate(prompt):
+        r2.forward(tok, i, True)
+    assert np.array_equal(r1.logits().view(np.uint32), r2.logits().view(np.uint32))
+    r1.close()
+    r2.close()
