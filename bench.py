@@ -275,7 +275,7 @@ def bench_decode_1b(torch, qk, wl) -> dict:
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
             # Per layer: QKV, attention + split merge, o, gate/up, down; then
             # embedding, LM head and the two argmax stages.
-            "kernels_per_token": 6 * cfg["layers"] + 4}
+            "kernels_per_token": 6 * cfg["layers"] + 3}
 
 
 def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:

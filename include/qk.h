@@ -144,6 +144,17 @@ int qk_q6k_split(const void *src, void *dst, int cols, int rows, qk_stream strea
 int qk_embedding(int type, const void *w, const int32_t *tokens, int n_tokens, float *out,
                  int cols, int vocab, qk_stream stream);
 
+/* y = W x as qk_gemv_f32, and out[0] = the lowest row index among the
+   maxima of y (NaN never wins; 0 when no value exceeds -inf): the LM head and
+   the greedy pick of argmax_blocks_cuda / argmax_final_cuda
+   (inferencer.cu:1414, 1523-1526, 1063-1099) in two launches -- each GEMV
+   workgroup keeps the best of the rows it stores, one small kernel reduces
+   those partials.  workspace: qk_gemv_argmax_workspace_bytes() bytes, 4-byte
+   aligned; calls sharing it must not overlap. */
+size_t qk_gemv_argmax_workspace_bytes(void);
+int qk_gemv_argmax_f32(int type, const void *w, const float *x, float *y, int cols, int rows, int32_t *out,
+                       void *workspace, qk_stream stream);
+
 /* ---------------------------------------------------------- INT8 mode -- */
 
 /* Per 32 values: scale = amax/127 (1 if amax == 0), xq = clamp(rne(x/scale),

@@ -97,6 +97,8 @@ SIGNATURES = {
     "qk_dequant_rows": (_i, [_i, _vp, _vp, _i, _i, _i, _vp]),
     "qk_embedding": (_i, [_i, _vp, _vp, _i, _vp, _i, _i, _vp]),
     "qk_q6k_split": (_i, [_vp, _vp, _i, _i, _vp]),
+    "qk_gemv_argmax_workspace_bytes": (ctypes.c_size_t, []),
+    "qk_gemv_argmax_f32": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "qk_rmsnorm_quantize_x32": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
@@ -223,6 +225,15 @@ def matvec(t: Tensor, inp, out, expected_cols: int, expected_rows: int, stream=N
         raise QKError("matvec", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
     check(lib().qk_gemv_f32(t.type, t.gpu, ptr(inp), ptr(out), expected_cols, expected_rows,
                             stream_handle(stream)), "quantized matrix launch")
+
+
+def matvec_argmax(t: Tensor, inp, out, token_out, workspace, stream=None) -> None:
+    """The LM head with its greedy pick (inferencer.cu:1414, 1523-1526): out = W inp and token_out[0] = the
+    lowest index among the maxima of out; workspace of qk_gemv_argmax_workspace_bytes() bytes."""
+    if t.type not in QUANT_TYPES:
+        raise QKError("matvec_argmax", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
+    check(lib().qk_gemv_argmax_f32(t.type, t.gpu, ptr(inp), ptr(out), t.cols(), t.rows(), ptr(token_out),
+                                   ptr(workspace), stream_handle(stream)), "LM head with greedy pick")
 
 
 def _matrices(pairs) -> ctypes.Array:

@@ -86,6 +86,9 @@ struct GemvParams {
     float norm_eps;
     const float *up;      // stage x / (1 + exp(-x)) * up instead of x
     int accumulate;       // y += W x instead of y = W x
+    float *arg_v;         // greedy-token epilogue: per-workgroup best value / row
+    int *arg_i;
+    int *grid_out;        // host: receives the launch's workgroup count (not read on the device)
 };
 
 struct Raw {
@@ -251,6 +254,7 @@ struct F32Policy {
     };
 
     static constexpr bool kFused = false;
+    static constexpr bool kArgmax = false;   // greedy-token epilogue
 
     // LDS bytes of the prepared activations of one token.
     __host__ __device__ static size_t lds_bytes(int cols) { return static_cast<size_t>(cols / 16) * sizeof(XGroup); }
@@ -389,9 +393,17 @@ struct F32FusedPolicy : F32Policy {
 
 // ------------------------------------------------------------ INT8 path --
 
+// The LM head with the greedy pick: F32FusedPolicy's staging plus every
+// wave's best (value, row) written at the end (arg_epilogue).  A policy of
+// its own so the other fused GEMVs carry none of the bookkeeping.
+struct F32ArgPolicy : F32FusedPolicy {
+    static constexpr bool kArgmax = true;
+};
+
 struct I8Policy {
     static constexpr bool kPrepLds = false;
     static constexpr bool kFused = false;
+    static constexpr bool kArgmax = false;
     __host__ __device__ static size_t lds_bytes(int) { return 0; }
     __device__ static void prep(const GemvParams &, int, int, XGroup *) {}
 
@@ -522,12 +534,40 @@ __device__ __forceinline__ float piece_dot(int type, const Raw &r, const typenam
 }
 
 // Output store: overwrite, or (fused policy with accumulate) add into y.
+// Returns the stored value.
 template <class Policy>
-__device__ __forceinline__ void store_y(const GemvParams &p, float *y, float v) {
+__device__ __forceinline__ float store_y(const GemvParams &p, float *y, float v) {
     if constexpr (Policy::kFused) {
         if (p.accumulate) v += *y;
     }
     *y = v;
+    return v;
+}
+
+// A lane's running best row (greedy-token policy only).
+template <class Policy>
+__device__ __forceinline__ void keep_best(float &bv, int &bi, float v, int row) {
+    if constexpr (Policy::kArgmax) arg_better(bv, bi, v, row);
+}
+
+// Greedy-token epilogue: the wave's best (value, row) over its lanes'
+// running bests, written to arg_v / arg_i[blockIdx.x * waves + wave] -- one
+// partial per wave, so no wave waits for another.
+template <class Policy>
+__device__ __forceinline__ void arg_epilogue(const GemvParams &p, float bv, int bi) {
+    if constexpr (Policy::kArgmax) {
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            arg_better(bv, bi, ov, oi);
+        }
+        if ((threadIdx.x & 63) == 0) {
+            const int slot = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+            p.arg_v[slot] = bv;
+            p.arg_i[slot] = bi;
+        }
+    }
 }
 
 // One prefetched tile: where its result goes and its raw bytes.
@@ -571,19 +611,21 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     }
     typename Policy::Lane L;
     Policy::load(L, p, token, piece, xg);
-    if (first >= p.total_tiles) return;
-    const int n_iter = (last - first) / stride + 1;
+    float bv = -INFINITY;   // greedy-token epilogue: this lane's best row so far
+    int bi = 0x7FFFFFFF;
+    const int n_iter = first < p.total_tiles ? (last - first) / stride + 1 : 0;
     int k = 0;
-    while (true) {
+    while (k < n_iter) {
         float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(a.t.type, a.r, L, g, h));
-        if (piece == 0 && a.t.valid) store_y<Policy>(p, a.t.y + a.t.row, v);
+        if (piece == 0 && a.t.valid) keep_best<Policy>(bv, bi, store_y<Policy>(p, a.t.y + a.t.row, v), a.t.row);
         a = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
         if (++k == n_iter) break;
         v = group_sum<GROUP>(piece_dot<Policy, TYPE>(b.t.type, b.r, L, g, h));
-        if (piece == 0 && b.t.valid) store_y<Policy>(p, b.t.y + b.t.row, v);
+        if (piece == 0 && b.t.valid) keep_best<Policy>(bv, bi, store_y<Policy>(p, b.t.y + b.t.row, v), b.t.row);
         b = prep<TYPE>(p, min(first + (k + 2) * stride, last), rit, piece, token, g, h);
-        if (++k == n_iter) break;
+        ++k;
     }
+    arg_epilogue<Policy>(p, bv, bi);
 }
 
 // C > 1: the C waves of a wave-group share each tile; the group sums of a
@@ -592,7 +634,7 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
 template <class Policy, int TYPE, int GROUP>
 __device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, const typename Policy::Lane &L,
                                            float *red, int k, int tile, int wgroup, int chunk, int lane, int q,
-                                           int g, int h, int token) {
+                                           int g, int h, int token, float &bv, int &bi) {
     const int slots = p.tile_rows * p.chunks;
     float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(s.t.type, s.r, L, g, h));
     float *buf = red + (wgroup * 2 + (k & 1)) * slots;
@@ -603,7 +645,7 @@ __device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, c
         if (rowref.valid) {
             float sum = 0.f;
             for (int c = 0; c < p.chunks; ++c) sum += buf[lane * p.chunks + c];
-            store_y<Policy>(p, rowref.y + rowref.row, sum);
+            keep_best<Policy>(bv, bi, store_y<Policy>(p, rowref.y + rowref.row, sum), rowref.row);
         }
     }
 }
@@ -634,15 +676,20 @@ __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
     }
     typename Policy::Lane L;
     Policy::load(L, p, token, piece, xg);
+    float bv = -INFINITY;   // greedy-token epilogue: this lane's best row so far
+    int bi = 0x7FFFFFFF;
     int k = 0;
     while (true) {
-        split_step<Policy, TYPE, GROUP>(p, a, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token);
+        split_step<Policy, TYPE, GROUP>(p, a, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token,
+                                        bv, bi);
         a = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
         if (++k == iters) break;
-        split_step<Policy, TYPE, GROUP>(p, b, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token);
+        split_step<Policy, TYPE, GROUP>(p, b, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token,
+                                        bv, bi);
         b = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
         if (++k == iters) break;
     }
+    arg_epilogue<Policy>(p, bv, bi);
 }
 
 // Rows whose chunk count exceeds kMaxChunks: one wave per row, lanes stride
@@ -720,7 +767,11 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
             static_cast<int64_t>(p.total_tiles) * n_tokens >= int64_t(kWaveLongTiles) * kWaveBlocksPerCu * waves * cus;
         const int per_cu = aligned && long_launch ? kWaveBlocksPerCuLong : kWaveBlocksPerCu;
         const int cap = std::max(1, std::min(resident_blocks(k, block, x_lds), per_cu * cus) / n_tokens);
-        const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
+        const int grid_all = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
+        // Grid-stride tiles: clamping keeps the argmax partials (one per wave)
+        // in their buffer.
+        const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / waves : grid_all);
+        if (p.grid_out) *p.grid_out = grid * waves;
         hipLaunchKernelGGL((gemv_wave<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
     } else {
         const int wgroups = std::max(1, 4 / p.chunks);
@@ -735,7 +786,9 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
                                   int64_t(kSplitShortTiles) * kSplitBlocksPerCu * wgroups * cus;
         const int per_cu = short_launch ? 1 : kSplitBlocksPerCu;
         const int cap = std::max(1, std::min(resident_blocks(k, block, lds), per_cu * cus) / n_tokens);
-        const int grid = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
+        const int grid_all = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
+        const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / (block / 64) : grid_all);
+        if (p.grid_out) *p.grid_out = grid * (block / 64);
         hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
     }
 }
@@ -827,7 +880,19 @@ int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx
     p.norm_eps = f.norm_eps;
     p.up = f.up;
     p.accumulate = f.accumulate;
-    return launch<F32FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "fused GEMV launch");
+    if (f.arg_v) {
+        if (!f.arg_i || !f.arg_parts || n_mats != 1 || n_tokens != 1)
+            return fail(QK_ERR_INVALID_ARG, "fused GEMV: the argmax epilogue takes one matrix and one token");
+        p.arg_v = f.arg_v;
+        p.arg_i = f.arg_i;
+        p.grid_out = f.arg_parts;
+        *f.arg_parts = 0;
+    }
+    const int st = f.arg_v ? launch<F32ArgPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "fused GEMV launch")
+                           : launch<F32FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "fused GEMV launch");
+    if (!st && f.arg_v && (*f.arg_parts < 1 || *f.arg_parts > kArgPartsMax))
+        return fail(QK_ERR_LIMIT, "fused GEMV: argmax partials beyond their buffer");
+    return st;
 }
 
 }  // namespace qk
@@ -842,6 +907,28 @@ int qk_gemv_f32(int type, const void *w, const float *x, float *y, int cols, int
         return qk::fail(QK_ERR_ALIGN, "qk_gemv_f32: x must be 16-byte and y 4-byte aligned");
     const qk_matrix m{type, rows, w, y};
     return qk::launch_gemv_f32(&m, 1, x, cols, cols, 1, nullptr, static_cast<hipStream_t>(stream));
+}
+
+size_t qk_gemv_argmax_workspace_bytes(void) { return 2 * qk::kArgPartsMax * sizeof(float); }
+
+int qk_gemv_argmax_f32(int type, const void *w, const float *x, float *y, int cols, int rows, int32_t *out,
+                       void *workspace, qk_stream stream) {
+    int st = qk::check_weights("qk_gemv_argmax_f32", type, w, cols, rows);
+    if (st) return st;
+    if (!x || !y || !out || !workspace)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_argmax_f32: null activation, output or workspace pointer");
+    if (!qk::aligned(x, 16) || !qk::aligned(y, 4) || !qk::aligned(workspace, 4))
+        return qk::fail(QK_ERR_ALIGN, "qk_gemv_argmax_f32: x must be 16-byte, y and workspace 4-byte aligned");
+    if (!qk::gemv_fusable(cols)) return qk::fail(QK_ERR_LIMIT, "qk_gemv_argmax_f32: rows too long to stage");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const qk_matrix m{type, rows, w, y};
+    qk::GemvFusion f;
+    f.arg_v = static_cast<float *>(workspace);
+    f.arg_i = reinterpret_cast<int *>(f.arg_v + qk::kArgPartsMax);
+    int parts = 0;
+    f.arg_parts = &parts;
+    if ((st = qk::launch_gemv_fused(&m, 1, x, cols, cols, 1, nullptr, f, s))) return st;
+    return qk::launch_argmax_final(f.arg_v, f.arg_i, parts, out, s);
 }
 
 int qk_gemv_multi_f32(const qk_matrix *mats, int n_mats, const float *x, int cols, qk_stream stream) {

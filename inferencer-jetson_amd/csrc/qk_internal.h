@@ -54,7 +54,27 @@ struct GemvFusion {
     float norm_eps = 0.f;
     const float *up = nullptr;
     int accumulate = 0;
+    // Greedy-token epilogue (one matrix, one token): every wave writes the
+    // best (value, row) of the rows it stored to arg_v / arg_i and the launch
+    // reports the number of such partials in *arg_parts (at most
+    // kArgPartsMax).
+    float *arg_v = nullptr;
+    int *arg_i = nullptr;
+    int *arg_parts = nullptr;
 };
+constexpr int kArgPartsMax = 16384;
+// The argmax partials -> out[0] (the lowest row among maxima; 0 if none).
+int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream);
+
+// The greedy-token order (argmax_blocks_cuda / argmax_final_cuda,
+// inferencer.cu:1063-1099): a larger value wins, equal values keep the lower
+// index; NaN never wins.
+__device__ __forceinline__ void arg_better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
 // Whether a row of cols columns can stage its activations for the fusions.
 bool gemv_fusable(int cols);
 // n_tokens tokens (x + t*ldx; y + t*ldy[m], NULL: rows), arguments already

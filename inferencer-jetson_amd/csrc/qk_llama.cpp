@@ -150,8 +150,8 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
         (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
         (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
-        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_workspace_bytes(c.vocab),
-                        "argmax workspace")) ||
+        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), 2 * qk::kArgPartsMax * sizeof(float),
+                        "argmax partials")) ||
         (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token"))) {
         release(m);
         return st;
@@ -279,14 +279,20 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         if (next_token) *next_token = -1;
         return qk::ok();
     }
+    // The LM head's epilogue keeps each workgroup's best logit (argmax_blocks_cuda
+    // folded in); one small kernel picks the token from those partials.
     qk::GemvFusion out_in;
     out_in.norm_w = m->w.output_norm;
     out_in.norm_eps = c.eps;
+    out_in.arg_v = static_cast<float *>(m->argmax_ws);
+    out_in.arg_i = reinterpret_cast<int *>(out_in.arg_v + qk::kArgPartsMax);
+    int parts = 0;
+    out_in.arg_parts = &parts;
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
     if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, dim, 1, nullptr, out_in, s))) return st;
-    if ((st = qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s))) return st;
+    if ((st = qk::launch_argmax_final(out_in.arg_v, out_in.arg_i, parts, m->d_next, s))) return st;
     if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");

@@ -586,12 +586,6 @@ __global__ void silu_mul_kernel(float *gate, const float *up, int n) {
 // (value, index) order of argmax_blocks_cuda / argmax_final_cuda
 // (inferencer.cu:1063-1099): larger value wins, equal values keep the lower
 // index.
-__device__ __forceinline__ void arg_better(float &bv, int &bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
-        bv = v;
-        bi = i;
-    }
-}
 
 constexpr int kArgmaxBlock = 1024;
 
@@ -767,6 +761,11 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
 }
 
 bool attention_supported(int group, int head_dim) { return split_instance(group, head_dim) != nullptr; }
+
+int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
+    return launch_status("argmax final launch");
+}
 
 }  // namespace qk
 
