@@ -133,6 +133,22 @@ def bench_small_gemvs(torch, qk, wl, stream) -> dict:
     return sec
 
 
+def bench_q4k_lm_shape(torch, qk, wl, stream, copies: int) -> dict:
+    """Q4_K GEMV at the LM-head shape 128256 x 2048 (147.7 MB of super-blocks,
+    rotating copies): the Q4_K kernel's sustained rate, which the 1B / 3B
+    Q4_K projections (2.4-14 MB each) are too small to show in one launch."""
+    cols, rows = 2048, 128256
+    ts = [qk.Tensor((cols, rows), qk.Q4_K,
+                    torch.from_numpy(wl.synth.quant_matrix(qk.Q4_K, cols, rows, 6, 1 + 16 * c, 0.02)).to("cuda"))
+          for c in range(copies)]
+    x = torch.from_numpy(wl.synth.normal_f32(cols, 6, 2)).to("cuda")
+    y = torch.empty(rows, device="cuda")
+    _, k = time_launches(torch, lambda i: qk.matvec(ts[i % copies], x, y, cols, rows, stream), 2000, 2000, stream)
+    b = qk.tensor_bytes(qk.Q4_K, cols, rows) + cols * 4 + rows * 4
+    return {"kernel_us": round(k * 1e3, 2), "GBps_kernel": round(b / (k * 1e-3) / 1e9, 1),
+            "frac_of_peak": round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "bytes_per_launch": b}
+
+
 def _workspace(torch, qk, cols, rows, ntok):
     n = qk.batch_workspace_bytes(cols, rows, ntok)
     return torch.empty(max(n, 256), dtype=torch.uint8, device="cuda"), n
@@ -455,6 +471,8 @@ def main() -> int:
                                           "GBps_kernel": round(step_bytes / (kg * 1e-3) / 1e9, 1),
                                           "frac_of_peak": round(step_bytes / (kg * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
         log(f"[bench] lm_head_q6k_gguf_layout: {json.dumps(sec['lm_head_q6k_gguf_layout'])}")
+        sec["gemv_q4k_128256x2048"] = bench_q4k_lm_shape(torch, qk, wl, stream, args.copies)
+        log(f"[bench] gemv_q4k_128256x2048: {json.dumps(sec['gemv_q4k_128256x2048'])}")
         sec.update(bench_small_gemvs(torch, qk, wl, stream))
         sec["ffn_3b_ragged_t32"] = bench_ffn_3b_ragged(torch, qk, wl, stream)
         log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")

@@ -36,7 +36,7 @@
 //                     over several workgroups (to put enough waves on the
 //                     chip), each writes its partial sums to the workspace;
 //   reduce_splits     adds them in split order, so results are deterministic,
-//                     and applies the call's epilogue.
+//                     and applies the call's epilogue (one thread per output).
 #include "qk_internal.h"
 
 #include <algorithm>
@@ -59,6 +59,7 @@ constexpr int kRowTiles = 2;            // 32-row tiles per wave
 constexpr int kGroupRows = 128 * kRowTiles;   // weight rows per workgroup (4 waves)
 constexpr int kPartialFloats = 4 * kRowTiles * 16 * 64;   // one workgroup's partial sums per token tile
 constexpr int kMaxSplit = 16;           // workgroups splitting one row group's blocks
+static_assert(kPartialFloats % 256 == 0, "reduce_splits covers whole partial slots with 256-thread workgroups");
 
 // LDS tile of one block's activations for one 32-token tile, in MFMA A
 // operand order:
@@ -608,56 +609,39 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
 }
 
 // y = the sum of a row group's split partials, in split order (deterministic),
-// stored with the call's epilogue (overwrite or add).  One 64-thread
-// workgroup per (row group, GEMM wave, row tile, token tile): lane l owns the
-// outputs lane l of that GEMM wave produced for that row tile.
-__global__ __launch_bounds__(64) void reduce_splits(BatchParams p) {
+// stored with the call's epilogue (overwrite or add).  One thread per output
+// value: thread u owns float u % kPartialFloats of slot u / kPartialFloats
+// (slot = group * tiles + tile) -- GEMM wave, row tile, accumulator register
+// and lane in the partials' own order, so a wave reads 64 consecutive floats
+// per split -- and issues every split's load before the first add: the
+// kernel is latency-bound, so it spreads over the whole chip.
+__global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
     constexpr int RT = kRowTiles;
-    const int group = blockIdx.x / (4 * RT), sub = blockIdx.x % (4 * RT);
-    const int wave = sub % 4, i = sub / 4, tile = blockIdx.y;
-    const int lane = threadIdx.x;
+    const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    const int64_t slot = u / kPartialFloats;
+    const int rem = static_cast<int>(u - slot * kPartialFloats);
+    const int group = static_cast<int>(slot / p.tiles), tile = static_cast<int>(slot - static_cast<int64_t>(group) * p.tiles);
+    const int wave = rem / (RT * 1024), i = (rem / 1024) % RT, k = (rem / 64) % 16, lane = rem % 64;
     const int kh = lane >> 5, col = lane & 31;
     int m = 0;
     #pragma unroll
     for (int j = 1; j < QK_MAX_FUSED; ++j) m += (j < p.n_mats && group >= p.mat[j].group_begin) ? 1 : 0;
     const BatchMatrix &M = p.mat[m];
-    const size_t slot = static_cast<size_t>(group) * p.tiles + tile;
-    const float *part = p.partials + slot * p.splits * kPartialFloats + wave * (RT * 1024) + i * 1024 + lane;
-    const int tbase = tile * kTokTile + 4 * kh;
+    const float *part = p.partials + slot * p.splits * kPartialFloats + rem;
+    float v[kMaxSplit];
+    #pragma unroll
+    for (int sp = 0; sp < kMaxSplit; ++sp) v[sp] = sp < p.splits ? part[static_cast<int64_t>(sp) * kPartialFloats] : 0.f;
+    float sum = v[0];
+    #pragma unroll
+    for (int sp = 1; sp < kMaxSplit; ++sp)
+        if (sp < p.splits) sum += v[sp];
+    // Accumulator register k holds token 8*(k/4) + 4*kh + k%4 of its tile.
     const int row = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
-    // Every load of a split run is issued before the first add: the kernel is latency-bound.
-    float sum[16];
-    #pragma unroll
-    for (int k = 0; k < 16; ++k) sum[k] = part[k * 64];
-    for (int sp0 = 1; sp0 < p.splits; sp0 += 4) {
-        float v[4][16];
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            #pragma unroll
-            for (int k = 0; k < 16; ++k) v[q][k] = sp0 + q < p.splits ? part[(sp0 + q) * kPartialFloats + k * 64] : 0.f;
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                if (sp0 + q < p.splits) sum[k] += v[q][k];
-    }
-    if (row >= M.rows) return;
-    if (p.accumulate) {
-        // The residual values, all loaded before the first store.
-        float yv[16];
-        #pragma unroll
-        for (int k = 0; k < 16; ++k) {
-            const int t = tbase + 8 * (k >> 2) + (k & 3);
-            yv[k] = t < p.n_tokens ? M.y[static_cast<int64_t>(t) * M.ldy + row] : 0.f;
-        }
-        #pragma unroll
-        for (int k = 0; k < 16; ++k) sum[k] = yv[k] + sum[k];
-    }
-    #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-        const int t = tbase + 8 * (k >> 2) + (k & 3);
-        if (t < p.n_tokens) M.y[static_cast<int64_t>(t) * M.ldy + row] = sum[k];
-    }
+    const int t = tile * kTokTile + 8 * (k >> 2) + 4 * kh + (k & 3);
+    if (row >= M.rows || t >= p.n_tokens) return;
+    float *yp = M.y + static_cast<int64_t>(t) * M.ldy + row;
+    if (p.accumulate) sum = *yp + sum;
+    *yp = sum;
 }
 
 int check_batched(const char *where, const float *x, int ldx, int cols, int n_tokens) {
@@ -804,8 +788,8 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     else
         launch_gemm<1>(type, grid, lds, stream, p);
     if (p.splits > 1)
-        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups * 4 * kRowTiles), tiles), dim3(64), 0, stream,
-                           p);
+        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups * tiles * (kPartialFloats / 256))), dim3(256),
+                           0, stream, p);
     return launch_status(where);
 }
 
