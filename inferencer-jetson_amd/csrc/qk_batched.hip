@@ -119,34 +119,36 @@ struct XStage {
     float v[32];
 };
 
-// With norm_w, the token's RMSNorm scale 1/sqrt(mean(x^2) + eps) over all
-// cols (eight lanes per token, rmsnorm_cuda's arithmetic, inferencer.cu:
-// 821-834) multiplies x and the gain is applied; with up, x / (1 + exp(-x))
-// * up (silu_cuda, inferencer.cu:1053-1056).
-__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, int tl, int q, XStage &s) {
+// The token's RMSNorm scale 1/sqrt(mean(x^2) + eps) over all cols
+// (rmsnorm_cuda's arithmetic, inferencer.cu:821-834), from the 32 lanes
+// r = 0..31 of the token: each reads every 32nd float4 of the row, all in
+// flight at once (the kernel is latency-bound), and the lanes meet in five
+// xor shuffles.
+__device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int tile, int tl, int r) {
     const int t = tile * kTokTile + tl;
     const int cols = p.nb * 256;
-    float scale = 1.f;
-    if (p.norm_w) {
-        float ss = 0.f;
-        if (t < p.n_tokens) {
-            // Sixteen float4 per lane in flight at a time: the row is long and
-            // only nb x tiles workgroups share the work.
-            const float4 *row = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx);
-            #pragma unroll 16
-            for (int i = q; i < cols / 4; i += 8) {
-                const float4 v = row[i];
-                ss = fmaf(v.x, v.x, ss);
-                ss = fmaf(v.y, v.y, ss);
-                ss = fmaf(v.z, v.z, ss);
-                ss = fmaf(v.w, v.w, ss);
-            }
+    float ss = 0.f;
+    if (t < p.n_tokens) {
+        const float4 *row = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx);
+        #pragma unroll 8
+        for (int i = r; i < cols / 4; i += 32) {
+            const float4 v = row[i];
+            ss = fmaf(v.x, v.x, ss);
+            ss = fmaf(v.y, v.y, ss);
+            ss = fmaf(v.z, v.z, ss);
+            ss = fmaf(v.w, v.w, ss);
         }
-        ss += __shfl_xor(ss, 1);
-        ss += __shfl_xor(ss, 2);
-        ss += __shfl_xor(ss, 4);
-        scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
     }
+    #pragma unroll
+    for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off);
+    return 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
+}
+
+// With norm_w, x times the token's RMSNorm scale times the gain; with up,
+// x / (1 + exp(-x)) * up (silu_cuda, inferencer.cu:1053-1056).
+__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, int tl, int q, float scale,
+                                           XStage &s) {
+    const int t = tile * kTokTile + tl;
     if (t < p.n_tokens) {
         const int64_t at = static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32;
         const float4 *src = reinterpret_cast<const float4 *>(p.x + at);
@@ -249,19 +251,22 @@ __device__ __forceinline__ void stage_store(const XStage &s, int tl, int q, uint
     }
 }
 
-// One 64-thread workgroup per (block, eight tokens of a 32-token tile): the
+// One 256-thread workgroup per (block, eight tokens of a 32-token tile): the
 // tokens' activations of the block, packed into the workspace record the
-// GEMM copies into LDS.  Thread (token tl, sub-block q); the eight lanes of a
-// token meet in shuffles.
+// GEMM copies into LDS.  32 lanes per token (r = 0..31) share the RMSNorm
+// sum of squares; lanes r < 8 then stage sub-block q = r and meet in
+// shuffles within their eight.
 constexpr int kPackTokens = 8;
-__global__ __launch_bounds__(64) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
+__global__ __launch_bounds__(256) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
     const int b = blockIdx.x;
     const int tile = blockIdx.y / (kTokTile / kPackTokens);
-    const int tl = (blockIdx.y % (kTokTile / kPackTokens)) * kPackTokens + (threadIdx.x >> 3);
-    const int q = threadIdx.x & 7;
+    const int tl = (blockIdx.y % (kTokTile / kPackTokens)) * kPackTokens + (threadIdx.x >> 5);
+    const int r = threadIdx.x & 31;
+    const float scale = p.norm_w ? stage_norm_scale(p, tile, tl, r) : 1.f;
+    if (r >= 8) return;
     XStage xs;
-    stage_load(p, tile, b, tl, q, xs);
-    stage_store(xs, tl, q, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
+    stage_load(p, tile, b, tl, r, scale, xs);
+    stage_store(xs, tl, r, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
 }
 
 // ------------------------------------------------------- weight operands --
@@ -780,7 +785,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         p.up = fusion->up;
         p.accumulate = fusion->accumulate;
     }
-    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(64), 0, stream, p, ws);
+    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(256), 0, stream, p, ws);
     const dim3 grid(static_cast<unsigned>(groups * p.splits), tgroups);
     const size_t lds = 2 * static_cast<size_t>(tt) * kTileBytes;
     if (tt == 2)
