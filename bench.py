@@ -256,16 +256,19 @@ def bench_mixed_1b_256(torch, qk, wl, stream, steps: int = 20, warmup: int = 3) 
             "mfma_ops_per_useful_product": 2, "launches_per_step": 5 * cfg["layers"]}
 
 
-def bench_decode_1b(torch, qk, wl) -> dict:
+def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
     """Random-init Llama-3.2-1B decode, one sequence: KV prefilled at 0..511,
     16 prompt tokens at 512..527, then 64 greedy tokens, each step ending in
     the 4-byte token download (FastRunner::forward, inferencer.cu:1424-1531).
-    Timed: the 64 greedy steps, wall clock."""
+    int8: the reference's default INT8 GEMVs (use_dp4a, use_q6_dp4a) with
+    --fused-norm-quant.  Timed: the 64 greedy steps, wall clock."""
     w = wl.LLAMA_1B_DECODE
     cfg = w.cfg
     W = wl.llama_weights(cfg, w.seed)
     kc, vc = wl.llama_kv_prefill(cfg, w.seed, w.prefill_positions)
     run = qk.Runner(cfg, W)
+    if int8:
+        run.set_int8(True, True)
     run.load_kv(kc, vc)
     prompt = wl.llama_prompt(cfg, w.seed, w.prompt_tokens)
     pos = w.prefill_positions
@@ -289,9 +292,12 @@ def bench_decode_1b(torch, qk, wl) -> dict:
     return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
             "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            # Per layer: QKV, attention + split merge, o, gate/up, down; then
-            # embedding, LM head and the two argmax stages.
-            "kernels_per_token": 6 * cfg["layers"] + 3}
+            # FP32, per layer: QKV, attention + split merge, o, gate/up, down;
+            # then embedding, LM head and the two argmax stages.  INT8, per
+            # layer: norm+quantize, QKV, attention + merge, quantize, o, add,
+            # norm+quantize, gate/up, SiLU*up, quantize, down, add; then
+            # embedding, norm+quantize, LM head and two argmax stages.
+            "kernels_per_token": (13 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3)}
 
 
 def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
@@ -387,7 +393,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
-    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "decode", "batch_decode"],
+    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "decode", "decode_int8",
+                                       "batch_decode"],
                     default="gemv",
                     help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
                          "(a plain 256 MiB copy calibrates FETCH_SIZE / WRITE_SIZE; a streaming read gives "
@@ -412,6 +419,7 @@ def main() -> int:
         run = {"ffn": lambda: bench_ffn_3b_ragged(torch, qk, wl, stream),
                "mixed": lambda: bench_mixed_1b_256(torch, qk, wl, stream),
                "decode": lambda: bench_decode_1b(torch, qk, wl),
+               "decode_int8": lambda: bench_decode_1b(torch, qk, wl, int8=True),
                "batch_decode": lambda: bench_batch_decode_1b(torch, qk, wl)}[args.only]
         print(json.dumps({args.only: run()}), flush=True)
         return 0
@@ -480,6 +488,8 @@ def main() -> int:
         log(f"[bench] mixed_1b_256: {json.dumps(sec['mixed_1b_256'])}")
         sec["llama_1b_decode"] = bench_decode_1b(torch, qk, wl)
         log(f"[bench] llama_1b_decode: {json.dumps(sec['llama_1b_decode'])}")
+        sec["llama_1b_decode_int8"] = bench_decode_1b(torch, qk, wl, int8=True)
+        log(f"[bench] llama_1b_decode_int8: {json.dumps(sec['llama_1b_decode_int8'])}")
         sec["llama_1b_batch_decode_32"] = bench_batch_decode_1b(torch, qk, wl)
         log(f"[bench] llama_1b_batch_decode_32: {json.dumps(sec['llama_1b_batch_decode_32'])}")
         result["secondary"] = sec

@@ -187,6 +187,13 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
                int ldscale, float *y, int ldy, int cols, int rows, int n_tokens,
                qk_stream stream);
 
+/* Fused INT8 GEMV over 1..QK_MAX_FUSED matrices sharing one token's
+   quantized activations (xq: cols int8, xscale: cols/32): the dp4a branch of
+   qkv_cuda / gate_up_cuda (inferencer.cu:753-804) for any mix of Q4_K and
+   Q6_K (either layout).  Each matrix's rows go to its own y. */
+int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const float *xscale, int cols,
+                     qk_stream stream);
+
 /* -------------------------------------------------------- step kernels -- */
 
 /* out = x * 1/sqrt(mean(x^2) + eps) * weight per token of n values.
@@ -316,6 +323,14 @@ typedef struct qk_llama qk_llama;
 int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream,
                     qk_llama **out);
 int qk_llama_destroy(qk_llama *m);
+/* The reference's INT8 GEMV modes (FastGPU's use_dp4a for Q4_K and
+   use_q6_dp4a for Q6_K, inferencer.cu:1159-1166, 1611; both on by default
+   there, both off here): enabled types run their GEMVs on per-32 int8
+   activations -- RMSNorm and quantization fused before QKV and gate/up
+   (--fused-norm-quant), the attention and FFN outputs quantized before o
+   and down, residual adds and SiLU * up as separate launches -- and the
+   other types stay FP32.  Takes effect at the next qk_llama_forward. */
+int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8);
 /* Device pointers to the fp32 caches, [layer][context][kv_dim]. */
 int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
 /* Device pointer to the fp32 logits of the last step with need_logits. */

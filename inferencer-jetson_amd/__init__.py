@@ -100,6 +100,8 @@ SIGNATURES = {
     "qk_gemv_argmax_workspace_bytes": (ctypes.c_size_t, []),
     "qk_gemv_argmax_f32": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
     "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
+    "qk_gemv_multi_i8": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _vp, _i, _vp]),
+    "qk_llama_set_int8": (_i, [_vp, _i, _i]),
     "qk_rmsnorm_quantize_x32": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
@@ -234,6 +236,16 @@ def matvec_argmax(t: Tensor, inp, out, token_out, workspace, stream=None) -> Non
         raise QKError("matvec_argmax", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
     check(lib().qk_gemv_argmax_f32(t.type, t.gpu, ptr(inp), ptr(out), t.cols(), t.rows(), ptr(token_out),
                                    ptr(workspace), stream_handle(stream)), "LM head with greedy pick")
+
+
+def multi_matvec_i8(pairs, xq, xscale, cols: int, stream=None) -> None:
+    """qkv_cuda / gate_up_cuda with dp4a (inferencer.cu:753-804): one fused INT8 launch over (Tensor, out) pairs."""
+    for t, _ in pairs:
+        if t.cols() != cols:
+            raise QKError("multi_matvec_i8", QK_ERR_SHAPE, "Unexpected quantized matrix shape")
+    arr = _matrices(pairs)
+    check(lib().qk_gemv_multi_i8(arr, len(pairs), ptr(xq), ptr(xscale), cols, stream_handle(stream)),
+          "fused INT8 matrix launch")
 
 
 def _matrices(pairs) -> ctypes.Array:
@@ -493,6 +505,10 @@ class Runner:
         self.handle = None
 
     __del__ = close
+
+    def set_int8(self, q4k: bool = True, q6k: bool = True) -> None:
+        """The reference's INT8 GEMV modes (use_dp4a, use_q6_dp4a; inferencer.cu:1159-1166)."""
+        check(lib().qk_llama_set_int8(self.handle, int(q4k), int(q6k)), "set_int8")
 
     def kv_cache(self) -> tuple[int, int]:
         k, v = ctypes.c_void_p(), ctypes.c_void_p()

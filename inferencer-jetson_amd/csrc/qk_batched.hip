@@ -42,11 +42,6 @@
 #include <algorithm>
 
 namespace qk {
-int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
-                    const int *ldy, hipStream_t stream);
-}
-
-namespace qk {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));

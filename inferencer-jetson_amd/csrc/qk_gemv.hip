@@ -863,6 +863,18 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
     return launch<F32Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "qk_gemv_f32 launch");
 }
 
+// INT8 path shared by qk_gemv_i8 and qk_gemv_multi_i8 (arguments already
+// validated): quantized activations xq / xscale of n_tokens tokens.
+int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
+                   int cols, int n_tokens, const int *ldy, hipStream_t stream) {
+    GemvParams p{};
+    p.x = xq;
+    p.xscale = xscale;
+    p.ldx = ldxq;
+    p.ldscale = ldscale;
+    return launch<I8Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "INT8 GEMV launch");
+}
+
 bool gemv_fusable(int cols) {
     if (cols <= 0 || cols % 256) return false;
     const int pieces = cols / 64;
@@ -957,14 +969,27 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
         return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_i8: leading dimension smaller than the row");
     if (!qk::aligned(xq, 16) || ldxq % 16 || !qk::aligned(xscale, 4) || !qk::aligned(y, 4))
         return qk::fail(QK_ERR_ALIGN, "qk_gemv_i8: xq and ldxq must keep 16-byte alignment");
-    qk::GemvParams p{};
-    p.x = xq;
-    p.xscale = xscale;
-    p.ldx = ldxq;
-    p.ldscale = ldscale;
     const qk_matrix m{type, rows, w, y};
-    return qk::launch<qk::I8Policy>(p, &m, 1, cols, n_tokens, &ldy, static_cast<hipStream_t>(stream),
-                                    "qk_gemv_i8 launch");
+    return qk::launch_gemv_i8(&m, 1, xq, ldxq, xscale, ldscale, cols, n_tokens, &ldy, static_cast<hipStream_t>(stream));
+}
+
+int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const float *xscale, int cols,
+                     qk_stream stream) {
+    if (!mats || n_mats < 1 || n_mats > QK_MAX_FUSED)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_multi_i8: need 1.." + std::to_string(QK_MAX_FUSED) + " matrices");
+    if (!xq || !xscale) return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_multi_i8: null activation pointer");
+    if (!qk::aligned(xq, 16) || !qk::aligned(xscale, 4))
+        return qk::fail(QK_ERR_ALIGN, "qk_gemv_multi_i8: xq must be 16-byte and xscale 4-byte aligned");
+    int ldy[QK_MAX_FUSED];
+    for (int m = 0; m < n_mats; ++m) {
+        int st = qk::check_weights("qk_gemv_multi_i8", mats[m].type, mats[m].w, cols, mats[m].rows);
+        if (st) return st;
+        if (!mats[m].y) return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_multi_i8: null output pointer");
+        if (!qk::aligned(mats[m].y, 4)) return qk::fail(QK_ERR_ALIGN, "qk_gemv_multi_i8: misaligned output");
+        ldy[m] = mats[m].rows;
+    }
+    return qk::launch_gemv_i8(mats, n_mats, xq, cols, xscale, cols / 32, cols, 1, ldy,
+                              static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -75,6 +75,14 @@ __device__ __forceinline__ void arg_better(float &bv, int &bi, float v, int i) {
         bi = i;
     }
 }
+// FP32 GEMV of n_tokens activation rows (x + t*ldx; y + t*ldy[m], NULL:
+// rows), arguments already validated.
+int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
+                    const int *ldy, hipStream_t stream);
+// INT8 GEMV of n_tokens quantized activation rows (xq + t*ldxq, xscale +
+// t*ldscale; y + t*ldy[m]), arguments already validated.
+int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
+                   int cols, int n_tokens, const int *ldy, hipStream_t stream);
 // Whether a row of cols columns can stage its activations for the fusions.
 bool gemv_fusable(int cols);
 // n_tokens tokens (x + t*ldx; y + t*ldy[m], NULL: rows), arguments already

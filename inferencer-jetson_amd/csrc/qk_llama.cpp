@@ -36,6 +36,9 @@ struct qk_llama {
     hipEvent_t upload_done = nullptr;   // the last token upload from h_token[0] has read it
     bool upload_pending = false;
     int last_next = -1;
+    int int8_q4k = 0, int8_q6k = 0;            // INT8 GEMV mode (use_dp4a / use_q6_dp4a)
+    int8_t *xq = nullptr;                      // INT8 mode: quantized activations, max(dim, hidden)
+    float *xscale = nullptr;
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
 };
 
@@ -50,7 +53,8 @@ int dev_alloc(T **p, size_t count, const char *what) {
 
 void release(qk_llama *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
-                    m->value_cache, m->cosine, m->sine, m->argmax_ws, m->attn_ws, m->d_next, m->d_token};
+                    m->value_cache, m->cosine, m->sine, m->argmax_ws, m->attn_ws, m->d_next, m->d_token,
+                    m->xq, m->xscale};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
@@ -96,9 +100,95 @@ int split_weights(std::vector<void *> &owned, qk_llama_weights &w, std::vector<q
     return QK_OK;
 }
 
+bool int8_type(const qk_llama *m, int type) {
+    return (type == QK_TYPE_Q4_K && m->int8_q4k) ||
+           ((type == QK_TYPE_Q6_K || type == QK_TYPE_Q6_K_SPLIT) && m->int8_q6k);
+}
+
+// y_m = W_m x for each matrix: the INT8 kernels on m->xq / m->xscale (already
+// quantized from x) for the types in INT8 mode, the FP32 kernels on x for the
+// others -- FastGPU::matvec's per-type choice (inferencer.cu:1159-1168) and
+// qkv_cuda's per-row branch (inferencer.cu:776-780).
+int gemv_by_mode(qk_llama *m, const qk_matrix *mats, int n, const float *x, int cols, hipStream_t s) {
+    qk_matrix i8[QK_MAX_FUSED], f32[QK_MAX_FUSED];
+    int ni = 0, nf = 0, st;
+    for (int k = 0; k < n; ++k) (int8_type(m, mats[k].type) ? i8[ni++] : f32[nf++]) = mats[k];
+    if (ni && (st = qk::launch_gemv_i8(i8, ni, m->xq, cols, m->xscale, cols / 32, cols, 1, nullptr, s))) return st;
+    if (nf && (st = qk::launch_gemv_f32(f32, nf, x, cols, cols, 1, nullptr, s))) return st;
+    return QK_OK;
+}
+
+// The INT8 mode of FastRunner::forward (inferencer.cu:1424-1531 with use_dp4a /
+// use_q6_dp4a and --fused-norm-quant): RMSNorm and the per-32 quantization in
+// one launch before the QKV and gate/up GEMVs, the attention and FFN outputs
+// quantized before the o and down GEMVs, the residual adds and SiLU * up as
+// separate launches, as in the reference.
+int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
+    const qk_llama_config &c = m->cfg;
+    const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
+    int st;
+    if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
+    qk::SplitAttention attn{};
+    attn.q = m->q;
+    attn.k = m->k;
+    attn.v = m->v;
+    attn.cosine = m->cosine;
+    attn.sine = m->sine;
+    attn.key_cache = m->key_cache;
+    attn.value_cache = m->value_cache;
+    attn.out = m->attn;
+    attn.cache_rows = c.context;
+    attn.rows_hint = pos + 1;
+    attn.pos = attn.max_pos = pos;
+    attn.n_tokens = 1;
+    attn.heads = c.heads;
+    attn.kv_heads = c.kv_heads;
+    attn.head_dim = hd;
+    auto norm_quant = [&](const float *w) {
+        return qk_rmsnorm_quantize_x32(m->x, dim, w, m->xn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, c.eps, s);
+    };
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        if ((st = norm_quant(L.attn_norm))) return st;
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = gemv_by_mode(m, qkv, 3, m->xn, dim, s))) return st;
+        attn.layer = l;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->tmp};
+        if (int8_type(m, L.o_type) &&
+            (st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, s)))
+            return st;
+        if ((st = gemv_by_mode(m, &o, 1, m->attn, dim, s)) || (st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
+        if ((st = norm_quant(L.ffn_norm))) return st;
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+        if ((st = gemv_by_mode(m, gu, 2, m->xn, dim, s)) || (st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s)))
+            return st;
+        const qk_matrix down{L.down_type, dim, L.down, m->tmp};
+        if (int8_type(m, L.down_type) &&
+            (st = qk_quantize_x32(m->gate, c.hidden, m->xq, c.hidden, m->xscale, c.hidden / 32, c.hidden, 1, s)))
+            return st;
+        if ((st = gemv_by_mode(m, &down, 1, m->gate, c.hidden, s)) || (st = qk_add_f32(m->x, m->tmp, dim, s)))
+            return st;
+    }
+    if (!need_logits) return QK_OK;
+    if ((st = norm_quant(m->w.output_norm))) return st;
+    const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
+    const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
+    const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+    if ((st = gemv_by_mode(m, &head, 1, m->xn, dim, s))) return st;
+    return qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s);
+}
+
 }  // namespace
 
 extern "C" {
+
+int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_set_int8: null handle");
+    m->int8_q4k = q4k_int8 != 0;
+    m->int8_q6k = q6k_int8 != 0;
+    return qk::ok();
+}
 
 int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream, qk_llama **out) {
     if (!cfg || !w || !out || !w->layers || !w->token_embd || !w->output_norm)
@@ -152,7 +242,9 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
         (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), 2 * qk::kArgPartsMax * sizeof(float),
                         "argmax partials")) ||
-        (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token"))) {
+        (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token")) ||
+        (st = dev_alloc(&m->xq, std::max(c.dim, c.hidden), "quantized activations")) ||
+        (st = dev_alloc(&m->xscale, std::max(c.dim, c.hidden) / 32, "activation scales"))) {
         release(m);
         return st;
     }
@@ -236,63 +328,71 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         tok = m->d_token;
     }
     m->last_next = -1;
-    if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
-    // Five launches per layer: RMSNorm is staged inside the QKV / gate-up
-    // GEMVs, SiLU * up inside the down GEMV, the residual adds are their
-    // epilogues, and RoPE + the KV write open the attention kernel.
-    qk::GemvFusion attn_in, ffn_in, residual, down_in;
-    attn_in.norm_eps = ffn_in.norm_eps = c.eps;
-    residual.accumulate = down_in.accumulate = 1;
-    down_in.up = m->up;
-    qk::SplitAttention attn{};
-    attn.q = m->q;
-    attn.k = m->k;
-    attn.v = m->v;
-    attn.cosine = m->cosine;
-    attn.sine = m->sine;
-    attn.key_cache = m->key_cache;
-    attn.value_cache = m->value_cache;
-    attn.out = m->attn;
-    attn.cache_rows = c.context;
-    attn.rows_hint = pos + 1;
-    attn.pos = attn.max_pos = pos;
-    attn.n_tokens = 1;
-    attn.heads = c.heads;
-    attn.kv_heads = c.kv_heads;
-    attn.head_dim = hd;
-    for (int l = 0; l < c.layers; ++l) {
-        const qk_llama_layer &L = m->layers[l];
-        attn_in.norm_w = L.attn_norm;
-        ffn_in.norm_w = L.ffn_norm;
-        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, dim, 1, nullptr, attn_in, s))) return st;
-        attn.layer = l;
-        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
-        const qk_matrix o{L.o_type, dim, L.o, m->x};
-        if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, dim, 1, nullptr, residual, s))) return st;
-        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, dim, 1, nullptr, ffn_in, s))) return st;
-        const qk_matrix down{L.down_type, dim, L.down, m->x};
-        if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, c.hidden, 1, nullptr, down_in, s))) return st;
+    if (m->int8_q4k || m->int8_q6k) {
+        if ((st = forward_int8(m, tok, pos, need_logits != 0, s))) return st;
+        if (!need_logits) {
+            if (next_token) *next_token = -1;
+            return qk::ok();
+        }
+    } else {
+        if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
+        // Five launches per layer: RMSNorm is staged inside the QKV / gate-up
+        // GEMVs, SiLU * up inside the down GEMV, the residual adds are their
+        // epilogues, and RoPE + the KV write open the attention kernel.
+        qk::GemvFusion attn_in, ffn_in, residual, down_in;
+        attn_in.norm_eps = ffn_in.norm_eps = c.eps;
+        residual.accumulate = down_in.accumulate = 1;
+        down_in.up = m->up;
+        qk::SplitAttention attn{};
+        attn.q = m->q;
+        attn.k = m->k;
+        attn.v = m->v;
+        attn.cosine = m->cosine;
+        attn.sine = m->sine;
+        attn.key_cache = m->key_cache;
+        attn.value_cache = m->value_cache;
+        attn.out = m->attn;
+        attn.cache_rows = c.context;
+        attn.rows_hint = pos + 1;
+        attn.pos = attn.max_pos = pos;
+        attn.n_tokens = 1;
+        attn.heads = c.heads;
+        attn.kv_heads = c.kv_heads;
+        attn.head_dim = hd;
+        for (int l = 0; l < c.layers; ++l) {
+            const qk_llama_layer &L = m->layers[l];
+            attn_in.norm_w = L.attn_norm;
+            ffn_in.norm_w = L.ffn_norm;
+            const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+            if ((st = qk::launch_gemv_fused(qkv, 3, m->x, dim, dim, 1, nullptr, attn_in, s))) return st;
+            attn.layer = l;
+            if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+            const qk_matrix o{L.o_type, dim, L.o, m->x};
+            if ((st = qk::launch_gemv_fused(&o, 1, m->attn, dim, dim, 1, nullptr, residual, s))) return st;
+            const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+            if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, dim, 1, nullptr, ffn_in, s))) return st;
+            const qk_matrix down{L.down_type, dim, L.down, m->x};
+            if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, c.hidden, 1, nullptr, down_in, s))) return st;
+        }
+        if (!need_logits) {
+            if (next_token) *next_token = -1;
+            return qk::ok();
+        }
+        // The LM head's epilogue keeps each workgroup's best logit (argmax_blocks_cuda
+        // folded in); one small kernel picks the token from those partials.
+        qk::GemvFusion out_in;
+        out_in.norm_w = m->w.output_norm;
+        out_in.norm_eps = c.eps;
+        out_in.arg_v = static_cast<float *>(m->argmax_ws);
+        out_in.arg_i = reinterpret_cast<int *>(out_in.arg_v + qk::kArgPartsMax);
+        int parts = 0;
+        out_in.arg_parts = &parts;
+        const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
+        const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
+        const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+        if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, dim, 1, nullptr, out_in, s))) return st;
+        if ((st = qk::launch_argmax_final(out_in.arg_v, out_in.arg_i, parts, m->d_next, s))) return st;
     }
-    if (!need_logits) {
-        if (next_token) *next_token = -1;
-        return qk::ok();
-    }
-    // The LM head's epilogue keeps each workgroup's best logit (argmax_blocks_cuda
-    // folded in); one small kernel picks the token from those partials.
-    qk::GemvFusion out_in;
-    out_in.norm_w = m->w.output_norm;
-    out_in.norm_eps = c.eps;
-    out_in.arg_v = static_cast<float *>(m->argmax_ws);
-    out_in.arg_i = reinterpret_cast<int *>(out_in.arg_v + qk::kArgPartsMax);
-    int parts = 0;
-    out_in.arg_parts = &parts;
-    const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
-    const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
-    const qk_matrix head{out_type, c.vocab, out_w, m->logits};
-    if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, dim, 1, nullptr, out_in, s))) return st;
-    if ((st = qk::launch_argmax_final(out_in.arg_v, out_in.arg_i, parts, m->d_next, s))) return st;
     if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");

@@ -69,6 +69,7 @@ def lib() -> ctypes.CDLL:
         h.oq_llama_load_cache.argtypes, h.oq_llama_load_cache.restype = [vp, vp, vp, i32], i32
         h.oq_llama_forward.argtypes = [vp, i32, i32, i32, vp, ctypes.POINTER(i32)]
         h.oq_llama_forward.restype = i32
+        h.oq_llama_set_int8.argtypes, h.oq_llama_set_int8.restype = [vp, i32, i32], None
         _LIB = h
     return _LIB
 
@@ -219,6 +220,12 @@ class Llama:
     def load_cache(self, key_cache: np.ndarray, value_cache: np.ndarray, n_positions: int) -> None:
         assert lib().oq_llama_load_cache(self.handle, _p(np.ascontiguousarray(key_cache, dtype=np.float32)),
                                          _p(np.ascontiguousarray(value_cache, dtype=np.float32)), n_positions) == 0
+
+    def set_int8(self, q4k: bool = True, q6k: bool = True) -> None:
+        """INT8 GEMV modes of the decode step (the reference's use_dp4a and
+        use_q6_dp4a): each GEMV on a matrix of an enabled type quantizes its
+        input per 32 values and takes exact integer sub-block dots."""
+        lib().oq_llama_set_int8(self.handle, int(q4k), int(q6k))
 
     def forward(self, token: int, pos: int, need_logits: bool = True):
         logits = np.empty(self.cfg.vocab, dtype=np.float64) if need_logits else None

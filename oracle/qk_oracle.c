@@ -452,6 +452,7 @@ struct oq_llama {
     float *cosine, *sine;
     double *key_cache, *value_cache;     /* [layer][context][kv_dim] */
     double *x, *xn, *q, *k, *v, *attn, *tmp, *gate, *up;
+    int int8_q4k, int8_q6k;              /* the reference's use_dp4a / use_q6_dp4a */
 };
 
 oq_llama *oq_llama_create(const oq_llama_config *cfg, const oq_llama_weights *w) {
@@ -523,8 +524,38 @@ static void matvec_f64(int type, const uint8_t *w, const double *x, double *y, i
     }
 }
 
+/* INT8 mode of FastGPU::matvec (inferencer.cu:1159-1166): the activation,
+   rounded to fp32 as the device holds it, is quantized per 32 values
+   (quantize_x32_cuda, 544-556) and the product is the exact integer
+   sub-block dots combined in fp64 (oq_gemv_i8_f64). */
+static void matvec_i8(int type, const uint8_t *w, const double *x, double *y, int64_t cols, int64_t rows) {
+    float *xf = (float *)malloc((size_t)cols * sizeof(float));
+    int8_t *xq = (int8_t *)malloc((size_t)cols);
+    float *xs = (float *)malloc((size_t)(cols / 32) * sizeof(float));
+    for (int64_t i = 0; i < cols; ++i) xf[i] = (float)x[i];
+    oq_quantize_x32(xf, xq, xs, cols);
+    oq_gemv_i8_f64(type, w, xq, xs, y, cols, rows);
+    free(xf);
+    free(xq);
+    free(xs);
+}
+
+static void matvec_mode(const oq_llama *m, int type, const uint8_t *w, const double *x, double *y, int64_t cols,
+                        int64_t rows) {
+    if ((type == 12 && m->int8_q4k) || (type == 14 && m->int8_q6k))
+        matvec_i8(type, w, x, y, cols, rows);
+    else
+        matvec_f64(type, w, x, y, cols, rows);
+}
+
+void oq_llama_set_int8(oq_llama *m, int q4k_int8, int q6k_int8) {
+    m->int8_q4k = q4k_int8 != 0;
+    m->int8_q6k = q6k_int8 != 0;
+}
+
 /* FastRunner::forward, inferencer.cu:1424-1531, with head_dim, heads and the
-   frequency count generalised. */
+   frequency count generalised; the GEMVs follow the INT8 modes set by
+   oq_llama_set_int8 (FP32 by default). */
 int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *logits, int *next_token) {
     const oq_llama_config *c = &m->cfg;
     if (pos < 0 || pos >= c->context || token < 0 || token >= c->vocab) return -1;
@@ -541,21 +572,21 @@ int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *l
         double *kc = m->key_cache + (int64_t)l * c->context * kv;
         double *vc = m->value_cache + (int64_t)l * c->context * kv;
         oq_rmsnorm(m->x, L->attn_norm, m->xn, dim, c->eps);
-        matvec_f64(L->q_type, L->q, m->xn, m->q, dim, dim);
-        matvec_f64(L->k_type, L->k, m->xn, m->k, dim, kv);
-        matvec_f64(L->v_type, L->v, m->xn, m->v, dim, kv);
+        matvec_mode(m, L->q_type, L->q, m->xn, m->q, dim, dim);
+        matvec_mode(m, L->k_type, L->k, m->xn, m->k, dim, kv);
+        matvec_mode(m, L->v_type, L->v, m->xn, m->v, dim, kv);
         oq_rope(m->q, dim, m->cosine, m->sine, pos, hd);
         oq_rope(m->k, kv, m->cosine, m->sine, pos, hd);
         memcpy(kc + (int64_t)pos * kv, m->k, (size_t)kv * sizeof(double));
         memcpy(vc + (int64_t)pos * kv, m->v, (size_t)kv * sizeof(double));
         oq_attention(m->q, kc, vc, m->attn, pos, c->heads, c->kv_heads, hd);
-        matvec_f64(L->o_type, L->o, m->attn, m->tmp, dim, dim);
+        matvec_mode(m, L->o_type, L->o, m->attn, m->tmp, dim, dim);
         for (int i = 0; i < dim; ++i) m->x[i] += m->tmp[i];
         oq_rmsnorm(m->x, L->ffn_norm, m->xn, dim, c->eps);
-        matvec_f64(L->gate_type, L->gate, m->xn, m->gate, dim, c->hidden);
-        matvec_f64(L->up_type, L->up, m->xn, m->up, dim, c->hidden);
+        matvec_mode(m, L->gate_type, L->gate, m->xn, m->gate, dim, c->hidden);
+        matvec_mode(m, L->up_type, L->up, m->xn, m->up, dim, c->hidden);
         oq_silu_mul(m->gate, m->up, c->hidden);
-        matvec_f64(L->down_type, L->down, m->gate, m->tmp, c->hidden, dim);
+        matvec_mode(m, L->down_type, L->down, m->gate, m->tmp, c->hidden, dim);
         for (int i = 0; i < dim; ++i) m->x[i] += m->tmp[i];
     }
     if (!need_logits) {
@@ -566,7 +597,7 @@ int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *l
     const uint8_t *out_w = m->w.output ? m->w.output : m->w.token_embd;
     int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     double *lg = logits ? logits : (double *)malloc((size_t)c->vocab * sizeof(double));
-    matvec_f64(out_type, out_w, m->xn, lg, dim, c->vocab);
+    matvec_mode(m, out_type, out_w, m->xn, lg, dim, c->vocab);
     if (next_token) *next_token = (int)oq_argmax_f64(lg, c->vocab);
     if (!logits) free(lg);
     return 0;

@@ -103,6 +103,9 @@ void oq_llama_destroy(oq_llama *m);
 int oq_llama_load_cache(oq_llama *m, const float *key_cache, const float *value_cache, int n_positions);
 /* One decode step (inferencer.cu:1424-1531).  Writes the fp64 logits when
    logits != NULL and need_logits, and the greedy token. */
+/* INT8 GEMV modes of the decode step (use_dp4a for Q4_K, use_q6_dp4a for
+   Q6_K; both off after create). */
+void oq_llama_set_int8(oq_llama *m, int q4k_int8, int q6k_int8);
 int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *logits, int *next_token);
 
 #ifdef __cplusplus

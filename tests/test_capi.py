@@ -126,6 +126,15 @@ def test_int8_validation(qk):
     assert lib.qk_gemv_i8(12, w, xq, 1024, xs, 64, y, 16, 2048, 16, 1, None) == qk.QK_ERR_INVALID_ARG
     assert lib.qk_gemv_i8(12, w, xq + 1, 2048, xs, 64, y, 16, 2048, 16, 1, None) == qk.QK_ERR_ALIGN
     assert lib.qk_gemv_i8(12, w, None, 2048, xs, 64, y, 16, 2048, 16, 1, None) == qk.QK_ERR_INVALID_ARG
+    mats = (qk.qk_matrix * 2)()
+    for m in mats:
+        m.type, m.rows, m.w, m.y = 12, 16, w, y
+    assert lib.qk_gemv_multi_i8(mats, 0, xq, xs, 2048, None) == qk.QK_ERR_INVALID_ARG
+    assert lib.qk_gemv_multi_i8(mats, 2, None, xs, 2048, None) == qk.QK_ERR_INVALID_ARG
+    assert lib.qk_gemv_multi_i8(mats, 2, xq + 8, xs, 2048, None) == qk.QK_ERR_ALIGN
+    mats[1].type = 13
+    assert lib.qk_gemv_multi_i8(mats, 2, xq, xs, 2048, None) == qk.QK_ERR_TYPE
+    assert lib.qk_llama_set_int8(None, 1, 1) == qk.QK_ERR_INVALID_ARG
 
 
 def test_rmsnorm_quantize_validation(qk):

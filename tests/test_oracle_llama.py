@@ -26,8 +26,15 @@ def _rope(v, cos_row, sin_row, head_dim):
 
 
 class TorchStep:
-    def __init__(self, oracle, cfg, weights, kc, vc):
+    def __init__(self, oracle, cfg, weights, kc, vc, int8_types=()):
+        """int8_types: storage types whose products take the activation
+        quantized per 32 values (rounded to fp32 first, then
+        oracle.quantize_x32, pinned by test_oracle_int8) and dequantized
+        again; the INT8 sub-block formula equals the dequantized weight
+        times that activation in exact arithmetic."""
         self.cfg = cfg
+        self.oracle = oracle
+        self.int8_types = set(int8_types)
         dq = lambda t, a, cols, rows: torch.from_numpy(oracle.dequant(t, a, cols, rows).astype(np.float64))
         dim, hidden = cfg["dim"], cfg["hidden"]
         self.hd = dim // cfg["heads"]
@@ -35,6 +42,7 @@ class TorchStep:
         self.layers = []
         for L in weights["layers"]:
             self.layers.append(dict(
+                types={n: L[n + "_type"] for n in ("q", "k", "v", "o", "gate", "up", "down")},
                 q=dq(L["q_type"], L["q"], dim, dim), k=dq(L["k_type"], L["k"], dim, kv),
                 v=dq(L["v_type"], L["v"], dim, kv), o=dq(L["o_type"], L["o"], dim, dim),
                 gate=dq(L["gate_type"], L["gate"], dim, hidden), up=dq(L["up_type"], L["up"], dim, hidden),
@@ -42,22 +50,31 @@ class TorchStep:
                 attn_norm=torch.from_numpy(L["attn_norm"].astype(np.float64)),
                 ffn_norm=torch.from_numpy(L["ffn_norm"].astype(np.float64))))
         self.embd = dq(weights["embd_type"], weights["token_embd"], dim, cfg["vocab"])
+        self.embd_type = weights["embd_type"]
         self.out_norm = torch.from_numpy(weights["output_norm"].astype(np.float64))
         c, s = oracle.rope_tables(cfg["context"], self.hd, cfg["rope_theta"])
         self.cos, self.sin = torch.from_numpy(c.astype(np.float64)), torch.from_numpy(s.astype(np.float64))
         self.kc = torch.from_numpy(kc.astype(np.float64)).clone()
         self.vc = torch.from_numpy(vc.astype(np.float64)).clone()
 
+    def mv(self, qtype, w, x):
+        if qtype in self.int8_types:
+            xq, xs = self.oracle.quantize_x32(x.numpy().astype(np.float32))
+            x = torch.from_numpy(xq.astype(np.float64) * np.repeat(xs.astype(np.float64), 32))
+        return w @ x
+
     def forward(self, token, pos):
         cfg, hd = self.cfg, self.hd
+        mv = self.mv
         group = cfg["heads"] // cfg["kv_heads"]
         x = self.embd[token].clone()
         for l, L in enumerate(self.layers):
             xn = _rms(x, L["attn_norm"], cfg["eps"])
-            q = _rope(L["q"] @ xn, self.cos[pos], self.sin[pos], hd)
-            k = _rope(L["k"] @ xn, self.cos[pos], self.sin[pos], hd)
+            t = L["types"]
+            q = _rope(mv(t["q"], L["q"], xn), self.cos[pos], self.sin[pos], hd)
+            k = _rope(mv(t["k"], L["k"], xn), self.cos[pos], self.sin[pos], hd)
             self.kc[l, pos] = k
-            self.vc[l, pos] = L["v"] @ xn
+            self.vc[l, pos] = mv(t["v"], L["v"], xn)
             keys = self.kc[l, : pos + 1].reshape(pos + 1, cfg["kv_heads"], hd)
             vals = self.vc[l, : pos + 1].reshape(pos + 1, cfg["kv_heads"], hd)
             heads = []
@@ -65,11 +82,11 @@ class TorchStep:
                 kvh = h // group
                 p = torch.softmax(keys[:, kvh] @ q[h * hd:(h + 1) * hd] / np.sqrt(hd), dim=0)
                 heads.append(p @ vals[:, kvh])
-            x = x + L["o"] @ torch.cat(heads)
+            x = x + mv(t["o"], L["o"], torch.cat(heads))
             xn = _rms(x, L["ffn_norm"], cfg["eps"])
-            g = L["gate"] @ xn
-            x = x + L["down"] @ (g * torch.sigmoid(g) * (L["up"] @ xn))
-        return self.embd @ _rms(x, self.out_norm, cfg["eps"])
+            g = mv(t["gate"], L["gate"], xn)
+            x = x + mv(t["down"], L["down"], g * torch.sigmoid(g) * mv(t["up"], L["up"], xn))
+        return mv(self.embd_type, self.embd, _rms(x, self.out_norm, cfg["eps"]))
 
 
 @pytest.mark.parametrize("seed", [21, 22])
@@ -105,3 +122,35 @@ def test_llama_step_without_logits_still_writes_cache(oracle, workloads):
     n_a, la = a.forward(11, 4)
     n_b, lb = b.forward(11, 4)
     assert n_a == n_b and np.array_equal(la, lb)
+
+
+@pytest.mark.parametrize("q4k,q6k", [(True, True), (True, False), (False, True)])
+def test_llama_int8_modes_match_torch_restatement(oracle, workloads, q4k, q6k):
+    """The INT8 modes (use_dp4a / use_q6_dp4a, inferencer.cu:1159-1166):
+    only the enabled storage types quantize their input, each from the
+    fp32-rounded activation the device holds.  The restatement differs from
+    the oracle only by the fp32 rounding of dequantized weights (~1e-7), far
+    below the INT8-vs-FP32 difference the test also requires, so a product
+    quantized that should not be (or the reverse) fails."""
+    cfg = CFG
+    seed = 23
+    weights = workloads.llama_weights(cfg, seed)
+    n_prefill = 9
+    kc, vc = workloads.llama_kv_prefill(cfg, seed, n_prefill)
+    ref = oracle.Llama(cfg, weights)
+    ref.set_int8(q4k, q6k)
+    fp = oracle.Llama(cfg, weights)
+    ref.load_cache(kc, vc, n_prefill)
+    fp.load_cache(kc, vc, n_prefill)
+    types = [t for t, on in ((12, q4k), (14, q6k)) if on]
+    tstep = TorchStep(oracle, cfg, weights, kc, vc, int8_types=types)
+    token = int(workloads.llama_prompt(cfg, seed, 1)[0])
+    for pos in range(n_prefill, n_prefill + 3):
+        nxt, logits = ref.forward(token, pos)
+        _, lf = fp.forward(token, pos)
+        want = tstep.forward(token, pos).numpy()
+        err, gap = rel_l2(logits, want), rel_l2(logits, lf)
+        print(f"pos {pos}: rel-L2 vs restatement {err:.2e}, vs FP32 mode {gap:.2e}")
+        assert err < 1e-5, pos
+        assert gap > 100 * err and gap > 1e-4, pos
+        token = nxt
