@@ -294,10 +294,10 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
             # FP32, per layer: QKV, attention + split merge, o, gate/up, down;
             # then embedding, LM head and the two argmax stages.  INT8, per
-            # layer: norm+quantize, QKV, attention + merge, quantize, o, add,
-            # norm+quantize, gate/up, SiLU*up, quantize, down, add; then
+            # layer: norm+quantize, QKV, attention + merge, quantize, o (+add),
+            # norm+quantize, gate/up, SiLU*up+quantize, down (+add); then
             # embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (13 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3)}
+            "kernels_per_token": (10 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3)}
 
 
 def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
@@ -478,6 +478,18 @@ def main() -> int:
         sec["lm_head_q6k_gguf_layout"] = {"kernel_us": round(kg * 1e3, 2),
                                           "GBps_kernel": round(step_bytes / (kg * 1e-3) / 1e9, 1),
                                           "frac_of_peak": round(step_bytes / (kg * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        # The INT8 mode's kernel on the same split copies (gemv_q6_dp4a,
+        # inferencer.cu:597-643): x quantized once outside the timed launches.
+        xq = torch.empty(cols, dtype=torch.int8, device="cuda")
+        xs = torch.empty(cols // 32, dtype=torch.float32, device="cuda")
+        qk.quantize(x, xq, xs, cols, stream=stream)
+        _, ki = time_launches(torch, lambda i: qk.matvec_i8(tensors[i % len(tensors)], xq, xs, y, cols, rows,
+                                                           stream=stream), 2000, 2000, stream)
+        i8_bytes = weight_bytes + cols + cols // 32 * 4 + rows * 4
+        sec["lm_head_q6k_int8"] = {"kernel_us": round(ki * 1e3, 2), "bytes_per_launch": i8_bytes,
+                                   "GBps_kernel": round(i8_bytes / (ki * 1e-3) / 1e9, 1),
+                                   "frac_of_peak": round(i8_bytes / (ki * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"[bench] lm_head_q6k_int8: {json.dumps(sec['lm_head_q6k_int8'])}")
         log(f"[bench] lm_head_q6k_gguf_layout: {json.dumps(sec['lm_head_q6k_gguf_layout'])}")
         sec["gemv_q4k_128256x2048"] = bench_q4k_lm_shape(torch, qk, wl, stream, args.copies)
         log(f"[bench] gemv_q4k_128256x2048: {json.dumps(sec['gemv_q4k_128256x2048'])}")

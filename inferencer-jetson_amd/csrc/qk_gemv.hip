@@ -253,7 +253,7 @@ struct F32Policy {
         float X[4];
     };
 
-    static constexpr bool kFused = false;
+    static constexpr bool kAccumulate = false;   // y += W x when p.accumulate
     static constexpr bool kArgmax = false;   // greedy-token epilogue
 
     // LDS bytes of the prepared activations of one token.
@@ -335,7 +335,7 @@ struct F32Policy {
 // activations are staged, and the residual add in the epilogue.  A policy
 // of its own so the plain kernels carry none of it.
 struct F32FusedPolicy : F32Policy {
-    static constexpr bool kFused = true;
+    static constexpr bool kAccumulate = true;
 
     // LDS bytes of the prepared activations of one token, plus 64 bytes of
     // reduction scratch for the fused RMSNorm.
@@ -402,7 +402,7 @@ struct F32ArgPolicy : F32FusedPolicy {
 
 struct I8Policy {
     static constexpr bool kPrepLds = false;
-    static constexpr bool kFused = false;
+    static constexpr bool kAccumulate = true;   // the INT8 step's residual adds
     static constexpr bool kArgmax = false;
     __host__ __device__ static size_t lds_bytes(int) { return 0; }
     __device__ static void prep(const GemvParams &, int, int, XGroup *) {}
@@ -533,11 +533,11 @@ __device__ __forceinline__ float piece_dot(int type, const Raw &r, const typenam
     return is_q4k<TYPE>(type) ? Policy::q4k(r, L, g) : Policy::q6k(r, L, h);
 }
 
-// Output store: overwrite, or (fused policy with accumulate) add into y.
-// Returns the stored value.
+// Output store: overwrite, or (policies that carry it, with p.accumulate)
+// add into y.  Returns the stored value.
 template <class Policy>
 __device__ __forceinline__ float store_y(const GemvParams &p, float *y, float v) {
-    if constexpr (Policy::kFused) {
+    if constexpr (Policy::kAccumulate) {
         if (p.accumulate) v += *y;
     }
     *y = v;
@@ -866,12 +866,13 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
 // INT8 path shared by qk_gemv_i8 and qk_gemv_multi_i8 (arguments already
 // validated): quantized activations xq / xscale of n_tokens tokens.
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
-                   int cols, int n_tokens, const int *ldy, hipStream_t stream) {
+                   int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream) {
     GemvParams p{};
     p.x = xq;
     p.xscale = xscale;
     p.ldx = ldxq;
     p.ldscale = ldscale;
+    p.accumulate = accumulate;
     return launch<I8Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "INT8 GEMV launch");
 }
 
@@ -970,7 +971,8 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
     if (!qk::aligned(xq, 16) || ldxq % 16 || !qk::aligned(xscale, 4) || !qk::aligned(y, 4))
         return qk::fail(QK_ERR_ALIGN, "qk_gemv_i8: xq and ldxq must keep 16-byte alignment");
     const qk_matrix m{type, rows, w, y};
-    return qk::launch_gemv_i8(&m, 1, xq, ldxq, xscale, ldscale, cols, n_tokens, &ldy, static_cast<hipStream_t>(stream));
+    return qk::launch_gemv_i8(&m, 1, xq, ldxq, xscale, ldscale, cols, n_tokens, &ldy, 0,
+                              static_cast<hipStream_t>(stream));
 }
 
 int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const float *xscale, int cols,
@@ -988,7 +990,7 @@ int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const 
         if (!qk::aligned(mats[m].y, 4)) return qk::fail(QK_ERR_ALIGN, "qk_gemv_multi_i8: misaligned output");
         ldy[m] = mats[m].rows;
     }
-    return qk::launch_gemv_i8(mats, n_mats, xq, cols, xscale, cols / 32, cols, 1, ldy,
+    return qk::launch_gemv_i8(mats, n_mats, xq, cols, xscale, cols / 32, cols, 1, ldy, 0,
                               static_cast<hipStream_t>(stream));
 }
 

@@ -80,9 +80,37 @@ __device__ __forceinline__ void arg_better(float &bv, int &bi, float v, int i) {
 int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                     const int *ldy, hipStream_t stream);
 // INT8 GEMV of n_tokens quantized activation rows (xq + t*ldxq, xscale +
-// t*ldscale; y + t*ldy[m]), arguments already validated.
+// t*ldscale; y + t*ldy[m]), arguments already validated; accumulate != 0
+// adds W x into y instead of overwriting it.
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
-                   int cols, int n_tokens, const int *ldy, hipStream_t stream);
+                   int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
+// SiLU(gate) * up quantized per 32 values straight into xq / xscale (n a
+// multiple of 32): bit-identical to qk_silu_mul_f32 then qk_quantize_x32,
+// without the fp32 product written.  Arguments already validated.
+int launch_silu_mul_quantize(const float *gate, const float *up, int8_t *xq, float *xscale, int n,
+                             hipStream_t stream);
+
+// SiLU(g) * u in silu_cuda's expression (inferencer.cu:1053-1057), shared by
+// every kernel that forms it so their results agree bit for bit.
+__device__ __forceinline__ float silu_mul_value(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+// quantize_x32_cuda (inferencer.cu:544-556) for the value a lane holds: the
+// 32 lanes of its half-wave form one group; lanes past the row hold 0.
+// scale = amax/127 (1 when amax is 0), q = clamp(rne(value/scale), +-127),
+// IEEE divide.  Lane 0 of the group stores the scale.
+__device__ __forceinline__ void quantize_group_store(float value, bool in_row, int lane32, int8_t *q_out,
+                                                     float *scale_out) {
+    float amax = fabsf(value);
+    #pragma unroll
+    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    const float scale = amax > 0.f ? amax / 127.f : 1.f;
+    if (lane32 == 0 && in_row) *scale_out = scale;
+    if (in_row) {
+        int q = static_cast<int>(rintf(value / scale));
+        q = q < -127 ? -127 : (q > 127 ? 127 : q);
+        *q_out = static_cast<int8_t>(q);
+    }
+}
 // Whether a row of cols columns can stage its activations for the fusions.
 bool gemv_fusable(int cols);
 // n_tokens tokens (x + t*ldx; y + t*ldy[m], NULL: rows), arguments already

@@ -109,20 +109,39 @@ bool int8_type(const qk_llama *m, int type) {
 // quantized from x) for the types in INT8 mode, the FP32 kernels on x for the
 // others -- FastGPU::matvec's per-type choice (inferencer.cu:1159-1168) and
 // qkv_cuda's per-row branch (inferencer.cu:776-780).
-int gemv_by_mode(qk_llama *m, const qk_matrix *mats, int n, const float *x, int cols, hipStream_t s) {
+// Matrices in FP32 mode cannot add into y (the plain kernels overwrite), so
+// callers pass accumulate only for a single INT8 matrix.
+int gemv_by_mode(qk_llama *m, const qk_matrix *mats, int n, const float *x, int cols, hipStream_t s,
+                 int accumulate = 0) {
     qk_matrix i8[QK_MAX_FUSED], f32[QK_MAX_FUSED];
     int ni = 0, nf = 0, st;
     for (int k = 0; k < n; ++k) (int8_type(m, mats[k].type) ? i8[ni++] : f32[nf++]) = mats[k];
-    if (ni && (st = qk::launch_gemv_i8(i8, ni, m->xq, cols, m->xscale, cols / 32, cols, 1, nullptr, s))) return st;
+    if (ni && (st = qk::launch_gemv_i8(i8, ni, m->xq, cols, m->xscale, cols / 32, cols, 1, nullptr, accumulate, s)))
+        return st;
     if (nf && (st = qk::launch_gemv_f32(f32, nf, x, cols, cols, 1, nullptr, s))) return st;
     return QK_OK;
 }
 
+// x += W in for the o / down projections: an INT8 matrix adds in its own
+// epilogue (y = x, accumulate); an FP32 one writes tmp and a separate add
+// follows, as add_cuda does (inferencer.cu:1464, 1507).
+int residual_by_mode(qk_llama *m, int type, int rows, const void *w, const float *in, int cols, hipStream_t s) {
+    int st;
+    if (int8_type(m, type)) {
+        const qk_matrix mat{type, rows, w, m->x};
+        return gemv_by_mode(m, &mat, 1, in, cols, s, 1);
+    }
+    const qk_matrix mat{type, rows, w, m->tmp};
+    if ((st = gemv_by_mode(m, &mat, 1, in, cols, s))) return st;
+    return qk_add_f32(m->x, m->tmp, rows, s);
+}
+
 // The INT8 mode of FastRunner::forward (inferencer.cu:1424-1531 with use_dp4a /
 // use_q6_dp4a and --fused-norm-quant): RMSNorm and the per-32 quantization in
-// one launch before the QKV and gate/up GEMVs, the attention and FFN outputs
-// quantized before the o and down GEMVs, the residual adds and SiLU * up as
-// separate launches, as in the reference.
+// one launch before the QKV and gate/up GEMVs, the attention output quantized
+// before the o GEMV, SiLU * up and its quantization in one launch before the
+// down GEMV, and the residual adds in the INT8 GEMVs' epilogues (the same
+// fp32 sums as the reference's separate add launches).
 int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
     const qk_llama_config &c = m->cfg;
     const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
@@ -154,21 +173,18 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
         if ((st = gemv_by_mode(m, qkv, 3, m->xn, dim, s))) return st;
         attn.layer = l;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
-        const qk_matrix o{L.o_type, dim, L.o, m->tmp};
         if (int8_type(m, L.o_type) &&
             (st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, s)))
             return st;
-        if ((st = gemv_by_mode(m, &o, 1, m->attn, dim, s)) || (st = qk_add_f32(m->x, m->tmp, dim, s))) return st;
+        if ((st = residual_by_mode(m, L.o_type, dim, L.o, m->attn, dim, s))) return st;
         if ((st = norm_quant(L.ffn_norm))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = gemv_by_mode(m, gu, 2, m->xn, dim, s)) || (st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s)))
-            return st;
-        const qk_matrix down{L.down_type, dim, L.down, m->tmp};
-        if (int8_type(m, L.down_type) &&
-            (st = qk_quantize_x32(m->gate, c.hidden, m->xq, c.hidden, m->xscale, c.hidden / 32, c.hidden, 1, s)))
-            return st;
-        if ((st = gemv_by_mode(m, &down, 1, m->gate, c.hidden, s)) || (st = qk_add_f32(m->x, m->tmp, dim, s)))
-            return st;
+        if ((st = gemv_by_mode(m, gu, 2, m->xn, dim, s))) return st;
+        if (int8_type(m, L.down_type))
+            st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s);
+        else
+            st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s);
+        if (st || (st = residual_by_mode(m, L.down_type, dim, L.down, m->gate, c.hidden, s))) return st;
     }
     if (!need_logits) return QK_OK;
     if ((st = norm_quant(m->w.output_norm))) return st;

@@ -15,21 +15,30 @@ __global__ __launch_bounds__(256) void quantize_x32_kernel(const float *x, int l
                                                            float *xscale, int ldscale, int cols) {
     const int token = blockIdx.y;
     const int index = blockIdx.x * 256 + threadIdx.x;
-    const float value = index < cols ? x[static_cast<int64_t>(token) * ldx + index] : 0.f;
-    float amax = fabsf(value);
-    #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-    const float scale = amax > 0.f ? amax / 127.f : 1.f;
-    const int group = index >> 5;
-    if ((threadIdx.x & 31) == 0 && index < cols) xscale[static_cast<int64_t>(token) * ldscale + group] = scale;
-    if (index < cols) {
-        int q = static_cast<int>(rintf(value / scale));
-        q = q < -127 ? -127 : (q > 127 ? 127 : q);
-        xq[static_cast<int64_t>(token) * ldxq + index] = static_cast<int8_t>(q);
-    }
+    const bool in_row = index < cols;
+    const float value = in_row ? x[static_cast<int64_t>(token) * ldx + index] : 0.f;
+    quantize_group_store(value, in_row, threadIdx.x & 31, xq + static_cast<int64_t>(token) * ldxq + index,
+                         xscale + static_cast<int64_t>(token) * ldscale + (index >> 5));
+}
+
+// SiLU * up and the per-32 quantization in one pass (the INT8 step's input
+// of the down GEMV): one thread per value, n a multiple of 32.
+__global__ __launch_bounds__(256) void silu_mul_quantize_kernel(const float *gate, const float *up, int8_t *xq,
+                                                                float *xscale, int n) {
+    const int index = blockIdx.x * 256 + threadIdx.x;
+    const bool in_row = index < n;
+    const float value = in_row ? silu_mul_value(gate[index], up[index]) : 0.f;
+    quantize_group_store(value, in_row, threadIdx.x & 31, xq + index, xscale + (index >> 5));
 }
 
 }  // namespace
+
+int launch_silu_mul_quantize(const float *gate, const float *up, int8_t *xq, float *xscale, int n,
+                             hipStream_t stream) {
+    hipLaunchKernelGGL(silu_mul_quantize_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, gate, up, xq, xscale,
+                       n);
+    return launch_status("SiLU * up quantization launch");
+}
 }  // namespace qk
 
 extern "C" int qk_quantize_x32(const float *x, int ldx, int8_t *xq, int ldxq, float *xscale, int ldscale, int cols,

@@ -578,8 +578,7 @@ __global__ void add_kernel(float *x, const float *y, int n) {
 __global__ void silu_mul_kernel(float *gate, const float *up, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) {
-        const float g = gate[i];
-        gate[i] = g / (1.f + expf(-g)) * up[i];
+        gate[i] = silu_mul_value(gate[i], up[i]);
     }
 }
 
