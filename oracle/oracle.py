@@ -2,7 +2,7 @@
 Q4_K / Q6_K path.
 
 TEST INFRASTRUCTURE ONLY.  Loaded by tests/, by __graft_entry__.smoke() and by
-the cpu_baseline leg of bench.py -- always as the checker or the reported CPU
+the cpu_baseline leg of bench.py -- always as the oracle results are compared with, or the reported CPU
 baseline, never as the product path.  See qk_oracle.h for how each function is
 pinned.
 """

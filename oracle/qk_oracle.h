@@ -2,7 +2,7 @@
  * qk_oracle.h - CPU restatement of inferencer.cu's Q4_K / Q6_K decode, GEMV,
  * INT8-mode and decode-step semantics.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: only tests/, the
+ * TEST INFRASTRUCTURE ONLY.  This library is the test oracle: only tests/, the
  * smoke() entry of __graft_entry__.py and the cpu_baseline leg of bench.py
  * load it.  The product (libqk.so) never links, calls or falls back to it.
  *
