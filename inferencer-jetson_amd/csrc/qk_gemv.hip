@@ -45,14 +45,16 @@ constexpr int kMaxChunks = 16;
 // the activations once, so a launch with few tiles per wave runs fewer
 // workgroups; a long launch over 16-byte aligned weight fields runs more
 // waves to keep more loads in flight (measured on MI355X, 1 token):
-//   gemv_wave, 128256 x 2048 split Q6_K: 40.0 us at 2 / CU, 38.6 us at 4
-//     (the GGUF Q6_K layout, bound by its misaligned field loads, slows to
-//     41.3 us at 4); Q4_K gate/up 2 x 8192 x 2048: 9.6 us at 2, 10.2 at 4.
+//   gemv_wave, 128256 x 2048 split Q6_K: 40.0 us at 2 / CU, 39.7 at 3,
+//     38.8 at 4, 5 and 6 (the GGUF Q6_K layout, bound by its misaligned
+//     field loads, slows to 41.3 us at 4); Q4_K 128256 x 2048: 30.5 us at 3,
+//     30.1 at 4, 29.3 at 5 and 6; Q4_K gate/up 2 x 8192 x 2048 (a short
+//     launch): 9.6 us at 2, 10.2 at 4.
 //   gemv_split, split Q6_K 2048 x 8192: 9.6 us at 2 / CU, 8.6 at 1; Q4_K
 //     3072 x 3072: 6.6 / 6.1; Q4_K 8192 x 3072: 8.7 / 10.1; split Q6_K
 //     128256 x 3072: 73.5 / 111.
 constexpr int kWaveBlocksPerCu = 2;
-constexpr int kWaveBlocksPerCuLong = 4;
+constexpr int kWaveBlocksPerCuLong = 5;
 constexpr int kWaveLongTiles = 16;      // tiles per wave at kWaveBlocksPerCu
 constexpr int kSplitBlocksPerCu = 2;
 constexpr int kSplitShortTiles = 3;     // tiles per wave-group at kSplitBlocksPerCu
