@@ -132,3 +132,30 @@ def test_llama_lookup_rejects_wrong_tensors(qk, torch_gpu, workloads, synth, tmp
     assert st == qk.QK_ERR_INVALID_ARG and "blk.1.ffn_down.weight" in msg
     st, msg = status_of(drop_param)
     assert st == qk.QK_ERR_INVALID_ARG and "feed_forward_length" in msg
+
+
+def test_runner_from_gguf_int8_matches_direct(qk, torch_gpu, workloads, synth, tmp_path):
+    """The reference's default INT8 modes on a model loaded from a GGUF file:
+    bit-identical logits and tokens to the same weights passed directly."""
+    W = _weights(workloads, synth, 24, False)
+    path = tmp_path / "model.gguf"
+    gw.llama_writer(CFG, W, workloads.tensor_shape).write(path)
+    g = qk.GGUF(path)
+    g.upload()
+    rf = qk.Runner.from_gguf(g, CFG["context"])
+    rd = qk.Runner(CFG, W)
+    for r in (rf, rd):
+        r.set_int8(True, True)
+    kc, vc = workloads.llama_kv_prefill(CFG, 24, 4)
+    rf.load_kv(kc, vc)
+    rd.load_kv(kc, vc)
+    tok = 11
+    for pos in range(4, 12):
+        a = rf.forward(tok, pos, True)
+        b = rd.forward(tok, pos, True)
+        assert a == b, pos
+        assert np.array_equal(rf.logits().view(np.uint32), rd.logits().view(np.uint32)), pos
+        tok = a
+    rf.close()
+    rd.close()
+    g.close()
