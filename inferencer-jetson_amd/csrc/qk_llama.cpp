@@ -122,14 +122,21 @@ int gemv_by_mode(qk_llama *m, const qk_matrix *mats, int n, const float *x, int 
     return QK_OK;
 }
 
-// x += W in for the o / down projections: an INT8 matrix adds in its own
-// epilogue (y = x, accumulate); an FP32 one writes tmp and a separate add
-// follows, as add_cuda does (inferencer.cu:1464, 1507).
+// x += W in for the o / down projections, the sum add_cuda forms
+// (inferencer.cu:1464, 1507): an INT8 matrix adds in its own epilogue
+// (y = x, accumulate), an FP32 one in the fused kernel's residual epilogue;
+// rows too long to stage write tmp and a separate add follows.
 int residual_by_mode(qk_llama *m, int type, int rows, const void *w, const float *in, int cols, hipStream_t s) {
     int st;
     if (int8_type(m, type)) {
         const qk_matrix mat{type, rows, w, m->x};
         return gemv_by_mode(m, &mat, 1, in, cols, s, 1);
+    }
+    if (qk::gemv_fusable(cols)) {
+        qk::GemvFusion residual;
+        residual.accumulate = 1;
+        const qk_matrix mat{type, rows, w, m->x};
+        return qk::launch_gemv_fused(&mat, 1, in, cols, cols, 1, nullptr, residual, s);
     }
     const qk_matrix mat{type, rows, w, m->tmp};
     if ((st = gemv_by_mode(m, &mat, 1, in, cols, s))) return st;
