@@ -231,16 +231,18 @@ int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_strea
 
 /* ----------------------------------------------- ragged decode batches -- */
 
-/* One token of a ragged decode batch: the position of the token in its
-   sequence and the first row of that sequence in the packed KV caches
+/* One token of a ragged batch: the position of the token in its sequence
+   and the first row of that sequence in the packed KV caches
    ([layer][cache_rows][kv_dim]; a sequence owns rows kv_row .. kv_row +
-   capacity - 1).  The nearest reference code serves one sequence at
-   contiguous positions (start_pos + token, inferencer.cu:956-959,
-   1012-1016); this descriptor lets every token of a batch belong to a
-   different sequence. */
+   capacity - 1).  The token's key / value go to row kv_row + pos and it
+   attends to rows kv_row .. kv_row + pos.  The nearest reference code serves
+   one sequence at contiguous positions (start_pos + token,
+   inferencer.cu:956-959, 1012-1016); this descriptor lets the tokens of a
+   batch come from any mix of sequences -- one decode token each, or a chunk
+   of consecutive positions of one sequence (prefill). */
 typedef struct qk_batch_token {
     int32_t pos;
-    int32_t seq;       /* sequence id; informational */
+    int32_t seq;       /* sequence id; informational (kv_row identifies the rows) */
     int64_t kv_row;
 } qk_batch_token;
 
@@ -326,10 +328,11 @@ int qk_llama_destroy(qk_llama *m);
 /* The reference's INT8 GEMV modes (FastGPU's use_dp4a for Q4_K and
    use_q6_dp4a for Q6_K, inferencer.cu:1159-1166, 1611; both on by default
    there, both off here): enabled types run their GEMVs on per-32 int8
-   activations -- RMSNorm and quantization fused before QKV and gate/up
-   (--fused-norm-quant), the attention and FFN outputs quantized before o
-   and down, residual adds and SiLU * up as separate launches -- and the
-   other types stay FP32.  Takes effect at the next qk_llama_forward. */
+   activations -- RMSNorm and quantization in one launch before QKV, gate/up
+   and the LM head (--fused-norm-quant), the attention output quantized
+   before o, SiLU * up and its quantization in one launch before down, and
+   the residual adds in the o / down GEMVs' epilogues -- and the other types
+   stay FP32.  Takes effect at the next qk_llama_forward. */
 int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8);
 /* Device pointers to the fp32 caches, [layer][context][kv_dim]. */
 int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
@@ -343,14 +346,16 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
 
 /* ------------------------------------------- batched decode-step driver -- */
 
-/* A decode step for a ragged batch: up to max_tokens tokens, each from its
-   own sequence, with packed KV caches of cache_rows rows per layer
-   ([layer][cache_rows][kv_dim], fp32).  The multi-sequence counterpart of
-   FastRunner::prefill's batched path (inferencer.cu:1279-1423), which serves
-   one sequence; every projection runs through qk_gemv_multi_batched_f32 /
-   qk_gemv_batched_f32 (matrix cores from 8 tokens on).  Buffers, caches and
-   workspaces are allocated once at create; weights are handled as by
-   qk_llama_create (Q6_K copied into the split layout, the rest read in place). */
+/* A step for a ragged batch of up to max_tokens tokens -- decode tokens of
+   different sequences, prefill chunks of consecutive positions of one
+   sequence, or any mix (a continuous batch) -- with packed KV caches of
+   cache_rows rows per layer ([layer][cache_rows][kv_dim], fp32).  The
+   multi-sequence counterpart of FastRunner::prefill's batched path
+   (inferencer.cu:1279-1423), which serves one sequence; every projection
+   runs through qk_gemv_multi_batched_f32 / qk_gemv_batched_f32 (matrix cores
+   from 8 tokens on).  Buffers, caches and workspaces are allocated once at
+   create; weights are handled as by qk_llama_create (Q6_K copied into the
+   split layout, the rest read in place). */
 typedef struct qk_llama_batch qk_llama_batch;
 
 int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens,
@@ -361,11 +366,25 @@ int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_
 /* Device pointer to the fp32 logits of the last step with need_logits,
    [n_tokens][vocab]. */
 int qk_llama_batch_logits(qk_llama_batch *m, const float **logits);
-/* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  With
-   need_logits, next_tokens[t] (host) receives each token's greedy successor
-   and the call synchronises the stream; otherwise it stays asynchronous. */
+/* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  Every
+   token writes its key / value row kv_row + pos before any token's
+   attention reads the cache, so a token sees the rows of earlier positions
+   of its sequence written in the same step (causal within a prefill chunk,
+   rope_cache_batch_cuda before attention_batch_cuda, inferencer.cu:953-1041).
+   Two tokens writing the same row is QK_ERR_INVALID_ARG.  With need_logits,
+   next_tokens[t] (host) receives each token's greedy successor and the call
+   synchronises the stream; otherwise it stays asynchronous. */
 int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
                            int need_logits, int32_t *next_tokens);
+/* The same step with the LM head run only for the n_rows tokens listed in
+   logit_rows (host, token indices in [0, n_tokens), any order): logits are
+   [n_rows][vocab] in list order and next_tokens[i] (host) is the greedy
+   successor of token logit_rows[i].  The reference's prefill computes the
+   logits of a chunk's last token only (inferencer.cu:1410-1414); a
+   continuous batch needs them for each chunk end and each decode token.
+   n_rows = 0 runs no LM head and stays asynchronous. */
+int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
+                                const int32_t *logit_rows, int n_rows, int32_t *next_tokens);
 
 /* --------------------------------------------------------------- GGUF -- */
 

@@ -132,6 +132,8 @@ SIGNATURES = {
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
+    "qk_llama_batch_forward_rows": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i,
+                                         ctypes.POINTER(ctypes.c_int32), _i, ctypes.POINTER(ctypes.c_int32)]),
     "qk_gguf_open": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_gguf_close": (_i, [_vp]),
     "qk_gguf_param": (_i, [_vp, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]),
@@ -568,18 +570,27 @@ class BatchRunner:
         check(lib().qk_llama_batch_kv_cache(self.handle, ctypes.byref(k), ctypes.byref(v)), "kv_cache")
         return k.value, v.value
 
-    def forward(self, tokens, pos, kv_row, need_logits: bool = True, seq=None):
-        """tokens, pos, kv_row: per-token sequences; returns the greedy next
-        tokens (list) or None."""
+    def forward(self, tokens, pos, kv_row, need_logits: bool = True, seq=None, logit_rows=None):
+        """tokens, pos, kv_row: per-token sequences (several tokens of one
+        sequence share its kv_row: a prefill chunk).  Returns the greedy next
+        tokens (list) or None.  logit_rows: the token indices whose logits
+        and successors are computed (qk_llama_batch_forward_rows); by default
+        every token when need_logits, none otherwise."""
         n = len(tokens)
         tok = (ctypes.c_int32 * n)(*[int(t) for t in tokens])
         desc = (qk_batch_token * n)()
         for i in range(n):
             desc[i].pos, desc[i].kv_row = int(pos[i]), int(kv_row[i])
             desc[i].seq = int(seq[i]) if seq is not None else i
-        nxt = (ctypes.c_int32 * n)()
-        check(lib().qk_llama_batch_forward(self.handle, tok, desc, n, int(need_logits), nxt), "batched forward")
-        return list(nxt) if need_logits else None
+        if logit_rows is None:
+            nxt = (ctypes.c_int32 * n)()
+            check(lib().qk_llama_batch_forward(self.handle, tok, desc, n, int(need_logits), nxt), "batched forward")
+            return list(nxt) if need_logits else None
+        r = len(logit_rows)
+        rows = (ctypes.c_int32 * max(r, 1))(*[int(i) for i in logit_rows])
+        nxt = (ctypes.c_int32 * max(r, 1))()
+        check(lib().qk_llama_batch_forward_rows(self.handle, tok, desc, n, rows, r, nxt), "batched forward")
+        return list(nxt)[:r]
 
     def logits(self, n_tokens: int):
         import numpy as np
@@ -589,9 +600,11 @@ class BatchRunner:
 
     def load_kv(self, key_cache, value_cache) -> None:
         """Copy fp32 caches laid out [layer][cache_rows][kv_dim]."""
+        c = self.cfg
+        n = c["layers"] * self.cache_rows * (c["dim"] // c["heads"] * c["kv_heads"])
         k, v = self.kv_cache()
-        copy_to_device(k, key_cache)
-        copy_to_device(v, value_cache)
+        copy_to_device(k, _cache_array(key_cache, n), n * 4)
+        copy_to_device(v, _cache_array(value_cache, n), n * 4)
 
 
 _HIP = None
@@ -604,30 +617,52 @@ def _hip() -> ctypes.CDLL:
         h = ctypes.CDLL("libamdhip64.so")
         h.hipMemcpy.argtypes = [_vp, _vp, ctypes.c_size_t, _i]
         h.hipMemcpy.restype = _i
+        h.hipDeviceSynchronize.argtypes = []
+        h.hipDeviceSynchronize.restype = _i
         _HIP = h
     return _HIP
 
 
-def copy_to_device(dst: int, host_array) -> None:
+def _cache_array(a, count: int):
+    """a as a contiguous float32 array of exactly count values (QKError
+    otherwise): caches are copied whole, never partly or past their end."""
+    import numpy as np
+    a = np.asarray(a)
+    if a.dtype != np.float32 or a.size != count:
+        raise QKError("load_kv", QK_ERR_INVALID_ARG,
+                      f"cache must be float32 with {count} values, got {a.dtype} with {a.size}")
+    return np.ascontiguousarray(a)
+
+
+def copy_to_device(dst: int, host_array, nbytes: int | None = None) -> None:
+    """Copy host_array into device memory at dst.  nbytes, when given, is the
+    destination's size and must equal the array's.  The device is
+    synchronised first, so no queued step on any stream still uses dst."""
     import numpy as np
     a = np.ascontiguousarray(host_array)
-    if _hip().hipMemcpy(dst, a.ctypes.data, a.nbytes, 1) != 0:
+    if nbytes is not None and a.nbytes != nbytes:
+        raise QKError("copy_to_device", QK_ERR_INVALID_ARG, f"{a.nbytes} bytes for a {nbytes}-byte buffer")
+    h = _hip()
+    if h.hipDeviceSynchronize() != 0 or h.hipMemcpy(dst, a.ctypes.data, a.nbytes, 1) != 0:
         raise QKError("copy_to_device", QK_ERR_DEVICE, "hipMemcpy host->device failed")
 
 
 def copy_to_host(src: int, count: int, dtype) -> "object":
     import numpy as np
     out = np.empty(count, dtype=dtype)
-    if _hip().hipMemcpy(out.ctypes.data, src, out.nbytes, 2) != 0:
+    h = _hip()
+    if h.hipDeviceSynchronize() != 0 or h.hipMemcpy(out.ctypes.data, src, out.nbytes, 2) != 0:
         raise QKError("copy_to_host", QK_ERR_DEVICE, "hipMemcpy device->host failed")
     return out
 
 
 def _runner_load_kv(self, key_cache, value_cache) -> None:
     """Copy fp32 caches laid out [layer][context][kv_dim] into the runner."""
+    c = self.cfg
+    n = c["layers"] * c["context"] * (c["dim"] // c["heads"] * c["kv_heads"])
     k, v = self.kv_cache()
-    copy_to_device(k, key_cache)
-    copy_to_device(v, value_cache)
+    copy_to_device(k, _cache_array(key_cache, n), n * 4)
+    copy_to_device(v, _cache_array(value_cache, n), n * 4)
 
 
 def _runner_logits(self):

@@ -66,6 +66,12 @@ constexpr int kArgPartsMax = 16384;
 // The argmax partials -> out[0] (the lowest row among maxima; 0 if none).
 int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream);
 
+// dst[i][0..cols) = src[idx[i]][0..cols) (row stride ld) for i < n; idx is a
+// device array of n row indices.  cols and ld multiples of 4, src and dst
+// 16-byte aligned.
+int launch_gather_rows(const float *src, int64_t ld, const int32_t *idx, int n, int cols, float *dst,
+                       hipStream_t stream);
+
 // The greedy-token order (argmax_blocks_cuda / argmax_final_cuda,
 // inferencer.cu:1063-1099): a larger value wins, equal values keep the lower
 // index; NaN never wins.

@@ -263,7 +263,10 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
         (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
         (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
-        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), 2 * qk::kArgPartsMax * sizeof(float),
+        // The FP32 step's LM-head partials, or the INT8 step's qk_argmax_f32
+        // workspace, whichever is larger (the latter grows with vocab).
+        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws),
+                        std::max(2 * qk::kArgPartsMax * sizeof(float), qk_argmax_workspace_bytes(c.vocab)),
                         "argmax partials")) ||
         (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token")) ||
         (st = dev_alloc(&m->xq, std::max(c.dim, c.hidden), "quantized activations")) ||
@@ -441,10 +444,11 @@ struct qk_llama_batch {
     float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
     void *gemm_ws = nullptr, *argmax_ws = nullptr, *attn_ws = nullptr;
     size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
-    int32_t *d_tokens = nullptr, *d_next = nullptr;
+    int32_t *d_tokens = nullptr, *d_next = nullptr, *d_rows = nullptr;
     qk_batch_token *d_desc = nullptr;
-    uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, results
+    uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, logit rows, results
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
+    std::vector<int64_t> kv_writes;   // host scratch of the KV-row check
 };
 
 namespace {
@@ -452,7 +456,7 @@ namespace {
 void release_batch(qk_llama_batch *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->attn_ws, m->d_tokens, m->d_next,
-                    m->d_desc};
+                    m->d_rows, m->d_desc};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
@@ -460,8 +464,33 @@ void release_batch(qk_llama_batch *m) {
     delete m;
 }
 
+// Pinned staging of one step: tokens, next tokens and logit rows (int32 each),
+// then the descriptors.
 size_t stage_bytes(int max_tokens) {
-    return static_cast<size_t>(max_tokens) * (2 * sizeof(int32_t) + sizeof(qk_batch_token));
+    return static_cast<size_t>(max_tokens) * (3 * sizeof(int32_t) + sizeof(qk_batch_token));
+}
+
+// The KV rows a step writes are kv_row + pos, one per token.  Two tokens
+// writing one row race, so that is an error.  A token reads rows kv_row ..
+// kv_row + pos; when some of those are written by other tokens of the same
+// step (several tokens of one sequence: a prefill chunk), every row must be
+// written before attention reads any (*chained).  Descriptors are already
+// range-checked, so kv_row + pos does not overflow.
+int check_kv_rows(const qk_batch_token *desc, int n, std::vector<int64_t> &writes, bool *chained) {
+    writes.resize(n);
+    for (int t = 0; t < n; ++t) writes[t] = desc[t].kv_row + desc[t].pos;
+    std::sort(writes.begin(), writes.end());
+    for (int t = 1; t < n; ++t)
+        if (writes[t] == writes[t - 1])
+            return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: two tokens write KV row " +
+                                                    std::to_string(writes[t]) + " (same sequence and position)");
+    *chained = false;
+    for (int t = 0; t < n && !*chained; ++t) {
+        const auto lo = std::lower_bound(writes.begin(), writes.end(), desc[t].kv_row);
+        const auto hi = std::lower_bound(writes.begin(), writes.end(), desc[t].kv_row + desc[t].pos);
+        *chained = lo != hi;   // another token writes a row this one reads
+    }
+    return QK_OK;
 }
 
 }  // namespace
@@ -534,7 +563,7 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
                         "argmax workspace")) ||
         (st = dev_alloc(&m->d_tokens, T, "input tokens")) || (st = dev_alloc(&m->d_next, T, "next tokens")) ||
-        (st = dev_alloc(&m->d_desc, T, "batch descriptor"))) {
+        (st = dev_alloc(&m->d_rows, T, "logit rows")) || (st = dev_alloc(&m->d_desc, T, "batch descriptor"))) {
         release_batch(m);
         return st;
     }
@@ -588,51 +617,70 @@ int qk_llama_batch_logits(qk_llama_batch *m, const float **logits) {
     return qk::ok();
 }
 
-int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
-                           int need_logits, int32_t *next_tokens) {
-    if (!m || !tokens || !desc || (need_logits && !next_tokens))
+int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
+                                const int32_t *logit_rows, int n_rows, int32_t *next_tokens) {
+    if (!m || !tokens || !desc || (n_rows > 0 && (!logit_rows || !next_tokens)))
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: null argument");
     const qk_llama_config &c = m->cfg;
     if (n_tokens < 1 || n_tokens > m->max_tokens)
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token count outside 1..max_tokens");
+    if (n_rows < 0 || n_rows > n_tokens)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: logit row count outside 0..n_tokens");
     int max_pos = 0;
     int64_t rows = 0;
     for (int t = 0; t < n_tokens; ++t) {
         const qk_batch_token &d = desc[t];
+        // kv_row + pos < cache_rows, written so a huge kv_row cannot overflow.
         if (tokens[t] < 0 || tokens[t] >= c.vocab || d.pos < 0 || d.pos >= c.context || d.kv_row < 0 ||
-            d.kv_row + d.pos >= m->cache_rows)
+            d.kv_row > m->cache_rows - 1 - d.pos)
             return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token " + std::to_string(t) +
                                                     " outside the vocabulary, the context or the cache");
         max_pos = std::max(max_pos, d.pos);
         rows += d.pos + 1;
     }
+    bool identity = n_rows == n_tokens;   // logits of every token, in order
+    for (int i = 0; i < n_rows; ++i) {
+        if (logit_rows[i] < 0 || logit_rows[i] >= n_tokens)
+            return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: logit row outside the batch");
+        identity = identity && logit_rows[i] == i;
+    }
+    bool chained = false;
+    int st;
+    if ((st = check_kv_rows(desc, n_tokens, m->kv_writes, &chained))) return st;
     hipStream_t s = m->stream;
     const int T = n_tokens, dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
     int32_t *h_tokens = reinterpret_cast<int32_t *>(m->h_stage);
     int32_t *h_next = h_tokens + m->max_tokens;
-    qk_batch_token *h_desc = reinterpret_cast<qk_batch_token *>(h_next + m->max_tokens);
+    int32_t *h_rows = h_next + m->max_tokens;
+    qk_batch_token *h_desc = reinterpret_cast<qk_batch_token *>(h_rows + m->max_tokens);
     // The pinned staging is reused: the previous step's copies must be done.
     if (hipStreamSynchronize(s) != hipSuccess) return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: stream error");
     std::copy(tokens, tokens + T, h_tokens);
     std::copy(desc, desc + T, h_desc);
+    if (n_rows) std::copy(logit_rows, logit_rows + n_rows, h_rows);
     if (hipMemcpyAsync(m->d_tokens, h_tokens, T * sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess ||
-        hipMemcpyAsync(m->d_desc, h_desc, T * sizeof(qk_batch_token), hipMemcpyHostToDevice, s) != hipSuccess)
+        hipMemcpyAsync(m->d_desc, h_desc, T * sizeof(qk_batch_token), hipMemcpyHostToDevice, s) != hipSuccess ||
+        (n_rows && !identity &&
+         hipMemcpyAsync(m->d_rows, h_rows, n_rows * sizeof(int32_t), hipMemcpyHostToDevice, s) != hipSuccess))
         return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: batch upload failed");
-    int st;
     void *ws = m->gemm_ws;
     const size_t wsb = m->gemm_ws_bytes;
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, m->d_tokens, T, m->x, dim, c.vocab, s))) return st;
     // Per layer: fused QKV (RMSNorm staged), RoPE + KV write + attention,
     // o (+ residual), fused gate/up (RMSNorm staged), down (SiLU * up staged,
-    // + residual).
+    // + residual).  When tokens of the step read rows that other tokens of
+    // it write (a prefill chunk), RoPE and the KV write run as a launch of
+    // their own before the attention, as rope_cache_batch_cuda precedes
+    // attention_batch_cuda (inferencer.cu:953-1041): every token then sees
+    // the rows of the tokens before it and none after (causal).
     qk::GemvFusion attn_in, ffn_in, residual, down_in;
     attn_in.norm_eps = ffn_in.norm_eps = c.eps;
     residual.accumulate = down_in.accumulate = 1;
     down_in.up = m->up;
     qk::SplitAttention attn{};
     attn.q = m->q;
-    attn.k = m->k;
-    attn.v = m->v;
+    attn.k = chained ? nullptr : m->k;
+    attn.v = chained ? nullptr : m->v;
     attn.cosine = m->cosine;
     attn.sine = m->sine;
     attn.key_cache = m->key_cache;
@@ -652,6 +700,10 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
         ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
         if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, attn_in, ws, wsb, s))) return st;
+        if (chained &&
+            (st = qk_rope_kv_write_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
+                                           m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
+            return st;
         attn.layer = l;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
@@ -661,20 +713,40 @@ int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_ba
         const qk_matrix down{L.down_type, dim, L.down, m->x};
         if ((st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s))) return st;
     }
-    if (!need_logits) return qk::ok();
+    if (!n_rows) return qk::ok();
+    // The LM head over the selected tokens only (the reference's prefill
+    // computes the chunk's last token, inferencer.cu:1410-1414): their rows
+    // of x are gathered first unless the selection is every token in order.
+    const float *head_x = m->x;
+    if (!identity) {
+        if ((st = qk::launch_gather_rows(m->x, dim, m->d_rows, n_rows, dim, m->tmp, s))) return st;
+        head_x = m->tmp;
+    }
     qk::GemvFusion out_in;
     out_in.norm_w = m->w.output_norm;
     out_in.norm_eps = c.eps;
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
-    if ((st = qk::launch_batched_fused(&head, 1, m->x, dim, dim, T, out_in, ws, wsb, s))) return st;
-    if ((st = qk_argmax_rows_f32(m->logits, c.vocab, c.vocab, T, m->d_next, m->argmax_ws, s))) return st;
-    if (hipMemcpyAsync(h_next, m->d_next, T * sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+    if ((st = qk::launch_batched_fused(&head, 1, head_x, dim, dim, n_rows, out_in, ws, wsb, s))) return st;
+    if ((st = qk_argmax_rows_f32(m->logits, c.vocab, c.vocab, n_rows, m->d_next, m->argmax_ws, s))) return st;
+    if (hipMemcpyAsync(h_next, m->d_next, n_rows * sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
         return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: next token download failed");
-    std::copy(h_next, h_next + T, next_tokens);
+    std::copy(h_next, h_next + n_rows, next_tokens);
     return qk::ok();
+}
+
+int qk_llama_batch_forward(qk_llama_batch *m, const int32_t *tokens, const qk_batch_token *desc, int n_tokens,
+                           int need_logits, int32_t *next_tokens) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: null handle");
+    if (need_logits && !next_tokens) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: null argument");
+    if (!need_logits) return qk_llama_batch_forward_rows(m, tokens, desc, n_tokens, nullptr, 0, nullptr);
+    if (n_tokens < 1 || n_tokens > m->max_tokens)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_forward: token count outside 1..max_tokens");
+    std::vector<int32_t> all(n_tokens);
+    for (int t = 0; t < n_tokens; ++t) all[t] = t;
+    return qk_llama_batch_forward_rows(m, tokens, desc, n_tokens, all.data(), n_tokens, next_tokens);
 }
 
 }  // extern "C"

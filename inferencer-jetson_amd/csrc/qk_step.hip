@@ -190,8 +190,9 @@ __device__ __forceinline__ float dot4(const float4 &a, const float4 &b, float ac
 // a ragged batch.  A token whose descriptor falls outside the cache is not
 // written and its attention output is NaN.
 
+// Written without kv_row + pos, which a huge kv_row would overflow.
 __device__ __forceinline__ bool token_ok(const qk_batch_token &d, int64_t cache_rows, int max_pos) {
-    return d.pos >= 0 && d.pos <= max_pos && d.kv_row >= 0 && d.kv_row + d.pos < cache_rows;
+    return d.pos >= 0 && d.pos <= max_pos && d.kv_row >= 0 && d.kv_row < cache_rows - d.pos;
 }
 
 __global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v, const float *cosine,
@@ -570,6 +571,16 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
     }
 }
 
+// dst row i = src row idx[i] (cols floats, cols % 4 == 0, 16-byte aligned
+// rows): the activations of the tokens whose logits a step computes.
+__global__ void gather_rows_kernel(const float *src, int64_t ld, const int32_t *idx, int cols, float *dst) {
+    const int i = blockIdx.y;
+    const int c = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (c >= cols) return;
+    const float4 v = *reinterpret_cast<const float4 *>(src + static_cast<int64_t>(idx[i]) * ld + c);
+    *reinterpret_cast<float4 *>(dst + static_cast<int64_t>(i) * cols + c) = v;
+}
+
 __global__ void add_kernel(float *x, const float *y, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) x[i] += y[i];
@@ -764,6 +775,16 @@ bool attention_supported(int group, int head_dim) { return split_instance(group,
 int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream) {
     hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
     return launch_status("argmax final launch");
+}
+
+int launch_gather_rows(const float *src, int64_t ld, const int32_t *idx, int n, int cols, float *dst,
+                       hipStream_t stream) {
+    if (n < 1) return QK_OK;
+    if (n > 65535 || cols % 4 || ld % 4 || !aligned(src, 16) || !aligned(dst, 16))
+        return fail(QK_ERR_LIMIT, "row gather: unsupported shape");
+    hipLaunchKernelGGL(gather_rows_kernel, dim3((cols / 4 + 255) / 256, n), dim3(256), 0, stream, src, ld, idx, cols,
+                       dst);
+    return launch_status("row gather launch");
 }
 
 }  // namespace qk
