@@ -83,26 +83,29 @@ def time_launches(torch, launch, steps: int, warmup: int, stream):
 
 
 def cpu_baseline_lm_head(workloads, sample_rows: int, target_s: float) -> dict:
-    """The oracle's OpenMP restatement of gemv_quant<14> on a row sample."""
+    """The oracle's OpenMP restatement of gemv_quant<14> on a row sample of
+    the LM-head matrix: warm-up, then timed repetitions for about target_s
+    seconds (at least 20); the median repetition is reported."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle  # noqa: E402  (the CPU baseline leg only)
     import numpy as np
     w, x = workloads.lm_head_q6k()
     row_bytes = 8 * 210
     ws = np.ascontiguousarray(w[: sample_rows * row_bytes])
-    oracle.gemv_f32_ref(14, ws, x, 2048, sample_rows)           # warm
-    reps, t0 = 0, time.perf_counter()
-    while True:
+    for _ in range(3):
+        oracle.gemv_f32_ref(14, ws, x, 2048, sample_rows)           # warm
+    times, t0 = [], time.perf_counter()
+    while len(times) < 20 or time.perf_counter() - t0 < target_s:
+        t = time.perf_counter()
         oracle.gemv_f32_ref(14, ws, x, 2048, sample_rows)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= target_s:
-            break
+        times.append(time.perf_counter() - t)
+    med = float(np.median(times))
     sample_bytes = sample_rows * row_bytes + 2048 * 4 + sample_rows * 4
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(sample_bytes * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"Q6_K GEMV over the first {sample_rows} rows (x 2048) of the LM-head matrix, "
-                      f"{reps} repetitions in {el:.1f} s, OpenMP static rows, nproc={os.cpu_count()}"}
+    threads = oracle.omp_max_threads()
+    return {"value": round(sample_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"Q6_K GEMV over the first {sample_rows} rows (x 2048) of the LM-head matrix; median of "
+                      f"{len(times)} timed repetitions ({sum(times):.1f} s); OpenMP static rows, "
+                      f"omp_get_max_threads()={threads}, nproc={os.cpu_count()}"}
 
 
 def bench_small_gemvs(torch, qk, wl, stream) -> dict:
@@ -282,6 +285,7 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
         nxt = run.forward(nxt, pos, True)
         pos += 1
     el = time.perf_counter() - t0
+    mem = run.memory()
     run.close()
     kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
     weights = sum(qk.tensor_bytes(wl.MIX_1B[n], *wl.tensor_shape(cfg, n)) for n in wl.TENSORS) * cfg["layers"] + \
@@ -297,7 +301,72 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             # layer: norm+quantize, QKV, attention + merge, quantize, o (+add),
             # norm+quantize, gate/up, SiLU*up+quantize, down (+add); then
             # embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (10 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3)}
+            "kernels_per_token": (10 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3),
+            "device_bytes": mem}
+
+
+def _fill_caches(torch, runner, cfg, rows: int, seed: int) -> None:
+    """N(0,1) in every row of the runner's packed caches, drawn on the device."""
+    import ctypes
+    kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
+    kp, vp = runner.kv_cache()
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    per_layer = rows * kv_dim
+    for dst in (kp, vp):
+        for l in range(cfg["layers"]):
+            blk = torch.randn(per_layer, device="cuda", generator=g)
+            if hip.hipMemcpy(dst + l * per_layer * 4, blk.data_ptr(), per_layer * 4, 3) != 0:
+                raise RuntimeError("device copy failed")
+            del blk
+    torch.cuda.synchronize()
+
+
+def bench_mixed_1b_step(torch, qk, wl, steps: int = 10, warmup: int = 3) -> dict:
+    """The mixed continuous batch end to end: one step of the random-init
+    Llama-3.2-1B (seed 4) over 256 packed tokens -- two fresh 96-token
+    prefill chunks (positions 0..95, causal within the chunk) and 64 decode
+    tokens at positions ctx - 1, ctx ~ U[64, 2048] -- through
+    qk_llama_batch_forward_rows: embedding, 16 layers (projections on the
+    matrix cores, RoPE + KV write, attention), and the LM head plus greedy
+    pick for the 66 tokens that produce logits (each chunk's last token and
+    every decode).  Every step repeats the same positions."""
+    import numpy as np
+    cfg = dict(wl.LLAMA_1B, context=2048)
+    W = wl.llama_weights(cfg, 4)
+    d = wl.mixed_1b_256()["desc"]
+    seq, pos = d.seq_id.astype(int), d.pos.astype(int)
+    n_seq = int(seq.max()) + 1
+    cap = [int(d.ctx_len[np.flatnonzero(seq == s)[0]]) for s in range(n_seq)]
+    start = np.concatenate([[0], np.cumsum(cap[:-1])]).astype(int)
+    rows = int(sum(cap))
+    runner = qk.BatchRunner(cfg, W, max_tokens=d.n_tokens, cache_rows=rows)
+    _fill_caches(torch, runner, cfg, rows, 4)
+    tokens = [int(x) for x in wl.synth.uniform_i32(d.n_tokens, 4, 7, 0, cfg["vocab"] - 1)]
+    kv_row = [int(start[s]) for s in seq]
+    last = {s: i for i, s in enumerate(seq)}
+    logit_rows = sorted(last.values())
+    for _ in range(warmup):
+        runner.forward(tokens, pos, kv_row, seq=seq, logit_rows=logit_rows)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        runner.forward(tokens, pos, kv_row, seq=seq, logit_rows=logit_rows)
+    el = time.perf_counter() - t0
+    runner.close()
+    ms = el / steps * 1e3
+    per_layer = sum(wl.tensor_shape(cfg, n)[0] * wl.tensor_shape(cfg, n)[1] for n in wl.TENSORS)
+    proj = 2.0 * d.n_tokens * per_layer * cfg["layers"]
+    head = 2.0 * len(logit_rows) * cfg["dim"] * cfg["vocab"]
+    tflops = (proj + head) / (ms * 1e-3) / 1e12
+    return {"tokens": d.n_tokens, "logit_tokens": len(logit_rows),
+            "packing": "2 prefill chunks x 96 (positions 0..95) + 64 decodes (ctx ~ U[64, 2048])",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(d.n_tokens / (ms * 1e-3), 1),
+            "useful_matrix_TFLOPs": round(tflops, 1),
+            "mfma_util_of_fp16_dense_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "mfma_ops_per_useful_product": 2}
 
 
 def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
@@ -306,7 +375,6 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
     ragged descriptor of the 3B FFN workload, seed 3), its KV rows packed in
     one cache and filled with N(0,1) on the device.  Timed: `steps` steps,
     each ending in the 32 greedy tokens' download; positions advance."""
-    import ctypes
     cfg = dict(wl.LLAMA_1B, context=2048 + steps + warmup)
     W = wl.llama_weights(cfg, 2)
     desc = wl.ffn_3b_ragged()["desc"]
@@ -316,19 +384,7 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
     rows = int(cap.sum())
     runner = qk.BatchRunner(cfg, W, max_tokens=n, cache_rows=rows)
     kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
-    kp, vp = runner.kv_cache()
-    g = torch.Generator(device="cuda")
-    g.manual_seed(2)
-    hip = ctypes.CDLL("libamdhip64.so")
-    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    for dst in (kp, vp):
-        per_layer = rows * kv_dim
-        for l in range(cfg["layers"]):
-            blk = torch.randn(per_layer, device="cuda", generator=g)
-            if hip.hipMemcpy(dst + l * per_layer * 4, blk.data_ptr(), per_layer * 4, 3) != 0:
-                raise RuntimeError("device copy failed")
-            del blk
-    torch.cuda.synchronize()
+    _fill_caches(torch, runner, cfg, rows, 2)
     tokens = [int(x) for x in wl.synth.uniform_i32(n, 3, 6, 0, cfg["vocab"] - 1)]
     pos = [int(c) - 1 for c in desc.ctx_len]
     for _ in range(warmup):
@@ -342,6 +398,7 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
         kv_read += sum(cfg["layers"] * (p + 1) * kv_dim * 4 * 2 for p in pos)
         pos = [p + 1 for p in pos]
     el = time.perf_counter() - t0
+    mem = runner.memory()
     runner.close()
     weights = sum(qk.tensor_bytes(wl.MIX_1B[t], *wl.tensor_shape(cfg, t)) for t in wl.TENSORS) * cfg["layers"] + \
         qk.tensor_bytes(qk.Q6_K, cfg["dim"], cfg["vocab"])
@@ -350,7 +407,7 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
     return {"sequences": n, "ms_per_step": round(ms, 4), "tokens_per_s": round(n * steps / el, 1),
             "weight_bytes_per_step": weights, "kv_bytes_per_step": int(kv_read / steps),
             "GBps": round(moved / el / 1e9, 1), "frac_of_peak": round(moved / el / 1e9 / HBM_PEAK_GBPS, 4),
-            "context": "ctx ~ U[64, 2048] per sequence (seed 3)"}
+            "context": "ctx ~ U[64, 2048] per sequence (seed 3)", "device_bytes": mem}
 
 def reference_kernels(torch, args) -> int:
     """Plain copy / streaming read of 256 MiB buffers (4 rotating sources)."""
@@ -393,8 +450,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
-    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "decode", "decode_int8",
-                                       "batch_decode"],
+    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "mixed_step", "decode",
+                                       "decode_int8", "batch_decode"],
                     default="gemv",
                     help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
                          "(a plain 256 MiB copy calibrates FETCH_SIZE / WRITE_SIZE; a streaming read gives "
@@ -418,6 +475,7 @@ def main() -> int:
         stream = torch.cuda.current_stream()
         run = {"ffn": lambda: bench_ffn_3b_ragged(torch, qk, wl, stream),
                "mixed": lambda: bench_mixed_1b_256(torch, qk, wl, stream),
+               "mixed_step": lambda: bench_mixed_1b_step(torch, qk, wl),
                "decode": lambda: bench_decode_1b(torch, qk, wl),
                "decode_int8": lambda: bench_decode_1b(torch, qk, wl, int8=True),
                "batch_decode": lambda: bench_batch_decode_1b(torch, qk, wl)}[args.only]
@@ -461,7 +519,9 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        # fp32 in and out; inside the kernel each 16-value activation group
+        # is 22-bit fixed point (exact int8-limb dots), combined in fp32.
+        "dtype": "f32 (activations as 22-bit block fixed point)",
         "data": "synthetic (seeded random Q6_K super-blocks, x ~ N(0,1))",
         "config": {"workload": "lm_head_q6k: Q6_K GEMV 128256x2048 (tied LM head), batch 1, "
                                f"{args.copies} rotating weight copies, split Q6_K layout",
@@ -498,6 +558,8 @@ def main() -> int:
         log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")
         sec["mixed_1b_256"] = bench_mixed_1b_256(torch, qk, wl, stream)
         log(f"[bench] mixed_1b_256: {json.dumps(sec['mixed_1b_256'])}")
+        sec["mixed_1b_256_step"] = bench_mixed_1b_step(torch, qk, wl)
+        log(f"[bench] mixed_1b_256_step: {json.dumps(sec['mixed_1b_256_step'])}")
         sec["llama_1b_decode"] = bench_decode_1b(torch, qk, wl)
         log(f"[bench] llama_1b_decode: {json.dumps(sec['llama_1b_decode'])}")
         sec["llama_1b_decode_int8"] = bench_decode_1b(torch, qk, wl, int8=True)
@@ -508,7 +570,7 @@ def main() -> int:
 
     if not args.no_cpu_baseline:
         log(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)")
-        result["cpu_baseline"] = cpu_baseline_lm_head(wl, sample_rows=16384, target_s=args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline_lm_head(wl, sample_rows=65536, target_s=args.cpu_seconds)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -321,9 +321,23 @@ typedef struct qk_llama qk_llama;
    tensor is copied once into the split layout (QK_TYPE_Q6_K_SPLIT, owned by
    the handle, freed by destroy); create returns after those copies, so the
    caller's Q6_K buffers may be released then.  Q4_K, split Q6_K and norm
-   tensors are read in place at every step and stay owned by the caller. */
+   tensors are read in place at every step and stay owned by the caller.
+   Like the reference's upload (inferencer.cu:329-333), create first checks
+   that the caches and split copies fit in free device memory with a 64 MiB
+   margin (QK_ERR_DEVICE otherwise). */
 int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream,
                     qk_llama **out);
+
+/* Device bytes a decode handle holds: the split-layout Q6_K copies, the two
+   KV caches, and every other buffer (activations, logits, workspaces, RoPE
+   tables).  The copies cost as much as the model's Q6_K tensors (449 MB for
+   the Llama-3.2-1B Q4_K_M-style mix). */
+typedef struct qk_llama_memory {
+    uint64_t weight_copies;
+    uint64_t kv_cache;
+    uint64_t buffers;
+} qk_llama_memory;
+int qk_llama_memory_bytes(const qk_llama *m, qk_llama_memory *out);
 int qk_llama_destroy(qk_llama *m);
 /* The reference's INT8 GEMV modes (FastGPU's use_dp4a for Q4_K and
    use_q6_dp4a for Q6_K, inferencer.cu:1159-1166, 1611; both on by default
@@ -361,6 +375,8 @@ typedef struct qk_llama_batch qk_llama_batch;
 int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens,
                           int64_t cache_rows, qk_stream stream, qk_llama_batch **out);
 int qk_llama_batch_destroy(qk_llama_batch *m);
+/* The handle's device bytes, as qk_llama_memory_bytes. */
+int qk_llama_batch_memory_bytes(const qk_llama_batch *m, qk_llama_memory *out);
 /* Device pointers to the fp32 caches, [layer][cache_rows][kv_dim]. */
 int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_cache);
 /* Device pointer to the fp32 logits of the last step with need_logits,

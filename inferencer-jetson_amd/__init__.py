@@ -75,6 +75,10 @@ class qk_llama_weights(ctypes.Structure):
                 ("layers", ctypes.POINTER(qk_llama_layer))]
 
 
+class qk_llama_memory(ctypes.Structure):
+    _fields_ = [("weight_copies", ctypes.c_uint64), ("kv_cache", ctypes.c_uint64), ("buffers", ctypes.c_uint64)]
+
+
 class qk_gguf_tensor(ctypes.Structure):
     """One tensor-table entry of a GGUF file (include/qk.h)."""
     _fields_ = [("name", ctypes.c_char_p), ("type", ctypes.c_int), ("n_dims", ctypes.c_int),
@@ -128,6 +132,8 @@ SIGNATURES = {
     "qk_llama_batch_create": (_i, [ctypes.POINTER(qk_llama_config), ctypes.POINTER(qk_llama_weights), _i,
                                    ctypes.c_int64, _vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_destroy": (_i, [_vp]),
+    "qk_llama_memory_bytes": (_i, [_vp, ctypes.POINTER(qk_llama_memory)]),
+    "qk_llama_batch_memory_bytes": (_i, [_vp, ctypes.POINTER(qk_llama_memory)]),
     "qk_llama_batch_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
@@ -508,6 +514,12 @@ class Runner:
 
     __del__ = close
 
+    def memory(self) -> dict:
+        """Device bytes the handle holds (qk_llama_memory_bytes)."""
+        m = qk_llama_memory()
+        check(lib().qk_llama_memory_bytes(self.handle, ctypes.byref(m)), "memory")
+        return {k: int(getattr(m, k)) for k, _ in m._fields_}
+
     def set_int8(self, q4k: bool = True, q6k: bool = True) -> None:
         """The reference's INT8 GEMV modes (use_dp4a, use_q6_dp4a; inferencer.cu:1159-1166)."""
         check(lib().qk_llama_set_int8(self.handle, int(q4k), int(q6k)), "set_int8")
@@ -569,6 +581,12 @@ class BatchRunner:
         k, v = ctypes.c_void_p(), ctypes.c_void_p()
         check(lib().qk_llama_batch_kv_cache(self.handle, ctypes.byref(k), ctypes.byref(v)), "kv_cache")
         return k.value, v.value
+
+    def memory(self) -> dict:
+        """Device bytes the handle holds (qk_llama_batch_memory_bytes)."""
+        m = qk_llama_memory()
+        check(lib().qk_llama_batch_memory_bytes(self.handle, ctypes.byref(m)), "memory")
+        return {k: int(getattr(m, k)) for k, _ in m._fields_}
 
     def forward(self, tokens, pos, kv_row, need_logits: bool = True, seq=None, logit_rows=None):
         """tokens, pos, kv_row: per-token sequences (several tokens of one

@@ -40,14 +40,16 @@ struct qk_llama {
     int8_t *xq = nullptr;                      // INT8 mode: quantized activations, max(dim, hidden)
     float *xscale = nullptr;
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
+    qk_llama_memory mem{};        // device bytes the handle holds
 };
 
 namespace {
 
 template <class T>
-int dev_alloc(T **p, size_t count, const char *what) {
+int dev_alloc(uint64_t &total, T **p, size_t count, const char *what) {
     if (hipMalloc(reinterpret_cast<void **>(p), count * sizeof(T)) != hipSuccess)
         return qk::fail(QK_ERR_DEVICE, std::string("qk_llama_create: cannot allocate ") + what);
+    total += count * sizeof(T);
     return QK_OK;
 }
 
@@ -68,35 +70,65 @@ bool quant_type(int t) { return t == QK_TYPE_Q4_K || t == QK_TYPE_Q6_K || t == Q
 // A Q6_K tensor in the GGUF layout is copied once into the split layout
 // (QK_TYPE_Q6_K_SPLIT: every field a kernel reads 16-byte aligned) and the
 // driver uses the copy; the caller keeps its weights.
-int split_tensor(std::vector<void *> &owned, int &type, const void *&w, int cols, int rows, hipStream_t s) {
+int split_tensor(std::vector<void *> &owned, uint64_t &total, int &type, const void *&w, int cols, int rows,
+                 hipStream_t s) {
     if (type != QK_TYPE_Q6_K) return QK_OK;
     void *dst = nullptr;
-    if (hipMalloc(&dst, static_cast<size_t>(qk_tensor_bytes(QK_TYPE_Q6_K_SPLIT, cols, rows))) != hipSuccess)
-        return qk::fail(QK_ERR_DEVICE, "cannot allocate a split-layout Q6_K copy");
+    const size_t bytes = static_cast<size_t>(qk_tensor_bytes(QK_TYPE_Q6_K_SPLIT, cols, rows));
+    if (hipMalloc(&dst, bytes) != hipSuccess) return qk::fail(QK_ERR_DEVICE, "cannot allocate a split-layout Q6_K copy");
     owned.push_back(dst);
+    total += bytes;
     if (int st = qk_q6k_split(w, dst, cols, rows, s)) return st;
     type = QK_TYPE_Q6_K_SPLIT;
     w = dst;
     return QK_OK;
 }
 
-int split_weights(std::vector<void *> &owned, qk_llama_weights &w, std::vector<qk_llama_layer> &layers,
-                  const qk_llama_config &c, int kv_dim, hipStream_t s) {
+int split_weights(std::vector<void *> &owned, uint64_t &total, qk_llama_weights &w,
+                  std::vector<qk_llama_layer> &layers, const qk_llama_config &c, int kv_dim, hipStream_t s) {
     int st;
     for (qk_llama_layer &L : layers)
-        if ((st = split_tensor(owned, L.q_type, L.q, c.dim, c.dim, s)) ||
-            (st = split_tensor(owned, L.k_type, L.k, c.dim, kv_dim, s)) ||
-            (st = split_tensor(owned, L.v_type, L.v, c.dim, kv_dim, s)) ||
-            (st = split_tensor(owned, L.o_type, L.o, c.dim, c.dim, s)) ||
-            (st = split_tensor(owned, L.gate_type, L.gate, c.dim, c.hidden, s)) ||
-            (st = split_tensor(owned, L.up_type, L.up, c.dim, c.hidden, s)) ||
-            (st = split_tensor(owned, L.down_type, L.down, c.hidden, c.dim, s)))
+        if ((st = split_tensor(owned, total, L.q_type, L.q, c.dim, c.dim, s)) ||
+            (st = split_tensor(owned, total, L.k_type, L.k, c.dim, kv_dim, s)) ||
+            (st = split_tensor(owned, total, L.v_type, L.v, c.dim, kv_dim, s)) ||
+            (st = split_tensor(owned, total, L.o_type, L.o, c.dim, c.dim, s)) ||
+            (st = split_tensor(owned, total, L.gate_type, L.gate, c.dim, c.hidden, s)) ||
+            (st = split_tensor(owned, total, L.up_type, L.up, c.dim, c.hidden, s)) ||
+            (st = split_tensor(owned, total, L.down_type, L.down, c.hidden, c.dim, s)))
             return st;
-    if ((st = split_tensor(owned, w.embd_type, w.token_embd, c.dim, c.vocab, s))) return st;
-    if (w.output && (st = split_tensor(owned, w.output_type, w.output, c.dim, c.vocab, s))) return st;
+    if ((st = split_tensor(owned, total, w.embd_type, w.token_embd, c.dim, c.vocab, s))) return st;
+    if (w.output && (st = split_tensor(owned, total, w.output_type, w.output, c.dim, c.vocab, s))) return st;
     // The copies are complete before create returns: the caller may release
     // its Q6_K buffers from then on.
     if (hipStreamSynchronize(s) != hipSuccess) return qk::fail(QK_ERR_DEVICE, "Q6_K split copies failed");
+    return QK_OK;
+}
+
+// Bytes of the split-layout copies create makes (every GGUF-layout Q6_K tensor).
+uint64_t split_copy_bytes(const qk_llama_weights &w, const qk_llama_config &c, int kv_dim) {
+    auto one = [](int type, int cols, int rows) -> uint64_t {
+        return type == QK_TYPE_Q6_K ? static_cast<uint64_t>(qk_tensor_bytes(QK_TYPE_Q6_K_SPLIT, cols, rows)) : 0;
+    };
+    uint64_t b = one(w.embd_type, c.dim, c.vocab) + (w.output ? one(w.output_type, c.dim, c.vocab) : 0);
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = w.layers[l];
+        b += one(L.q_type, c.dim, c.dim) + one(L.k_type, c.dim, kv_dim) + one(L.v_type, c.dim, kv_dim) +
+             one(L.o_type, c.dim, c.dim) + one(L.gate_type, c.dim, c.hidden) + one(L.up_type, c.dim, c.hidden) +
+             one(L.down_type, c.hidden, c.dim);
+    }
+    return b;
+}
+
+// The reference's upload check (inferencer.cu:329-333): the device must have
+// the bytes about to be allocated plus a 64 MiB margin free.
+int check_free_memory(const char *where, uint64_t need) {
+    size_t free_bytes = 0, total_bytes = 0;
+    if (hipMemGetInfo(&free_bytes, &total_bytes) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, std::string(where) + ": device memory query failed");
+    if (free_bytes < need + (uint64_t(64) << 20))
+        return qk::fail(QK_ERR_DEVICE, std::string(where) + ": not enough free device memory (" +
+                                           std::to_string(need) + " bytes needed for caches, buffers and "
+                                           "split Q6_K copies, " + std::to_string(free_bytes) + " free)");
     return QK_OK;
 }
 
@@ -253,30 +285,34 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
     m->kv_dim = head_dim * c.kv_heads;
     const size_t cache = static_cast<size_t>(c.layers) * c.context * m->kv_dim;
     const int half = head_dim / 2;
-    int st = QK_OK;
-    if ((st = dev_alloc(&m->x, c.dim, "residual")) || (st = dev_alloc(&m->xn, c.dim, "normalized state")) ||
-        (st = dev_alloc(&m->q, c.dim, "query")) || (st = dev_alloc(&m->k, m->kv_dim, "key")) ||
-        (st = dev_alloc(&m->v, m->kv_dim, "value")) || (st = dev_alloc(&m->attn, c.dim, "attention")) ||
-        (st = dev_alloc(&m->tmp, c.dim, "residual update")) || (st = dev_alloc(&m->gate, c.hidden, "gate")) ||
-        (st = dev_alloc(&m->up, c.hidden, "up projection")) || (st = dev_alloc(&m->logits, c.vocab, "logits")) ||
-        (st = dev_alloc(&m->key_cache, cache, "key cache")) ||
-        (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
-        (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
-        (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
+    int st = check_free_memory("qk_llama_create", 2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim));
+    if (st) {
+        delete m;
+        return st;
+    }
+    if ((st = dev_alloc(m->mem.buffers, &m->x, c.dim, "residual")) || (st = dev_alloc(m->mem.buffers, &m->xn, c.dim, "normalized state")) ||
+        (st = dev_alloc(m->mem.buffers, &m->q, c.dim, "query")) || (st = dev_alloc(m->mem.buffers, &m->k, m->kv_dim, "key")) ||
+        (st = dev_alloc(m->mem.buffers, &m->v, m->kv_dim, "value")) || (st = dev_alloc(m->mem.buffers, &m->attn, c.dim, "attention")) ||
+        (st = dev_alloc(m->mem.buffers, &m->tmp, c.dim, "residual update")) || (st = dev_alloc(m->mem.buffers, &m->gate, c.hidden, "gate")) ||
+        (st = dev_alloc(m->mem.buffers, &m->up, c.hidden, "up projection")) || (st = dev_alloc(m->mem.buffers, &m->logits, c.vocab, "logits")) ||
+        (st = dev_alloc(m->mem.kv_cache, &m->key_cache, cache, "key cache")) ||
+        (st = dev_alloc(m->mem.kv_cache, &m->value_cache, cache, "value cache")) ||
+        (st = dev_alloc(m->mem.buffers, &m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
+        (st = dev_alloc(m->mem.buffers, &m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
         // The FP32 step's LM-head partials, or the INT8 step's qk_argmax_f32
         // workspace, whichever is larger (the latter grows with vocab).
-        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws),
+        (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->argmax_ws),
                         std::max(2 * qk::kArgPartsMax * sizeof(float), qk_argmax_workspace_bytes(c.vocab)),
                         "argmax partials")) ||
-        (st = dev_alloc(&m->d_next, 1, "next token")) || (st = dev_alloc(&m->d_token, 1, "input token")) ||
-        (st = dev_alloc(&m->xq, std::max(c.dim, c.hidden), "quantized activations")) ||
-        (st = dev_alloc(&m->xscale, std::max(c.dim, c.hidden) / 32, "activation scales"))) {
+        (st = dev_alloc(m->mem.buffers, &m->d_next, 1, "next token")) || (st = dev_alloc(m->mem.buffers, &m->d_token, 1, "input token")) ||
+        (st = dev_alloc(m->mem.buffers, &m->xq, std::max(c.dim, c.hidden), "quantized activations")) ||
+        (st = dev_alloc(m->mem.buffers, &m->xscale, std::max(c.dim, c.hidden) / 32, "activation scales"))) {
         release(m);
         return st;
     }
     m->attn_ws_bytes = qk::split_attention_workspace_bytes(1, c.heads, c.kv_heads, head_dim, c.context);
     if (m->attn_ws_bytes &&
-        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) {
+        (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) {
         release(m);
         return st;
     }
@@ -303,7 +339,7 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         release(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_create: table upload failed");
     }
-    if ((st = split_weights(m->owned, m->w, m->layers, c, m->kv_dim, m->stream))) {
+    if ((st = split_weights(m->owned, m->mem.weight_copies, m->w, m->layers, c, m->kv_dim, m->stream))) {
         release(m);
         return st;
     }
@@ -323,6 +359,12 @@ int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache) {
     if (!m || !key_cache || !value_cache) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_kv_cache: null argument");
     *key_cache = m->key_cache;
     *value_cache = m->value_cache;
+    return qk::ok();
+}
+
+int qk_llama_memory_bytes(const qk_llama *m, qk_llama_memory *out) {
+    if (!m || !out) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_memory_bytes: null argument");
+    *out = m->mem;
     return qk::ok();
 }
 
@@ -449,6 +491,7 @@ struct qk_llama_batch {
     uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, logit rows, results
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
     std::vector<int64_t> kv_writes;   // host scratch of the KV-row check
+    qk_llama_memory mem{};        // device bytes the handle holds
 };
 
 namespace {
@@ -539,6 +582,11 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     m->cache_rows = cache_rows;
     const size_t T = static_cast<size_t>(max_tokens);
     const size_t cache = static_cast<size_t>(c.layers) * cache_rows * m->kv_dim;
+    if (int st0 = check_free_memory("qk_llama_batch_create",
+                                    2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim))) {
+        delete m;
+        return st0;
+    }
     const int half = head_dim / 2;
     size_t ws = 0;
     const int kv = m->kv_dim;
@@ -548,22 +596,23 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     m->gemm_ws_bytes = ws;
     m->attn_ws_bytes = qk::split_attention_workspace_bytes(max_tokens, c.heads, c.kv_heads, head_dim, c.context);
     int st = QK_OK;
-    if ((st = dev_alloc(&m->x, T * c.dim, "residual")) || (st = dev_alloc(&m->xn, T * c.dim, "normalized state")) ||
-        (st = dev_alloc(&m->q, T * c.dim, "query")) || (st = dev_alloc(&m->k, T * kv, "key")) ||
-        (st = dev_alloc(&m->v, T * kv, "value")) || (st = dev_alloc(&m->attn, T * c.dim, "attention")) ||
-        (st = dev_alloc(&m->tmp, T * c.dim, "residual update")) || (st = dev_alloc(&m->gate, T * c.hidden, "gate")) ||
-        (st = dev_alloc(&m->up, T * c.hidden, "up projection")) ||
-        (st = dev_alloc(&m->logits, T * c.vocab, "logits")) || (st = dev_alloc(&m->key_cache, cache, "key cache")) ||
-        (st = dev_alloc(&m->value_cache, cache, "value cache")) ||
-        (st = dev_alloc(&m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
-        (st = dev_alloc(&m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
-        (ws && (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->gemm_ws), ws, "matrix workspace"))) ||
+    if ((st = dev_alloc(m->mem.buffers, &m->x, T * c.dim, "residual")) || (st = dev_alloc(m->mem.buffers, &m->xn, T * c.dim, "normalized state")) ||
+        (st = dev_alloc(m->mem.buffers, &m->q, T * c.dim, "query")) || (st = dev_alloc(m->mem.buffers, &m->k, T * kv, "key")) ||
+        (st = dev_alloc(m->mem.buffers, &m->v, T * kv, "value")) || (st = dev_alloc(m->mem.buffers, &m->attn, T * c.dim, "attention")) ||
+        (st = dev_alloc(m->mem.buffers, &m->tmp, T * c.dim, "residual update")) || (st = dev_alloc(m->mem.buffers, &m->gate, T * c.hidden, "gate")) ||
+        (st = dev_alloc(m->mem.buffers, &m->up, T * c.hidden, "up projection")) ||
+        (st = dev_alloc(m->mem.buffers, &m->logits, T * c.vocab, "logits")) ||
+        (st = dev_alloc(m->mem.kv_cache, &m->key_cache, cache, "key cache")) ||
+        (st = dev_alloc(m->mem.kv_cache, &m->value_cache, cache, "value cache")) ||
+        (st = dev_alloc(m->mem.buffers, &m->cosine, static_cast<size_t>(c.context) * half, "RoPE cosine")) ||
+        (st = dev_alloc(m->mem.buffers, &m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
+        (ws && (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->gemm_ws), ws, "matrix workspace"))) ||
         (m->attn_ws_bytes &&
-         (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) ||
-        (st = dev_alloc(reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
+         (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) ||
+        (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
                         "argmax workspace")) ||
-        (st = dev_alloc(&m->d_tokens, T, "input tokens")) || (st = dev_alloc(&m->d_next, T, "next tokens")) ||
-        (st = dev_alloc(&m->d_rows, T, "logit rows")) || (st = dev_alloc(&m->d_desc, T, "batch descriptor"))) {
+        (st = dev_alloc(m->mem.buffers, &m->d_tokens, T, "input tokens")) || (st = dev_alloc(m->mem.buffers, &m->d_next, T, "next tokens")) ||
+        (st = dev_alloc(m->mem.buffers, &m->d_rows, T, "logit rows")) || (st = dev_alloc(m->mem.buffers, &m->d_desc, T, "batch descriptor"))) {
         release_batch(m);
         return st;
     }
@@ -587,7 +636,7 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         release_batch(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_create: table upload failed");
     }
-    if ((st = split_weights(m->owned, m->w, m->layers, c, m->kv_dim, m->stream))) {
+    if ((st = split_weights(m->owned, m->mem.weight_copies, m->w, m->layers, c, m->kv_dim, m->stream))) {
         release_batch(m);
         return st;
     }
@@ -608,6 +657,12 @@ int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_
         return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_kv_cache: null argument");
     *key_cache = m->key_cache;
     *value_cache = m->value_cache;
+    return qk::ok();
+}
+
+int qk_llama_batch_memory_bytes(const qk_llama_batch *m, qk_llama_memory *out) {
+    if (!m || !out) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_memory_bytes: null argument");
+    *out = m->mem;
     return qk::ok();
 }
 

@@ -70,6 +70,7 @@ def lib() -> ctypes.CDLL:
         h.oq_llama_forward.argtypes = [vp, i32, i32, i32, vp, ctypes.POINTER(i32)]
         h.oq_llama_forward.restype = i32
         h.oq_llama_set_int8.argtypes, h.oq_llama_set_int8.restype = [vp, i32, i32], None
+        h.oq_omp_max_threads.argtypes, h.oq_omp_max_threads.restype = [], i32
         _LIB = h
     return _LIB
 
@@ -77,6 +78,11 @@ def lib() -> ctypes.CDLL:
 def _p(a: np.ndarray) -> int:
     assert a.flags["C_CONTIGUOUS"]
     return a.ctypes.data
+
+
+def omp_max_threads() -> int:
+    """Threads the oracle's OpenMP loops run on (omp_get_max_threads)."""
+    return int(lib().oq_omp_max_threads())
 
 
 def f16_to_f32(bits: int) -> float:

@@ -602,3 +602,5 @@ int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *l
     if (!logits) free(lg);
     return 0;
 }
+
+int oq_omp_max_threads(void) { return omp_get_max_threads(); }

@@ -108,6 +108,10 @@ int oq_llama_load_cache(oq_llama *m, const float *key_cache, const float *value_
 void oq_llama_set_int8(oq_llama *m, int q4k_int8, int q6k_int8);
 int oq_llama_forward(oq_llama *m, int token, int pos, int need_logits, double *logits, int *next_token);
 
+/* omp_get_max_threads() of this library's OpenMP runtime: the threads its
+   parallel loops use (the CPU baseline reports it). */
+int oq_omp_max_threads(void);
+
 #ifdef __cplusplus
 }
 #endif
