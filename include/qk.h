@@ -155,6 +155,19 @@ size_t qk_gemv_argmax_workspace_bytes(void);
 int qk_gemv_argmax_f32(int type, const void *w, const float *x, float *y, int cols, int rows, int32_t *out,
                        void *workspace, qk_stream stream);
 
+/* qk_gemv_argmax_f32 without a workspace argument and without any device
+   allocation: the partials live in a 128 KiB array compiled into the library
+   (one per GPU, held until the process ends).  No reference counterpart: it
+   serves callers that cannot allocate or pass a workspace (code under HIP
+   graph capture, tight serving loops).  Any rows / cols that
+   qk_gemv_argmax_f32 accepts fit the array (the GEMV keeps at most 16384
+   partials); the call otherwise fails with QK_ERR_LIMIT before its
+   argmax launch.  Every call on one GPU shares the array and leaves its
+   partials there: calls that overlap on one GPU (two streams, two host
+   threads) race and must be serialised by the caller. */
+int qk_gemv_argmax_f32_noalloc(int type, const void *w, const float *x, float *y, int cols, int rows,
+                               int32_t *out, qk_stream stream);
+
 /* ---------------------------------------------------------- INT8 mode -- */
 
 /* Per 32 values: scale = amax/127 (1 if amax == 0), xq = clamp(rne(x/scale),

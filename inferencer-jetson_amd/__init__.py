@@ -103,6 +103,7 @@ SIGNATURES = {
     "qk_q6k_split": (_i, [_vp, _vp, _i, _i, _vp]),
     "qk_gemv_argmax_workspace_bytes": (ctypes.c_size_t, []),
     "qk_gemv_argmax_f32": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp, _vp, _vp]),
+    "qk_gemv_argmax_f32_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp, _vp]),
     "qk_quantize_x32": (_i, [_vp, _i, _vp, _i, _vp, _i, _i, _i, _vp]),
     "qk_gemv_multi_i8": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _vp, _i, _vp]),
     "qk_llama_set_int8": (_i, [_vp, _i, _i]),

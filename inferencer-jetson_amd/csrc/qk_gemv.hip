@@ -853,6 +853,36 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
     return launch_status(where);
 }
 
+// ------------------------------------------------ no-allocation variant --
+//
+// Scratch of qk_gemv_argmax_f32_noalloc: the per-wave (value, row) partials
+// of the LM head's greedy-pick epilogue, kArgPartsMax of each, in a
+// file-scope device array -- one copy per GPU, held until the process ends.
+// On the host `scratch` names a host-side stand-in, not device memory: host
+// code uses only the address hipGetSymbolAddress returns for the current
+// device, looked up once per device and kept.
+constexpr size_t kNoAllocScratchBytes = 2 * kArgPartsMax * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+int scratch_address(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0)
+        return fail(QK_ERR_DEVICE, "qk_gemv_argmax_f32_noalloc: no current device");
+    static std::mutex mutex;
+    static std::vector<void *> addr;   // by device ordinal
+    std::lock_guard<std::mutex> lock(mutex);
+    if (static_cast<size_t>(dev) >= addr.size()) addr.resize(dev + 1, nullptr);
+    if (!addr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p)
+            return fail(QK_ERR_DEVICE, "qk_gemv_argmax_f32_noalloc: cannot resolve the scratch array on device " +
+                                           std::to_string(dev));
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return QK_OK;
+}
+
 }  // namespace
 
 // FP32 path shared by the single, fused and few-token entry points (arguments
@@ -942,6 +972,31 @@ int qk_gemv_argmax_f32(int type, const void *w, const float *x, float *y, int co
     f.arg_i = reinterpret_cast<int *>(f.arg_v + qk::kArgPartsMax);
     int parts = 0;
     f.arg_parts = &parts;
+    if ((st = qk::launch_gemv_fused(&m, 1, x, cols, cols, 1, nullptr, f, s))) return st;
+    return qk::launch_argmax_final(f.arg_v, f.arg_i, parts, out, s);
+}
+
+int qk_gemv_argmax_f32_noalloc(int type, const void *w, const float *x, float *y, int cols, int rows, int32_t *out,
+                               qk_stream stream) {
+    int st = qk::check_weights("qk_gemv_argmax_f32_noalloc", type, w, cols, rows);
+    if (st) return st;
+    if (!x || !y || !out)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_argmax_f32_noalloc: null activation or output pointer");
+    if (!qk::aligned(x, 16) || !qk::aligned(y, 4))
+        return qk::fail(QK_ERR_ALIGN, "qk_gemv_argmax_f32_noalloc: x must be 16-byte and y 4-byte aligned");
+    if (!qk::gemv_fusable(cols)) return qk::fail(QK_ERR_LIMIT, "qk_gemv_argmax_f32_noalloc: rows too long to stage");
+    void *ws = nullptr;
+    if ((st = qk::scratch_address(&ws))) return st;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const qk_matrix m{type, rows, w, y};
+    qk::GemvFusion f;
+    f.arg_v = static_cast<float *>(ws);
+    f.arg_i = reinterpret_cast<int *>(f.arg_v + qk::kArgPartsMax);
+    int parts = 0;
+    f.arg_parts = &parts;
+    // The launch keeps its partials within kArgPartsMax (the grid is clamped)
+    // and fails with QK_ERR_LIMIT otherwise, so the scratch always suffices.
+    static_assert(qk::kNoAllocScratchBytes >= 2 * qk::kArgPartsMax * sizeof(float), "scratch holds every partial");
     if ((st = qk::launch_gemv_fused(&m, 1, x, cols, cols, 1, nullptr, f, s))) return st;
     return qk::launch_argmax_final(f.arg_v, f.arg_i, parts, out, s);
 }
