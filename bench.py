@@ -296,12 +296,13 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
     return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
             "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            # FP32, per layer: QKV, attention + split merge, o, gate/up, down;
-            # then embedding, LM head and the two argmax stages.  INT8, per
-            # layer: norm+quantize, QKV, attention + merge, quantize, o (+add),
-            # norm+quantize, gate/up, SiLU*up+quantize, down (+add); then
-            # embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (10 * cfg["layers"] + 5) if int8 else (6 * cfg["layers"] + 3),
+            # FP32 (activation records), per layer: QKV, attention (one
+            # workgroup per query head at these positions, no merge), o,
+            # gate/up, down; then the embedding, the LM head and the greedy
+            # pick.  INT8, per layer: norm+quantize, QKV, attention, quantize,
+            # o (+add), norm+quantize, gate/up, SiLU*up+quantize, down (+add);
+            # then embedding, norm+quantize, LM head and two argmax stages.
+            "kernels_per_token": (9 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
             "device_bytes": mem}
 
 

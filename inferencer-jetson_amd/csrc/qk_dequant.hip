@@ -45,6 +45,33 @@ __global__ __launch_bounds__(256) void embedding_kernel(const uint8_t *w, const 
     }
 }
 
+// One token's embedding row, block b = blockIdx.x (embedding_kernel's
+// arithmetic), plus the activation records of out * gain for the first GEMV
+// that reads it and their sums of squares of out.
+__global__ __launch_bounds__(256) void embedding_records_kernel(const uint8_t *w, const int32_t *token, float *out,
+                                                                int type, int nb, int64_t row_bytes, int vocab,
+                                                                const float *gain, XGroup *rec, float *ss) {
+    __shared__ float v[256];
+    const int i = threadIdx.x, b = blockIdx.x;
+    const int t = *token;
+    const float x = t < 0 || t >= vocab ? __builtin_nanf("")
+                                        : block_value(w + static_cast<int64_t>(t) * row_bytes, type, nb, b, i);
+    out[b * 256 + i] = x;
+    v[i] = x;
+    __syncthreads();
+    if (i < 16) {
+        float g[16], sq = 0.f;
+        #pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const float xv = v[i * 16 + k];
+            sq = fmaf(xv, xv, sq);
+            g[k] = gain ? xv * gain[b * 256 + i * 16 + k] : xv;
+        }
+        rec[b * 16 + i] = make_group_regs(g);
+        ss[b * 16 + i] = sq;
+    }
+}
+
 // GGUF Q6_K rows -> split rows: one 64-thread workgroup per block moves its
 // 105 two-byte units (the source block is only 2-byte aligned): units 0..63
 // are ql, 64..95 qh, 96..103 scales, 104 d.  The workgroup of a row's last
@@ -73,6 +100,15 @@ int grid_for(int64_t blocks) {
 }
 
 }  // namespace
+
+int launch_embedding_records(int type, const void *w, const int32_t *token, int cols, int vocab, float *out,
+                             const float *gain, XGroup *rec, float *ss, hipStream_t stream) {
+    const int nb = cols / 256;
+    hipLaunchKernelGGL(embedding_records_kernel, dim3(nb), dim3(256), 0, stream, static_cast<const uint8_t *>(w),
+                       token, out, type, nb, row_bytes(type, nb), vocab, gain, rec, ss);
+    return launch_status("embedding records launch");
+}
+
 }  // namespace qk
 
 extern "C" {

@@ -161,73 +161,6 @@ __device__ __forceinline__ void q6k_scales(const uint2 &s, int h, float *sc) {
 
 extern __shared__ __align__(16) unsigned char qk_smem[];
 
-struct XGroup {
-    int limb[12];   // L0 x16, L1 x16, L2 x16 as int8, four per dword
-    float scale;    // 2^(e-21); 0 for an all-zero group, NaN/inf if x is not finite
-    float sum;      // fp32 sum of the 16 activations (min / code-offset terms)
-    int pad[2];
-};
-static_assert(sizeof(XGroup) == 64, "XGroup is one 64-byte LDS record");
-
-__device__ __forceinline__ void load16f(const float *x16, float *v) {
-    #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const float4 q = *reinterpret_cast<const float4 *>(x16 + 4 * k);
-        v[4 * k] = q.x;
-        v[4 * k + 1] = q.y;
-        v[4 * k + 2] = q.z;
-        v[4 * k + 3] = q.w;
-    }
-}
-
-__device__ __forceinline__ XGroup make_group_regs(const float *v);
-
-__device__ __forceinline__ XGroup make_group(const float *x16) {
-    float v[16];
-    load16f(x16, v);
-    return make_group_regs(v);
-}
-
-__device__ __forceinline__ XGroup make_group_regs(const float *v) {
-    float m = 0.f, s = 0.f;
-    #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        m = fmaxf(m, fabsf(v[i]));
-        s += v[i];
-    }
-    XGroup gr;
-    gr.sum = s;
-    gr.pad[0] = gr.pad[1] = 0;
-    if (!(m > 0.f) || !isfinite(m)) {
-        #pragma unroll
-        for (int i = 0; i < 12; ++i) gr.limb[i] = 0;
-        gr.scale = m == 0.f ? 0.f : __builtin_nanf("");   // a non-finite input poisons its rows
-        return gr;
-    }
-    // v_frexp_exp gives e+1 for m in [2^e, 2^(e+1)).
-    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
-    uint32_t l0[4] = {0, 0, 0, 0}, l1[4] = {0, 0, 0, 0}, l2[4] = {0, 0, 0, 0};
-    #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int X = static_cast<int>(rintf(ldexpf(v[i], 21 - e)));
-        const int b0 = (X << 24) >> 24;
-        const int X1 = (X - b0) >> 8;
-        const int b1 = (X1 << 24) >> 24;
-        const int b2 = (X1 - b1) >> 8;
-        l0[i >> 2] |= (static_cast<uint32_t>(b0) & 0xFFu) << (8 * (i & 3));
-        l1[i >> 2] |= (static_cast<uint32_t>(b1) & 0xFFu) << (8 * (i & 3));
-        l2[i >> 2] |= (static_cast<uint32_t>(b2) & 0xFFu) << (8 * (i & 3));
-    }
-    #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        gr.limb[k] = static_cast<int>(l0[k]);
-        gr.limb[4 + k] = static_cast<int>(l1[k]);
-        gr.limb[8 + k] = static_cast<int>(l2[k]);
-    }
-    gr.scale = ldexpf(1.f, e - 21);
-    return gr;
-}
-
 // sum_i code_i * x_i of one part: codes are four dwords of byte codes 0..63.
 // The L1 and L0 dots share one integer accumulator: for 16 codes below 64
 // and limbs of at most 128 in magnitude, |256 * sum(c * L1) + sum(c * L0)|
@@ -853,6 +786,406 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
     return launch_status(where);
 }
 
+// ------------------------------------------- decode GEMV over records --
+//
+// The decode driver's FP32 GEMVs read activation records that the kernel
+// producing the activations made (no staging, no barrier before the first
+// dot), and can make the next GEMV's records in their epilogue.  A
+// workgroup of W waves walks row blocks of kRecRows rows -- of one matrix,
+// or of matrices 0 and 1 together (gate and up: `pair`) -- grid-stride.
+// Within a block, step s of wave w covers the (row, piece) pairs
+// q = s*64W + 64w + lane in row-major order; 64W is a multiple of P, so a
+// lane's piece q % P is the same at every step and its four records are
+// loaded once.  Aligned groups of G = gcd(P, 64) lanes share a row; their
+// sums meet in LDS when a row spans waves (C = P/G > 1) or an epilogue needs
+// the block's values together.  With an RMSNorm on the input, the records
+// hold x * gain and every output is scaled by 1/sqrt(mean(x^2) + eps) after
+// the dot (W (s x * g) = s W (x * g)), the scale reduced from the records'
+// sums of squares by each wave on its own.
+constexpr int kRecRows = 16;
+constexpr int kRecMaxChunks = 16;
+
+struct RecMatrix {
+    const uint8_t *w;
+    float *y;
+    int rows, type, row_bytes, block_begin;
+};
+
+constexpr int kRecMaxMats = 4;   // matrices of one record launch (QKV: 3, gate/up: 2)
+
+struct RecParams {
+    RecMatrix mat[kRecMaxMats];
+    int n_mats;
+    int pair;              // blocks cover rows of matrices 0 and 1 (SiLU records)
+    int nb, pieces;        // blocks per row, P = 4 nb
+    int steps;             // per wave and block: W * steps * 64 = (pair ? 2 : 1) * kRecRows * P
+    int waves;             // W (the workgroup's size in waves)
+    int n_blocks;
+    const XGroup *rec;     // input records, cols / 16
+    const float *ss;       // input: sum of squares of the raw activations per record (RMSNorm), or NULL
+    float norm_eps;
+    int accumulate;        // y += W x
+    XGroup *rec_out;       // output records (NULL: none): y * gain, or SiLU(gate) * up with pair
+    float *ss_out;         // their sums of squares of y (not with pair)
+    const float *gain;     // NULL: 1
+    float *arg_v;          // greedy-pick partials, one per wave (NULL: none)
+    int *arg_i;
+};
+
+struct RecSlot {
+    Raw r;
+    int m;         // matrix (wave-uniform)
+    int row;       // row of the lane's pair (may be past the matrix: not stored)
+    float yold;    // residual input of the row (the lane that stores it)
+};
+
+// Matrix m of the launch with every field read at a static offset and
+// selected (m wave-uniform): the parameter loads of all matrices go out at
+// once instead of one dependent load per field.
+__device__ __forceinline__ RecMatrix rec_mat(const RecParams &p, int m) {
+    RecMatrix r;
+    r.w = p.mat[0].w;
+    r.y = p.mat[0].y;
+    r.rows = p.mat[0].rows;
+    r.type = p.mat[0].type;
+    r.row_bytes = p.mat[0].row_bytes;
+    r.block_begin = p.mat[0].block_begin;
+    #pragma unroll
+    for (int i = 1; i < kRecMaxMats; ++i) {
+        const bool s = m == i;
+        r.w = s ? p.mat[i].w : r.w;
+        r.y = s ? p.mat[i].y : r.y;
+        r.rows = s ? p.mat[i].rows : r.rows;
+        r.type = s ? p.mat[i].type : r.type;
+        r.row_bytes = s ? p.mat[i].row_bytes : r.row_bytes;
+        r.block_begin = s ? p.mat[i].block_begin : r.block_begin;
+    }
+    return r;
+}
+
+// Matrix and first row of row block blk (wave-uniform), without a loop over
+// the matrices.
+__device__ __forceinline__ void rec_block(const RecParams &p, int blk, int m_local, int &m, int &row0) {
+    if (p.pair) {
+        m = m_local;
+        row0 = blk * kRecRows;
+        return;
+    }
+    m = 0;
+    int begin = 0;
+    #pragma unroll
+    for (int i = 1; i < kRecMaxMats; ++i) {
+        const bool in = i < p.n_mats && blk >= p.mat[i].block_begin;
+        m += in ? 1 : 0;
+        begin = in ? p.mat[i].block_begin : begin;
+    }
+    row0 = (blk - begin) * kRecRows;
+}
+
+template <int TYPE>
+__device__ __forceinline__ RecSlot rec_fetch(const RecParams &p, int blk, int s, int q0, int W, int g, int h,
+                                             bool loads_yold) {
+    const int P = p.pieces;
+    const int q = s * 64 * W + q0;
+    const int ri = q / P;                                   // row index within the block (all matrices)
+    const int m_local = __builtin_amdgcn_readfirstlane(ri / kRecRows);   // one block half per wave step
+    const int piece = q - ri * P;
+    int m, row0;
+    rec_block(p, blk, m_local, m, row0);
+    RecSlot t;
+    t.m = __builtin_amdgcn_readfirstlane(m);
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    const RecMatrix M = rec_mat(p, t.m);
+    t.row = row0 + ri - m_local * kRecRows;
+    const bool valid = t.row < M.rows;
+    const int row = valid ? t.row : M.rows - 1;   // keep loads in bounds
+    TileRef ref;
+    ref.type = M.type;
+    ref.b = piece >> 2;
+    const int bpb = M.type == QK_TYPE_Q4_K ? 144 : M.type == QK_TYPE_Q6_K ? 210 : 0;
+    ref.blk = M.w + static_cast<size_t>(row) * M.row_bytes + static_cast<size_t>(piece >> 2) * bpb;
+    t.r = fetch_typed<TYPE>(ref, g, h, p.nb);
+    t.yold = M.y[row];   // unconditional (any valid row); used only where loads_yold
+    if (!loads_yold) t.yold = 0.f;
+    return t;
+}
+
+// EPI: the block's row sums go through LDS (rows spanning waves, output
+// records or the gate/up pair); otherwise each row's group stores it.
+// Every wave keeps D tiles' loads in flight (2 when it has at most two).
+constexpr int kRecMaxWaves = 8;
+constexpr int kRecSsPerLane = 8;    // sums of squares a lane reads: nb <= 32
+
+// The record of the 16 values x held by lanes 0..15 of a wave (the other
+// lanes' values are ignored), made by those lanes together: the group's
+// maximum, sum and exponent through xor shuffles, each lane's three limb
+// bytes packed four lanes to a dword, and lane i storing dword i of the
+// 64-byte record -- make_group_regs' arithmetic, with the sum of the 16
+// values taken as a tree.  sq: the lanes' squares, summed into *ss when ss
+// is given.  Every lane of the wave must call it.
+__device__ __forceinline__ void record16(float x, float sq, int lane, XGroup *dst, float *ss) {
+    const bool in = lane < 16;
+    x = in ? x : 0.f;
+    sq = in ? sq : 0.f;
+    float m = fabsf(x), sum = x;
+    #pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off));
+        sum += __shfl_xor(sum, off);
+        sq += __shfl_xor(sq, off);
+    }
+    const bool ok = m > 0.f && isfinite(m);
+    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
+    const int X = ok ? static_cast<int>(rintf(ldexpf(x, 21 - e))) : 0;
+    const int b0 = (X << 24) >> 24;
+    const int X1 = (X - b0) >> 8;
+    const int b1 = (X1 << 24) >> 24;
+    const int b2 = (X1 - b1) >> 8;
+    const int sh = 8 * (lane & 3);
+    uint32_t u0 = (static_cast<uint32_t>(b0) & 0xFFu) << sh;
+    uint32_t u1 = (static_cast<uint32_t>(b1) & 0xFFu) << sh;
+    uint32_t u2 = (static_cast<uint32_t>(b2) & 0xFFu) << sh;
+    #pragma unroll
+    for (int off = 1; off < 4; off <<= 1) {
+        u0 |= __shfl_xor(u0, off);
+        u1 |= __shfl_xor(u1, off);
+        u2 |= __shfl_xor(u2, off);
+    }
+    // Dword k of limb set j sits in lanes 4k..4k+3 of u_j.
+    const int k = lane & 3;
+    const uint32_t d0 = __shfl(u0, 4 * k), d1 = __shfl(u1, 4 * k), d2 = __shfl(u2, 4 * k);
+    const float scale = ok ? ldexpf(1.f, e - 21) : (m == 0.f ? 0.f : __builtin_nanf(""));
+    uint32_t word = 0;
+    if (lane < 4) word = d0;
+    else if (lane < 8) word = d1;
+    else if (lane < 12) word = d2;
+    else if (lane == 12) word = __builtin_bit_cast(uint32_t, scale);
+    else if (lane == 13) word = __builtin_bit_cast(uint32_t, sum);
+    if (in) reinterpret_cast<uint32_t *>(dst)[lane] = word;
+    if (ss && lane == 0) *ss = sq;
+}
+
+template <int TYPE, int G, bool EPI, int D>
+__device__ __forceinline__ void rec_body(const RecParams &p) {
+    __shared__ float part[2 * kRecRows * kRecMaxChunks];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = p.waves;   // not blockDim.x: that reads the dispatch packet before any other load
+    const int P = p.pieces;
+    const int C = P / G;
+    const int nm = p.pair ? 2 : 1;
+    const int q0 = wave * 64 + lane;
+    const int piece = q0 % P;
+    const int g = (piece >> 1) & 1, h = piece & 1;
+    const bool head = (lane & (G - 1)) == 0;   // the lane that holds its group's sum
+
+    // Every load below is unconditional (indices clamped into range), so no
+    // branch makes a wave wait for the loads in flight.  The first D tiles'
+    // weight loads go out first, then the block's residual inputs and gains,
+    // the activation records and the sums of squares.
+    // Tile k of this wave: block blockIdx.x + (k / steps) * gridDim.x, step k % steps.
+    const int my_blocks = static_cast<int>(blockIdx.x) < p.n_blocks
+                              ? (p.n_blocks - 1 - static_cast<int>(blockIdx.x)) / static_cast<int>(gridDim.x) + 1
+                              : 0;
+    const int n_iter = my_blocks * p.steps;
+    auto fetch = [&](int k) {
+        const int blk = static_cast<int>(blockIdx.x) + (k / p.steps) * static_cast<int>(gridDim.x);
+        return rec_fetch<TYPE>(p, blk, k % p.steps, q0, W, g, h, !EPI && head && p.accumulate);
+    };
+    const int last = max(n_iter - 1, 0);
+    RecSlot sl[D];
+    #pragma unroll
+    for (int i = 0; i < D; ++i) sl[i] = fetch(min(i, last));
+    // With EPI, thread t < nm * kRecRows finishes row t of each block: it
+    // reads the row's residual input one block ahead (never with pair).  The
+    // matrix index stays wave-uniform, so its fields are scalar loads.
+    auto load_yold = [&](int blk) -> float {
+        if (!EPI || p.pair || !p.accumulate || blk >= p.n_blocks) return 0.f;
+        int m, row0;
+        rec_block(p, blk, 0, m, row0);
+        const RecMatrix M = rec_mat(p, __builtin_amdgcn_readfirstlane(m));
+        row0 = __builtin_amdgcn_readfirstlane(row0);
+        return M.y[min(row0 + static_cast<int>(threadIdx.x & (kRecRows - 1)), M.rows - 1)];
+    };
+    float yold_blk = load_yold(blockIdx.x);
+    // Output records of y * gain: lane t < 16 of wave 0 holds the gain of
+    // row t of its block, read one block ahead.
+    auto load_gain = [&](int blk) -> float {
+        if (!EPI || !p.gain || blk >= p.n_blocks) return 1.f;
+        return p.gain[blk * kRecRows + (threadIdx.x & (kRecRows - 1))];   // one matrix: block_begin 0
+    };
+    float gain_blk = load_gain(blockIdx.x);
+    // Each lane reads its piece's four records straight from memory (they
+    // stay in L1 / L2 for the workgroup's other lanes), and the sums of
+    // squares, with no LDS copy and no barrier before the first dot.
+    F32Policy::Lane L;
+    #pragma unroll
+    for (int part_i = 0; part_i < 4; ++part_i) F32Policy::set_part(L, part_i, p.rec[F32Policy::group_of(piece, part_i)]);
+    const float *ssp = p.ss ? p.ss : reinterpret_cast<const float *>(p.rec);   // any readable address
+    float ssv[kRecSsPerLane];
+    #pragma unroll
+    for (int i = 0; i < kRecSsPerLane; ++i) ssv[i] = ssp[min(lane + 64 * i, p.nb * 16 - 1)];
+    float nscale = 1.f;
+    if (p.ss) {
+        float acc = 0.f;
+        #pragma unroll
+        for (int i = 0; i < kRecSsPerLane; ++i) acc += lane + 64 * i < p.nb * 16 ? ssv[i] : 0.f;
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        nscale = 1.0f / sqrtf(acc / static_cast<float>(p.nb * 256) + p.norm_eps);
+    }
+    float bv = -INFINITY;
+    int bi = 0x7FFFFFFF;
+
+    auto block_epilogue = [&](int blk) {
+        __syncthreads();
+        const int t = threadIdx.x;
+        float v = 0.f;
+        if (t < nm * kRecRows) {
+            // The block's matrix (wave-uniform); with pair, rows t >= 16 go
+            // to matrix 1 (selected, not indexed, to keep scalar loads).
+            int m, row0;
+            rec_block(p, blk, 0, m, row0);
+            const RecMatrix M = rec_mat(p, __builtin_amdgcn_readfirstlane(m));
+            row0 = __builtin_amdgcn_readfirstlane(row0);
+            float *ybase = p.pair && t >= kRecRows ? p.mat[1].y : M.y;
+            const int rows = M.rows;
+            const int row = row0 + (t & (kRecRows - 1));
+            for (int c = 0; c < C; ++c) v += part[t * C + c];
+            v *= nscale;
+            if (p.accumulate) v += yold_blk;
+            yold_blk = load_yold(blk + gridDim.x);
+            if (row < rows) {
+                ybase[row] = v;
+                if (p.arg_v) arg_better(bv, bi, v, row);
+            } else {
+                v = 0.f;
+            }
+        }
+        if (p.rec_out && wave == 0) {
+            // Lanes 0..15 of wave 0 hold the block's 16 values (gate rows;
+            // up rows in lanes 16..31 with pair) and make its record together.
+            float x;
+            if (p.pair) {
+                x = silu_mul_value(v, __shfl(v, (lane + kRecRows) & 63));
+            } else {
+                x = v * gain_blk;
+                gain_blk = load_gain(blk + gridDim.x);
+            }
+            const int rec_index = blk;   // one matrix (block_begin 0) or the pair
+            record16(x, v * v, lane, p.rec_out + rec_index, p.pair ? nullptr : p.ss_out + rec_index);
+        }
+        __syncthreads();   // part is reused by the next block
+    };
+
+    auto consume = [&](const RecSlot &t, int k) {
+        const RecMatrix M = rec_mat(p, t.m);
+        float v = group_sum<G>(piece_dot<F32Policy, TYPE>(M.type, t.r, L, g, h));
+        const int s = k % p.steps;
+        if constexpr (EPI) {
+            if (head) part[((s * 64 * W + q0) / P) * C + piece / G] = v;
+            if (s == p.steps - 1)
+                block_epilogue(static_cast<int>(blockIdx.x) + (k / p.steps) * static_cast<int>(gridDim.x));
+        } else {
+            if (head && t.row < M.rows) {
+                v *= nscale;
+                if (p.accumulate) v += t.yold;
+                M.y[t.row] = v;
+                if (p.arg_v) arg_better(bv, bi, v, t.row);
+            }
+        }
+    };
+
+    // D tiles in flight: tile k + D is fetched as tile k is consumed (past
+    // the wave's last tile the last one is fetched again, unconditionally).
+    for (int k = 0; k < n_iter; k += D) {
+        #pragma unroll
+        for (int i = 0; i < D; ++i) {
+            if (k + i < n_iter) {
+                consume(sl[i], k + i);
+                sl[i] = fetch(min(k + i + D, last));
+            }
+        }
+    }
+    if (p.arg_v) {
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            arg_better(bv, bi, ov, oi);
+        }
+        if (lane == 0) {
+            p.arg_v[blockIdx.x * W + wave] = bv;
+            p.arg_i[blockIdx.x * W + wave] = bi;
+        }
+    }
+}
+
+// TYPE 0 (Q4_K and split Q6_K matrices in one launch): one row block per
+// workgroup, run by the body of its matrix's type.
+template <int TYPE, int G, bool EPI, int D>
+__global__ __launch_bounds__(kRecMaxWaves * 64) void rec_gemv(RecParams p) {
+    if constexpr (TYPE != 0) {
+        rec_body<TYPE, G, EPI, D>(p);
+    } else {
+        int m, row0;
+        rec_block(p, blockIdx.x, 0, m, row0);
+        const int type = __builtin_amdgcn_readfirstlane(rec_mat(p, __builtin_amdgcn_readfirstlane(m)).type);
+        if (type == QK_TYPE_Q4_K)
+            rec_body<QK_TYPE_Q4_K, G, EPI, D>(p);
+        else
+            rec_body<QK_TYPE_Q6_K_SPLIT, G, EPI, D>(p);
+    }
+}
+
+// Waves per workgroup W and steps S of a launch: W * S = (pair ? 2 : 1) * nb
+// with 64 W a multiple of P = 4 nb (S divides 16 * (pair ? 2 : 1)), the
+// fewest steps that keep W <= kRecMaxWaves (up to kRecDepth steps, every
+// tile's loads go out at once), and at most kRecMaxChunks group sums per
+// row.  False when no such plan exists.
+bool rec_plan(int nb, bool pair, int &waves, int &steps, int &group) {
+    const int units = (pair ? 2 : 1) * nb;
+    group = gcd_int(4 * nb, 64);
+    if ((4 * nb) / group > kRecMaxChunks) return false;
+    if (nb * 16 > 64 * kRecSsPerLane) return false;   // the sums of squares fit kRecSsPerLane per lane
+    // A gate/up pair runs four steps per wave (one 32-row block per 4-wave
+    // workgroup, 512 of them at 1B shapes: 11.5 us against 12.4 with 8-wave
+    // workgroups of two blocks each); the others two (o 5.0 us, 6.3 at four).
+    const int pair_order[5] = {4, 2, 1, 8, 16}, order[5] = {2, 1, 4, 8, 16};
+    for (int s : (pair ? pair_order : order)) {
+        if (units % s || (16 * (pair ? 2 : 1)) % s) continue;
+        const int w = units / s;
+        if (w < 1 || w > kRecMaxWaves) continue;
+        waves = w;
+        steps = s;
+        return true;
+    }
+    return false;
+}
+
+template <int TYPE, bool EPI, int D>
+const void *rec_kernel_g(int group) {
+    switch (group) {
+        case 4: return reinterpret_cast<const void *>(rec_gemv<TYPE, 4, EPI, D>);
+        case 8: return reinterpret_cast<const void *>(rec_gemv<TYPE, 8, EPI, D>);
+        case 16: return reinterpret_cast<const void *>(rec_gemv<TYPE, 16, EPI, D>);
+        case 32: return reinterpret_cast<const void *>(rec_gemv<TYPE, 32, EPI, D>);
+        default: return reinterpret_cast<const void *>(rec_gemv<TYPE, 64, EPI, D>);
+    }
+}
+
+template <int TYPE>
+const void *rec_kernel_t(int group, bool epi, bool deep) {
+    if (deep) return epi ? rec_kernel_g<TYPE, true, 4>(group) : rec_kernel_g<TYPE, false, 4>(group);
+    return epi ? rec_kernel_g<TYPE, true, 2>(group) : rec_kernel_g<TYPE, false, 2>(group);
+}
+
+const void *rec_kernel(int type, int group, bool epi, bool deep) {
+    return type == QK_TYPE_Q4_K         ? rec_kernel_t<QK_TYPE_Q4_K>(group, epi, deep)
+           : type == QK_TYPE_Q6_K_SPLIT ? rec_kernel_t<QK_TYPE_Q6_K_SPLIT>(group, epi, deep)
+                                        : rec_kernel_t<0>(group, epi, deep);
+}
+
 // ------------------------------------------------ no-allocation variant --
 //
 // Scratch of qk_gemv_argmax_f32_noalloc: the per-wave (value, row) partials
@@ -913,6 +1246,89 @@ bool gemv_fusable(int cols) {
     const int pieces = cols / 64;
     const int chunks = pieces / gcd_int(pieces, 64);
     return chunks <= kMaxChunks && F32FusedPolicy::lds_bytes(cols) + 4096 <= kMaxLds;
+}
+
+bool rec_gemv_supported(int cols, bool pair) {
+    int w, s, g;
+    return cols > 0 && cols % 256 == 0 && rec_plan(cols / 256, pair, w, s, g);
+}
+
+bool rec_gemv_types(const qk_matrix *mats, int n_mats, bool pair) {
+    // Q4_K and split Q6_K (the decode drivers repack every GGUF Q6_K tensor).
+    if (n_mats < 1 || n_mats > kRecMaxMats) return false;
+    bool mixed = false;
+    for (int m = 0; m < n_mats; ++m) {
+        if (mats[m].type != QK_TYPE_Q4_K && mats[m].type != QK_TYPE_Q6_K_SPLIT) return false;
+        mixed |= mats[m].type != mats[0].type;
+    }
+    return !pair || (n_mats == 2 && !mixed);
+}
+
+int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &r, hipStream_t stream) {
+    const int nb = cols / 256;
+    int W, S, G;
+    if (n_mats < 1 || n_mats > kRecMaxMats || !rec_plan(nb, r.pair, W, S, G))
+        return fail(QK_ERR_LIMIT, "record GEMV: unsupported launch");
+    if (r.pair && (n_mats != 2 || mats[0].rows != mats[1].rows))
+        return fail(QK_ERR_INVALID_ARG, "record GEMV: a SiLU pair is two matrices of equal rows");
+    if (!rec_gemv_types(mats, n_mats, r.pair))
+        return fail(QK_ERR_TYPE, "record GEMV: unsupported matrix types");
+    if (r.rec_out && !r.pair && (n_mats != 1 || mats[0].rows % kRecRows))
+        return fail(QK_ERR_INVALID_ARG, "record GEMV: output records need one matrix of whole 16-row blocks");
+    RecParams p{};
+    p.n_mats = n_mats;
+    p.pair = r.pair;
+    p.nb = nb;
+    p.pieces = 4 * nb;
+    p.steps = S;
+    p.waves = W;
+    int64_t blocks = 0;
+    int type = mats[0].type;
+    for (int m = 0; m < n_mats; ++m) {
+        RecMatrix &M = p.mat[m];
+        M.w = static_cast<const uint8_t *>(mats[m].w);
+        M.y = mats[m].y;
+        M.rows = mats[m].rows;
+        M.type = mats[m].type;
+        M.row_bytes = static_cast<int>(row_bytes(M.type, nb));
+        M.block_begin = static_cast<int>(blocks);
+        if (!r.pair || m == 0) blocks += (M.rows + kRecRows - 1) / kRecRows;
+        if (static_cast<int64_t>(M.rows) * M.row_bytes > (int64_t(1) << 40))
+            return fail(QK_ERR_LIMIT, "record GEMV: matrix too large");
+        if (M.type != type) type = 0;
+    }
+    if (blocks > (1 << 30)) return fail(QK_ERR_LIMIT, "record GEMV: too many rows");
+    p.n_blocks = static_cast<int>(blocks);
+    p.rec = r.rec;
+    p.ss = r.ss;
+    p.norm_eps = r.norm_eps;
+    p.accumulate = r.accumulate;
+    p.rec_out = r.rec_out;
+    p.ss_out = r.ss_out;
+    p.gain = r.gain;
+    p.arg_v = r.arg_v;
+    p.arg_i = r.arg_i;
+    const bool epi = (4 * nb) / G > 1 || r.rec_out || r.pair;
+    // One row block per workgroup when they all fit at once (always for
+    // mixed types); grid-stride otherwise (the LM head), within the argmax
+    // partials' buffer.  Two tiles in flight per wave when a wave has no
+    // more, four otherwise.
+    int grid = type == 0 ? static_cast<int>(blocks)
+                         : static_cast<int>(
+                               std::min<int64_t>(blocks, resident_blocks(rec_kernel(type, G, epi, true), W * 64, 0)));
+    if (r.arg_v) {
+        if (type == 0 && grid > kArgPartsMax / W)
+            return fail(QK_ERR_LIMIT, "record GEMV: too many argmax partials for mixed types");
+        grid = std::min(grid, kArgPartsMax / W);
+    }
+    grid = std::max(grid, 1);
+    const int64_t tiles_per_wave = (blocks + grid - 1) / grid * S;
+    const void *fn = rec_kernel(type, G, epi, tiles_per_wave > 2);
+    if (r.arg_parts) *r.arg_parts = grid * W;
+    void *args[] = {&p};
+    if (hipLaunchKernel(fn, dim3(grid), dim3(W * 64), args, 0, stream) != hipSuccess)
+        return launch_status("record GEMV launch");
+    return launch_status("record GEMV launch");
 }
 
 int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,

@@ -129,6 +129,85 @@ int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx
 // qk_gemv_multi_batched_f32.
 int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                          const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream);
+// ------------------------------------------------ activation records --
+//
+// The FP32 GEMVs read activations as 64-byte records, one per 16 columns:
+// the 16 values as X = rint(x * 2^(21-e)) with e = ilogb(max|x|), |X| <=
+// 2^22, split into three signed bytes X = L2*65536 + L1*256 + L0 (packed
+// four per dword: L0 x16, L1 x16, L2 x16), the scale 2^(e-21) and the fp32
+// sum of the 16 values.  A dot of 16 integer codes with a record is then
+// three exact v_dot4 sums.  Records are made by the GEMV workgroups
+// themselves (staging) or, in the decode driver, by the kernel that
+// produces the activations.
+struct XGroup {
+    int limb[12];   // L0 x16, L1 x16, L2 x16 as int8, four per dword
+    float scale;    // 2^(e-21); 0 for an all-zero group, NaN/inf if x is not finite
+    float sum;      // fp32 sum of the 16 activations (min / code-offset terms)
+    int pad[2];
+};
+static_assert(sizeof(XGroup) == 64, "XGroup is one 64-byte record");
+
+__device__ __forceinline__ void load16f(const float *x16, float *v) {
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 q = *reinterpret_cast<const float4 *>(x16 + 4 * k);
+        v[4 * k] = q.x;
+        v[4 * k + 1] = q.y;
+        v[4 * k + 2] = q.z;
+        v[4 * k + 3] = q.w;
+    }
+}
+
+__device__ __forceinline__ XGroup make_group_regs(const float *v);
+
+__device__ __forceinline__ XGroup make_group(const float *x16) {
+    float v[16];
+    load16f(x16, v);
+    return make_group_regs(v);
+}
+
+__device__ __forceinline__ XGroup make_group_regs(const float *v) {
+    float m = 0.f, s = 0.f;
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        m = fmaxf(m, fabsf(v[i]));
+        s += v[i];
+    }
+    XGroup gr;
+    gr.sum = s;
+    gr.pad[0] = gr.pad[1] = 0;
+    if (!(m > 0.f) || !isfinite(m)) {
+        #pragma unroll
+        for (int i = 0; i < 12; ++i) gr.limb[i] = 0;
+        gr.scale = m == 0.f ? 0.f : __builtin_nanf("");   // a non-finite input poisons its rows
+        return gr;
+    }
+    // v_frexp_exp gives e+1 for m in [2^e, 2^(e+1)).
+    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
+    uint32_t l0[4] = {0, 0, 0, 0}, l1[4] = {0, 0, 0, 0}, l2[4] = {0, 0, 0, 0};
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int X = static_cast<int>(rintf(ldexpf(v[i], 21 - e)));
+        const int b0 = (X << 24) >> 24;
+        const int X1 = (X - b0) >> 8;
+        const int b1 = (X1 << 24) >> 24;
+        const int b2 = (X1 - b1) >> 8;
+        l0[i >> 2] |= (static_cast<uint32_t>(b0) & 0xFFu) << (8 * (i & 3));
+        l1[i >> 2] |= (static_cast<uint32_t>(b1) & 0xFFu) << (8 * (i & 3));
+        l2[i >> 2] |= (static_cast<uint32_t>(b2) & 0xFFu) << (8 * (i & 3));
+    }
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        gr.limb[k] = static_cast<int>(l0[k]);
+        gr.limb[4 + k] = static_cast<int>(l1[k]);
+        gr.limb[8 + k] = static_cast<int>(l2[k]);
+    }
+    gr.scale = ldexpf(1.f, e - 21);
+    return gr;
+}
+
+
+
 // Whether the attention kernel serves `group` query heads per KV head and
 // head_dim (group in {1, 2, 3, 4, 6, 8}; head_dim a multiple of 4 dividing 256).
 bool attention_supported(int group, int head_dim);
@@ -147,6 +226,7 @@ struct SplitAttention {
     float *key_cache, *value_cache;  // [layers][cache_rows][kv_heads * head_dim]
     float *out;                      // [n_tokens][heads * head_dim]
     const qk_batch_token *desc;      // device, n_tokens entries; NULL: one token at pos, kv_row 0
+    XGroup *rec_out;                 // the outputs' activation records too (head_dim % 16 == 0), or NULL
     int64_t cache_rows;
     int64_t rows_hint;               // sum over tokens of pos + 1 (0: n_tokens * (max_pos + 1))
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
@@ -292,5 +372,36 @@ __device__ __forceinline__ void q4k_scale_min4(const uint4 &hdr, int g, uint32_t
     sc = g ? ((s811 & M) | ((s03 >> 2) & 0x30303030u)) : (s03 & 0x3F3F3F3Fu);
     mn = g ? (((s811 >> 4) & M) | ((s47 >> 2) & 0x30303030u)) : (s47 & 0x3F3F3F3Fu);
 }
+
+// The decode driver's FP32 GEMV over activation records (no staging): y_m =
+// W_m x for the matrices, x given as records (cols/16 of them), optionally
+// scaled by an RMSNorm factor reduced from the records' sums of squares
+// (the records then hold x * gain), added into y (residual), and leaving the
+// next GEMV's records: of y * gain with sums of squares (one matrix of whole
+// 16-row blocks), or of SiLU(y_0) * y_1 (pair: gate and up).  With arg_v,
+// the greedy pick's per-wave partials (count in *arg_parts).
+struct RecGemv {
+    const XGroup *rec = nullptr;
+    const float *ss = nullptr;
+    float norm_eps = 0.f;
+    int accumulate = 0;
+    int pair = 0;
+    XGroup *rec_out = nullptr;
+    float *ss_out = nullptr;
+    const float *gain = nullptr;
+    float *arg_v = nullptr;
+    int *arg_i = nullptr;
+    int *arg_parts = nullptr;
+};
+// Whether rows of cols columns have a record-GEMV launch plan, and whether
+// the matrices' types can share one launch (a pair needs one type).
+bool rec_gemv_supported(int cols, bool pair);
+bool rec_gemv_types(const qk_matrix *mats, int n_mats, bool pair);
+int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &r, hipStream_t stream);
+// The embedding of one token (device id) into out (cols fp32) and the
+// records of out * gain with their sums of squares: embedding_cuda
+// (inferencer.cu:806-819) plus the first QKV's activation records.
+int launch_embedding_records(int type, const void *w, const int32_t *token, int cols, int vocab, float *out,
+                             const float *gain, XGroup *rec, float *ss, hipStream_t stream);
 
 }  // namespace qk

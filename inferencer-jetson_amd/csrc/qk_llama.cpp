@@ -39,6 +39,15 @@ struct qk_llama {
     int int8_q4k = 0, int8_q6k = 0;            // INT8 GEMV mode (use_dp4a / use_q6_dp4a)
     int8_t *xq = nullptr;                      // INT8 mode: quantized activations, max(dim, hidden)
     float *xscale = nullptr;
+    // FP32 step over activation records (records = true): each GEMV reads the
+    // records its producer made -- x * attn_norm for QKV (rec_norm, made by
+    // the embedding or the previous down projection; x * output_norm for the
+    // LM head), the attention output for o (rec_attn), x * ffn_norm for
+    // gate/up (rec_ffn, made by o), SiLU(gate) * up for down (rec_silu) --
+    // with the sums of squares of x for the RMSNorms (ss_norm, ss_ffn).
+    bool records = false;
+    qk::XGroup *rec_norm = nullptr, *rec_attn = nullptr, *rec_ffn = nullptr, *rec_silu = nullptr;
+    float *ss_norm = nullptr, *ss_ffn = nullptr;
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
     qk_llama_memory mem{};        // device bytes the handle holds
 };
@@ -56,7 +65,7 @@ int dev_alloc(uint64_t &total, T **p, size_t count, const char *what) {
 void release(qk_llama *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->argmax_ws, m->attn_ws, m->d_next, m->d_token,
-                    m->xq, m->xscale};
+                    m->xq, m->xscale, m->rec_norm, m->rec_attn, m->rec_ffn, m->rec_silu, m->ss_norm, m->ss_ffn};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
@@ -234,6 +243,103 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     return qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s);
 }
 
+// Whether the FP32 step can run over activation records: every GEMV shape
+// has a record launch plan, gate and up share a type, and head_dim splits
+// into whole 16-value records.
+bool records_supported(const qk_llama_config &c, const std::vector<qk_llama_layer> &layers, int head_dim) {
+    if (head_dim % 16 || !qk::rec_gemv_supported(c.dim, false) || !qk::rec_gemv_supported(c.dim, true) ||
+        !qk::rec_gemv_supported(c.hidden, false))
+        return false;
+    for (const qk_llama_layer &L : layers) {
+        const qk_matrix qkv[3] = {{L.q_type, c.dim, L.q, nullptr}, {L.k_type, 1, L.k, nullptr},
+                                  {L.v_type, 1, L.v, nullptr}};
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, nullptr}, {L.up_type, c.hidden, L.up, nullptr}};
+        const qk_matrix o{L.o_type, c.dim, L.o, nullptr}, down{L.down_type, c.dim, L.down, nullptr};
+        if (!qk::rec_gemv_types(qkv, 3, false) || !qk::rec_gemv_types(gu, 2, true) ||
+            !qk::rec_gemv_types(&o, 1, false) || !qk::rec_gemv_types(&down, 1, false))
+            return false;
+    }
+    return true;
+}
+
+// The FP32 step over activation records, in five launches per layer with
+// no activation staging inside any GEMV: QKV (RMSNorm as an output scale),
+// attention (RoPE + KV write, records of its output), o (+ residual,
+// records of x * ffn_norm), gate/up (records of SiLU(gate) * up), down
+// (+ residual, records of x * the next RMSNorm's gain); then the LM head
+// with its greedy pick.
+int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
+    const qk_llama_config &c = m->cfg;
+    const int dim = c.dim, kv = m->kv_dim;
+    int st;
+    if ((st = qk::launch_embedding_records(m->w.embd_type, m->w.token_embd, tok, dim, c.vocab, m->x,
+                                           m->layers[0].attn_norm, m->rec_norm, m->ss_norm, s)))
+        return st;
+    qk::SplitAttention attn{};
+    attn.q = m->q;
+    attn.k = m->k;
+    attn.v = m->v;
+    attn.cosine = m->cosine;
+    attn.sine = m->sine;
+    attn.key_cache = m->key_cache;
+    attn.value_cache = m->value_cache;
+    attn.out = m->attn;
+    attn.rec_out = m->rec_attn;
+    attn.cache_rows = c.context;
+    attn.rows_hint = pos + 1;
+    attn.pos = attn.max_pos = pos;
+    attn.n_tokens = 1;
+    attn.heads = c.heads;
+    attn.kv_heads = c.kv_heads;
+    attn.head_dim = m->head_dim;
+    qk::RecGemv qkv_in, o_out, gu_io, down_out;
+    qkv_in.rec = m->rec_norm;
+    qkv_in.ss = m->ss_norm;
+    qkv_in.norm_eps = c.eps;
+    o_out.rec = m->rec_attn;
+    o_out.accumulate = 1;
+    o_out.rec_out = m->rec_ffn;
+    o_out.ss_out = m->ss_ffn;
+    gu_io.rec = m->rec_ffn;
+    gu_io.ss = m->ss_ffn;
+    gu_io.norm_eps = c.eps;
+    gu_io.pair = 1;
+    gu_io.rec_out = m->rec_silu;
+    down_out.rec = m->rec_silu;
+    down_out.accumulate = 1;
+    down_out.rec_out = m->rec_norm;
+    down_out.ss_out = m->ss_norm;
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = qk::launch_rec_gemv(qkv, 3, dim, qkv_in, s))) return st;
+        attn.layer = l;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->x};
+        o_out.gain = L.ffn_norm;
+        if ((st = qk::launch_rec_gemv(&o, 1, dim, o_out, s))) return st;
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+        if ((st = qk::launch_rec_gemv(gu, 2, dim, gu_io, s))) return st;
+        const qk_matrix down{L.down_type, dim, L.down, m->x};
+        down_out.gain = l + 1 < c.layers ? m->layers[l + 1].attn_norm : m->w.output_norm;
+        if ((st = qk::launch_rec_gemv(&down, 1, c.hidden, down_out, s))) return st;
+    }
+    if (!need_logits) return QK_OK;
+    qk::RecGemv head_in;
+    head_in.rec = m->rec_norm;
+    head_in.ss = m->ss_norm;
+    head_in.norm_eps = c.eps;
+    head_in.arg_v = static_cast<float *>(m->argmax_ws);
+    head_in.arg_i = reinterpret_cast<int *>(head_in.arg_v + qk::kArgPartsMax);
+    int parts = 0;
+    head_in.arg_parts = &parts;
+    const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
+    const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
+    const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+    if ((st = qk::launch_rec_gemv(&head, 1, dim, head_in, s))) return st;
+    return qk::launch_argmax_final(head_in.arg_v, head_in.arg_i, parts, m->d_next, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -344,6 +450,21 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         return st;
     }
     m->w.layers = m->layers.data();
+    const int head_type = m->w.output ? m->w.output_type : m->w.embd_type;
+    const qk_matrix head{head_type, c.vocab, m->w.output ? m->w.output : m->w.token_embd, nullptr};
+    m->records = records_supported(c, m->layers, head_dim) && qk::rec_gemv_types(&head, 1, false);
+    if (m->records) {
+        const size_t gd = static_cast<size_t>(c.dim) / 16, gh = static_cast<size_t>(c.hidden) / 16;
+        if ((st = dev_alloc(m->mem.buffers, &m->rec_norm, gd, "activation records")) ||
+            (st = dev_alloc(m->mem.buffers, &m->rec_attn, gd, "activation records")) ||
+            (st = dev_alloc(m->mem.buffers, &m->rec_ffn, gd, "activation records")) ||
+            (st = dev_alloc(m->mem.buffers, &m->rec_silu, gh, "activation records")) ||
+            (st = dev_alloc(m->mem.buffers, &m->ss_norm, gd, "record sums of squares")) ||
+            (st = dev_alloc(m->mem.buffers, &m->ss_ffn, gd, "record sums of squares"))) {
+            release(m);
+            return st;
+        }
+    }
     *out = m;
     return qk::ok();
 }
@@ -398,6 +519,12 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     m->last_next = -1;
     if (m->int8_q4k || m->int8_q6k) {
         if ((st = forward_int8(m, tok, pos, need_logits != 0, s))) return st;
+        if (!need_logits) {
+            if (next_token) *next_token = -1;
+            return qk::ok();
+        }
+    } else if (m->records) {
+        if ((st = forward_records(m, tok, pos, need_logits != 0, s))) return st;
         if (!need_logits) {
             if (next_token) *next_token = -1;
             return qk::ok();

@@ -242,17 +242,19 @@ __global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v,
 // to finish needs a device-scope release per workgroup, an L2 write-back
 // that costs about a microsecond each and serialises per XCD.)
 constexpr int kSplitThreads = 256;
-constexpr int kSplitWaves = kSplitThreads / 64;
 constexpr int kMaxSplits = 64;        // splits per token at most
 constexpr int kMinSplitRows = 64;     // rows per split at least
 constexpr int kSplitTarget = 128;     // workgroups a call aims at
 constexpr size_t kMaxSplitWorkspace = size_t(64) << 20;
+constexpr int kWideMaxPairs = 64;              // (token, KV head) pairs of a wide launch at most
+constexpr int64_t kWideMaxBytes = 512 << 10;   // K + V bytes of one pair's rows at most
 
 struct SplitAttnKernelArgs {
     SplitAttention a;
-    float *partials;   // [n_tokens * kv_heads][splits][split_header(G) + G * head_dim]
+    float *partials;   // [n_tokens * gridDim.x][splits][split_header(G) + G * head_dim]
     int split_rows;
     int splits;        // most splits of any token (the partials' stride)
+    int head_split;    // workgroups sharing a KV head, each with heads / kv_heads / head_split query heads
 };
 
 // A split partial: max [G], sum of exp [G], padded to 16 bytes, then the
@@ -333,8 +335,10 @@ __device__ __forceinline__ void merge_scales(float &m, float &l, float mo, float
     m = mn;
 }
 
-template <int G, int NF, int L>
-__global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAttnKernelArgs ka) {
+template <int G, int NF, int L, int NW>
+__global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKernelArgs ka) {
+    constexpr int kSplitWaves = NW;
+    constexpr int kSplitThreads = NW * 64;
     constexpr int NU = split_steps<G, NF>();
     constexpr int R = 64 / L;          // rows per load instruction
     constexpr int HD = 4 * NF * L;     // dimensions a lane group covers (>= head_dim)
@@ -344,7 +348,11 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
     __shared__ float4 part[kSplitWaves][G * HD / 4];
     __shared__ float wm[kSplitWaves][G], wl[kSplitWaves][G];
     const SplitAttention &a = ka.a;
+    // Workgroup x serves query heads x*G .. x*G + G - 1 of KV head
+    // x / head_split; the first of a KV head's workgroups writes its row.
     const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
+    const int cache_kvh = kvh / ka.head_split;
+    const bool writer = kvh % ka.head_split == 0;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane % L, rq = lane / L;
@@ -363,7 +371,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
     const int nsplit = (n + ka.split_rows - 1) / ka.split_rows;
     const bool fresh = a.k != nullptr && r1 == n;   // this split holds row pos and writes it
     const int rows = (fresh ? r1 - 1 : r1) - r0;    // rows read from the caches
-    const int64_t head0 = (static_cast<int64_t>(a.layer) * a.cache_rows + d.kv_row) * kv_dim + kvh * hd;
+    const int64_t head0 = (static_cast<int64_t>(a.layer) * a.cache_rows + d.kv_row) * kv_dim + cache_kvh * hd;
     const int64_t first = head0 + static_cast<int64_t>(r0) * kv_dim;
     const int row_bytes = kv_dim * 4;
     const bool act = sub < hv;   // head_dim < 4L leaves lanes idle
@@ -401,8 +409,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
             qsf[g * HD + 2 * f + 1] = q0 * si + q1 * c;
         }
         if (fresh) {
-            const float *kt = a.k + static_cast<int64_t>(b) * kv_dim + kvh * hd;
-            const float *vt = a.v + static_cast<int64_t>(b) * kv_dim + kvh * hd;
+            const float *kt = a.k + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
+            const float *vt = a.v + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
             float *kn = reinterpret_cast<float *>(knew), *vn = reinterpret_cast<float *>(vnew);
             const int64_t row = head0 + static_cast<int64_t>(d.pos) * kv_dim;
             for (int f = tid; f < half; f += kSplitThreads) {
@@ -414,10 +422,12 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
                 kn[2 * f + 1] = kr1;
                 vn[2 * f] = v0;
                 vn[2 * f + 1] = v1;
-                a.key_cache[row + 2 * f] = kr0;
-                a.key_cache[row + 2 * f + 1] = kr1;
-                a.value_cache[row + 2 * f] = v0;
-                a.value_cache[row + 2 * f + 1] = v1;
+                if (writer) {
+                    a.key_cache[row + 2 * f] = kr0;
+                    a.key_cache[row + 2 * f + 1] = kr1;
+                    a.value_cache[row + 2 * f] = v0;
+                    a.value_cache[row + 2 * f + 1] = v1;
+                }
             }
         }
     } else {
@@ -513,7 +523,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
 
     constexpr int kHdr = split_header(G);
     const int pstride = kHdr + G * hd;
-    float *mine = ka.partials + ((static_cast<int64_t>(b) * a.kv_heads + kvh) * ka.splits + split) * pstride;
+    float *mine = ka.partials + ((static_cast<int64_t>(b) * gridDim.x + kvh) * ka.splits + split) * pstride;
     for (int i = tid; i < G * hv; i += kSplitThreads) {
         const int g = i / hv, e = i - g * hv;
         float mw = wm[0][g], lw = wl[0][g];
@@ -529,7 +539,9 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
             x.w = x.w * f + y.w * fo;
         }
         if (nsplit == 1) {
-            *reinterpret_cast<float4 *>(o + g * hd + 4 * e) = scale4(x, 1.0f / lw);
+            const float4 r = scale4(x, 1.0f / lw);
+            *reinterpret_cast<float4 *>(o + g * hd + 4 * e) = r;
+            if (a.rec_out) qs[g * HD / 4 + e] = r;   // the query rows are in registers by now
         } else {
             if (e == 0) {
                 mine[g] = mw;
@@ -538,12 +550,26 @@ __global__ __launch_bounds__(kSplitThreads) void split_attention_kernel(SplitAtt
             *reinterpret_cast<float4 *>(mine + kHdr + g * hd + 4 * e) = x;
         }
     }
+    if (nsplit == 1 && a.rec_out) {
+        // The o projection's activation records of this token's G heads.
+        __syncthreads();
+        const float *of = reinterpret_cast<const float *>(qs);
+        XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
+        for (int i = tid; i < G * hd / 16; i += kSplitThreads) {
+            const int g = i / (hd / 16), c = (i - g * (hd / 16)) * 16;
+            float v[16];
+            #pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = of[g * HD + c + k];
+            rec[i] = make_group_regs(v);
+        }
+    }
 }
 
 // The splits of (token, KV head) with more than one: the partials merged in
 // split order.
 template <int G>
 __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka) {
+    __shared__ float mo[G * 256];   // the merged outputs, for the records (head_dim <= 256)
     const SplitAttention &a = ka.a;
     const int kvh = blockIdx.x, b = blockIdx.y;
     const qk_batch_token d = a.desc ? a.desc[b] : qk_batch_token{a.pos, 0, 0};
@@ -553,7 +579,7 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
     const int hd = a.head_dim;
     constexpr int kHdr = split_header(G);
     const int pstride = kHdr + G * hd;
-    const float *all = ka.partials + (static_cast<int64_t>(b) * a.kv_heads + kvh) * ka.splits * pstride;
+    const float *all = ka.partials + (static_cast<int64_t>(b) * gridDim.x + kvh) * ka.splits * pstride;
     float *o = a.out + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
     for (int i = threadIdx.x; i < G * hd; i += 256) {
         const int g = i / hd;
@@ -568,6 +594,12 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
             num = fmaf(w, all[p * pstride + kHdr + i], num);
         }
         o[i] = num / den;
+        if (a.rec_out) mo[i] = num / den;
+    }
+    if (a.rec_out) {
+        __syncthreads();
+        XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
+        for (int i = threadIdx.x; i < G * hd / 16; i += 256) rec[i] = make_group_regs(mo + 16 * i);
     }
 }
 
@@ -657,40 +689,49 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
 
 // Split-attention instance for G and head_dim: 8 lanes per cache row when
 // G * head_dim <= 512, else 16; NF float4 per lane.  NULL when unsupported.
-template <int G, int NF, int L>
+// NW: waves per workgroup -- 4 for splits, kWideWaves for the one-split
+// form that needs no merge (section below).
+template <int G, int NF, int L, int NW>
 const void *split_fn() {
-    return reinterpret_cast<const void *>(split_attention_kernel<G, NF, L>);
+    return reinterpret_cast<const void *>(split_attention_kernel<G, NF, L, NW>);
 }
 
-template <int G>
+template <int G, int NW>
 const void *split_for(int head_dim) {
     if (G * head_dim <= 512) {
-        if (head_dim <= 32) return split_fn<G, 1, 8>();
-        if (head_dim == 64) return split_fn<G, 2, 8>();
+        if (head_dim <= 32) return split_fn<G, 1, 8, NW>();
+        if (head_dim == 64) return split_fn<G, 2, 8, NW>();
         if constexpr (G <= 4)
-            if (head_dim == 128) return split_fn<G, 4, 8>();
+            if (head_dim == 128) return split_fn<G, 4, 8, NW>();
         if constexpr (G <= 2)
-            if (head_dim == 256) return split_fn<G, 8, 8>();
+            if (head_dim == 256) return split_fn<G, 8, 8, NW>();
         return nullptr;
     }
     if constexpr (G >= 6)
-        if (head_dim == 128) return split_fn<G, 2, 16>();
+        if (head_dim == 128) return split_fn<G, 2, 16, NW>();
     if constexpr (G >= 3)
-        if (head_dim == 256) return split_fn<G, 4, 16>();
+        if (head_dim == 256) return split_fn<G, 4, 16, NW>();
     return nullptr;
 }
 
-const void *split_instance(int G, int head_dim) {
+template <int NW>
+const void *split_instance_w(int G, int head_dim) {
     if (head_dim < 4 || head_dim % 4 || 256 % head_dim) return nullptr;
     switch (G) {
-        case 1: return split_for<1>(head_dim);
-        case 2: return split_for<2>(head_dim);
-        case 3: return split_for<3>(head_dim);
-        case 4: return split_for<4>(head_dim);
-        case 6: return split_for<6>(head_dim);
-        case 8: return split_for<8>(head_dim);
+        case 1: return split_for<1, NW>(head_dim);
+        case 2: return split_for<2, NW>(head_dim);
+        case 3: return split_for<3, NW>(head_dim);
+        case 4: return split_for<4, NW>(head_dim);
+        case 6: return split_for<6, NW>(head_dim);
+        case 8: return split_for<8, NW>(head_dim);
         default: return nullptr;
     }
+}
+
+constexpr int kWideWaves = 8;
+
+const void *split_instance(int G, int head_dim, bool wide = false) {
+    return wide ? split_instance_w<kWideWaves>(G, head_dim) : split_instance_w<4>(G, head_dim);
 }
 
 const void *split_merge_instance(int G) {
@@ -732,7 +773,26 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     const void *fn = split_instance(G, a.head_dim);
     if (!fn) return fail(QK_ERR_LIMIT, "split attention: unsupported head layout");
     if (a.n_tokens > 65535) return fail(QK_ERR_LIMIT, "split attention: too many tokens in one launch");
+    if (a.rec_out && a.head_dim % 16) return fail(QK_ERR_LIMIT, "split attention: records need head_dim % 16 == 0");
     const int max_rows = a.max_pos + 1;
+    // Few (token, KV head) pairs over short rows: one wide workgroup each
+    // reads all of its rows, and no merge kernel runs.  A CU alone streams
+    // its 2 x 531 rows of 256 B (one 1B token at position ~530) in about
+    // 3.5 us, against 2.9 us for splits of 64 rows plus a 4 us merge.
+    // Each wide workgroup serves one query head (its KV head's rows are read
+    // by G workgroups, mostly from cache), so the softmax arithmetic spreads
+    // over heads CUs instead of kv_heads.
+    const bool wide = split_rows <= 0 && static_cast<int64_t>(a.n_tokens) * a.heads <= kWideMaxPairs &&
+                      int64_t(2) * max_rows * a.head_dim * static_cast<int64_t>(sizeof(float)) <= kWideMaxBytes &&
+                      split_instance(1, a.head_dim, true) != nullptr;
+    int head_split = 1, Gk = G;
+    if (wide) {
+        head_split = G;
+        Gk = 1;
+        fn = split_instance(1, a.head_dim, true);
+        split_rows = max_rows;
+    }
+    const int groups = a.kv_heads * head_split;   // workgroups per token and split
     if (split_rows <= 0) {
         const int64_t rows = a.rows_hint > 0 ? a.rows_hint : static_cast<int64_t>(a.n_tokens) * max_rows;
         split_rows = split_attention_rows(rows * a.kv_heads, max_rows);
@@ -741,8 +801,8 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     int nsplit = (max_rows + split_rows - 1) / split_rows;
     if (nsplit > 1) {
         // Fewer, longer splits when the workspace is short; one without it.
-        const size_t per = static_cast<size_t>(a.n_tokens) * a.kv_heads *
-                           static_cast<size_t>(split_header(G) + G * a.head_dim) * sizeof(float);
+        const size_t per = static_cast<size_t>(a.n_tokens) * groups *
+                           static_cast<size_t>(split_header(Gk) + Gk * a.head_dim) * sizeof(float);
         const int64_t fit = workspace ? static_cast<int64_t>(workspace_size / per) : 0;
         if (fit < 2)
             split_rows = max_rows;
@@ -759,12 +819,14 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     ka.partials = nsplit > 1 ? static_cast<float *>(workspace) : nullptr;
     ka.split_rows = split_rows;
     ka.splits = nsplit;
+    ka.head_split = head_split;
     void *args[] = {&ka};
-    if (hipLaunchKernel(fn, dim3(a.kv_heads, a.n_tokens, nsplit), dim3(kSplitThreads), args, 0, stream) != hipSuccess)
+    if (hipLaunchKernel(fn, dim3(groups, a.n_tokens, nsplit), dim3(wide ? kWideWaves * 64 : kSplitThreads), args,
+                        0, stream) != hipSuccess)
         return launch_status("split attention launch");
     if (nsplit > 1) {
-        const void *merge = split_merge_instance(G);
-        if (hipLaunchKernel(merge, dim3(a.kv_heads, a.n_tokens), dim3(256), args, 0, stream) != hipSuccess)
+        const void *merge = split_merge_instance(Gk);
+        if (hipLaunchKernel(merge, dim3(groups, a.n_tokens), dim3(256), args, 0, stream) != hipSuccess)
             return launch_status("split attention merge launch");
     }
     return launch_status("split attention launch");
