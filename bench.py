@@ -52,14 +52,20 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def measured_traffic(name: str):
-    """HBM bytes per launch from a committed rocprofv3 PMC summary
-    (profiles/<name>.md, a line 'traffic_bytes_per_launch: N'), or None."""
+def profile_value(name: str, key: str):
+    """A figure from a committed rocprofv3 summary (profiles/<name>.md, a line
+    '<key>: N'), or None."""
     path = ROOT / "profiles" / f"{name}.md"
     if not path.exists():
         return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    m = re.search(re.escape(key) + r":\s*([0-9.eE+]+)", path.read_text())
     return float(m.group(1)) if m else None
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 PMC summary
+    (profiles/<name>.md, a line 'traffic_bytes_per_launch: N'), or None."""
+    return profile_value(name, "traffic_bytes_per_launch")
 
 
 def time_launches(torch, launch, steps: int, warmup: int, stream):
@@ -256,7 +262,11 @@ def bench_mixed_1b_256(torch, qk, wl, stream, steps: int = 20, warmup: int = 3) 
     return {"tokens": ntok, "packing": "2 prefill chunks x 96 + 64 decodes", "ms_per_step": round(ms, 4),
             "tokens_per_s": round(ntok / (ms * 1e-3), 1), "useful_TFLOPs": round(tflops, 1),
             "mfma_util_of_fp16_dense_peak": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-            "mfma_ops_per_useful_product": 2, "launches_per_step": 5 * cfg["layers"]}
+            "mfma_ops_per_useful_product": 2,
+            # SQ_VALU_MFMA_BUSY_CYCLES over the summed dispatch time, from the
+            # committed rocprofv3 counter run of this workload.
+            "mfma_busy_counters": profile_value("batched_gemm_mfma_counters", "mfma_busy_mixed_256"),
+            "launches_per_step": 5 * cfg["layers"]}
 
 
 def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
