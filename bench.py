@@ -163,12 +163,17 @@ def _workspace(torch, qk, cols, rows, ntok):
     return torch.empty(max(n, 256), dtype=torch.uint8, device="cuda"), n
 
 
-def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200, warmup: int = 16) -> dict:
+def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200, warmup: int = 16,
+                        int8: bool = False) -> dict:
     """Llama-3.2-3B FFN for 32 decode tokens of 32 sequences (ragged context
     lengths 64..2048 in the batch descriptor; the FFN reads only the token
     count): fused gate/up (Q4_K 2 x 8192 x 3072), SiLU * up, down (Q6_K
     3072 x 8192).  `copies` weight sets rotate so the last-level cache cannot
-    hold them (8 x 49 MB)."""
+    hold them (8 x 49 MB).  With int8, the reference's INT8 mode
+    (FastRunner's batched INT8 FFN, inferencer.cu:1362-1380): x quantized
+    per 32, gate and up by the INT8 batched GEMM, SiLU * up, the product
+    quantized, down by the INT8 batched GEMM (5 launches, quantization
+    included in the timed step)."""
     dim, hidden, ntok = 3072, 8192, 32
     sets = []
     x_host = None
@@ -184,6 +189,36 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
     ws_d, n_d = _workspace(torch, qk, hidden, dim, ntok)
     L = qk.lib()
     s = qk.stream_handle(stream)
+
+    if int8:
+        xq = torch.empty((ntok, hidden), dtype=torch.int8, device="cuda")
+        xs = torch.empty((ntok, hidden // 32), dtype=torch.float32, device="cuda")
+        ws_i, n_i = _workspace(torch, qk, hidden, hidden, ntok)
+
+        def step(i):
+            wg, wu, wd = sets[i % copies]
+            qk.quantize(x, xq, xs, dim, n_tokens=ntok, ldxq=hidden, ldscale=hidden // 32, stream=stream)
+            for w, out in ((wg, gate), (wu, up)):
+                qk.check(L.qk_gemv_batched_i8(qk.Q4_K, w.data_ptr(), xq.data_ptr(), hidden, xs.data_ptr(),
+                                              hidden // 32, out.data_ptr(), hidden, dim, hidden, ntok,
+                                              ws_i.data_ptr(), n_i, s), "INT8 gate/up")
+            qk.check(L.qk_silu_mul_f32(gate.data_ptr(), up.data_ptr(), ntok * hidden, s), "silu")
+            qk.quantize(gate, xq, xs, hidden, n_tokens=ntok, stream=stream)
+            qk.check(L.qk_gemv_batched_i8(qk.Q6_K, wd.data_ptr(), xq.data_ptr(), hidden, xs.data_ptr(), hidden // 32,
+                                          y.data_ptr(), dim, hidden, dim, ntok, ws_i.data_ptr(), n_i, s), "INT8 down")
+
+        wall, ms = time_launches(torch, step, steps, warmup, stream)
+        weights = 2 * qk.tensor_bytes(qk.Q4_K, dim, hidden) + qk.tensor_bytes(qk.Q6_K, hidden, dim)
+        # Per token: quantize x (4 dim in, dim + dim/8 out), gate and up
+        # (codes + scales in, 4 hidden out each), SiLU * up (8 hidden in,
+        # 4 hidden out), quantize h (4 hidden in, hidden + hidden/8 out),
+        # down (hidden + hidden/8 in, 4 dim out).
+        act = ntok * (4 * dim + 3 * (dim + dim // 8) + 8 * hidden + 12 * hidden + 4 * hidden
+                      + 2 * (hidden + hidden // 8) + 4 * dim)
+        return {"tokens": ntok, "ms_per_step": round(ms, 4), "tokens_per_s": round(ntok / (ms * 1e-3), 1),
+                "bytes_per_step": weights + act, "GBps": round((weights + act) / (ms * 1e-3) / 1e9, 1),
+                "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                "weight_copies": copies, "calls_per_step": 6}
 
     def step(i):
         wg, wu, wd = sets[i % copies]
@@ -461,7 +496,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
-    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "mixed", "mixed_step", "decode",
+    ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "ffn_int8", "mixed", "mixed_step", "decode",
                                        "decode_int8", "batch_decode"],
                     default="gemv",
                     help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
@@ -485,6 +520,7 @@ def main() -> int:
     if args.only != "gemv":
         stream = torch.cuda.current_stream()
         run = {"ffn": lambda: bench_ffn_3b_ragged(torch, qk, wl, stream),
+               "ffn_int8": lambda: bench_ffn_3b_ragged(torch, qk, wl, stream, int8=True),
                "mixed": lambda: bench_mixed_1b_256(torch, qk, wl, stream),
                "mixed_step": lambda: bench_mixed_1b_step(torch, qk, wl),
                "decode": lambda: bench_decode_1b(torch, qk, wl),
@@ -567,6 +603,8 @@ def main() -> int:
         sec.update(bench_small_gemvs(torch, qk, wl, stream))
         sec["ffn_3b_ragged_t32"] = bench_ffn_3b_ragged(torch, qk, wl, stream)
         log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")
+        sec["ffn_3b_ragged_t32_int8"] = bench_ffn_3b_ragged(torch, qk, wl, stream, int8=True)
+        log(f"[bench] ffn_3b_ragged_t32_int8: {json.dumps(sec['ffn_3b_ragged_t32_int8'])}")
         sec["mixed_1b_256"] = bench_mixed_1b_256(torch, qk, wl, stream)
         log(f"[bench] mixed_1b_256: {json.dumps(sec['mixed_1b_256'])}")
         sec["mixed_1b_256_step"] = bench_mixed_1b_step(torch, qk, wl)

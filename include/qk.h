@@ -200,6 +200,23 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
                int ldscale, float *y, int ldy, int cols, int rows, int n_tokens,
                qk_stream stream);
 
+/* qk_gemv_i8 for a batch of tokens on the matrix cores: y[t*ldy + r] for
+   t < n_tokens, the reference's INT8 multi-token semantics (gemv_batch_dp4a,
+   qkv_batch_cuda, gate_up_batch_cuda, inferencer.cu:678-751; its default
+   batched mode, inferencer.cu:1611) without the 32-token cap and without
+   re-reading the weights per token.  From 8 tokens on, each token's codes
+   are multiplied by their per-32 scale while the activations are packed
+   (one fp32 rounding per value; exact when the scale is a power of two) and
+   the products with the exact integer weights d*sc*q - dmin*m (Q4_K) /
+   d*scale*(code - 32) (Q6_K) are summed by the FP32 matrix-core GEMM
+   (v_mfma_f32_32x32x16_f16 over fp16 integer weights and hi / lo halves of
+   the activations); below 8 tokens it is qk_gemv_i8.  workspace as for
+   qk_gemv_batched_f32 (qk_gemv_batched_workspace_bytes(cols, rows,
+   n_tokens)). */
+int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
+                       float *y, int ldy, int cols, int rows, int n_tokens, void *workspace, size_t workspace_bytes,
+                       qk_stream stream);
+
 /* Fused INT8 GEMV over 1..QK_MAX_FUSED matrices sharing one token's
    quantized activations (xq: cols int8, xscale: cols/32): the dp4a branch of
    qkv_cuda / gate_up_cuda (inferencer.cu:753-804) for any mix of Q4_K and

@@ -109,6 +109,7 @@ SIGNATURES = {
     "qk_llama_set_int8": (_i, [_vp, _i, _i]),
     "qk_rmsnorm_quantize_x32": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
+    "qk_gemv_batched_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
     "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "qk_rope_kv_write": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "qk_attention_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),

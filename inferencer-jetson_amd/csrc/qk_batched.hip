@@ -103,6 +103,11 @@ struct BatchParams {
     float norm_eps;
     const float *up;        // stage x / (1 + exp(-x)) * up (up has x's layout)
     int accumulate;         // y += W x
+    // INT8 mode (x unused): activations xq[t*ldxq + c] * xscale[t*ldscale + c/32],
+    // the reference's per-32 quantized inputs.
+    const int8_t *xq;
+    const float *xscale;
+    int ldxq, ldscale;
 };
 
 // ---------------------------------------------------- activation staging --
@@ -144,7 +149,20 @@ __device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int tile
 __device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, int tl, int q, float scale,
                                            XStage &s) {
     const int t = tile * kTokTile + tl;
-    if (t < p.n_tokens) {
+    if (p.xq && t < p.n_tokens) {
+        // INT8 mode: the 32 codes of quantization group b*8 + q times its
+        // scale (exact products of an int8 and the fp32 scale, rounded once).
+        const int8_t *src = p.xq + static_cast<int64_t>(t) * p.ldxq + b * 256 + q * 32;
+        const float xs = p.xscale[static_cast<int64_t>(t) * p.ldscale + b * 8 + q];
+        #pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint4 w = *reinterpret_cast<const uint4 *>(src + 16 * i);
+            const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+            #pragma unroll
+            for (int k = 0; k < 16; ++k)
+                s.v[16 * i + k] = static_cast<float>(static_cast<int8_t>((wd[k >> 2] >> (8 * (k & 3))) & 0xFFu)) * xs;
+        }
+    } else if (t < p.n_tokens) {
         const int64_t at = static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32;
         const float4 *src = reinterpret_cast<const float4 *>(p.x + at);
         #pragma unroll
@@ -734,9 +752,16 @@ void launch_gemm(int type, const dim3 &grid, size_t lds, hipStream_t stream, con
         hipLaunchKernelGGL((batch_gemm<0, TT>), grid, dim3(256), lds, stream, p);
 }
 
+// INT8 activations of the matrix-core path (xq / xscale of n_tokens tokens).
+struct I8Input {
+    const int8_t *xq;
+    const float *xscale;
+    int ldxq, ldscale;
+};
+
 int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *x, int ldx, int cols, int n_tokens,
                 void *workspace, size_t workspace_size, hipStream_t stream, const char *where,
-                const GemvFusion *fusion = nullptr) {
+                const GemvFusion *fusion = nullptr, const I8Input *i8 = nullptr) {
     const int nb = cols / 256;
     const int tiles = tile_count(n_tokens);
     const int tt = token_tiles_per_group(tiles);
@@ -782,6 +807,12 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         p.norm_eps = fusion->norm_eps;
         p.up = fusion->up;
         p.accumulate = fusion->accumulate;
+    }
+    if (i8) {
+        p.xq = i8->xq;
+        p.xscale = i8->xscale;
+        p.ldxq = i8->ldxq;
+        p.ldscale = i8->ldscale;
     }
     hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(256), 0, stream, p, ws);
     const dim3 grid(static_cast<unsigned>(groups * p.splits), tgroups);
@@ -829,6 +860,28 @@ int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float 
         return qk::launch_mfma(&m, 1, &ldy, x, ldx, cols, n_tokens, workspace, workspace_bytes,
                                static_cast<hipStream_t>(stream), "qk_gemv_batched_f32");
     return qk::launch_gemv_f32(&m, 1, x, ldx, cols, n_tokens, &ldy, static_cast<hipStream_t>(stream));
+}
+
+int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
+                       float *y, int ldy, int cols, int rows, int n_tokens, void *workspace, size_t workspace_bytes,
+                       qk_stream stream) {
+    int st = qk::check_weights("qk_gemv_batched_i8", type, w, cols, rows);
+    if (st) return st;
+    if (!xq || !xscale || !y || n_tokens < 0)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_batched_i8: null pointer or negative token count");
+    if (n_tokens == 0) return qk::ok();
+    if (ldxq < cols || ldscale < cols / 32 || ldy < rows)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_batched_i8: leading dimension smaller than the row");
+    if (!qk::aligned(xq, 16) || ldxq % 16 || !qk::aligned(xscale, 4) || !qk::aligned(y, 4))
+        return qk::fail(QK_ERR_ALIGN, "qk_gemv_batched_i8: xq and ldxq must keep 16-byte alignment");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const qk_matrix m{type, rows, w, y};
+    if (n_tokens < qk::kMfmaMinTokens)
+        return qk::launch_gemv_i8(&m, 1, xq, ldxq, xscale, ldscale, cols, n_tokens, &ldy, 0, s);
+    const qk::I8Input in{xq, xscale, ldxq, ldscale};
+    // x is unused in INT8 mode; any 16-byte aligned pointer passes the packer's checks.
+    return qk::launch_mfma(&m, 1, &ldy, reinterpret_cast<const float *>(xq), cols, cols, n_tokens, workspace,
+                           workspace_bytes, s, "qk_gemv_batched_i8", nullptr, &in);
 }
 
 int qk_gemv_multi_batched_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
