@@ -12,8 +12,12 @@
 //   Y[t][r] = sum_b d_rb * sum_{c in b} W_int[r][c] * x[t][c]
 //             - dmin_rb * sum_j m_rbj * X[t][b][j]          (Q4_K only)
 //
-// with W_int = sc*q (Q4_K, 0..945) or sc*(code-32) (Q6_K, -1024..1024):
-// integers that fp16 holds exactly.  Activations are scaled per (token,
+// with W_int = sc*q (Q4_K, 0..945) or sc*(code-32) (Q6_K): integers that
+// fp16 holds exactly while |sc| <= 62 (|W_int| <= 1984); a block with a
+// wider Q6_K scale (real GGUF Q6_K tensors use the whole int8 range) carries
+// each weight as an fp16 pair W_a + W_b and adds a third MFMA chain (W_b
+// times the high halves; W_b x the low halves is below 2^-22 of the block's
+// terms and is left out).  Activations are scaled per (token,
 // block) by a power of two so the block maximum lies in [2^14, 2^15) and
 // split into fp16 high and low halves (22 significant bits), so each block
 // is two v_mfma_f32_32x32x16_f16 chains over exact operands; the block's d
@@ -360,6 +364,48 @@ __device__ __forceinline__ half8 decode_b(const RawBlock &r, int type, int hf, i
     return __builtin_bit_cast(half8, out);
 }
 
+// Q6_K with a sub-block scale beyond +-62: the narrow decode's bias
+// -1056 * s leaves fp16's range (65504), and s * (code - 32) reaches 4096 in
+// magnitude, which fp16 holds only to even integers above 2048.  The weight
+// is then written as W_a + W_b with W_a = fp16(s * (code - 32)) and W_b =
+// fma(code - 32, s, -W_a), the exact rounding residual of an fp16 product
+// (|W_b| <= 1), so B operand pairs (W_a, W_b) carry the integer weight
+// exactly; code - 32 itself is exact (1024 + code - 1056).
+__device__ __forceinline__ void q6_wide_h2(uint32_t v, uint32_t sel, half2v s, uint32_t &wa, uint32_t &wb) {
+    const half2v off = {static_cast<_Float16>(-1056.f), static_cast<_Float16>(-1056.f)};
+    const half2v c = __builtin_bit_cast(half2v, __builtin_amdgcn_perm(0x64646464u, v, sel)) + off;
+    const half2v a = c * s;
+    wa = __builtin_bit_cast(uint32_t, a);
+    wb = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(c, s, -a));
+}
+
+__device__ __forceinline__ void decode_b_wide(const RawBlock &r, int hf, int j, half2v sa, half2v sb, half8 &wa,
+                                              half8 &wb) {
+    const uint32_t la = word(r.q, j), lb = word(r.q, 8 + j), hq = word(r.h, j);
+    const int sh = 4 * hf;
+    const uint32_t c0 = ((la >> sh) & 0x0F0F0F0Fu) | (((hq >> sh) & 0x03030303u) << 4);
+    const uint32_t c1 = ((lb >> sh) & 0x0F0F0F0Fu) | (((hq >> (sh + 2)) & 0x03030303u) << 4);
+    uint4 a, b;
+    q6_wide_h2(c0, 0x04020400u, sa, a.x, b.x);
+    q6_wide_h2(c0, 0x04030401u, sa, a.y, b.y);
+    q6_wide_h2(c1, 0x04020400u, sb, a.z, b.z);
+    q6_wide_h2(c1, 0x04030401u, sb, a.w, b.w);
+    wa = __builtin_bit_cast(half8, a);
+    wb = __builtin_bit_cast(half8, b);
+}
+
+// Whether any of the lane's eight Q6_K scales (scales[kh*8 .. +8)) lies
+// outside [-62, 62], where the narrow decode is not exact.
+__device__ __forceinline__ bool q6_scales_wide(const RawBlock &r) {
+    bool w = false;
+    #pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const int s = static_cast<int8_t>(((k < 4 ? r.hdr.x : r.hdr.y) >> (8 * (k & 3))) & 0xFFu);
+        w |= s > 62 || s < -62;
+    }
+    return w;
+}
+
 __device__ __forceinline__ _Float16 u8_to_h(uint32_t v) { return static_cast<_Float16>(static_cast<float>(v & 0xFFu)); }
 __device__ __forceinline__ _Float16 s8_to_h(uint32_t v) {
     return static_cast<_Float16>(static_cast<float>(static_cast<int8_t>(v & 0xFFu)));
@@ -392,7 +438,7 @@ __device__ __forceinline__ void step_scales(const RawBlock &r, int type, uint32_
 // lane l -> row l%32, block half l/32) x TT token tiles (32 tokens each).
 // Each decoded weight operand feeds TT token tiles; each activation operand
 // read from LDS feeds RT row tiles.
-template <int TYPE, int RT, int TT>
+template <int TYPE, int RT, int TT, bool WIDE = false>
 __device__ __forceinline__ void block_mma(const RawBlock (&r)[RT], int type, const uint8_t *buf_lds, int kh, int col,
                                           float16v (&acc)[RT][TT]) {
     float d[RT], dmin[RT];
@@ -441,11 +487,23 @@ __device__ __forceinline__ void block_mma(const RawBlock (&r)[RT], int type, con
             for (int i = 0; i < RT; ++i) {
                 half2v sa2, ba2, sb2, bb2;
                 step_scales<TYPE>(r[i], type, sc4[i], hf, j, sa2, ba2, sb2, bb2);
-                const half8 bw = decode_b<TYPE>(r[i], type, hf, j, sa2, ba2, sb2, bb2);
-                #pragma unroll
-                for (int u = 0; u < TT; ++u) {
-                    t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[u], bw, t[i][u], 0, 0, 0);
-                    t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[u], bw, t[i][u], 0, 0, 0);
+                if constexpr (WIDE) {
+                    // Q6_K with wide scales: W = W_a + W_b exactly.
+                    half8 wa, wb;
+                    decode_b_wide(r[i], hf, j, sa2, sb2, wa, wb);
+                    #pragma unroll
+                    for (int u = 0; u < TT; ++u) {
+                        t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[u], wa, t[i][u], 0, 0, 0);
+                        t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[u], wa, t[i][u], 0, 0, 0);
+                        t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[u], wb, t[i][u], 0, 0, 0);
+                    }
+                } else {
+                    const half8 bw = decode_b<TYPE>(r[i], type, hf, j, sa2, ba2, sb2, bb2);
+                    #pragma unroll
+                    for (int u = 0; u < TT; ++u) {
+                        t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[u], bw, t[i][u], 0, 0, 0);
+                        t[i][u] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[u], bw, t[i][u], 0, 0, 0);
+                    }
                 }
             }
             #pragma unroll
@@ -586,7 +644,21 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
         RawBlock nxt[RT];
         #pragma unroll
         for (int i = 0; i < RT; ++i) nxt[i] = load_block<TYPE>(wrow[i], bn, p.nb, type, kh);
-        block_mma<TYPE, RT, TT>(cur, type, lds + buf * TT * kTileBytes, kh, col, acc);
+        // A Q6_K block whose scales leave [-62, 62] in any of the wave's rows
+        // takes the exact three-chain decode (wave-uniform branch).
+        bool wide = false;
+        if constexpr (TYPE != QK_TYPE_Q4_K) {
+            if (!is_q4<TYPE>(type)) {
+                bool lane_wide = false;
+                #pragma unroll
+                for (int i = 0; i < RT; ++i) lane_wide |= q6_scales_wide(cur[i]);
+                wide = __builtin_amdgcn_ballot_w64(lane_wide) != 0;
+            }
+        }
+        if (wide)
+            block_mma<TYPE, RT, TT, true>(cur, type, lds + buf * TT * kTileBytes, kh, col, acc);
+        else
+            block_mma<TYPE, RT, TT>(cur, type, lds + buf * TT * kTileBytes, kh, col, acc);
         #pragma unroll
         for (int i = 0; i < RT; ++i) cur[i] = nxt[i];
         wait_loads();
