@@ -1313,9 +1313,16 @@ int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &
     // mixed types); grid-stride otherwise (the LM head), within the argmax
     // partials' buffer.  Two tiles in flight per wave when a wave has no
     // more, four otherwise.
+    // A grid-stride launch (more blocks than resident workgroups: the LM
+    // head) runs the two-deep kernel, whose fewer registers fit one more
+    // workgroup per CU: more waves keep more loads in flight than deeper
+    // prefetch per wave (LM head 128256 x 2048: 48.9 us with four tiles in
+    // flight at 3 workgroups per CU).
+    const int deep_resident = type == 0 ? 0 : resident_blocks(rec_kernel(type, G, epi, true), W * 64, 0);
+    const bool strided = type != 0 && blocks > deep_resident;
     int grid = type == 0 ? static_cast<int>(blocks)
-                         : static_cast<int>(
-                               std::min<int64_t>(blocks, resident_blocks(rec_kernel(type, G, epi, true), W * 64, 0)));
+               : static_cast<int>(std::min<int64_t>(
+                     blocks, strided ? resident_blocks(rec_kernel(type, G, epi, false), W * 64, 0) : deep_resident));
     if (r.arg_v) {
         if (type == 0 && grid > kArgPartsMax / W)
             return fail(QK_ERR_LIMIT, "record GEMV: too many argmax partials for mixed types");
@@ -1323,7 +1330,7 @@ int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &
     }
     grid = std::max(grid, 1);
     const int64_t tiles_per_wave = (blocks + grid - 1) / grid * S;
-    const void *fn = rec_kernel(type, G, epi, tiles_per_wave > 2);
+    const void *fn = rec_kernel(type, G, epi, !strided && tiles_per_wave > 2);
     if (r.arg_parts) *r.arg_parts = grid * W;
     void *args[] = {&p};
     if (hipLaunchKernel(fn, dim3(grid), dim3(W * 64), args, 0, stream) != hipSuccess)
