@@ -819,6 +819,7 @@ struct RecParams {
     int pair;              // blocks cover rows of matrices 0 and 1 (SiLU records)
     int nb, pieces;        // blocks per row, P = 4 nb
     int steps;             // per wave and block: W * steps * 64 = (pair ? 2 : 1) * kRecRows * P
+    int steps_log2;        // steps is a power of two
     int waves;             // W (the workgroup's size in waves)
     int n_blocks;
     const XGroup *rec;     // input records, cols / 16
@@ -843,6 +844,7 @@ struct RecSlot {
 // selected (m wave-uniform): the parameter loads of all matrices go out at
 // once instead of one dependent load per field.
 __device__ __forceinline__ RecMatrix rec_mat(const RecParams &p, int m) {
+    if (p.n_mats == 1) return p.mat[0];
     RecMatrix r;
     r.w = p.mat[0].w;
     r.y = p.mat[0].y;
@@ -871,6 +873,11 @@ __device__ __forceinline__ void rec_block(const RecParams &p, int blk, int m_loc
         row0 = blk * kRecRows;
         return;
     }
+    if (p.n_mats == 1) {
+        m = 0;
+        row0 = blk * kRecRows;
+        return;
+    }
     m = 0;
     int begin = 0;
     #pragma unroll
@@ -882,14 +889,12 @@ __device__ __forceinline__ void rec_block(const RecParams &p, int blk, int m_loc
     row0 = (blk - begin) * kRecRows;
 }
 
+// ri: the lane's row within the block (all matrices) at this step, piece:
+// the lane's piece (the same at every step: 64 W is a multiple of P).
 template <int TYPE>
-__device__ __forceinline__ RecSlot rec_fetch(const RecParams &p, int blk, int s, int q0, int W, int g, int h,
+__device__ __forceinline__ RecSlot rec_fetch(const RecParams &p, int blk, int ri, int piece, int g, int h,
                                              bool loads_yold) {
-    const int P = p.pieces;
-    const int q = s * 64 * W + q0;
-    const int ri = q / P;                                   // row index within the block (all matrices)
     const int m_local = __builtin_amdgcn_readfirstlane(ri / kRecRows);   // one block half per wave step
-    const int piece = q - ri * P;
     int m, row0;
     rec_block(p, blk, m_local, m, row0);
     RecSlot t;
@@ -976,6 +981,10 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
     const int nm = p.pair ? 2 : 1;
     const int q0 = wave * 64 + lane;
     const int piece = q0 % P;
+    // Step s of a block puts the lane on row s * step_rows + ri0 of it (64 W
+    // is a multiple of P, so the lane's piece never changes).
+    const int step_rows = 64 * W / P, ri0 = q0 / P;
+    const int sl2 = p.steps_log2, smask = p.steps - 1;
     const int g = (piece >> 1) & 1, h = piece & 1;
     const bool head = (lane & (G - 1)) == 0;   // the lane that holds its group's sum
 
@@ -989,8 +998,8 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
                               : 0;
     const int n_iter = my_blocks * p.steps;
     auto fetch = [&](int k) {
-        const int blk = static_cast<int>(blockIdx.x) + (k / p.steps) * static_cast<int>(gridDim.x);
-        return rec_fetch<TYPE>(p, blk, k % p.steps, q0, W, g, h, !EPI && head && p.accumulate);
+        const int blk = static_cast<int>(blockIdx.x) + (k >> sl2) * static_cast<int>(gridDim.x);
+        return rec_fetch<TYPE>(p, blk, (k & smask) * step_rows + ri0, piece, g, h, !EPI && head && p.accumulate);
     };
     const int last = max(n_iter - 1, 0);
     RecSlot sl[D];
@@ -1081,11 +1090,11 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
     auto consume = [&](const RecSlot &t, int k) {
         const RecMatrix M = rec_mat(p, t.m);
         float v = group_sum<G>(piece_dot<F32Policy, TYPE>(M.type, t.r, L, g, h));
-        const int s = k % p.steps;
+        const int s = k & smask;
         if constexpr (EPI) {
-            if (head) part[((s * 64 * W + q0) / P) * C + piece / G] = v;
-            if (s == p.steps - 1)
-                block_epilogue(static_cast<int>(blockIdx.x) + (k / p.steps) * static_cast<int>(gridDim.x));
+            if (head) part[(s * step_rows + ri0) * C + piece / G] = v;
+            if (s == smask)
+                block_epilogue(static_cast<int>(blockIdx.x) + (k >> sl2) * static_cast<int>(gridDim.x));
         } else {
             if (head && t.row < M.rows) {
                 v *= nscale;
@@ -1281,6 +1290,7 @@ int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &
     p.nb = nb;
     p.pieces = 4 * nb;
     p.steps = S;
+    p.steps_log2 = __builtin_ctz(static_cast<unsigned>(S));
     p.waves = W;
     int64_t blocks = 0;
     int type = mats[0].type;

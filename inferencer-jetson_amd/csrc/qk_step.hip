@@ -670,7 +670,22 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
     __shared__ int si[4];
     float bv = -INFINITY;
     int bi = 0x7FFFFFFF;
-    for (int k = threadIdx.x; k < parts; k += 256) arg_better(bv, bi, pv[k], pi[k]);
+    // Every load of a round is issued before the first comparison (the
+    // kernel is one workgroup: its time is the loads' round trips).
+    // arg_better keeps the lowest index among maxima whatever the order.
+    constexpr int kPer = 16;
+    for (int base = 0; base < parts; base += 256 * kPer) {
+        float v[kPer];
+        int ix[kPer];
+        #pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int k = base + j * 256 + static_cast<int>(threadIdx.x);
+            v[j] = k < parts ? pv[k] : -INFINITY;
+            ix[j] = k < parts ? pi[k] : 0x7FFFFFFF;
+        }
+        #pragma unroll
+        for (int j = 0; j < kPer; ++j) arg_better(bv, bi, v[j], ix[j]);
+    }
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         float ov = __shfl_xor(bv, off);
