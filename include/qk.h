@@ -382,6 +382,10 @@ int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8);
 int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
 /* Device pointer to the fp32 logits of the last step with need_logits. */
 int qk_llama_logits(qk_llama *m, const float **logits);
+/* Device pointer to the fp32 residual stream x (dim values) after the last
+   step: the state --compare-prefill downloads from FastGPU::x
+   (inferencer.cu:1744). */
+int qk_llama_residual(qk_llama *m, const float **x);
 /* One decode step at position pos (FastRunner::forward, inferencer.cu:1424-1531).
    With need_logits, *next_token receives the greedy token (synchronises the
    stream like the reference's 4-byte copy, inferencer.cu:1529); otherwise
@@ -412,6 +416,9 @@ int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_
 /* Device pointer to the fp32 logits of the last step with need_logits,
    [n_tokens][vocab]. */
 int qk_llama_batch_logits(qk_llama_batch *m, const float **logits);
+/* Device pointer to the fp32 residual streams after the last step,
+   [n_tokens][dim] in the step's token order (inferencer.cu:1744). */
+int qk_llama_batch_residual(qk_llama_batch *m, const float **x);
 /* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  Every
    token writes its key / value row kv_row + pos before any token's
    attention reads the cache, so a token sees the rows of earlier positions

@@ -122,6 +122,7 @@ SIGNATURES = {
     "qk_llama_destroy": (_i, [_vp]),
     "qk_llama_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_forward": (_i, [_vp, _i, _i, _i, ctypes.POINTER(ctypes.c_int)]),
     "qk_rope_kv_write_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i,
                                       _vp]),
@@ -138,6 +139,7 @@ SIGNATURES = {
     "qk_llama_batch_memory_bytes": (_i, [_vp, ctypes.POINTER(qk_llama_memory)]),
     "qk_llama_batch_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_batch_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
     "qk_llama_batch_forward_rows": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i,
@@ -536,6 +538,13 @@ class Runner:
         check(lib().qk_llama_logits(self.handle, ctypes.byref(p)), "logits")
         return p.value
 
+    def residual(self):
+        """The residual stream x after the last step (host copy, float32 [dim])."""
+        import numpy as np
+        p = ctypes.c_void_p()
+        check(lib().qk_llama_residual(self.handle, ctypes.byref(p)), "residual")
+        return copy_to_host(p.value, self.cfg["dim"], np.float32)
+
     def forward(self, token: int, pos: int, need_logits: bool = True) -> int:
         nxt = ctypes.c_int(-1)
         check(lib().qk_llama_forward(self.handle, token, pos, int(need_logits), ctypes.byref(nxt)), "forward")
@@ -555,6 +564,7 @@ class BatchRunner:
         self._create(c, w, max_tokens, cache_rows, stream)
 
     def _create(self, c, w, max_tokens, cache_rows, stream):
+        self.max_tokens = max_tokens
         h = ctypes.c_void_p()
         check(lib().qk_llama_batch_create(ctypes.byref(c), ctypes.byref(w), max_tokens, cache_rows,
                                           stream_handle(stream), ctypes.byref(h)), "batched runner")
@@ -618,6 +628,13 @@ class BatchRunner:
         check(lib().qk_llama_batch_logits(self.handle, ctypes.byref(p)), "logits")
         return copy_to_host(p.value, n_tokens * self.cfg["vocab"], np.float32).reshape(n_tokens, self.cfg["vocab"])
 
+    def residual(self, n_tokens: int):
+        """The residual streams after the last step (host copy, [n_tokens][dim])."""
+        import numpy as np
+        p = ctypes.c_void_p()
+        check(lib().qk_llama_batch_residual(self.handle, ctypes.byref(p)), "residual")
+        return copy_to_host(p.value, n_tokens * self.cfg["dim"], np.float32).reshape(n_tokens, self.cfg["dim"])
+
     def load_kv(self, key_cache, value_cache) -> None:
         """Copy fp32 caches laid out [layer][cache_rows][kv_dim]."""
         c = self.cfg
@@ -674,6 +691,13 @@ def copy_to_host(src: int, count: int, dtype) -> "object":
     if h.hipDeviceSynchronize() != 0 or h.hipMemcpy(out.ctypes.data, src, out.nbytes, 2) != 0:
         raise QKError("copy_to_host", QK_ERR_DEVICE, "hipMemcpy device->host failed")
     return out
+
+
+def copy_device(dst: int, src: int, nbytes: int) -> None:
+    """Device-to-device copy of nbytes (the device is synchronised first)."""
+    h = _hip()
+    if h.hipDeviceSynchronize() != 0 or h.hipMemcpy(dst, src, nbytes, 3) != 0:
+        raise QKError("copy_device", QK_ERR_DEVICE, "hipMemcpy device->device failed")
 
 
 def _runner_load_kv(self, key_cache, value_cache) -> None:

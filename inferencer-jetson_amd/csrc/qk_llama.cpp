@@ -495,6 +495,12 @@ int qk_llama_logits(qk_llama *m, const float **logits) {
     return qk::ok();
 }
 
+int qk_llama_residual(qk_llama *m, const float **x) {
+    if (!m || !x) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_residual: null argument");
+    *x = m->x;
+    return qk::ok();
+}
+
 int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next_token) {
     if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_forward: null handle");
     const qk_llama_config &c = m->cfg;
@@ -796,6 +802,12 @@ int qk_llama_batch_memory_bytes(const qk_llama_batch *m, qk_llama_memory *out) {
 int qk_llama_batch_logits(qk_llama_batch *m, const float **logits) {
     if (!m || !logits) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_logits: null argument");
     *logits = m->logits;
+    return qk::ok();
+}
+
+int qk_llama_batch_residual(qk_llama_batch *m, const float **x) {
+    if (!m || !x) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_residual: null argument");
+    *x = m->x;
     return qk::ok();
 }
 

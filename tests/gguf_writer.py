@@ -94,7 +94,7 @@ TENSOR_NAMES = {"q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
 
 
 def llama_writer(cfg: dict, W: dict, tensor_shape, alignment: int | None = None, tokens=None,
-                 vocab_size_key: bool = True) -> GGUFWriter:
+                 vocab_size_key: bool = True, merges=None) -> GGUFWriter:
     """A Llama model in the tensor naming of the reference's lookups
     (inferencer.cu:1196-1214, 1434-1523): llama.* hyper-parameters, token
     embedding, output norm, optional output, and blk.N.* tensors with dims
@@ -112,6 +112,8 @@ def llama_writer(cfg: dict, W: dict, tensor_shape, alignment: int | None = None,
     w.add("llama.rope.freq_base", F32, cfg["rope_theta"])
     if tokens is not None:
         w.add("tokenizer.ggml.tokens", ARRAY, (STRING, tokens))
+    if merges is not None:
+        w.add("tokenizer.ggml.merges", ARRAY, (STRING, merges))
     dim = cfg["dim"]
     w.add_tensor("token_embd.weight", [dim, cfg["vocab"]], W["embd_type"], W["token_embd"].tobytes())
     w.add_tensor("output_norm.weight", [dim], 0, np.asarray(W["output_norm"], dtype=np.float32).tobytes())
