@@ -28,9 +28,9 @@
 //   pack_activations  once per (block, 8 tokens): x -> the record of
 //                     MFMA A operands (fp16 hi / lo, sub-block sums, scales)
 //                     in the caller's workspace.
-//   batch_gemm        a workgroup (4 waves) owns 256 weight rows (two 32-row
-//                     tiles per wave) x one or two token tiles x a run of
-//                     blocks.  Per block it copies the token tiles' records
+//   batch_gemm        a workgroup (4 waves) owns 128 or 256 weight rows (one
+//                     or two 32-row tiles per wave, as many as its token
+//                     tiles) x one or two token tiles x a run of blocks.  Per block it copies the token tiles' records
 //                     into LDS with direct global->LDS loads (double-buffered:
 //                     the next block's records and weight bytes load while
 //                     this block computes); each wave decodes the raw bytes of
@@ -54,11 +54,16 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaMinTokens = 8;
 constexpr int kTokTile = 32;            // tokens per MFMA tile (the A rows)
-constexpr int kRowTiles = 2;            // 32-row tiles per wave
-constexpr int kGroupRows = 128 * kRowTiles;   // weight rows per workgroup (4 waves)
-constexpr int kPartialFloats = 4 * kRowTiles * 16 * 64;   // one workgroup's partial sums per token tile
+// 32-row tiles per wave (RT): one for a single 32-token tile, two from two
+// token tiles on, so a workgroup (4 waves) owns 128 * RT weight rows and
+// writes 4 * RT * 1024 partial sums per token tile when blocks are split.
+// Measured: one row tile at 32 tokens (two workgroups per CU share each
+// SIMD's VALU and MFMA pipes) took the 32-sequence 1B step 2.15 -> 1.94 ms;
+// at 256 tokens two row tiles stay faster (4.60 against 4.74-4.78 ms).
+__host__ __device__ constexpr int group_rows(int rt) { return 128 * rt; }
+__host__ __device__ constexpr int partial_floats(int rt) { return 4 * rt * 16 * 64; }
 constexpr int kMaxSplit = 16;           // workgroups splitting one row group's blocks
-static_assert(kPartialFloats % 256 == 0, "reduce_splits covers whole partial slots with 256-thread workgroups");
+static_assert(partial_floats(1) % 256 == 0, "reduce_splits covers whole partial slots with 256-thread workgroups");
 
 // LDS tile of one block's activations for one 32-token tile, in MFMA A
 // operand order:
@@ -87,7 +92,7 @@ struct BatchMatrix {
     int type;
     int row_bytes;
     int ldy;
-    int group_begin;   // first row group (kGroupRows rows) of this matrix in the launch
+    int group_begin;   // first row group (group_rows(RT) rows) of this matrix in the launch
 };
 
 struct BatchParams {
@@ -100,7 +105,7 @@ struct BatchParams {
     int tiles;
     int splits;             // workgroups sharing one row group's blocks
     int blocks_per_split;
-    float *partials;        // [group][tile][split][kPartialFloats] when splits > 1
+    float *partials;        // [group][tile][split][partial_floats(RT)] when splits > 1
     const uint8_t *records; // packed activations, [tile][block][kTileBytes]
     // Decode-driver fusions (zero: plain x, overwrite y):
     const float *norm_w;    // stage RMSNorm(x) * norm_w
@@ -558,7 +563,7 @@ __device__ __forceinline__ void store_out(const BatchParams &p, float *y, float 
 
 // ---------------------------------------------------------------- GEMM --
 //
-// Workgroup = 4 waves x kRowTiles row tiles = 256 weight rows, x TT token
+// Workgroup = 4 waves x RT row tiles = 128 RT weight rows, x TT token
 // tiles of 32 tokens, x a run of blocks.  Per block the workgroup copies the
 // TT activation records into LDS with direct global->LDS loads (no register
 // round trip), double-buffered: block b+1's records and weight bytes are in
@@ -588,7 +593,9 @@ __device__ __forceinline__ void wait_loads() { asm volatile("s_waitcnt vmcnt(0)"
 template <int TYPE, int TT>
 __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int RT = kRowTiles;
+    constexpr int RT = TT;
+    constexpr int kGroupRows = group_rows(RT);
+    constexpr int kPartialFloats = partial_floats(RT);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kh = lane >> 5, col = lane & 31;
@@ -705,8 +712,10 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
 // and lane in the partials' own order, so a wave reads 64 consecutive floats
 // per split -- and issues every split's load before the first add: the
 // kernel is latency-bound, so it spreads over the whole chip.
+template <int RT>
 __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
-    constexpr int RT = kRowTiles;
+    constexpr int kGroupRows = group_rows(RT);
+    constexpr int kPartialFloats = partial_floats(RT);
     const int64_t u = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
     const int64_t slot = u / kPartialFloats;
     const int rem = static_cast<int>(u - slot * kPartialFloats);
@@ -745,18 +754,21 @@ int check_batched(const char *where, const float *x, int ldx, int cols, int n_to
 int tile_count(int n_tokens) { return (n_tokens + kTokTile - 1) / kTokTile; }
 
 // Token tiles per workgroup: two once there are two tiles (each decoded
-// weight operand then feeds 64 tokens), else one.
+// weight operand then feeds 64 tokens), else one.  The row tiles per wave
+// follow it.
 int token_tiles_per_group(int tiles) { return tiles >= 2 ? 2 : 1; }
+int row_tiles(int tiles) { return token_tiles_per_group(tiles); }
 
 // Workgroups sharing a row group's blocks: enough that about one workgroup
-// per CU is in flight, at most kMaxSplit, at least one block each.  Every
-// split writes 32 KB of partial sums per token tile, as much as the weight
-// bytes of one block of 256 rows, so more splits cost more than the extra
-// workgroups gain (measured at 32 tokens: one per CU 2.14 ms per 1B step,
-// two per CU 2.20 ms; 3B FFN 54.7 against 56.5 us).
+// per CU is in flight (two with one row tile), at most kMaxSplit, at least
+// one block each.  Every split writes as many partial-sum bytes per token
+// tile as the weight bytes of one block of its rows, so more splits cost
+// more than the extra workgroups gain (measured with two row tiles at 32
+// tokens: one per CU 2.14 ms per 1B step, two per CU 2.20 ms; with one row
+// tile, two per CU 1.94 ms against 1.98 at one).
 void split_plan(int64_t groups, int nb, int tiles, int &splits, int &per_split) {
     const int tt = token_tiles_per_group(tiles);
-    const int64_t target = static_cast<int64_t>(device_info().cus);
+    const int64_t target = static_cast<int64_t>(device_info().cus) * (row_tiles(tiles) == 1 ? 2 : 1);
     const int64_t have = std::max<int64_t>(1, groups * ((tiles + tt - 1) / tt));
     const int64_t want = (target + have - 1) / have;
     int s = static_cast<int>(std::min<int64_t>(std::max<int64_t>(want, 1), std::min(kMaxSplit, nb)));
@@ -768,9 +780,9 @@ size_t records_bytes(int cols, int n_tokens) {
     return static_cast<size_t>(tile_count(n_tokens)) * (cols / 256) * kTileBytes;
 }
 
-int64_t group_count(const int *rows, int n) {
+int64_t group_count(const int *rows, int n, int rt) {
     int64_t g = 0;
-    for (int i = 0; i < n; ++i) g += (rows[i] + kGroupRows - 1) / kGroupRows;
+    for (int i = 0; i < n; ++i) g += (rows[i] + group_rows(rt) - 1) / group_rows(rt);
     return g;
 }
 
@@ -780,35 +792,38 @@ size_t workspace_bytes(int cols, const int *rows, int n_mats, int n_tokens) {
     if (cols <= 0 || cols % 256 || n_mats < 1 || n_tokens < kMfmaMinTokens) return 0;
     const int tiles = tile_count(n_tokens);
     size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
-    const int64_t groups = group_count(rows, n_mats);
+    const int rt = row_tiles(tiles);
+    const int64_t groups = group_count(rows, n_mats, rt);
     if (groups < 1) return 0;
     int splits, per_split;
     split_plan(groups, cols / 256, tiles, splits, per_split);
     if (splits == 1) return bytes;
-    return bytes + static_cast<size_t>(groups) * tiles * splits * kPartialFloats * sizeof(float);
+    return bytes + static_cast<size_t>(groups) * tiles * splits * partial_floats(rt) * sizeof(float);
 }
 
 // Workspace bound for the public query, which knows only the total row
 // count: the group count of any split of `rows_total` rows over at most
-// QK_MAX_FUSED matrices is at most rows_total/kGroupRows + QK_MAX_FUSED.
+// QK_MAX_FUSED matrices is at most rows_total/group_rows + QK_MAX_FUSED.
 size_t workspace_bound(int cols, int rows_total, int n_tokens) {
     if (rows_total <= 0) return 0;
     const int tiles = tile_count(n_tokens);
     if (cols <= 0 || cols % 256 || n_tokens < kMfmaMinTokens) return 0;
     size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
-    const int64_t gmin = (rows_total + kGroupRows - 1) / kGroupRows;
-    const int64_t gmax = rows_total / kGroupRows + QK_MAX_FUSED;
+    const int rt = row_tiles(tiles);
+    const int64_t gmin = (rows_total + group_rows(rt) - 1) / group_rows(rt);
+    const int64_t gmax = rows_total / group_rows(rt) + QK_MAX_FUSED;
+    const size_t slot = static_cast<size_t>(partial_floats(rt)) * sizeof(float);
     size_t best = 0;
     for (int64_t g : {gmin, gmax}) {
         int splits, per_split;
         split_plan(g, cols / 256, tiles, splits, per_split);
-        if (splits > 1) best = std::max(best, static_cast<size_t>(g) * tiles * splits * kPartialFloats * sizeof(float));
+        if (splits > 1) best = std::max(best, static_cast<size_t>(g) * tiles * splits * slot);
     }
     // Between gmin and gmax the split count only falls as groups grow, and the
     // partial bytes are groups * splits: bounded by gmax * splits(gmin).
     int s_min, ps;
     split_plan(gmin, cols / 256, tiles, s_min, ps);
-    if (s_min > 1) best = std::max(best, static_cast<size_t>(gmax) * tiles * s_min * kPartialFloats * sizeof(float));
+    if (s_min > 1) best = std::max(best, static_cast<size_t>(gmax) * tiles * s_min * slot);
     return bytes + best;
 }
 
@@ -837,6 +852,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     const int nb = cols / 256;
     const int tiles = tile_count(n_tokens);
     const int tt = token_tiles_per_group(tiles);
+    const int rt = row_tiles(tiles);
     if (tiles > 65535) return fail(QK_ERR_LIMIT, std::string(where) + ": too many tokens in one launch");
     BatchParams p{};
     p.n_mats = n_mats;
@@ -857,7 +873,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         M.row_bytes = static_cast<int>(row_bytes(M.type, nb));
         M.ldy = ldy[i];
         M.group_begin = static_cast<int>(groups);
-        groups += (M.rows + kGroupRows - 1) / kGroupRows;
+        groups += (M.rows + group_rows(rt) - 1) / group_rows(rt);
         rows[i] = M.rows;
         if (static_cast<int64_t>(M.rows) * M.row_bytes > (int64_t(1) << 40))
             return fail(QK_ERR_LIMIT, std::string(where) + ": matrix too large");
@@ -893,9 +909,13 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         launch_gemm<2>(type, grid, lds, stream, p);
     else
         launch_gemm<1>(type, grid, lds, stream, p);
-    if (p.splits > 1)
-        hipLaunchKernelGGL(reduce_splits, dim3(static_cast<unsigned>(groups * tiles * (kPartialFloats / 256))), dim3(256),
-                           0, stream, p);
+    if (p.splits > 1) {
+        const dim3 rgrid(static_cast<unsigned>(groups * tiles * (partial_floats(rt) / 256)));
+        if (rt == 2)
+            hipLaunchKernelGGL(reduce_splits<2>, rgrid, dim3(256), 0, stream, p);
+        else
+            hipLaunchKernelGGL(reduce_splits<1>, rgrid, dim3(256), 0, stream, p);
+    }
     return launch_status(where);
 }
 
