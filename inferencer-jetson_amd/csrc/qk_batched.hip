@@ -117,6 +117,19 @@ struct BatchParams {
     const int8_t *xq;
     const float *xscale;
     int ldxq, ldscale;
+    // Decode-driver chain (zero: none).  in_ss: per (token, input block) sums
+    // of squares of the unnormalised input, whose RMSNorm is applied as an
+    // output scale (W (s x * g) = s W (x * g)) where the outputs are final.
+    const float *in_ss;
+    // The reduction also packs the next GEMM's input into out_records
+    // (out_nb blocks of 256 of this call's output rows per token): x * gain
+    // with its sums of squares in out_ss when out_gain is set, SiLU(y0) * y1
+    // of a gate / up pair (matrices 0 and 1) when pair is set.
+    uint8_t *out_records;
+    int out_nb;
+    const float *out_gain;
+    float *out_ss;
+    int pair;
 };
 
 // ---------------------------------------------------- activation staging --
@@ -673,7 +686,7 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
     }
 
     // Accumulator register k holds token 8*(k/4) + 4*kh + k%4 of its tile.
-    if (p.splits == 1) {
+    if (!p.partials) {
         #pragma unroll
         for (int u = 0; u < TT; ++u) {
             const int tbase = (tile0 + u) * kTokTile + 4 * kh;
@@ -712,6 +725,15 @@ __global__ __launch_bounds__(256) void batch_gemm(BatchParams p) {
 // and lane in the partials' own order, so a wave reads 64 consecutive floats
 // per split -- and issues every split's load before the first add: the
 // kernel is latency-bound, so it spreads over the whole chip.
+// The RMSNorm factor 1/sqrt(mean(x^2) + eps) of token t's input, from the
+// per-block sums of squares its producer wrote (in block order).
+__device__ __forceinline__ float input_norm_scale(const BatchParams &p, int t) {
+    const float *ss = p.in_ss + static_cast<int64_t>(t) * p.nb;
+    float acc = 0.f;
+    for (int b = 0; b < p.nb; ++b) acc += ss[b];
+    return 1.0f / sqrtf(acc / static_cast<float>(p.nb * 256) + p.norm_eps);
+}
+
 template <int RT>
 __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
     constexpr int kGroupRows = group_rows(RT);
@@ -738,9 +760,103 @@ __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
     const int row = (group - M.group_begin) * kGroupRows + (i * 4 + wave) * 32 + col;
     const int t = tile * kTokTile + 8 * (k >> 2) + 4 * kh + (k & 3);
     if (row >= M.rows || t >= p.n_tokens) return;
+    if (p.in_ss) sum *= input_norm_scale(p, t);
     float *yp = M.y + static_cast<int64_t>(t) * M.ldy + row;
     if (p.accumulate) sum = *yp + sum;
     *yp = sum;
+}
+
+// One wave per (output block ob of 256 rows, token): as many workgroups as
+// output values / 256, so the latency-bound loads spread over the chip.
+// Lane (part, q) = (lane / 8, lane % 8) sums the split
+// partials of rows ob*256 + q*32 + part*4 .. +3 in split order, every
+// split's load in flight before the first add (the kernel is latency-bound:
+// a loop over splits would wait one L2 round trip per split), applies the
+// deferred input norm and the residual add and stores y (not for a gate /
+// up pair).  The values meet in LDS, and lanes q = 0..7 pack the next
+// GEMM's input block -- x * gain with the block's sum of squares of x, or
+// SiLU(gate) * up -- into its record (the pack kernel's layout).
+template <int RT>
+__global__ __launch_bounds__(64) void reduce_pack(BatchParams p) {
+    constexpr int kGroupRows = group_rows(RT);
+    constexpr int kPartialFloats = partial_floats(RT);
+    __shared__ float4 vals[8][8];   // [q][part]
+    const int ob = blockIdx.x;
+    const int tile = blockIdx.y / kTokTile;
+    const int lane = threadIdx.x;
+    const int tl = blockIdx.y % kTokTile;   // token within the tile
+    const int q = lane & 7, part = lane >> 3;
+    const int t = tile * kTokTile + tl;
+    const bool live = t < p.n_tokens;
+    const int row_q = ob * 256 + q * 32, row = row_q + part * 4;
+    // Partial float4 of (matrix m, split sp) for these four rows and the token.
+    const int k = 4 * (tl >> 3) + (tl & 3), kh = (tl >> 2) & 1;
+    auto partial = [&](int m, int sp) -> const float4 * {
+        const BatchMatrix &M = p.mat[m];
+        const int g = M.group_begin + row_q / kGroupRows, rr = (row_q % kGroupRows) / 32;
+        const int64_t slot = static_cast<int64_t>(g) * p.tiles + tile;
+        return reinterpret_cast<const float4 *>(p.partials + (slot * p.splits + sp) * kPartialFloats +
+                                                (rr & 3) * (RT * 1024) + (rr >> 2) * 1024 + k * 64 + kh * 32 +
+                                                part * 4);
+    };
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    float ss = 0.f;
+    if (live) {
+        const float s_in = p.in_ss ? input_norm_scale(p, t) : 1.f;
+        float4 a[kMaxSplit], b[kMaxSplit];
+        #pragma unroll
+        for (int sp = 0; sp < kMaxSplit; ++sp) {
+            a[sp] = sp < p.splits ? *partial(0, sp) : make_float4(0.f, 0.f, 0.f, 0.f);
+            b[sp] = sp < p.splits && p.pair ? *partial(1, sp) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float4 sa = a[0], sb = b[0];
+        #pragma unroll
+        for (int sp = 1; sp < kMaxSplit; ++sp)
+            if (sp < p.splits) {
+                sa = make_float4(sa.x + a[sp].x, sa.y + a[sp].y, sa.z + a[sp].z, sa.w + a[sp].w);
+                sb = make_float4(sb.x + b[sp].x, sb.y + b[sp].y, sb.z + b[sp].z, sb.w + b[sp].w);
+            }
+        sa = make_float4(sa.x * s_in, sa.y * s_in, sa.z * s_in, sa.w * s_in);
+        if (p.pair) {
+            sb = make_float4(sb.x * s_in, sb.y * s_in, sb.z * s_in, sb.w * s_in);
+            v = make_float4(silu_mul_value(sa.x, sb.x), silu_mul_value(sa.y, sb.y), silu_mul_value(sa.z, sb.z),
+                            silu_mul_value(sa.w, sb.w));
+        } else {
+            float4 *y = reinterpret_cast<float4 *>(p.mat[0].y + static_cast<int64_t>(t) * p.mat[0].ldy + row);
+            v = sa;
+            if (p.accumulate) {
+                const float4 o = *y;
+                v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+            }
+            *y = v;
+            if (p.out_gain) {
+                ss = v.x * v.x;
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+                const float4 g = *reinterpret_cast<const float4 *>(p.out_gain + row);
+                v = make_float4(v.x * g.x, v.y * g.y, v.z * g.z, v.w * g.w);
+            }
+        }
+    }
+    if (p.out_gain) {
+        #pragma unroll
+        for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
+        if (live && lane == 0) p.out_ss[static_cast<int64_t>(t) * p.out_nb + ob] = ss;
+    }
+    vals[q][part] = v;
+    __syncthreads();
+    if (part != 0) return;
+    XStage xs;
+    #pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float4 u = vals[q][j];
+        xs.v[4 * j] = u.x;
+        xs.v[4 * j + 1] = u.y;
+        xs.v[4 * j + 2] = u.z;
+        xs.v[4 * j + 3] = u.w;
+    }
+    stage_store(xs, tl, q, p.out_records + (static_cast<size_t>(tile) * p.out_nb + ob) * kTileBytes);
 }
 
 int check_batched(const char *where, const float *x, int ldx, int cols, int n_tokens) {
@@ -786,9 +902,10 @@ int64_t group_count(const int *rows, int n, int rt) {
     return g;
 }
 
-// Workspace: packed activation records, then (when blocks are split) the
-// partial sums of every (row group, token tile, split).
-size_t workspace_bytes(int cols, const int *rows, int n_mats, int n_tokens) {
+// Workspace: packed activation records, then (when blocks are split, or
+// always with `partials`: a reduction stage that must run) the partial sums
+// of every (row group, token tile, split).
+size_t workspace_bytes(int cols, const int *rows, int n_mats, int n_tokens, bool partials = false) {
     if (cols <= 0 || cols % 256 || n_mats < 1 || n_tokens < kMfmaMinTokens) return 0;
     const int tiles = tile_count(n_tokens);
     size_t bytes = (records_bytes(cols, n_tokens) + 255) / 256 * 256;
@@ -797,14 +914,14 @@ size_t workspace_bytes(int cols, const int *rows, int n_mats, int n_tokens) {
     if (groups < 1) return 0;
     int splits, per_split;
     split_plan(groups, cols / 256, tiles, splits, per_split);
-    if (splits == 1) return bytes;
+    if (splits == 1 && !partials) return bytes;
     return bytes + static_cast<size_t>(groups) * tiles * splits * partial_floats(rt) * sizeof(float);
 }
 
 // Workspace bound for the public query, which knows only the total row
 // count: the group count of any split of `rows_total` rows over at most
 // QK_MAX_FUSED matrices is at most rows_total/group_rows + QK_MAX_FUSED.
-size_t workspace_bound(int cols, int rows_total, int n_tokens) {
+size_t workspace_bound(int cols, int rows_total, int n_tokens, bool partials = false) {
     if (rows_total <= 0) return 0;
     const int tiles = tile_count(n_tokens);
     if (cols <= 0 || cols % 256 || n_tokens < kMfmaMinTokens) return 0;
@@ -817,13 +934,13 @@ size_t workspace_bound(int cols, int rows_total, int n_tokens) {
     for (int64_t g : {gmin, gmax}) {
         int splits, per_split;
         split_plan(g, cols / 256, tiles, splits, per_split);
-        if (splits > 1) best = std::max(best, static_cast<size_t>(g) * tiles * splits * slot);
+        if (splits > 1 || partials) best = std::max(best, static_cast<size_t>(g) * tiles * splits * slot);
     }
     // Between gmin and gmax the split count only falls as groups grow, and the
     // partial bytes are groups * splits: bounded by gmax * splits(gmin).
     int s_min, ps;
     split_plan(gmin, cols / 256, tiles, s_min, ps);
-    if (s_min > 1) best = std::max(best, static_cast<size_t>(gmax) * tiles * s_min * slot);
+    if (s_min > 1 || partials) best = std::max(best, static_cast<size_t>(gmax) * tiles * s_min * slot);
     return bytes + best;
 }
 
@@ -881,7 +998,17 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     }
     split_plan(groups, nb, tiles, p.splits, p.blocks_per_split);
     if (groups * p.splits > (1 << 30)) return fail(QK_ERR_LIMIT, std::string(where) + ": too many rows");
-    const size_t need = workspace_bytes(cols, rows, n_mats, n_tokens);
+    // A decode chain's reduction stage (deferred input norm, or packing the
+    // next call's records) runs even without a split.
+    const bool chain_out = fusion && fusion->out_records;
+    const bool need_partials = p.splits > 1 || (fusion && fusion->in_ss) || chain_out;
+    if (chain_out) {
+        const bool pair = fusion->pair != 0;
+        if ((pair && (n_mats != 2 || rows[0] != rows[1])) || (!pair && n_mats != 1) || rows[0] % 256 ||
+            (!pair && !fusion->out_gain) || (fusion->out_gain && !fusion->out_ss) || i8)
+            return fail(QK_ERR_INVALID_ARG, std::string(where) + ": unsupported chained reduction");
+    }
+    const size_t need = workspace_bytes(cols, rows, n_mats, n_tokens, need_partials);
     if (!workspace || workspace_size < need)
         return fail(QK_ERR_INVALID_ARG, std::string(where) + ": workspace smaller than " + std::to_string(need) +
                                             " bytes (qk_gemv_batched_workspace_bytes)");
@@ -889,12 +1016,19 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     const int tgroups = (tiles + tt - 1) / tt;
     p.records = ws;
-    if (p.splits > 1) p.partials = reinterpret_cast<float *>(ws + (records_bytes(cols, n_tokens) + 255) / 256 * 256);
+    if (need_partials) p.partials = reinterpret_cast<float *>(ws + (records_bytes(cols, n_tokens) + 255) / 256 * 256);
     if (fusion) {
         p.norm_w = fusion->norm_w;
         p.norm_eps = fusion->norm_eps;
         p.up = fusion->up;
         p.accumulate = fusion->accumulate;
+        p.in_ss = fusion->in_ss;
+        if (fusion->in_records) p.records = fusion->in_records;
+        p.out_records = fusion->out_records;
+        p.out_nb = rows[0] / 256;
+        p.out_gain = fusion->out_gain;
+        p.out_ss = fusion->out_ss;
+        p.pair = fusion->pair;
     }
     if (i8) {
         p.xq = i8->xq;
@@ -902,14 +1036,21 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         p.ldxq = i8->ldxq;
         p.ldscale = i8->ldscale;
     }
-    hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(256), 0, stream, p, ws);
+    if (!(fusion && fusion->in_records))
+        hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(256), 0, stream, p, ws);
     const dim3 grid(static_cast<unsigned>(groups * p.splits), tgroups);
     const size_t lds = 2 * static_cast<size_t>(tt) * kTileBytes;
     if (tt == 2)
         launch_gemm<2>(type, grid, lds, stream, p);
     else
         launch_gemm<1>(type, grid, lds, stream, p);
-    if (p.splits > 1) {
+    if (chain_out) {
+        const dim3 rgrid(static_cast<unsigned>(p.out_nb), static_cast<unsigned>(tiles * kTokTile));
+        if (rt == 2)
+            hipLaunchKernelGGL(reduce_pack<2>, rgrid, dim3(64), 0, stream, p);
+        else
+            hipLaunchKernelGGL(reduce_pack<1>, rgrid, dim3(64), 0, stream, p);
+    } else if (need_partials) {
         const dim3 rgrid(static_cast<unsigned>(groups * tiles * (partial_floats(rt) / 256)));
         if (rt == 2)
             hipLaunchKernelGGL(reduce_splits<2>, rgrid, dim3(256), 0, stream, p);
@@ -920,6 +1061,16 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
 }
 
 }  // namespace
+
+size_t batched_chain_workspace_bytes(int cols, int rows_total, int n_tokens) {
+    return workspace_bound(cols, rows_total, n_tokens, true);
+}
+
+size_t batched_records_bytes(int cols, int n_tokens) {
+    return n_tokens < kMfmaMinTokens || cols % 256 ? 0 : records_bytes(cols, n_tokens);
+}
+
+bool batched_chain_supported(int n_tokens) { return n_tokens >= kMfmaMinTokens; }
 
 int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                          const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream) {

@@ -54,6 +54,20 @@ struct GemvFusion {
     float norm_eps = 0.f;
     const float *up = nullptr;
     int accumulate = 0;
+    // Matrix-core decode chain (from 8 tokens on; all unset: none).  The
+    // input comes as records a previous call's reduction packed
+    // (in_records, cols / 256 blocks per 32-token tile), with per (token,
+    // block) sums of squares in_ss when its RMSNorm is deferred to the
+    // outputs (norm_eps).  out_records: the reduction packs this call's
+    // output as the next call's input -- y * out_gain with sums of squares in
+    // out_ss (one matrix, y after the residual add), or SiLU(y0) * y1 with
+    // pair (two matrices of equal rows, y not stored); rows % 256 == 0.
+    const uint8_t *in_records = nullptr;
+    const float *in_ss = nullptr;
+    uint8_t *out_records = nullptr;
+    const float *out_gain = nullptr;
+    float *out_ss = nullptr;
+    int pair = 0;
     // Greedy-token epilogue (one matrix, one token): every wave writes the
     // best (value, row) of the rows it stored to arg_v / arg_i and the launch
     // reports the number of such partials in *arg_parts (at most
@@ -127,6 +141,13 @@ int launch_gemv_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx
 // matrix-core GEMM from 8 tokens on (staging fused into its pack kernel, the
 // residual add into its epilogue), the fused GEMV below.  workspace as for
 // qk_gemv_multi_batched_f32.
+// Decode chains on the matrix cores (GemvFusion in_records / out_records):
+// whether n_tokens takes that path, the workspace a chained call needs
+// (partial sums even without a split), and the bytes of one call's packed
+// activation records of `cols` columns.
+bool batched_chain_supported(int n_tokens);
+size_t batched_chain_workspace_bytes(int cols, int rows_total, int n_tokens);
+size_t batched_records_bytes(int cols, int n_tokens);
 int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                          const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream);
 // ------------------------------------------------ activation records --

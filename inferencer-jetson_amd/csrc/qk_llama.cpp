@@ -619,6 +619,12 @@ struct qk_llama_batch {
     float *key_cache = nullptr, *value_cache = nullptr, *cosine = nullptr, *sine = nullptr;
     void *gemm_ws = nullptr, *argmax_ws = nullptr, *attn_ws = nullptr;
     size_t gemm_ws_bytes = 0, attn_ws_bytes = 0;
+    // Matrix-core steps (8 tokens and more) run as a chain: each projection's
+    // reduction packs the next one's input records (rec_a: o -> gate/up and
+    // down -> next QKV, with the RMSNorm deferred through ss; rec_b: gate/up
+    // -> down).
+    uint8_t *rec_a = nullptr, *rec_b = nullptr;
+    float *ss = nullptr;
     int32_t *d_tokens = nullptr, *d_next = nullptr, *d_rows = nullptr;
     qk_batch_token *d_desc = nullptr;
     uint8_t *h_stage = nullptr;   // pinned: tokens, descriptors, logit rows, results
@@ -632,7 +638,7 @@ namespace {
 void release_batch(qk_llama_batch *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->attn_ws, m->d_tokens, m->d_next,
-                    m->d_rows, m->d_desc};
+                    m->d_rows, m->d_desc, m->rec_a, m->rec_b, m->ss};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
@@ -725,8 +731,17 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     const int kv = m->kv_dim;
     const int shapes[][2] = {{c.dim, c.dim + 2 * kv}, {c.dim, c.dim}, {c.dim, 2 * c.hidden}, {c.hidden, c.dim},
                              {c.dim, c.vocab}};
-    for (const auto &sh : shapes) ws = std::max(ws, qk_gemv_batched_workspace_bytes(sh[0], sh[1], max_tokens));
+    // The workspace of a call depends on its token count through the number
+    // of 32-token tiles (fewer tiles can mean more splits), so the bound is
+    // taken over every tile count up to max_tokens.
+    for (int tiles = 1;; ++tiles) {
+        const int tq = std::min(tiles * 32, max_tokens);
+        for (const auto &sh : shapes) ws = std::max(ws, qk_gemv_batched_workspace_bytes(sh[0], sh[1], tq));
+        for (int i = 0; i < 4; ++i) ws = std::max(ws, qk::batched_chain_workspace_bytes(shapes[i][0], shapes[i][1], tq));
+        if (tq == max_tokens) break;
+    }
     m->gemm_ws_bytes = ws;
+    const size_t rec_bytes = qk::batched_records_bytes(std::max(c.dim, c.hidden), max_tokens);
     m->attn_ws_bytes = qk::split_attention_workspace_bytes(max_tokens, c.heads, c.kv_heads, head_dim, c.context);
     int st = QK_OK;
     if ((st = dev_alloc(m->mem.buffers, &m->x, T * c.dim, "residual")) || (st = dev_alloc(m->mem.buffers, &m->xn, T * c.dim, "normalized state")) ||
@@ -745,7 +760,10 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
         (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->argmax_ws), qk_argmax_rows_workspace_bytes(c.vocab, max_tokens),
                         "argmax workspace")) ||
         (st = dev_alloc(m->mem.buffers, &m->d_tokens, T, "input tokens")) || (st = dev_alloc(m->mem.buffers, &m->d_next, T, "next tokens")) ||
-        (st = dev_alloc(m->mem.buffers, &m->d_rows, T, "logit rows")) || (st = dev_alloc(m->mem.buffers, &m->d_desc, T, "batch descriptor"))) {
+        (st = dev_alloc(m->mem.buffers, &m->d_rows, T, "logit rows")) || (st = dev_alloc(m->mem.buffers, &m->d_desc, T, "batch descriptor")) ||
+        (rec_bytes && ((st = dev_alloc(m->mem.buffers, &m->rec_a, rec_bytes, "chained records")) ||
+                       (st = dev_alloc(m->mem.buffers, &m->rec_b, rec_bytes, "chained records")) ||
+                       (st = dev_alloc(m->mem.buffers, &m->ss, T * (c.dim / 256), "chained sums of squares"))))) {
         release_batch(m);
         return st;
     }
@@ -888,12 +906,25 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     attn.heads = c.heads;
     attn.kv_heads = c.kv_heads;
     attn.head_dim = hd;
+    // From 8 tokens on (matrix cores) the projections chain: o's reduction
+    // adds the residual and packs x * ffn_norm for gate/up (sums of squares
+    // for the deferred RMSNorm), gate/up's packs SiLU(gate) * up for down,
+    // down's adds the residual and packs x * the next attn_norm for the next
+    // QKV -- ten launches per layer instead of thirteen.
+    const bool chain = qk::batched_chain_supported(T) && m->rec_a;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
         ffn_in.norm_w = L.ffn_norm;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, attn_in, ws, wsb, s))) return st;
+        qk::GemvFusion qkv_in = attn_in;
+        if (chain && l > 0) {
+            qkv_in = qk::GemvFusion{};
+            qkv_in.in_records = m->rec_a;
+            qkv_in.in_ss = m->ss;
+            qkv_in.norm_eps = c.eps;
+        }
+        if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, qkv_in, ws, wsb, s))) return st;
         if (chained &&
             (st = qk_rope_kv_write_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
                                            m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
@@ -901,11 +932,35 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         attn.layer = l;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
-        if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, residual, ws, wsb, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
-        if ((st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, ffn_in, ws, wsb, s))) return st;
         const qk_matrix down{L.down_type, dim, L.down, m->x};
-        if ((st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s))) return st;
+        if (!chain) {
+            if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, residual, ws, wsb, s)) ||
+                (st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, ffn_in, ws, wsb, s)) ||
+                (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s)))
+                return st;
+            continue;
+        }
+        qk::GemvFusion o_f = residual, gu_f, down_f;
+        o_f.out_records = m->rec_a;
+        o_f.out_gain = L.ffn_norm;
+        o_f.out_ss = m->ss;
+        gu_f.in_records = m->rec_a;
+        gu_f.in_ss = m->ss;
+        gu_f.norm_eps = c.eps;
+        gu_f.pair = 1;
+        gu_f.out_records = m->rec_b;
+        down_f.in_records = m->rec_b;
+        down_f.accumulate = 1;
+        if (l + 1 < c.layers) {
+            down_f.out_records = m->rec_a;
+            down_f.out_gain = m->layers[l + 1].attn_norm;
+            down_f.out_ss = m->ss;
+        }
+        if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, o_f, ws, wsb, s)) ||
+            (st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, gu_f, ws, wsb, s)) ||
+            (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_f, ws, wsb, s)))
+            return st;
     }
     if (!n_rows) return qk::ok();
     // The LM head over the selected tokens only (the reference's prefill
