@@ -455,34 +455,39 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
             "GBps": round(moved / el / 1e9, 1), "frac_of_peak": round(moved / el / 1e9 / HBM_PEAK_GBPS, 4),
             "context": "ctx ~ U[64, 2048] per sequence (seed 3)", "device_bytes": mem}
 
-def reference_kernels(torch, args) -> int:
-    """Plain copy / streaming read of 256 MiB buffers (4 rotating sources)."""
+def bandwidth_kernel(torch, kind: str, nbytes: int, steps: int, warmup: int) -> tuple[float, int]:
+    """Times libqkbench's plain copy or streaming read over nbytes from 4
+    rotating sources; returns (mean us per launch, bytes moved per launch)."""
     import ctypes
     lib = ctypes.CDLL(str(ROOT / "inferencer-jetson_amd" / "libqkbench.so"))
     vp, sz = ctypes.c_void_p, ctypes.c_size_t
     lib.qkb_copy.argtypes, lib.qkb_copy.restype = [vp, vp, sz, vp], ctypes.c_int
     lib.qkb_stream_read.argtypes, lib.qkb_stream_read.restype = [vp, sz, vp, vp], ctypes.c_int
     lib.qkb_sink_words.restype = ctypes.c_int
-    nbytes = 256 << 20
     srcs = [torch.full((nbytes // 4,), float(i + 1), device="cuda") for i in range(4)]
-    dst = torch.empty(nbytes // 4, device="cuda")
+    dst = torch.empty(nbytes // 4, device="cuda") if kind == "copy" else None
     sink = torch.zeros(lib.qkb_sink_words(), dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
 
     def launch(i):
-        if args.only == "copy":
+        if kind == "copy":
             rc = lib.qkb_copy(srcs[i % 4].data_ptr(), dst.data_ptr(), nbytes, stream.cuda_stream)
         else:
             rc = lib.qkb_stream_read(srcs[i % 4].data_ptr(), nbytes, sink.data_ptr(), stream.cuda_stream)
         if rc:
             raise RuntimeError(f"bench kernel failed ({rc})")
 
-    wall, kern_ms = time_launches(torch, launch, args.steps, args.warmup, stream)
-    moved = nbytes * (2 if args.only == "copy" else 1)
+    _, kern_ms = time_launches(torch, launch, steps, warmup, stream)
+    return kern_ms * 1e3, nbytes * (2 if kind == "copy" else 1)
+
+
+def reference_kernels(torch, args) -> int:
+    """Plain copy / streaming read of 256 MiB buffers (4 rotating sources)."""
+    nbytes = 256 << 20
+    us, moved = bandwidth_kernel(torch, args.only, nbytes, args.steps, args.warmup)
     print(json.dumps({"kernel": args.only, "bytes_per_launch": moved, "read_bytes": nbytes,
                       "write_bytes": nbytes if args.only == "copy" else 0,
-                      "kernel_us": round(kern_ms * 1e3, 2), "GBps": round(moved / (kern_ms * 1e-3) / 1e9, 1)}),
-          flush=True)
+                      "kernel_us": round(us, 2), "GBps": round(moved / (us * 1e-6) / 1e9, 1)}), flush=True)
     return 0
 
 
@@ -598,6 +603,14 @@ def main() -> int:
                                    "frac_of_peak": round(i8_bytes / (ki * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
         log(f"[bench] lm_head_q6k_int8: {json.dumps(sec['lm_head_q6k_int8'])}")
         log(f"[bench] lm_head_q6k_gguf_layout: {json.dumps(sec['lm_head_q6k_gguf_layout'])}")
+        # The practical ceiling of a read-only kernel: a plain streaming read of
+        # the headline's weight bytes from 4 rotating buffers.
+        sr_us, sr_bytes = bandwidth_kernel(torch, "stream", weight_bytes // 16 * 16, 500, 200)
+        sr_gbps = sr_bytes / (sr_us * 1e-6) / 1e9
+        sec["stream_read_ceiling"] = {"bytes_per_launch": sr_bytes, "kernel_us": round(sr_us, 2),
+                                      "GBps": round(sr_gbps, 1), "frac_of_peak": round(sr_gbps / HBM_PEAK_GBPS, 4),
+                                      "lm_head_q6k_frac_of_ceiling": round(achieved / sr_gbps, 4)}
+        log(f"[bench] stream_read_ceiling: {json.dumps(sec['stream_read_ceiling'])}")
         sec["gemv_q4k_128256x2048"] = bench_q4k_lm_shape(torch, qk, wl, stream, args.copies)
         log(f"[bench] gemv_q4k_128256x2048: {json.dumps(sec['gemv_q4k_128256x2048'])}")
         sec.update(bench_small_gemvs(torch, qk, wl, stream))
