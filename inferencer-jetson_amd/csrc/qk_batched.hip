@@ -42,6 +42,7 @@
 //   reduce_splits     adds them in split order, so results are deterministic,
 //                     and applies the call's epilogue (one thread per output).
 #include "qk_internal.h"
+#include "qk_records.h"
 
 #include <algorithm>
 
@@ -49,11 +50,9 @@ namespace qk {
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kMfmaMinTokens = 8;
-constexpr int kTokTile = 32;            // tokens per MFMA tile (the A rows)
 // 32-row tiles per wave (RT): one for a single 32-token tile, two from two
 // token tiles on, so a workgroup (4 waves) owns 128 * RT weight rows and
 // writes 4 * RT * 1024 partial sums per token tile when blocks are split.
@@ -64,19 +63,6 @@ __host__ __device__ constexpr int group_rows(int rt) { return 128 * rt; }
 __host__ __device__ constexpr int partial_floats(int rt) { return 4 * rt * 16 * 64; }
 constexpr int kMaxSplit = 16;           // workgroups splitting one row group's blocks
 static_assert(partial_floats(1) % 256 == 0, "reduce_splits covers whole partial slots with 256-thread workgroups");
-
-// LDS tile of one block's activations for one 32-token tile, in MFMA A
-// operand order:
-//   hi   [16 steps][2 halves][32 tokens][8]  fp16   16 KiB
-//   lo   same                                fp16   16 KiB
-//   mhi  [2 halves][32 tokens][4]            fp16   512 B  (sub-block sums / 64)
-//   mlo  same                                fp16   512 B
-//   f    [2 halves][16]                      fp32   128 B  (2^-shift per token, lane order)
-constexpr int kTileA = 16384;
-constexpr int kTileM = 512;
-constexpr int kTileF = 128;
-constexpr int kTileBytes = 2 * kTileA + 2 * kTileM + kTileF;
-static_assert(kTileBytes % 16 == 0, "tiles keep 16-byte alignment");
 
 // K order of the A / B operands inside a block.  Step s (0..15) and half kh
 // (lane / 32) hold eight columns of the 64-column group G = 2*kh + s/8:
@@ -136,10 +122,6 @@ struct BatchParams {
 //
 // Thread (tl = tid/8, q = tid%8) owns token tl of the tile and the 32
 // columns q*32 .. q*32+31 (Q4_K sub-block q) of the block.
-
-struct XStage {
-    float v[32];
-};
 
 // The token's RMSNorm scale 1/sqrt(mean(x^2) + eps) over all cols
 // (rmsnorm_cuda's arithmetic, inferencer.cu:821-834), from the 32 lanes
@@ -221,68 +203,6 @@ __device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b
     } else {
         #pragma unroll
         for (int i = 0; i < 32; ++i) s.v[i] = 0.f;
-    }
-}
-
-// x' = x * 2^shift with the block maximum of the token in [2^14, 2^15)
-// (shift capped at 140 so 2^-shift stays a nonzero fp32), split into fp16
-// hi + lo; a non-finite activation makes the token's scale NaN.
-__device__ __forceinline__ void stage_store(const XStage &s, int tl, int q, uint8_t *tile) {
-    float m = 0.f;
-    bool bad = false;
-    #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        m = fmaxf(m, fabsf(s.v[i]));
-        bad |= !isfinite(s.v[i]);
-    }
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    int nb_bad = bad ? 1 : 0;
-    nb_bad |= __shfl_xor(nb_bad, 1);
-    nb_bad |= __shfl_xor(nb_bad, 2);
-    nb_bad |= __shfl_xor(nb_bad, 4);
-    int shift = 0;
-    float f = 0.f;
-    if (m > 0.f && isfinite(m)) {
-        shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
-        f = ldexpf(1.f, -shift);
-    }
-    if (nb_bad) f = __builtin_nanf("");
-
-    _Float16 *hi = reinterpret_cast<_Float16 *>(tile);
-    _Float16 *lo = reinterpret_cast<_Float16 *>(tile + kTileA);
-    const int G = q >> 1, half = q & 1, kh = G >> 1, hf = G & 1;
-    float sum = 0.f;
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int st = hf * 8 + j;
-        half4 h4, l4;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float xs = nb_bad ? 0.f : ldexpf(s.v[4 * j + i], shift);
-            sum += xs;
-            const _Float16 h = static_cast<_Float16>(xs);
-            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
-            h4[e] = h;
-            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
-        }
-        const int at = ((st * 2 + kh) * 32 + tl) * 8 + half * 4;
-        *reinterpret_cast<half4 *>(hi + at) = h4;
-        *reinterpret_cast<half4 *>(lo + at) = l4;
-    }
-    // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
-    const float s64 = sum * (1.f / 64.f);
-    const _Float16 sh = static_cast<_Float16>(s64);
-    _Float16 *mhi = reinterpret_cast<_Float16 *>(tile + 2 * kTileA);
-    _Float16 *mlo = reinterpret_cast<_Float16 *>(tile + 2 * kTileA + kTileM);
-    const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
-    mhi[mat] = sh;
-    mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
-    // Token scales in accumulator lane order: lane half (tl/4)%2, register 4*(tl/8) + tl%4.
-    if (q == 0) {
-        float *fr = reinterpret_cast<float *>(tile + 2 * kTileA + 2 * kTileM);
-        fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
     }
 }
 

@@ -248,6 +248,10 @@ struct SplitAttention {
     float *out;                      // [n_tokens][heads * head_dim]
     const qk_batch_token *desc;      // device, n_tokens entries; NULL: one token at pos, kv_row 0
     XGroup *rec_out;                 // the outputs' activation records too (head_dim % 16 == 0), or NULL
+    // The outputs as the matrix-core GEMM's records too ([tile][block][...],
+    // blocks of heads * head_dim / 256 per tile; needs G * head_dim % 256 ==
+    // 0 so each workgroup's heads fill whole blocks), or NULL.
+    uint8_t *gemm_rec;
     int64_t cache_rows;
     int64_t rows_hint;               // sum over tokens of pos + 1 (0: n_tokens * (max_pos + 1))
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
@@ -263,6 +267,9 @@ size_t split_attention_workspace_bytes(int n_tokens, int heads, int kv_heads, in
 // split_rows <= 0 takes the policy's value.  Arguments validated by the caller.
 int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
                            hipStream_t stream);
+// Whether a launch of a (split_rows <= 0, gemm_rec aside) can write the
+// matrix-core GEMM's records of its outputs (a.gemm_rec).
+bool attention_gemm_records(const SplitAttention &a);
 
 // Per-device properties, cached once per device (thread-safe).
 struct DeviceInfo {

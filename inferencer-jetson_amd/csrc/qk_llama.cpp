@@ -906,12 +906,14 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     attn.heads = c.heads;
     attn.kv_heads = c.kv_heads;
     attn.head_dim = hd;
-    // From 8 tokens on (matrix cores) the projections chain: o's reduction
-    // adds the residual and packs x * ffn_norm for gate/up (sums of squares
-    // for the deferred RMSNorm), gate/up's packs SiLU(gate) * up for down,
-    // down's adds the residual and packs x * the next attn_norm for the next
-    // QKV -- ten launches per layer instead of thirteen.
+    // From 8 tokens on (matrix cores) the projections chain: attention packs
+    // its outputs as o's records, o's reduction adds the residual and packs
+    // x * ffn_norm for gate/up (sums of squares for the deferred RMSNorm),
+    // gate/up's packs SiLU(gate) * up for down, down's adds the residual and
+    // packs x * the next attn_norm for the next QKV -- nine launches per
+    // layer (one more with split attention) instead of thirteen.
     const bool chain = qk::batched_chain_supported(T) && m->rec_a;
+    const bool attn_records = chain && qk::attention_gemm_records(attn);
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
@@ -930,6 +932,9 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
                                            m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
             return st;
         attn.layer = l;
+        // In the chain, attention packs the o projection's records itself
+        // (rec_b is free: down read it in the previous layer).
+        attn.gemm_rec = chain && attn_records ? m->rec_b : nullptr;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
@@ -942,6 +947,7 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
             continue;
         }
         qk::GemvFusion o_f = residual, gu_f, down_f;
+        if (attn_records) o_f.in_records = m->rec_b;
         o_f.out_records = m->rec_a;
         o_f.out_gain = L.ffn_norm;
         o_f.out_ss = m->ss;

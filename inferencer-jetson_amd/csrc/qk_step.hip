@@ -6,6 +6,7 @@
 // reference's hard-coded head_dim 128 / 64 RoPE frequencies to any even
 // head_dim, and written for wave64.
 #include "qk_internal.h"
+#include "qk_records.h"
 
 #include <algorithm>
 #include <cmath>
@@ -325,6 +326,78 @@ __device__ __forceinline__ void absorb_rows(const float (&s)[NU][G], const float
     }
 }
 
+// Token b's attention outputs of this workgroup's heads (G * hd values at
+// `of`, head g's at of + g * stride) as GEMM records, one 256-column block
+// at a time by the first wave: lane (q, j) = (lane / 8, lane % 8) stages
+// columns q*32 + 4j .. +3 in the record layout of stage_store (the same
+// power-of-two block scale, fp16 high / low halves and sub-block sums).
+template <int G>
+__device__ __forceinline__ void write_gemm_records(const SplitAttention &a, int b, int kvh, const float *of,
+                                                   int stride) {
+    const int hd = a.head_dim, blocks = G * hd / 256;
+    const int lane = threadIdx.x;
+    if (lane >= 64) return;
+    const int q = lane >> 3, j = lane & 7, tl = b % kTokTile;
+    const int nb = a.heads * hd / 256;
+    for (int blk = 0; blk < blocks; ++blk) {
+        float v[4];
+        const int c0 = blk * 256 + q * 32 + 4 * j;   // column within this workgroup's heads
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = c0 + i, g = c / hd;
+            v[i] = of[g * stride + (c - g * hd)];
+        }
+        float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+        int bad = isfinite(v[0]) && isfinite(v[1]) && isfinite(v[2]) && isfinite(v[3]) ? 0 : 1;
+        #pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            m = fmaxf(m, __shfl_xor(m, off));
+            bad |= __shfl_xor(bad, off);
+        }
+        int shift = 0;
+        float f = 0.f;
+        if (m > 0.f && isfinite(m)) {
+            shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
+            f = ldexpf(1.f, -shift);
+        }
+        if (bad) f = __builtin_nanf("");
+        uint8_t *tile = a.gemm_rec + (static_cast<size_t>(b / kTokTile) * nb + kvh * blocks + blk) * kTileBytes;
+        _Float16 *hi = reinterpret_cast<_Float16 *>(tile);
+        _Float16 *lo = reinterpret_cast<_Float16 *>(tile + kTileA);
+        const int Gq = q >> 1, half = q & 1, kh = Gq >> 1, hf = Gq & 1, st = hf * 8 + j;
+        half4 h4, l4;
+        float sum = 0.f;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float xs = bad ? 0.f : ldexpf(v[i], shift);
+            sum += xs;
+            const _Float16 h = static_cast<_Float16>(xs);
+            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
+            h4[e] = h;
+            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
+        }
+        const int at = ((st * 2 + kh) * 32 + tl) * 8 + half * 4;
+        *reinterpret_cast<half4 *>(hi + at) = h4;
+        *reinterpret_cast<half4 *>(lo + at) = l4;
+        #pragma unroll
+        for (int off = 1; off < 8; off <<= 1) sum += __shfl_xor(sum, off);
+        if (j == 0) {
+            // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
+            const float s64 = sum * (1.f / 64.f);
+            const _Float16 sh = static_cast<_Float16>(s64);
+            _Float16 *mhi = reinterpret_cast<_Float16 *>(tile + 2 * kTileA);
+            _Float16 *mlo = reinterpret_cast<_Float16 *>(tile + 2 * kTileA + kTileM);
+            const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
+            mhi[mat] = sh;
+            mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
+        }
+        if (lane == 0) {
+            float *fr = reinterpret_cast<float *>(tile + 2 * kTileA + 2 * kTileM);
+            fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
+        }
+    }
+}
+
 // Merge of two (max, sum) states: the scale factors of each side.
 __device__ __forceinline__ void merge_scales(float &m, float &l, float mo, float lo, float &f, float &fo) {
     const float mn = fmaxf(m, mo);
@@ -541,7 +614,7 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
         if (nsplit == 1) {
             const float4 r = scale4(x, 1.0f / lw);
             *reinterpret_cast<float4 *>(o + g * hd + 4 * e) = r;
-            if (a.rec_out) qs[g * HD / 4 + e] = r;   // the query rows are in registers by now
+            if (a.rec_out || a.gemm_rec) qs[g * HD / 4 + e] = r;   // the query rows are in registers by now
         } else {
             if (e == 0) {
                 mine[g] = mw;
@@ -549,6 +622,11 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
             }
             *reinterpret_cast<float4 *>(mine + kHdr + g * hd + 4 * e) = x;
         }
+    }
+    if (nsplit == 1 && a.gemm_rec) {
+        // The o projection's matrix-core records of this token's G heads.
+        __syncthreads();
+        write_gemm_records<G>(a, b, kvh, reinterpret_cast<const float *>(qs), HD);
     }
     if (nsplit == 1 && a.rec_out) {
         // The o projection's activation records of this token's G heads.
@@ -594,7 +672,11 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
             num = fmaf(w, all[p * pstride + kHdr + i], num);
         }
         o[i] = num / den;
-        if (a.rec_out) mo[i] = num / den;
+        if (a.rec_out || a.gemm_rec) mo[i] = num / den;
+    }
+    if (a.gemm_rec) {
+        __syncthreads();
+        write_gemm_records<G>(a, b, kvh, mo, hd);
     }
     if (a.rec_out) {
         __syncthreads();
@@ -785,6 +867,19 @@ size_t split_attention_workspace_bytes(int n_tokens, int heads, int kv_heads, in
     return std::min<size_t>(kMaxSplitWorkspace, static_cast<size_t>(n_tokens) * kv_heads * splits * part);
 }
 
+// Whether the policy runs a's tokens in the wide form (one workgroup per
+// query head, one split).
+bool wide_attention(const SplitAttention &a) {
+    return static_cast<int64_t>(a.n_tokens) * a.heads <= kWideMaxPairs &&
+           int64_t(2) * (a.max_pos + 1) * a.head_dim * static_cast<int64_t>(sizeof(float)) <= kWideMaxBytes &&
+           split_instance(1, a.head_dim, true) != nullptr;
+}
+
+bool attention_gemm_records(const SplitAttention &a) {
+    const int G = a.heads / a.kv_heads;
+    return !wide_attention(a) && G * a.head_dim % 256 == 0 && a.head_dim <= 256 && a.heads * a.head_dim % 256 == 0;
+}
+
 int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
                            hipStream_t stream) {
     const int G = a.heads / a.kv_heads;
@@ -800,9 +895,7 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     // Each wide workgroup serves one query head (its KV head's rows are read
     // by G workgroups, mostly from cache), so the softmax arithmetic spreads
     // over heads CUs instead of kv_heads.
-    const bool wide = split_rows <= 0 && static_cast<int64_t>(a.n_tokens) * a.heads <= kWideMaxPairs &&
-                      int64_t(2) * max_rows * a.head_dim * static_cast<int64_t>(sizeof(float)) <= kWideMaxBytes &&
-                      split_instance(1, a.head_dim, true) != nullptr;
+    const bool wide = split_rows <= 0 && wide_attention(a);
     int head_split = 1, Gk = G;
     if (wide) {
         head_split = G;
@@ -810,6 +903,10 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
         fn = split_instance(1, a.head_dim, true);
         split_rows = max_rows;
     }
+    // GEMM records: each workgroup's heads must fill whole 256-column blocks
+    // (never so in the one-head-per-workgroup form).
+    if (a.gemm_rec && (Gk * a.head_dim % 256 || a.head_dim > 256))
+        return fail(QK_ERR_LIMIT, "split attention: GEMM records need whole 256-column blocks per workgroup");
     const int groups = a.kv_heads * head_split;   // workgroups per token and split
     if (split_rows <= 0) {
         const int64_t rows = a.rows_hint > 0 ? a.rows_hint : static_cast<int64_t>(a.n_tokens) * max_rows;
