@@ -378,7 +378,11 @@ int qk_llama_destroy(qk_llama *m);
    the residual adds in the o / down GEMVs' epilogues -- and the other types
    stay FP32.  Takes effect at the next qk_llama_forward. */
 int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8);
-/* Device pointers to the fp32 caches, [layer][context][kv_dim]. */
+/* Device pointers to the fp32 caches, [layer][kv_heads][context][head_dim]:
+   the drivers keep each KV head's rows contiguous, so the attention
+   workgroup of a (token, KV head) streams one run of memory (the reference's
+   FastGPU caches are [layer][context][kv_dim]; the Python load_kv and
+   cache-row helpers convert). */
 int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
 /* Device pointer to the fp32 logits of the last step with need_logits. */
 int qk_llama_logits(qk_llama *m, const float **logits);
@@ -397,7 +401,8 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
 /* A step for a ragged batch of up to max_tokens tokens -- decode tokens of
    different sequences, prefill chunks of consecutive positions of one
    sequence, or any mix (a continuous batch) -- with packed KV caches of
-   cache_rows rows per layer ([layer][cache_rows][kv_dim], fp32).  The
+   cache_rows rows per layer ([layer][kv_heads][cache_rows][head_dim], fp32,
+   as qk_llama_kv_cache).  The
    multi-sequence counterpart of FastRunner::prefill's batched path
    (inferencer.cu:1279-1423), which serves one sequence; every projection
    runs through qk_gemv_multi_batched_f32 / qk_gemv_batched_f32 (matrix cores
@@ -411,7 +416,7 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
 int qk_llama_batch_destroy(qk_llama_batch *m);
 /* The handle's device bytes, as qk_llama_memory_bytes. */
 int qk_llama_batch_memory_bytes(const qk_llama_batch *m, qk_llama_memory *out);
-/* Device pointers to the fp32 caches, [layer][cache_rows][kv_dim]. */
+/* Device pointers to the fp32 caches, [layer][kv_heads][cache_rows][head_dim]. */
 int qk_llama_batch_kv_cache(qk_llama_batch *m, float **key_cache, float **value_cache);
 /* Device pointer to the fp32 logits of the last step with need_logits,
    [n_tokens][vocab]. */

@@ -636,12 +636,14 @@ class BatchRunner:
         return copy_to_host(p.value, n_tokens * self.cfg["dim"], np.float32).reshape(n_tokens, self.cfg["dim"])
 
     def load_kv(self, key_cache, value_cache) -> None:
-        """Copy fp32 caches laid out [layer][cache_rows][kv_dim]."""
-        c = self.cfg
-        n = c["layers"] * self.cache_rows * (c["dim"] // c["heads"] * c["kv_heads"])
-        k, v = self.kv_cache()
-        copy_to_device(k, _cache_array(key_cache, n), n * 4)
-        copy_to_device(v, _cache_array(value_cache, n), n * 4)
+        """Copy fp32 caches laid out [layer][cache_rows][kv_dim] (the
+        reference's layout) into the driver's head-major caches."""
+        _load_kv(self.kv_cache(), self.cfg, self.cache_rows, key_cache, value_cache)
+
+    def kv_rows(self, n: int):
+        """Rows 0..n-1 of every layer of both caches, as host arrays
+        [layer][n][kv_dim] (the reference's layout)."""
+        return _kv_rows(self.kv_cache(), self.cfg, self.cache_rows, n)
 
 
 _HIP = None
@@ -658,6 +660,54 @@ def _hip() -> ctypes.CDLL:
         h.hipDeviceSynchronize.restype = _i
         _HIP = h
     return _HIP
+
+
+def _kv_shape(cfg) -> tuple[int, int, int]:
+    """(layers, kv_heads, head_dim) of a model config."""
+    return cfg["layers"], cfg["kv_heads"], cfg["dim"] // cfg["heads"]
+
+
+def _load_kv(ptrs, cfg, rows: int, key_cache, value_cache) -> None:
+    """Host caches [layer][rows][kv_heads * head_dim] into a driver's
+    [layer][kv_heads][rows][head_dim] device caches."""
+    import numpy as np
+    layers, kvh, hd = _kv_shape(cfg)
+    n = layers * rows * kvh * hd
+    for dst, a in zip(ptrs, (key_cache, value_cache)):
+        a = _cache_array(a, n).reshape(layers, rows, kvh, hd)
+        copy_to_device(dst, np.ascontiguousarray(a.transpose(0, 2, 1, 3)), n * 4)
+
+
+def _kv_rows(ptrs, cfg, rows: int, n: int):
+    """Rows 0..n-1 of a driver's head-major caches as two host arrays
+    [layer][n][kv_heads * head_dim]."""
+    import numpy as np
+    layers, kvh, hd = _kv_shape(cfg)
+    if not 0 <= n <= rows:
+        raise QKError("kv_rows", QK_ERR_INVALID_ARG, f"{n} rows of a {rows}-row cache")
+    out = []
+    for src in ptrs:
+        a = np.empty((layers, n, kvh * hd), dtype=np.float32)
+        for layer in range(layers):
+            for h in range(kvh):
+                off = (layer * kvh + h) * rows * hd * 4
+                a[layer, :, h * hd:(h + 1) * hd] = copy_to_host(src + off, n * hd, np.float32).reshape(n, hd)
+        out.append(a)
+    return out[0], out[1]
+
+
+def copy_kv_rows(dst, src, n: int) -> None:
+    """Rows 0..n-1 of every layer and KV head of src's caches into dst's (a
+    Runner or BatchRunner each; same model), device to device."""
+    layers, kvh, hd = _kv_shape(dst.cfg)
+    rows_of = lambda r: r.cache_rows if hasattr(r, "cache_rows") else r.cfg["context"]
+    dr, sr = rows_of(dst), rows_of(src)
+    if not 0 <= n <= min(dr, sr):
+        raise QKError("copy_kv_rows", QK_ERR_INVALID_ARG, f"{n} rows between caches of {sr} and {dr} rows")
+    for d, s_ in zip(dst.kv_cache(), src.kv_cache()):
+        for layer in range(layers):
+            for h in range(kvh):
+                copy_device(d + (layer * kvh + h) * dr * hd * 4, s_ + (layer * kvh + h) * sr * hd * 4, n * hd * 4)
 
 
 def _cache_array(a, count: int):
@@ -701,12 +751,14 @@ def copy_device(dst: int, src: int, nbytes: int) -> None:
 
 
 def _runner_load_kv(self, key_cache, value_cache) -> None:
-    """Copy fp32 caches laid out [layer][context][kv_dim] into the runner."""
-    c = self.cfg
-    n = c["layers"] * c["context"] * (c["dim"] // c["heads"] * c["kv_heads"])
-    k, v = self.kv_cache()
-    copy_to_device(k, _cache_array(key_cache, n), n * 4)
-    copy_to_device(v, _cache_array(value_cache, n), n * 4)
+    """Copy fp32 caches laid out [layer][context][kv_dim] (the reference's
+    layout) into the runner's head-major caches."""
+    _load_kv(self.kv_cache(), self.cfg, self.cfg["context"], key_cache, value_cache)
+
+
+def _runner_kv_rows(self, n: int):
+    """Rows 0..n-1 of every layer of both caches, host arrays [layer][n][kv_dim]."""
+    return _kv_rows(self.kv_cache(), self.cfg, self.cfg["context"], n)
 
 
 def _runner_logits(self):
@@ -715,4 +767,5 @@ def _runner_logits(self):
 
 
 Runner.load_kv = _runner_load_kv
+Runner.kv_rows = _runner_kv_rows
 Runner.logits = _runner_logits

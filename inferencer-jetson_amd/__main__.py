@@ -154,12 +154,7 @@ def _prefill_batched(qk, runner, batch, ids: list[int]) -> int:
             nxt = batch.forward(part, list(range(c0, c0 + m)), [0] * m, seq=[0] * m, logit_rows=[m - 1])[0]
         else:
             batch.forward(part, list(range(c0, c0 + m)), [0] * m, False, seq=[0] * m)
-    c = runner.cfg
-    row = c["dim"] // c["heads"] * c["kv_heads"] * 4
-    for dst, src, rows in ((runner.kv_cache()[0], batch.kv_cache()[0], batch.cache_rows),
-                           (runner.kv_cache()[1], batch.kv_cache()[1], batch.cache_rows)):
-        for layer in range(c["layers"]):
-            qk.copy_device(dst + layer * c["context"] * row, src + layer * rows * row, n * row)
+    qk.copy_kv_rows(runner, batch, n)
     return nxt
 
 

@@ -37,15 +37,6 @@ def _rms(a) -> float:
     return float(np.sqrt(np.mean(a * a))) if a.size else 0.0
 
 
-def _cache_rows(qk, ptr: int, rows_per_layer: int, layers: int, kv_dim: int, n: int):
-    """Rows 0..n-1 of every layer of a [layer][rows][kv_dim] fp32 cache."""
-    out = np.empty((layers, n, kv_dim), dtype=np.float32)
-    for layer in range(layers):
-        off = (layer * rows_per_layer) * kv_dim * 4
-        out[layer] = qk.copy_to_host(ptr + off, n * kv_dim, np.float32).reshape(n, kv_dim)
-    return out
-
-
 def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dict:
     """Run both prefills of input_ids and `steps` greedy steps each.
 
@@ -57,16 +48,13 @@ def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dic
     if n < 1 or steps < 1 or chunk < 1:
         raise ValueError("compare_prefill needs a prompt, steps >= 1 and chunk >= 1")
     c = runner.cfg
-    kv_dim = c["dim"] // c["heads"] * c["kv_heads"]
 
     # Baseline: one token per step (inferencer.cu:1731-1740).
     nxt = 0
     for i, t in enumerate(ids):
         nxt = runner.forward(t, i, i + 1 == n)
     base_res = runner.residual()
-    kp, vp = runner.kv_cache()
-    base_k = _cache_rows(qk, kp, c["context"], c["layers"], kv_dim, n)
-    base_v = _cache_rows(qk, vp, c["context"], c["layers"], kv_dim, n)
+    base_k, base_v = runner.kv_rows(n)
     base_ids, base_logits = [], []
     for i in range(steps):
         base_ids.append(nxt)
@@ -85,9 +73,7 @@ def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dic
         else:
             batch.forward(part, list(range(c0, c0 + m)), [0] * m, False, seq=[0] * m)
     bat_res = batch.residual(len(ids[(n - 1) // chunk * chunk:]))[-1]
-    kb, vb = batch.kv_cache()
-    bat_k = _cache_rows(qk, kb, batch.cache_rows, c["layers"], kv_dim, n)
-    bat_v = _cache_rows(qk, vb, batch.cache_rows, c["layers"], kv_dim, n)
+    bat_k, bat_v = batch.kv_rows(n)
     bat_ids, bat_logits = [], []
     for i in range(steps):
         bat_ids.append(nxt)

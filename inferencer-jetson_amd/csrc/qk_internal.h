@@ -255,7 +255,27 @@ struct SplitAttention {
     int64_t cache_rows;
     int64_t rows_hint;               // sum over tokens of pos + 1 (0: n_tokens * (max_pos + 1))
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
+    // Cache layout: 0 the reference's [layers][cache_rows][kv_heads][head_dim],
+    // 1 [layers][kv_heads][cache_rows][head_dim] (the decode drivers' own: a
+    // (token, KV head) workgroup then reads one contiguous run of memory
+    // instead of head_dim floats out of every kv_heads * head_dim).
+    int head_major;
 };
+// Offset in floats of row `row` of KV head `h` in layer `layer` of a cache of
+// either layout.
+__host__ __device__ __forceinline__ int64_t kv_offset(int head_major, int layer, int64_t cache_rows, int kv_heads,
+                                                      int head_dim, int64_t row, int h) {
+    return head_major ? ((static_cast<int64_t>(layer) * kv_heads + h) * cache_rows + row) * head_dim
+                      : (static_cast<int64_t>(layer) * cache_rows + row) * kv_heads * head_dim +
+                            static_cast<int64_t>(h) * head_dim;
+}
+// RoPE of q and k at each token's position, k and v written to row kv_row +
+// pos of the caches in either layout (qk_rope_kv_write_batched's kernel;
+// arguments validated by the caller).
+int launch_rope_kv_batched(float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                           float *key_cache, float *value_cache, int layer, int64_t cache_rows,
+                           const qk_batch_token *desc, int n_tokens, int context, int heads, int kv_heads,
+                           int head_dim, int head_major, hipStream_t stream);
 // Rows per split for head_rows (token, KV head) rows in all, the longest
 // token max_rows rows (the split policy).
 int split_attention_rows(int64_t head_rows, int max_rows);

@@ -202,6 +202,7 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     attn.cosine = m->cosine;
     attn.sine = m->sine;
     attn.key_cache = m->key_cache;
+    attn.head_major = 1;
     attn.value_cache = m->value_cache;
     attn.out = m->attn;
     attn.cache_rows = c.context;
@@ -282,6 +283,7 @@ int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, 
     attn.cosine = m->cosine;
     attn.sine = m->sine;
     attn.key_cache = m->key_cache;
+    attn.head_major = 1;
     attn.value_cache = m->value_cache;
     attn.out = m->attn;
     attn.rec_out = m->rec_attn;
@@ -551,6 +553,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         attn.cosine = m->cosine;
         attn.sine = m->sine;
         attn.key_cache = m->key_cache;
+    attn.head_major = 1;
         attn.value_cache = m->value_cache;
         attn.out = m->attn;
         attn.cache_rows = c.context;
@@ -896,6 +899,7 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     attn.cosine = m->cosine;
     attn.sine = m->sine;
     attn.key_cache = m->key_cache;
+    attn.head_major = 1;
     attn.value_cache = m->value_cache;
     attn.out = m->attn;
     attn.desc = m->d_desc;
@@ -928,8 +932,8 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         }
         if ((st = qk::launch_batched_fused(qkv, 3, m->x, dim, dim, T, qkv_in, ws, wsb, s))) return st;
         if (chained &&
-            (st = qk_rope_kv_write_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
-                                           m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, s)))
+            (st = qk::launch_rope_kv_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
+                                             m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, 1, s)))
             return st;
         attn.layer = l;
         // In the chain, attention packs the o projection's records itself

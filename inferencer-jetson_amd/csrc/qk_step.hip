@@ -199,7 +199,7 @@ __device__ __forceinline__ bool token_ok(const qk_batch_token &d, int64_t cache_
 __global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v, const float *cosine,
                                        const float *sine, float *key_cache, float *value_cache, int layer,
                                        int64_t cache_rows, const qk_batch_token *desc, int context, int q_pairs,
-                                       int kv_pairs, int half_head) {
+                                       int kv_pairs, int half_head, int head_major) {
     const int t = blockIdx.y;
     const int pair = blockIdx.x * blockDim.x + threadIdx.x;
     if (pair >= q_pairs) return;
@@ -216,7 +216,8 @@ __global__ void rope_kv_batched_kernel(float *q, const float *k, const float *v,
     if (pair < kv_pairs) {
         const int kv_dim = kv_pairs * 2;
         const float *kt = k + static_cast<int64_t>(t) * kv_dim, *vt = v + static_cast<int64_t>(t) * kv_dim;
-        const int64_t o = (static_cast<int64_t>(layer) * cache_rows + d.kv_row + d.pos) * kv_dim + i;
+        const int hd = 2 * half_head;
+        const int64_t o = kv_offset(head_major, layer, cache_rows, kv_dim / hd, hd, d.kv_row + d.pos, i / hd) + i % hd;
         const float k0 = kt[i], k1 = kt[i + 1];
         key_cache[o] = k0 * c - k1 * s;
         key_cache[o + 1] = k0 * s + k1 * c;
@@ -444,11 +445,12 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
     const int nsplit = (n + ka.split_rows - 1) / ka.split_rows;
     const bool fresh = a.k != nullptr && r1 == n;   // this split holds row pos and writes it
     const int rows = (fresh ? r1 - 1 : r1) - r0;    // rows read from the caches
-    const int64_t head0 = (static_cast<int64_t>(a.layer) * a.cache_rows + d.kv_row) * kv_dim + cache_kvh * hd;
-    const int64_t first = head0 + static_cast<int64_t>(r0) * kv_dim;
-    const int row_bytes = kv_dim * 4;
+    const int rs = a.head_major ? hd : kv_dim;   // floats from one row of the head to the next
+    const int64_t head0 = kv_offset(a.head_major, a.layer, a.cache_rows, a.kv_heads, hd, d.kv_row, cache_kvh);
+    const int64_t first = head0 + static_cast<int64_t>(r0) * rs;
+    const int row_bytes = rs * 4;
     const bool act = sub < hv;   // head_dim < 4L leaves lanes idle
-    const int lane_off = (rq * kv_dim + 4 * min(sub, hv - 1)) * 4;
+    const int lane_off = (rq * rs + 4 * min(sub, hv - 1)) * 4;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(a.key_cache + first, 0, rows * row_bytes, 0x00020000);
     const __amdgpu_buffer_rsrc_t vrs =
@@ -485,7 +487,7 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
             const float *kt = a.k + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
             const float *vt = a.v + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
             float *kn = reinterpret_cast<float *>(knew), *vn = reinterpret_cast<float *>(vnew);
-            const int64_t row = head0 + static_cast<int64_t>(d.pos) * kv_dim;
+            const int64_t row = head0 + static_cast<int64_t>(d.pos) * rs;
             for (int f = tid; f < half; f += kSplitThreads) {
                 const float c = cs[f], si = sn[f];
                 const float k0 = kt[2 * f], k1 = kt[2 * f + 1];
@@ -964,6 +966,17 @@ int launch_gather_rows(const float *src, int64_t ld, const int32_t *idx, int n, 
     return launch_status("row gather launch");
 }
 
+int launch_rope_kv_batched(float *q, const float *k, const float *v, const float *cosine, const float *sine,
+                           float *key_cache, float *value_cache, int layer, int64_t cache_rows,
+                           const qk_batch_token *desc, int n_tokens, int context, int heads, int kv_heads,
+                           int head_dim, int head_major, hipStream_t stream) {
+    const int q_pairs = heads * head_dim / 2, kv_pairs = kv_heads * head_dim / 2;
+    hipLaunchKernelGGL(rope_kv_batched_kernel, dim3((q_pairs + 255) / 256, n_tokens), dim3(256), 0, stream, q, k, v,
+                       cosine, sine, key_cache, value_cache, layer, cache_rows, desc, context, q_pairs, kv_pairs,
+                       head_dim / 2, head_major);
+    return launch_status("qk_rope_kv_write_batched launch");
+}
+
 }  // namespace qk
 
 extern "C" {
@@ -1060,11 +1073,8 @@ int qk_rope_kv_write_batched(float *q, const float *k, const float *v, const flo
         return qk::fail(QK_ERR_INVALID_ARG, "qk_rope_kv_write_batched: bad head layout or cache shape");
     if (n_tokens == 0) return qk::ok();
     if (n_tokens > 65535) return qk::fail(QK_ERR_LIMIT, "qk_rope_kv_write_batched: too many tokens in one launch");
-    const int q_pairs = heads * head_dim / 2, kv_pairs = kv_heads * head_dim / 2;
-    hipLaunchKernelGGL(qk::rope_kv_batched_kernel, dim3((q_pairs + 255) / 256, n_tokens), dim3(256), 0, qk::S(stream),
-                       q, k, v, cosine, sine, key_cache, value_cache, layer, cache_rows, desc, context, q_pairs,
-                       kv_pairs, head_dim / 2);
-    return qk::launch_status("qk_rope_kv_write_batched launch");
+    return qk::launch_rope_kv_batched(q, k, v, cosine, sine, key_cache, value_cache, layer, cache_rows, desc, n_tokens,
+                                      context, heads, kv_heads, head_dim, 0, qk::S(stream));
 }
 
 int qk_attention_batched_f32(const float *q, const float *key_cache, const float *value_cache, float *out, int layer,

@@ -250,3 +250,32 @@ def test_llama_1b_ragged_batch(qk, torch_gpu, oracle, workloads, synth):
     cfg = dict(workloads.LLAMA_1B, context=640)
     positions = [64, 599, 130, 257, 401, 88, 512, 333]
     run_batch_decode(qk, oracle, workloads, synth, cfg, seed=2, positions=positions, steps=2, logits_tol=1e-2)
+
+
+def test_driver_cache_layout_round_trip(qk, torch_gpu, workloads, synth):
+    """The drivers' caches are head-major ([layer][kv_heads][rows][head_dim]):
+    load_kv converts the reference's [layer][rows][kv_dim], kv_rows converts
+    back, and copy_kv_rows moves rows between a BatchRunner and a Runner."""
+    cfg = SMALL
+    W = workloads.llama_weights(cfg, 5)
+    layers, kvh, hd = cfg["layers"], cfg["kv_heads"], cfg["dim"] // cfg["heads"]
+    rows = 3 * cfg["context"]
+    k = synth.normal_f32(layers * rows * kvh * hd, 70, 1).reshape(layers, rows, kvh * hd)
+    v = synth.normal_f32(layers * rows * kvh * hd, 70, 2).reshape(layers, rows, kvh * hd)
+    br = qk.BatchRunner(cfg, W, max_tokens=2, cache_rows=rows)
+    br.load_kv(k, v)
+    kp, _ = br.kv_cache()
+    raw = qk.copy_to_host(kp, layers * rows * kvh * hd, np.float32).reshape(layers, kvh, rows, hd)
+    assert np.array_equal(raw, k.reshape(layers, rows, kvh, hd).transpose(0, 2, 1, 3))
+    gk, gv = br.kv_rows(rows)
+    assert np.array_equal(gk, k) and np.array_equal(gv, v)
+    gk, gv = br.kv_rows(17)
+    assert np.array_equal(gk, k[:, :17]) and np.array_equal(gv, v[:, :17])
+    r = qk.Runner(cfg, W)
+    qk.copy_kv_rows(r, br, 40)
+    rk, rv = r.kv_rows(40)
+    assert np.array_equal(rk, k[:, :40]) and np.array_equal(rv, v[:, :40])
+    with pytest.raises(qk.QKError):
+        qk.copy_kv_rows(r, br, cfg["context"] + 1)
+    r.close()
+    br.close()
