@@ -185,8 +185,6 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
     gate = torch.empty((ntok, hidden), device="cuda")
     up = torch.empty((ntok, hidden), device="cuda")
     y = torch.empty((ntok, dim), device="cuda")
-    ws_gu, n_gu = _workspace(torch, qk, dim, 2 * hidden, ntok)
-    ws_d, n_d = _workspace(torch, qk, hidden, dim, ntok)
     L = qk.lib()
     s = qk.stream_handle(stream)
 
@@ -220,22 +218,27 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
                 "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                 "weight_copies": copies, "calls_per_step": 6}
 
+    # One call (qk_ffn_batched_f32): x packed once, gate / up on the matrix
+    # cores with SiLU(gate) * up packed by their reduction straight into the
+    # down projection's input records, down and its reduction.
+    n_f = L.qk_ffn_batched_workspace_bytes(dim, hidden, ntok)
+    ws_f = torch.empty(n_f, dtype=torch.uint8, device="cuda")
+
     def step(i):
         wg, wu, wd = sets[i % copies]
-        arr = qk._matrices([(qk.Tensor((dim, hidden), qk.Q4_K, wg), gate), (qk.Tensor((dim, hidden), qk.Q4_K, wu), up)])
-        qk.check(L.qk_gemv_multi_batched_f32(arr, 2, x.data_ptr(), dim, dim, ntok, ws_gu.data_ptr(), n_gu, s), "gate/up")
-        qk.check(L.qk_silu_mul_f32(gate.data_ptr(), up.data_ptr(), ntok * hidden, s), "silu")
-        qk.check(L.qk_gemv_batched_f32(qk.Q6_K, wd.data_ptr(), gate.data_ptr(), hidden, y.data_ptr(), dim, hidden,
-                                       dim, ntok, ws_d.data_ptr(), n_d, s), "down")
+        qk.check(L.qk_ffn_batched_f32(qk.Q4_K, wg.data_ptr(), qk.Q4_K, wu.data_ptr(), qk.Q6_K, wd.data_ptr(),
+                                      x.data_ptr(), dim, y.data_ptr(), dim, dim, hidden, ntok, 0, ws_f.data_ptr(), n_f,
+                                      s), "ffn")
 
     wall, ms = time_launches(torch, step, steps, warmup, stream)
     weights = 2 * qk.tensor_bytes(qk.Q4_K, dim, hidden) + qk.tensor_bytes(qk.Q6_K, hidden, dim)
-    # x, gate/up outputs, down input (h), down output, fp32, once each.
-    act = 4 * ntok * (dim + 2 * hidden + hidden + dim)
+    # x in, the SiLU * up product (4 bytes a value as fp16 high / low
+    # records), y out.
+    act = 4 * ntok * (dim + hidden + dim)
     return {"tokens": ntok, "ms_per_step": round(ms, 4), "tokens_per_s": round(ntok / (ms * 1e-3), 1),
             "bytes_per_step": weights + act, "GBps": round((weights + act) / (ms * 1e-3) / 1e9, 1),
             "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "weight_copies": copies, "launches_per_step": 3}
+            "weight_copies": copies, "calls_per_step": 1, "launches_per_step": 5}
 
 
 def bench_mixed_1b_256(torch, qk, wl, stream, steps: int = 20, warmup: int = 3) -> dict:

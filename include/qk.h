@@ -125,6 +125,25 @@ int qk_gemv_multi_batched_f32(const qk_matrix *mats, int n_mats, const float *x,
                               int cols, int n_tokens, void *workspace, size_t workspace_bytes,
                               qk_stream stream);
 
+/* The feed-forward block of n_tokens tokens: y[t*ldy + r] (+)= (W_down
+   (SiLU(W_gate x_t) * (W_up x_t)))[r] -- gate and up are hidden x dim (cols
+   dim), down dim x hidden; `accumulate` adds into y (the residual; y may be
+   x).  Replaces the reference's batched FFN sequence gate_up_batch_cuda +
+   silu_cuda + the down projection (inferencer.cu:733-751, 1043-1056,
+   1362-1380) with FP32 semantics.  From 8 tokens on it runs as five
+   launches on the matrix cores: the gate / up reduction packs SiLU(gate) *
+   up straight into the down projection's input records, so neither gate,
+   up nor their product is stored as fp32; below 8 tokens, the fused GEMV
+   pair of qk_gemv_multi_f32 and a down GEMV staging SiLU * up.  workspace:
+   qk_ffn_batched_workspace_bytes(dim, hidden, n_tokens) bytes (256-byte
+   aligned; also enough for fewer tokens), not shared by calls in flight at
+   the same time.  dim and hidden multiples of 256.  No reference
+   counterpart as one call. */
+size_t qk_ffn_batched_workspace_bytes(int dim, int hidden, int n_tokens);
+int qk_ffn_batched_f32(int gate_type, const void *gate, int up_type, const void *up, int down_type, const void *down,
+                       const float *x, int ldx, float *y, int ldy, int dim, int hidden, int n_tokens, int accumulate,
+                       void *workspace, size_t workspace_bytes, qk_stream stream);
+
 /* ------------------------------------------------------------ dequant -- */
 
 /* out[r*cols + c] = W[row0 + r][c] as fp32, bit-exact with q4_value /

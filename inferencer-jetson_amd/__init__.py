@@ -126,6 +126,9 @@ SIGNATURES = {
     "qk_llama_forward": (_i, [_vp, _i, _i, _i, ctypes.POINTER(ctypes.c_int)]),
     "qk_rope_kv_write_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i,
                                       _vp]),
+    "qk_ffn_batched_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i]),
+    "qk_ffn_batched_f32": (_i, [_i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp, ctypes.c_size_t,
+                                _vp]),
     "qk_attention_batched_f32": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i, _vp]),
     "qk_attention_split_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i, _i, _i, _i]),
     "qk_attention_split_f32": (_i, [_vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i, _i, _vp,

@@ -688,24 +688,23 @@ __global__ __launch_bounds__(256) void reduce_splits(BatchParams p) {
 
 // One wave per (output block ob of 256 rows, token): as many workgroups as
 // output values / 256, so the latency-bound loads spread over the chip.
-// Lane (part, q) = (lane / 8, lane % 8) sums the split
+// Lane (q, part) = (lane / 8, lane % 8) sums the split
 // partials of rows ob*256 + q*32 + part*4 .. +3 in split order, every
 // split's load in flight before the first add (the kernel is latency-bound:
 // a loop over splits would wait one L2 round trip per split), applies the
 // deferred input norm and the residual add and stores y (not for a gate /
-// up pair).  The values meet in LDS, and lanes q = 0..7 pack the next
-// GEMM's input block -- x * gain with the block's sum of squares of x, or
-// SiLU(gate) * up -- into its record (the pack kernel's layout).
+// up pair).  Then every lane packs its four values of the next GEMM's input
+// block -- x * gain with the block's sum of squares of x, or SiLU(gate) * up
+// -- into the record (the pack kernel's layout, stage_store_wave).
 template <int RT>
 __global__ __launch_bounds__(64) void reduce_pack(BatchParams p) {
     constexpr int kGroupRows = group_rows(RT);
     constexpr int kPartialFloats = partial_floats(RT);
-    __shared__ float4 vals[8][8];   // [q][part]
     const int ob = blockIdx.x;
     const int tile = blockIdx.y / kTokTile;
     const int lane = threadIdx.x;
     const int tl = blockIdx.y % kTokTile;   // token within the tile
-    const int q = lane & 7, part = lane >> 3;
+    const int q = lane >> 3, part = lane & 7;
     const int t = tile * kTokTile + tl;
     const bool live = t < p.n_tokens;
     const int row_q = ob * 256 + q * 32, row = row_q + part * 4;
@@ -764,19 +763,10 @@ __global__ __launch_bounds__(64) void reduce_pack(BatchParams p) {
         for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
         if (live && lane == 0) p.out_ss[static_cast<int64_t>(t) * p.out_nb + ob] = ss;
     }
-    vals[q][part] = v;
-    __syncthreads();
-    if (part != 0) return;
-    XStage xs;
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const float4 u = vals[q][j];
-        xs.v[4 * j] = u.x;
-        xs.v[4 * j + 1] = u.y;
-        xs.v[4 * j + 2] = u.z;
-        xs.v[4 * j + 3] = u.w;
-    }
-    stage_store(xs, tl, q, p.out_records + (static_cast<size_t>(tile) * p.out_nb + ob) * kTileBytes);
+    // Lane (q, part) holds values q*32 + 4*part .. +3 of the output block:
+    // the whole wave stages the block's record.
+    const float vr[4] = {v.x, v.y, v.z, v.w};
+    stage_store_wave(vr, lane, tl, p.out_records + (static_cast<size_t>(tile) * p.out_nb + ob) * kTileBytes);
 }
 
 int check_batched(const char *where, const float *x, int ldx, int cols, int n_tokens) {
@@ -992,6 +982,25 @@ size_t batched_records_bytes(int cols, int n_tokens) {
 
 bool batched_chain_supported(int n_tokens) { return n_tokens >= kMfmaMinTokens; }
 
+// The FFN's workspace from kMfmaMinTokens tokens on: the GEMM workspace the
+// gate / up chain and the down call share (the larger of the two, over
+// every token-tile count up to n_tokens, since the split plan -- not the
+// token count alone -- fixes the partials' size), then the SiLU * up
+// records the chain leaves for down.
+size_t ffn_shared_bytes(int dim, int hidden, int n_tokens) {
+    size_t ws = 0;
+    for (int tq = 1; tq <= tile_count(n_tokens); ++tq) {
+        const int n = std::min(n_tokens, std::max(kMfmaMinTokens, tq * kTokTile));
+        ws = std::max({ws, workspace_bound(dim, 2 * hidden, n, true), workspace_bound(hidden, dim, n)});
+    }
+    return (ws + 255) / 256 * 256;
+}
+
+// Below kMfmaMinTokens: the gate and up outputs, each 256-byte aligned.
+size_t ffn_gemv_slot(int hidden, int n_tokens) {
+    return (static_cast<size_t>(n_tokens) * hidden * sizeof(float) + 255) / 256 * 256;
+}
+
 int launch_batched_fused(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,
                          const GemvFusion &f, void *workspace, size_t workspace_size, hipStream_t stream) {
     int ldy[QK_MAX_FUSED];
@@ -1045,6 +1054,63 @@ int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, cons
     // x is unused in INT8 mode; any 16-byte aligned pointer passes the packer's checks.
     return qk::launch_mfma(&m, 1, &ldy, reinterpret_cast<const float *>(xq), cols, cols, n_tokens, workspace,
                            workspace_bytes, s, "qk_gemv_batched_i8", nullptr, &in);
+}
+
+size_t qk_ffn_batched_workspace_bytes(int dim, int hidden, int n_tokens) {
+    if (dim <= 0 || hidden <= 0 || n_tokens <= 0 || dim % 256 || hidden % 256) return 0;
+    if (n_tokens < qk::kMfmaMinTokens) return 2 * qk::ffn_gemv_slot(hidden, n_tokens);
+    // Also enough for any smaller call: the GEMV form's gate and up outputs.
+    return std::max(qk::ffn_shared_bytes(dim, hidden, n_tokens) + (qk::records_bytes(hidden, n_tokens) + 255) / 256 * 256,
+                    2 * qk::ffn_gemv_slot(hidden, qk::kMfmaMinTokens - 1));
+}
+
+int qk_ffn_batched_f32(int gate_type, const void *gate, int up_type, const void *up, int down_type, const void *down,
+                       const float *x, int ldx, float *y, int ldy, int dim, int hidden, int n_tokens, int accumulate,
+                       void *workspace, size_t workspace_bytes, qk_stream stream) {
+    const char *where = "qk_ffn_batched_f32";
+    int st;
+    if ((st = qk::check_weights(where, gate_type, gate, dim, hidden)) ||
+        (st = qk::check_weights(where, up_type, up, dim, hidden)) ||
+        (st = qk::check_weights(where, down_type, down, hidden, dim)) ||
+        (st = qk::check_batched(where, x, ldx, dim, n_tokens)))
+        return st;
+    if (!y || ldy < dim) return qk::fail(QK_ERR_INVALID_ARG, "qk_ffn_batched_f32: null y or ldy smaller than dim");
+    if (!qk::aligned(y, 4)) return qk::fail(QK_ERR_ALIGN, "qk_ffn_batched_f32: y must be 4-byte aligned");
+    if (n_tokens == 0) return qk::ok();
+    const size_t need = qk_ffn_batched_workspace_bytes(dim, hidden, n_tokens);
+    if (!workspace || workspace_bytes < need)
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_ffn_batched_f32: workspace smaller than " + std::to_string(need) +
+                                                " bytes (qk_ffn_batched_workspace_bytes)");
+    if (!qk::aligned(workspace, 256)) return qk::fail(QK_ERR_ALIGN, "qk_ffn_batched_f32: workspace not 256-byte aligned");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    const qk_matrix dm{down_type, dim, down, y};
+    qk::GemvFusion df;
+    df.accumulate = accumulate != 0;
+    if (n_tokens < qk::kMfmaMinTokens) {
+        // Gate and up into the workspace, then down with SiLU(gate) * up
+        // staged in its own activation load.
+        if (!qk::gemv_fusable(hidden)) return qk::fail(QK_ERR_LIMIT, "qk_ffn_batched_f32: hidden too long to stage");
+        float *g = reinterpret_cast<float *>(ws);
+        float *u = reinterpret_cast<float *>(ws + qk::ffn_gemv_slot(hidden, n_tokens));
+        const qk_matrix gu[2] = {{gate_type, hidden, gate, g}, {up_type, hidden, up, u}};
+        const int ldg[2] = {hidden, hidden};
+        if ((st = qk::launch_gemv_f32(gu, 2, x, ldx, dim, n_tokens, ldg, s))) return st;
+        df.up = u;
+        return qk::launch_gemv_fused(&dm, 1, g, hidden, hidden, n_tokens, &ldy, df, s);
+    }
+    // Matrix cores: gate / up's reduction writes the records of SiLU(gate) *
+    // up (gate and up themselves are never stored), which down reads.
+    const size_t shared = qk::ffn_shared_bytes(dim, hidden, n_tokens);
+    uint8_t *rec = ws + shared;
+    const qk_matrix gu[2] = {{gate_type, hidden, gate, y}, {up_type, hidden, up, y}};
+    const int ldg[2] = {hidden, hidden};
+    qk::GemvFusion gf;
+    gf.pair = 1;
+    gf.out_records = rec;
+    if ((st = qk::launch_mfma(gu, 2, ldg, x, ldx, dim, n_tokens, ws, shared, s, where, &gf))) return st;
+    df.in_records = rec;
+    return qk::launch_mfma(&dm, 1, &ldy, x, ldx, hidden, n_tokens, ws, shared, s, where, &df);
 }
 
 int qk_gemv_multi_batched_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, int cols, int n_tokens,

@@ -338,7 +338,7 @@ __device__ __forceinline__ void write_gemm_records(const SplitAttention &a, int 
     const int hd = a.head_dim, blocks = G * hd / 256;
     const int lane = threadIdx.x;
     if (lane >= 64) return;
-    const int q = lane >> 3, j = lane & 7, tl = b % kTokTile;
+    const int q = lane >> 3, j = lane & 7;
     const int nb = a.heads * hd / 256;
     for (int blk = 0; blk < blocks; ++blk) {
         float v[4];
@@ -348,54 +348,8 @@ __device__ __forceinline__ void write_gemm_records(const SplitAttention &a, int 
             const int c = c0 + i, g = c / hd;
             v[i] = of[g * stride + (c - g * hd)];
         }
-        float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        int bad = isfinite(v[0]) && isfinite(v[1]) && isfinite(v[2]) && isfinite(v[3]) ? 0 : 1;
-        #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            m = fmaxf(m, __shfl_xor(m, off));
-            bad |= __shfl_xor(bad, off);
-        }
-        int shift = 0;
-        float f = 0.f;
-        if (m > 0.f && isfinite(m)) {
-            shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
-            f = ldexpf(1.f, -shift);
-        }
-        if (bad) f = __builtin_nanf("");
-        uint8_t *tile = a.gemm_rec + (static_cast<size_t>(b / kTokTile) * nb + kvh * blocks + blk) * kTileBytes;
-        _Float16 *hi = reinterpret_cast<_Float16 *>(tile);
-        _Float16 *lo = reinterpret_cast<_Float16 *>(tile + kTileA);
-        const int Gq = q >> 1, half = q & 1, kh = Gq >> 1, hf = Gq & 1, st = hf * 8 + j;
-        half4 h4, l4;
-        float sum = 0.f;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float xs = bad ? 0.f : ldexpf(v[i], shift);
-            sum += xs;
-            const _Float16 h = static_cast<_Float16>(xs);
-            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
-            h4[e] = h;
-            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
-        }
-        const int at = ((st * 2 + kh) * 32 + tl) * 8 + half * 4;
-        *reinterpret_cast<half4 *>(hi + at) = h4;
-        *reinterpret_cast<half4 *>(lo + at) = l4;
-        #pragma unroll
-        for (int off = 1; off < 8; off <<= 1) sum += __shfl_xor(sum, off);
-        if (j == 0) {
-            // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
-            const float s64 = sum * (1.f / 64.f);
-            const _Float16 sh = static_cast<_Float16>(s64);
-            _Float16 *mhi = reinterpret_cast<_Float16 *>(tile + 2 * kTileA);
-            _Float16 *mlo = reinterpret_cast<_Float16 *>(tile + 2 * kTileA + kTileM);
-            const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
-            mhi[mat] = sh;
-            mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
-        }
-        if (lane == 0) {
-            float *fr = reinterpret_cast<float *>(tile + 2 * kTileA + 2 * kTileM);
-            fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
-        }
+        stage_store_wave(v, lane, b % kTokTile,
+                         a.gemm_rec + (static_cast<size_t>(b / kTokTile) * nb + kvh * blocks + blk) * kTileBytes);
     }
 }
 

@@ -184,3 +184,64 @@ def test_mfma_needs_workspace(qk, torch_gpu, workloads):
         qk.batch_matvec(qk.Tensor((cols, rows), Q4_K, to_dev(t, w)), to_dev(t, x), y, cols, rows, ntok, ws,
                         records - 16)
     assert e.value.status == qk.QK_ERR_INVALID_ARG
+
+
+def run_ffn(qk, t, ws_, types, x, dim, hidden, y0=None, accumulate=False, alias=False):
+    """qk_ffn_batched_f32 over host weights; y starts as y0 (NaN if None);
+    alias: y is x itself (the residual add in place)."""
+    ntok = x.shape[0]
+    n = qk.lib().qk_ffn_batched_workspace_bytes(dim, hidden, ntok)
+    ws = t.empty(max(n, 256), dtype=t.uint8, device="cuda")
+    gd, ud, dd = (to_dev(t, w) for w in ws_)
+    xd = to_dev(t, x)
+    y = xd if alias else (to_dev(t, y0) if y0 is not None else t.full((ntok, dim), float("nan"), device="cuda"))
+    qk.check(qk.lib().qk_ffn_batched_f32(types[0], gd.data_ptr(), types[1], ud.data_ptr(), types[2], dd.data_ptr(),
+                                         xd.data_ptr(), dim, y.data_ptr(), dim, dim, hidden, ntok, int(accumulate),
+                                         ws.data_ptr(), n, None), "ffn")
+    t.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def ffn_f64(oracle, ws_, types, x, dim, hidden):
+    g = oracle.gemv_f64(types[0], ws_[0], x, dim, hidden)
+    u = oracle.gemv_f64(types[1], ws_[1], x, dim, hidden)
+    h = g / (1.0 + np.exp(-np.clip(g, -80, 80))) * u
+    return oracle.gemv_f64(types[2], ws_[2], h.astype(np.float32), hidden, dim)
+
+
+@pytest.mark.parametrize("ntok", [1, 5, 8, 32, 33, 100])
+def test_ffn_entry(qk, torch_gpu, oracle, workloads, ntok):
+    """The FFN in one call (chained SiLU * up records from 8 tokens on, the
+    GEMV pair below) against gate / up / SiLU / down in fp64."""
+    dim, hidden = 1024, 2048
+    types = (Q4_K, Q4_K, Q6_K)
+    gw, x = workloads.gemv_case(Q4_K, dim, hidden, seed=90 + ntok, n_tokens=max(ntok, 2))
+    x = x[:ntok]
+    uw, _ = workloads.gemv_case(Q4_K, dim, hidden, seed=91 + ntok)
+    dw, _ = workloads.gemv_case(Q6_K, hidden, dim, seed=92 + ntok)
+    y = run_ffn(qk, torch_gpu, (gw, uw, dw), types, x, dim, hidden)
+    want = ffn_f64(oracle, (gw, uw, dw), types, x, dim, hidden)
+    for k in range(ntok):
+        assert rel_l2(y[k], want[k]) < TOL, k
+
+
+@pytest.mark.parametrize("ntok", [4, 32])
+def test_ffn_entry_residual_and_types(qk, torch_gpu, oracle, workloads, synth, ntok):
+    """accumulate adds into y, in place over x too; Q6_K gate / up, a split
+    Q6_K down."""
+    t = torch_gpu
+    dim, hidden = 512, 1536
+    gw, x = workloads.gemv_case(Q6_K, dim, hidden, seed=95, n_tokens=ntok)
+    uw, _ = workloads.gemv_case(Q4_K, dim, hidden, seed=96)
+    dw, _ = workloads.gemv_case(Q6_K, hidden, dim, seed=97)
+    want = ffn_f64(oracle, (gw, uw, dw), (Q6_K, Q4_K, Q6_K), x, dim, hidden)
+    split = qk.split_q6k(qk.Tensor((hidden, dim), Q6_K, to_dev(t, dw)))
+    dws = split.data.cpu().numpy()
+    y0 = synth.normal_f32(ntok * dim, 98, 1).reshape(ntok, dim)
+    for types, dwk in (((Q6_K, Q4_K, Q6_K), dw), ((Q6_K, Q4_K, qk.Q6_K_SPLIT), dws)):
+        y = run_ffn(qk, t, (gw, uw, dwk), types, x, dim, hidden, y0=y0, accumulate=True)
+        for k in range(ntok):
+            assert rel_l2(y[k] - y0[k], want[k]) < TOL, (types, k)
+        y = run_ffn(qk, t, (gw, uw, dwk), types, x, dim, hidden, accumulate=True, alias=True)
+        for k in range(ntok):
+            assert rel_l2(y[k] - x[k], want[k]) < TOL, (types, k)
