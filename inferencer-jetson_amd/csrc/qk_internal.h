@@ -187,6 +187,48 @@ __device__ __forceinline__ XGroup make_group(const float *x16) {
     return make_group_regs(v);
 }
 
+// The records of four 16-value groups at once: lanes 16g .. 16g+15 of a
+// wave hold group g's values (x) and make its 64-byte record at dst (each
+// lane passes its own group's; nothing is stored where store is false) --
+// make_group_regs' arithmetic, with the group's sum taken as a tree.  Every
+// lane of the wave must call it.
+__device__ __forceinline__ void record16_quads(float x, int lane, XGroup *dst, bool store) {
+    float m = fabsf(x), sum = x;
+    #pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+        m = fmaxf(m, __shfl_xor(m, off));
+        sum += __shfl_xor(sum, off);
+    }
+    const bool ok = m > 0.f && isfinite(m);
+    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
+    const int X = ok ? static_cast<int>(rintf(ldexpf(x, 21 - e))) : 0;
+    const int b0 = (X << 24) >> 24;
+    const int X1 = (X - b0) >> 8;
+    const int b1 = (X1 << 24) >> 24;
+    const int b2 = (X1 - b1) >> 8;
+    const int sh = 8 * (lane & 3);
+    uint32_t u0 = (static_cast<uint32_t>(b0) & 0xFFu) << sh;
+    uint32_t u1 = (static_cast<uint32_t>(b1) & 0xFFu) << sh;
+    uint32_t u2 = (static_cast<uint32_t>(b2) & 0xFFu) << sh;
+    #pragma unroll
+    for (int off = 1; off < 4; off <<= 1) {
+        u0 |= __shfl_xor(u0, off);
+        u1 |= __shfl_xor(u1, off);
+        u2 |= __shfl_xor(u2, off);
+    }
+    // Dword k of limb set j sits in lanes base + 4k .. +3 of u_j.
+    const int base = lane & 48, k = lane & 3, li = lane & 15;
+    const uint32_t d0 = __shfl(u0, base + 4 * k), d1 = __shfl(u1, base + 4 * k), d2 = __shfl(u2, base + 4 * k);
+    const float scale = ok ? ldexpf(1.f, e - 21) : (m == 0.f ? 0.f : __builtin_nanf(""));
+    uint32_t word = 0;   // the two pad words stay zero
+    if (li < 4) word = d0;
+    else if (li < 8) word = d1;
+    else if (li < 12) word = d2;
+    else if (li == 12) word = __builtin_bit_cast(uint32_t, scale);
+    else if (li == 13) word = __builtin_bit_cast(uint32_t, sum);
+    if (store) reinterpret_cast<uint32_t *>(dst)[li] = word;
+}
+
 __device__ __forceinline__ XGroup make_group_regs(const float *v) {
     float m = 0.f, s = 0.f;
     #pragma unroll

@@ -587,14 +587,14 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
     if (nsplit == 1 && a.rec_out) {
         // The o projection's activation records of this token's G heads.
         __syncthreads();
+        // Four groups per wave, 16 lanes each.
         const float *of = reinterpret_cast<const float *>(qs);
         XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
-        for (int i = tid; i < G * hd / 16; i += kSplitThreads) {
-            const int g = i / (hd / 16), c = (i - g * (hd / 16)) * 16;
-            float v[16];
-            #pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = of[g * HD + c + k];
-            rec[i] = make_group_regs(v);
+        const int groups = G * hd / 16;
+        for (int g0 = wave * 4; g0 < groups; g0 += kSplitWaves * 4) {
+            const int gi = g0 + (lane >> 4), live = gi < groups;
+            const int g = gi / (hd / 16), c = (gi - g * (hd / 16)) * 16;
+            record16_quads(live ? of[g * HD + c + (lane & 15)] : 0.f, lane, rec + gi, live);
         }
     }
 }
@@ -637,7 +637,11 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
     if (a.rec_out) {
         __syncthreads();
         XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
-        for (int i = threadIdx.x; i < G * hd / 16; i += 256) rec[i] = make_group_regs(mo + 16 * i);
+        const int groups = G * hd / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        for (int g0 = wave * 4; g0 < groups; g0 += 16) {   // four waves, four groups each
+            const int gi = g0 + (lane >> 4), live = gi < groups;
+            record16_quads(live ? mo[16 * gi + (lane & 15)] : 0.f, lane, rec + gi, live);
+        }
     }
 }
 
