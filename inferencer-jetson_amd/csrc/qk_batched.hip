@@ -120,22 +120,20 @@ struct BatchParams {
 
 // ---------------------------------------------------- activation staging --
 //
-// Thread (tl = tid/8, q = tid%8) owns token tl of the tile and the 32
-// columns q*32 .. q*32+31 (Q4_K sub-block q) of the block.
+// One wave per (token, 256-column block): lane (q, j) = (lane / 8, lane % 8)
+// stages columns q*32 + 4j .. +3 of the block (stage_store_wave's layout).
 
 // The token's RMSNorm scale 1/sqrt(mean(x^2) + eps) over all cols
-// (rmsnorm_cuda's arithmetic, inferencer.cu:821-834), from the 32 lanes
-// r = 0..31 of the token: each reads every 32nd float4 of the row, all in
-// flight at once (the kernel is latency-bound), and the lanes meet in five
-// xor shuffles.
-__device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int tile, int tl, int r) {
-    const int t = tile * kTokTile + tl;
+// (rmsnorm_cuda's arithmetic, inferencer.cu:821-834): each lane reads every
+// 64th float4 of the row, all in flight at once (the kernel is
+// latency-bound), and the lanes meet in six xor shuffles.
+__device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int t, int lane) {
     const int cols = p.nb * 256;
     float ss = 0.f;
     if (t < p.n_tokens) {
         const float4 *row = reinterpret_cast<const float4 *>(p.x + static_cast<int64_t>(t) * p.ldx);
         #pragma unroll 8
-        for (int i = r; i < cols / 4; i += 32) {
+        for (int i = lane; i < cols / 4; i += 64) {
             const float4 v = row[i];
             ss = fmaf(v.x, v.x, ss);
             ss = fmaf(v.y, v.y, ss);
@@ -144,84 +142,60 @@ __device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int tile
         }
     }
     #pragma unroll
-    for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off);
+    for (int off = 1; off < 64; off <<= 1) ss += __shfl_xor(ss, off);
     return 1.0f / sqrtf(ss / static_cast<float>(cols) + p.norm_eps);
 }
 
-// With norm_w, x times the token's RMSNorm scale times the gain; with up,
-// x / (1 + exp(-x)) * up (silu_cuda, inferencer.cu:1053-1056).
-__device__ __forceinline__ void stage_load(const BatchParams &p, int tile, int b, int tl, int q, float scale,
-                                           XStage &s) {
-    const int t = tile * kTokTile + tl;
-    if (p.xq && t < p.n_tokens) {
-        // INT8 mode: the 32 codes of quantization group b*8 + q times its
-        // scale (exact products of an int8 and the fp32 scale, rounded once).
-        const int8_t *src = p.xq + static_cast<int64_t>(t) * p.ldxq + b * 256 + q * 32;
-        const float xs = p.xscale[static_cast<int64_t>(t) * p.ldscale + b * 8 + q];
+// The lane's four values of column c = b*256 + q*32 + 4j: x (times the
+// token's RMSNorm scale and the gain with norm_w; x / (1 + exp(-x)) * up
+// with up, silu_cuda, inferencer.cu:1053-1056), or in INT8 mode the codes
+// times their per-32 scale (exact products, rounded once); zero past the
+// last token.
+__device__ __forceinline__ void stage_load4(const BatchParams &p, int t, int c, float scale, float (&v)[4]) {
+    v[0] = v[1] = v[2] = v[3] = 0.f;
+    if (t >= p.n_tokens) return;
+    if (p.xq) {
+        const uint32_t w = *reinterpret_cast<const uint32_t *>(p.xq + static_cast<int64_t>(t) * p.ldxq + c);
+        const float xs = p.xscale[static_cast<int64_t>(t) * p.ldscale + c / 32];
         #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint4 w = *reinterpret_cast<const uint4 *>(src + 16 * i);
-            const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-            #pragma unroll
-            for (int k = 0; k < 16; ++k)
-                s.v[16 * i + k] = static_cast<float>(static_cast<int8_t>((wd[k >> 2] >> (8 * (k & 3))) & 0xFFu)) * xs;
-        }
-    } else if (t < p.n_tokens) {
-        const int64_t at = static_cast<int64_t>(t) * p.ldx + b * 256 + q * 32;
-        const float4 *src = reinterpret_cast<const float4 *>(p.x + at);
+        for (int k = 0; k < 4; ++k) v[k] = static_cast<float>(static_cast<int8_t>((w >> (8 * k)) & 0xFFu)) * xs;
+        return;
+    }
+    const int64_t at = static_cast<int64_t>(t) * p.ldx + c;
+    const float4 u = *reinterpret_cast<const float4 *>(p.x + at);
+    v[0] = u.x;
+    v[1] = u.y;
+    v[2] = u.z;
+    v[3] = u.w;
+    if (p.norm_w) {
+        const float4 w = *reinterpret_cast<const float4 *>(p.norm_w + c);
+        v[0] = v[0] * scale * w.x;
+        v[1] = v[1] * scale * w.y;
+        v[2] = v[2] * scale * w.z;
+        v[3] = v[3] * scale * w.w;
+    }
+    if (p.up) {
+        const float4 w = *reinterpret_cast<const float4 *>(p.up + at);
+        const float up4[4] = {w.x, w.y, w.z, w.w};
         #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float4 u = src[i];
-            s.v[4 * i] = u.x;
-            s.v[4 * i + 1] = u.y;
-            s.v[4 * i + 2] = u.z;
-            s.v[4 * i + 3] = u.w;
-        }
-        if (p.norm_w) {
-            const float4 *w4 = reinterpret_cast<const float4 *>(p.norm_w + b * 256 + q * 32);
-            #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 w = w4[i];
-                s.v[4 * i] = s.v[4 * i] * scale * w.x;
-                s.v[4 * i + 1] = s.v[4 * i + 1] * scale * w.y;
-                s.v[4 * i + 2] = s.v[4 * i + 2] * scale * w.z;
-                s.v[4 * i + 3] = s.v[4 * i + 3] * scale * w.w;
-            }
-        }
-        if (p.up) {
-            const float4 *u4 = reinterpret_cast<const float4 *>(p.up + at);
-            #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float4 u = u4[i];
-                const float g0 = s.v[4 * i], g1 = s.v[4 * i + 1], g2 = s.v[4 * i + 2], g3 = s.v[4 * i + 3];
-                s.v[4 * i] = g0 / (1.f + expf(-g0)) * u.x;
-                s.v[4 * i + 1] = g1 / (1.f + expf(-g1)) * u.y;
-                s.v[4 * i + 2] = g2 / (1.f + expf(-g2)) * u.z;
-                s.v[4 * i + 3] = g3 / (1.f + expf(-g3)) * u.w;
-            }
-        }
-    } else {
-        #pragma unroll
-        for (int i = 0; i < 32; ++i) s.v[i] = 0.f;
+        for (int k = 0; k < 4; ++k) v[k] = v[k] / (1.f + expf(-v[k])) * up4[k];
     }
 }
 
-// One 256-thread workgroup per (block, eight tokens of a 32-token tile): the
-// tokens' activations of the block, packed into the workspace record the
-// GEMM copies into LDS.  32 lanes per token (r = 0..31) share the RMSNorm
-// sum of squares; lanes r < 8 then stage sub-block q = r and meet in
-// shuffles within their eight.
-constexpr int kPackTokens = 8;
+// One 256-thread workgroup per (block, four tokens of a 32-token tile), a
+// wave per token: the tokens' activations of the block, packed into the
+// workspace record the GEMM copies into LDS.
+constexpr int kPackTokens = 4;
 __global__ __launch_bounds__(256) void pack_activations(BatchParams p, uint8_t *__restrict__ records) {
     const int b = blockIdx.x;
     const int tile = blockIdx.y / (kTokTile / kPackTokens);
-    const int tl = (blockIdx.y % (kTokTile / kPackTokens)) * kPackTokens + (threadIdx.x >> 5);
-    const int r = threadIdx.x & 31;
-    const float scale = p.norm_w ? stage_norm_scale(p, tile, tl, r) : 1.f;
-    if (r >= 8) return;
-    XStage xs;
-    stage_load(p, tile, b, tl, r, scale, xs);
-    stage_store(xs, tl, r, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
+    const int tl = (blockIdx.y % (kTokTile / kPackTokens)) * kPackTokens + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int t = tile * kTokTile + tl;
+    const float scale = p.norm_w ? stage_norm_scale(p, t, lane) : 1.f;
+    float v[4];
+    stage_load4(p, t, b * 256 + (lane >> 3) * 32 + 4 * (lane & 7), scale, v);
+    stage_store_wave(v, lane, tl, records + (static_cast<size_t>(tile) * p.nb + b) * kTileBytes);
 }
 
 // ------------------------------------------------------- weight operands --

@@ -26,78 +26,12 @@ constexpr int kTileF = 128;
 constexpr int kTileBytes = 2 * kTileA + 2 * kTileM + kTileF;
 static_assert(kTileBytes % 16 == 0, "tiles keep 16-byte alignment");
 
-// 32 activations of one token: sub-block q (columns q*32 .. q*32+31) of a
-// block.
-struct XStage {
-    float v[32];
-};
-
-// x' = x * 2^shift with the block maximum of the token in [2^14, 2^15)
-// (shift capped at 140 so 2^-shift stays a nonzero fp32), split into fp16
-// hi + lo; a non-finite activation makes the token's scale NaN.
-__device__ __forceinline__ void stage_store(const XStage &s, int tl, int q, uint8_t *tile) {
-    float m = 0.f;
-    bool bad = false;
-    #pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        m = fmaxf(m, fabsf(s.v[i]));
-        bad |= !isfinite(s.v[i]);
-    }
-    m = fmaxf(m, __shfl_xor(m, 1));
-    m = fmaxf(m, __shfl_xor(m, 2));
-    m = fmaxf(m, __shfl_xor(m, 4));
-    int nb_bad = bad ? 1 : 0;
-    nb_bad |= __shfl_xor(nb_bad, 1);
-    nb_bad |= __shfl_xor(nb_bad, 2);
-    nb_bad |= __shfl_xor(nb_bad, 4);
-    int shift = 0;
-    float f = 0.f;
-    if (m > 0.f && isfinite(m)) {
-        shift = min(15 - __builtin_amdgcn_frexp_expf(m), 140);
-        f = ldexpf(1.f, -shift);
-    }
-    if (nb_bad) f = __builtin_nanf("");
-
-    _Float16 *hi = reinterpret_cast<_Float16 *>(tile);
-    _Float16 *lo = reinterpret_cast<_Float16 *>(tile + kTileA);
-    const int G = q >> 1, half = q & 1, kh = G >> 1, hf = G & 1;
-    float sum = 0.f;
-    #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int st = hf * 8 + j;
-        half4 h4, l4;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float xs = nb_bad ? 0.f : ldexpf(s.v[4 * j + i], shift);
-            sum += xs;
-            const _Float16 h = static_cast<_Float16>(xs);
-            const int e = (i == 1) ? 2 : (i == 2) ? 1 : i;   // column order {0, 2, 1, 3}
-            h4[e] = h;
-            l4[e] = static_cast<_Float16>(xs - static_cast<float>(h));
-        }
-        const int at = ((st * 2 + kh) * 32 + tl) * 8 + half * 4;
-        *reinterpret_cast<half4 *>(hi + at) = h4;
-        *reinterpret_cast<half4 *>(lo + at) = l4;
-    }
-    // |sum| < 32 * 2^15: stored / 64 to stay inside the fp16 range.
-    const float s64 = sum * (1.f / 64.f);
-    const _Float16 sh = static_cast<_Float16>(s64);
-    _Float16 *mhi = reinterpret_cast<_Float16 *>(tile + 2 * kTileA);
-    _Float16 *mlo = reinterpret_cast<_Float16 *>(tile + 2 * kTileA + kTileM);
-    const int mat = ((q >> 2) * 32 + tl) * 4 + (q & 3);
-    mhi[mat] = sh;
-    mlo[mat] = static_cast<_Float16>(s64 - static_cast<float>(sh));
-    // Token scales in accumulator lane order: lane half (tl/4)%2, register 4*(tl/8) + tl%4.
-    if (q == 0) {
-        float *fr = reinterpret_cast<float *>(tile + 2 * kTileA + 2 * kTileM);
-        fr[((tl >> 2) & 1) * 16 + 4 * (tl >> 3) + (tl & 3)] = f;
-    }
-}
-
-// stage_store by a whole wave: lane (q, j) = (lane / 8, lane % 8) holds
-// values q*32 + 4j .. +3 of the token's 256-value block (v) and writes their
-// fp16 high / low quads itself -- the same block scale and layout, with each
-// 32-value sum taken as a tree over its eight lanes instead of in sequence.
+// One token's 256-value block into its record, by a whole wave: lane (q, j)
+// = (lane / 8, lane % 8) holds values q*32 + 4j .. +3 (v).  x' = x * 2^shift
+// with the block maximum in [2^14, 2^15) (shift capped at 140 so 2^-shift
+// stays a nonzero fp32), split into fp16 hi + lo, each lane writing its own
+// quads; the 32-value sums (of x') are taken as a tree over their eight
+// lanes; a non-finite value makes the token's scale NaN.
 __device__ __forceinline__ void stage_store_wave(const float (&v)[4], int lane, int tl, uint8_t *tile) {
     const int q = lane >> 3, j = lane & 7;
     float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
