@@ -164,6 +164,31 @@ def test_batched_workspace_sizes(qk):
     assert lib.qk_argmax_workspace_bytes(128256) > 0
 
 
+def test_ffn_validation_and_workspace(qk):
+    lib = qk.lib()
+    ws_bytes = lib.qk_ffn_batched_workspace_bytes
+    n32 = ws_bytes(3072, 8192, 32)
+    assert n32 > 0 and n32 % 256 == 0
+    assert ws_bytes(3072, 8192, 0) == 0 and ws_bytes(3000, 8192, 32) == 0 and ws_bytes(3072, 8000, 32) == 0
+    for k in (1, 5, 7, 8, 31, 32):                    # a size for n tokens serves every smaller call
+        assert 0 < ws_bytes(3072, 8192, k) <= n32
+    assert ws_bytes(3072, 8192, 5) == 2 * 5 * 8192 * 4   # below 8 tokens: gate and up outputs
+    g, u, d, x, y, ws = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000
+
+    def f(gt=12, gp=g, dt=14, xp=x, ldy=3072, n=32, wsp=ws, wsn=n32):
+        return lib.qk_ffn_batched_f32(gt, gp, 12, u, dt, d, xp, 3072, y, ldy, 3072, 8192, n, 0, wsp, wsn, None)
+    assert f(n=0, wsp=None, wsn=0) == qk.QK_OK          # no tokens: nothing launched
+    assert f(gt=13) == qk.QK_ERR_TYPE
+    assert f(dt=0) == qk.QK_ERR_TYPE
+    assert f(gp=None) == qk.QK_ERR_INVALID_ARG
+    assert f(gp=g + 8) == qk.QK_ERR_ALIGN
+    assert f(xp=x + 4) == qk.QK_ERR_ALIGN
+    assert f(ldy=3000) == qk.QK_ERR_INVALID_ARG
+    assert f(wsn=n32 - 256) == qk.QK_ERR_INVALID_ARG
+    assert b"qk_ffn_batched_workspace_bytes" in lib.qk_last_error()
+    assert f(wsp=ws + 16) == qk.QK_ERR_ALIGN
+
+
 def test_python_mirror_rejects_wrong_shapes(qk):
     t = qk.Tensor((2048, 16), qk.Q4_K, None)
     assert t.cols() == 2048 and t.rows() == 16
