@@ -231,6 +231,17 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
                                       s), "ffn")
 
     wall, ms = time_launches(torch, step, steps, warmup, stream)
+    # The same call with down in the split Q6_K layout, as the decode drivers
+    # hold it (a copy made once at load time by qk_q6k_split).
+    split_down = [qk.split_q6k(qk.Tensor((hidden, dim), qk.Q6_K, wd), stream).data for _, _, wd in sets]
+
+    def step_split(i):
+        wg, wu, _ = sets[i % copies]
+        qk.check(L.qk_ffn_batched_f32(qk.Q4_K, wg.data_ptr(), qk.Q4_K, wu.data_ptr(), qk.Q6_K_SPLIT,
+                                      split_down[i % copies].data_ptr(), x.data_ptr(), dim, y.data_ptr(), dim, dim,
+                                      hidden, ntok, 0, ws_f.data_ptr(), n_f, s), "ffn")
+
+    _, ms_split = time_launches(torch, step_split, steps, warmup, stream)
     weights = 2 * qk.tensor_bytes(qk.Q4_K, dim, hidden) + qk.tensor_bytes(qk.Q6_K, hidden, dim)
     # x in, the SiLU * up product (4 bytes a value as fp16 high / low
     # records), y out.
@@ -238,7 +249,9 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
     return {"tokens": ntok, "ms_per_step": round(ms, 4), "tokens_per_s": round(ntok / (ms * 1e-3), 1),
             "bytes_per_step": weights + act, "GBps": round((weights + act) / (ms * 1e-3) / 1e9, 1),
             "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "weight_copies": copies, "calls_per_step": 1, "launches_per_step": 5}
+            "weight_copies": copies, "calls_per_step": 1, "launches_per_step": 5,
+            "split_q6k_down": {"ms_per_step": round(ms_split, 4),
+                               "frac_of_peak": round((weights + act) / (ms_split * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
 
 
 def bench_mixed_1b_256(torch, qk, wl, stream, steps: int = 20, warmup: int = 3) -> dict:
