@@ -154,8 +154,18 @@ def bench_q4k_lm_shape(torch, qk, wl, stream, copies: int) -> dict:
     y = torch.empty(rows, device="cuda")
     _, k = time_launches(torch, lambda i: qk.matvec(ts[i % copies], x, y, cols, rows, stream), 2000, 2000, stream)
     b = qk.tensor_bytes(qk.Q4_K, cols, rows) + cols * 4 + rows * 4
+    # The reference's default INT8 mode on the same copies (gemv_q4_dp4a,
+    # inferencer.cu:518-569): x quantized once outside the timed launches.
+    xq = torch.empty(cols, dtype=torch.int8, device="cuda")
+    xs = torch.empty(cols // 32, dtype=torch.float32, device="cuda")
+    qk.quantize(x, xq, xs, cols, stream=stream)
+    _, ki = time_launches(torch, lambda i: qk.matvec_i8(ts[i % copies], xq, xs, y, cols, rows, stream=stream),
+                          2000, 2000, stream)
+    bi = qk.tensor_bytes(qk.Q4_K, cols, rows) + cols + cols // 32 * 4 + rows * 4
     return {"kernel_us": round(k * 1e3, 2), "GBps_kernel": round(b / (k * 1e-3) / 1e9, 1),
-            "frac_of_peak": round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "bytes_per_launch": b}
+            "frac_of_peak": round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "bytes_per_launch": b,
+            "int8": {"kernel_us": round(ki * 1e3, 2), "bytes_per_launch": bi,
+                     "frac_of_peak": round(bi / (ki * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
 
 
 def _workspace(torch, qk, cols, rows, ntok):
