@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -563,6 +564,136 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     arg_epilogue<Policy>(p, bv, bi);
 }
 
+// ------------------------------------------- LDS-staged C == 1 variant --
+//
+// The INT8 kernel over the split Q6_K layout, for long launches over one
+// matrix of whole tiles.  A C == 1 tile is 16 blocks (TR rows of P/4
+// blocks, TR*P = 64): one contiguous span of TR * row_bytes bytes (3360-3584)
+// that starts 16-byte aligned.  Each wave copies its tiles into a
+// wave-private LDS ring of kLdsDepth slots with global_load_lds_dwordx4
+// (lane i of a copy instruction moves 16 bytes to slot + 16*i; the slot
+// address goes in M0), kLdsDepth - 1 tiles ahead of the one it computes, and
+// lanes read their fields from LDS: the weights never pass through VGPRs.
+// Measured on MI355X (128256 x 2048, 4 rotating copies, results bit-identical
+// to gemv_wave): INT8 split Q6_K 36.0 us against 37.8; no gain for the FP32
+// policies (38.7-40.0 against 38.5-38.7: the 3-limb arithmetic, not the
+// loads, sets their pace), the GGUF Q6_K layout (39.6-40.9 against 39.8-40.0)
+// or Q4_K (INT8 26.3-31.7 against 26.9), so those keep gemv_wave.
+//
+// The copies are inline assembly with an explicit s_waitcnt vmcnt: the
+// compiler's own tracking of LDS DMA waits for every copy in flight
+// (vmcnt(0)) before the first LDS read, which removes the pipelining.
+// Vector memory loads complete in issue order, so when at most
+// kLdsCopies * (kLdsDepth - 1) vector memory operations remain outstanding,
+// every copy of the oldest tile has landed (the copies of the younger tiles
+// are that many loads; stores and loads issued in between only make the
+// wait stricter).
+constexpr int kLdsDepth = 2;
+constexpr int kLdsBlocksPerCu = 2;
+constexpr int kLdsCopies = 4;                // 16-byte chunks per tile: 210-224, four instructions of 64
+constexpr int kLdsMaxTileBytes = 16 * 224;   // one block per row, padded to 224 B
+
+__device__ __forceinline__ uint32_t lds_offset(const void *p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void *)p));
+}
+
+// 16 bytes from global memory to LDS: this lane's `src` lands at
+// m0 + 16 * lane (m0 wave-uniform).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_copy16(const uint8_t *src, uint32_t m0) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Issue the copies of one tile (`chunks` 16-byte chunks at src, 210..224)
+// into the slot at LDS address dst.  Every instruction has at least one
+// active lane, so each tile is exactly kLdsCopies vector memory operations.
+__device__ __forceinline__ void copy_tile(const uint8_t *src, uint32_t dst, int chunks, int lane) {
+    constexpr int kFull = kLdsCopies - 1;
+    #pragma unroll
+    for (int i = 0; i < kFull; ++i) lds_copy16(src + static_cast<size_t>(i * 64 + lane) * 16, dst + i * 1024);
+    if (lane < chunks - kFull * 64) lds_copy16(src + static_cast<size_t>(kFull * 64 + lane) * 16, dst + kFull * 1024);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// A lane's fields from its tile's LDS copy: the bytes fetch_typed loads for
+// the split layout (rows padded to 16 bytes, so every field is aligned).
+// row_off = the lane's row within the tile times row_bytes.
+__device__ __forceinline__ Raw lds_fetch_split(const unsigned char *tb, int row_off, int nb, int b, int g, int h) {
+    const Q6Fields f = q6_fields(tb + row_off, nb, b, true);
+    Raw r;
+    r.a = *reinterpret_cast<const uint4 *>(f.ql + g * 64 + h * 16);
+    r.b = *reinterpret_cast<const uint4 *>(f.ql + 32 + g * 64 + h * 16);
+    r.c = *reinterpret_cast<const uint4 *>(f.qh + g * 32 + h * 16);
+    r.s = *reinterpret_cast<const uint2 *>(f.sc + g * 8);
+    r.d = *reinterpret_cast<const uint16_t *>(f.d);
+    return r;
+}
+
+template <class Policy, int GROUP>
+__global__ __launch_bounds__(256) void gemv_lds(GemvParams p) {
+    constexpr int TYPE = QK_TYPE_Q6_K_SPLIT;
+    constexpr int D = kLdsDepth;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_waves = blockDim.x >> 6;
+    const int token = blockIdx.y;
+    const int rit = lane / GROUP;
+    const int piece = lane & (GROUP - 1);
+    const int g = (piece >> 1) & 1, h = piece & 1;
+    const int nb = p.pieces >> 2;
+    const GemvMatrix &M = p.mat[0];
+    const int tile_bytes = p.tile_rows * M.row_bytes;
+    const int chunks = tile_bytes >> 4;
+    XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
+    const size_t x_lds = (Policy::lds_bytes(p.pieces * 64) + 15) & ~size_t(15);
+    unsigned char *ring = qk_smem + x_lds + static_cast<size_t>(wave) * D * kLdsMaxTileBytes;
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_offset(ring));
+    const int stride = gridDim.x * n_waves;
+    const int first = blockIdx.x * n_waves + wave;
+    const int last = p.total_tiles - 1;
+    const int n_iter = first < p.total_tiles ? (last - first) / stride + 1 : 0;
+    // Copies of the first D - 1 tiles are in flight while the block prepares
+    // the activations (indexes clamp to the last tile, so every wave issues
+    // the same number of copies and its last prefetches re-read a valid tile).
+    #pragma unroll
+    for (int k = 0; k < D - 1; ++k)
+        copy_tile(M.w + static_cast<size_t>(min(first + k * stride, last)) * tile_bytes,
+                  ring_lds + k * kLdsMaxTileBytes, chunks, lane);
+    if (Policy::kPrepLds) {
+        Policy::prep(p, token, p.pieces * 64, xg);
+        __syncthreads();
+    }
+    typename Policy::Lane L;
+    Policy::load(L, p, token, piece, xg);
+    float bv = -INFINITY;   // greedy-token epilogue: this lane's best row so far
+    int bi = 0x7FFFFFFF;
+    float *y = M.y + static_cast<int64_t>(token) * M.ldy;
+    const int row_off = rit * M.row_bytes;
+    for (int k = 0; k < n_iter; ++k) {
+        // The slot refilled here was read in iteration k - 1, whose values
+        // fed that iteration's store; the lgkmcnt wait makes the order explicit.
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int ahead = k + D - 1;
+        copy_tile(M.w + static_cast<size_t>(min(first + ahead * stride, last)) * tile_bytes,
+                  ring_lds + (ahead % D) * kLdsMaxTileBytes, chunks, lane);
+        wait_vm<kLdsCopies * (D - 1)>();
+        const Raw r = lds_fetch_split(ring + (k % D) * kLdsMaxTileBytes, row_off, nb, piece >> 2, g, h);
+        const float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(TYPE, r, L, g, h));
+        const int row = (first + k * stride) * p.tile_rows + rit;   // whole tiles: always < M.rows
+        if (piece == 0) keep_best<Policy>(bv, bi, store_y<Policy>(p, y + row, v), row);
+    }
+    // Nothing may still be writing this workgroup's LDS when it exits.
+    wait_vm<0>();
+    arg_epilogue<Policy>(p, bv, bi);
+}
+
 // C > 1: the C waves of a wave-group share each tile; the group sums of a
 // tile meet in LDS (double-buffered, one barrier per tile) and lane t of the
 // group's first wave adds row t's C sums in chunk order.
@@ -700,6 +831,23 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const bool aligned = TYPE == QK_TYPE_Q4_K || TYPE == QK_TYPE_Q6_K_SPLIT;
         const bool long_launch =
             static_cast<int64_t>(p.total_tiles) * n_tokens >= int64_t(kWaveLongTiles) * kWaveBlocksPerCu * waves * cus;
+        // The LDS-staged kernel (INT8, split Q6_K): one matrix of whole tiles
+        // at a 16-byte aligned address, in a launch long enough for its
+        // pipeline to fill.
+        if constexpr (std::is_same_v<Policy, I8Policy> && TYPE == QK_TYPE_Q6_K_SPLIT) {
+            if (long_launch && p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0 &&
+                (reinterpret_cast<uintptr_t>(p.mat[0].w) & 15) == 0 &&
+                p.tile_rows * p.mat[0].row_bytes <= kLdsMaxTileBytes) {
+                const size_t lds = ((x_lds + 15) & ~size_t(15)) + static_cast<size_t>(waves) * kLdsDepth * kLdsMaxTileBytes;
+                const void *kl = reinterpret_cast<const void *>(gemv_lds<Policy, GROUP>);
+                const int cap = std::max(1, std::min(resident_blocks(kl, block, lds), kLdsBlocksPerCu * cus) / n_tokens);
+                const int grid_all = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
+                const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / waves : grid_all);
+                if (p.grid_out) *p.grid_out = grid * waves;
+                hipLaunchKernelGGL((gemv_lds<Policy, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
+                return;
+            }
+        }
         const int per_cu = aligned && long_launch ? kWaveBlocksPerCuLong : kWaveBlocksPerCu;
         const int cap = std::max(1, std::min(resident_blocks(k, block, x_lds), per_cu * cus) / n_tokens);
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));

@@ -70,3 +70,37 @@ def test_gemv_i8_multi_token(qk, torch_gpu, oracle, workloads):
     for k in range(ntok):
         want = oracle.gemv_i8_f64(Q6_K, w, xq[k, :cols], xs[k, : cols // 32], cols, rows)
         assert rel_l2(y[k].cpu().numpy(), want) < 1e-5
+
+
+# Long INT8 launches over the split Q6_K layout (at least 32768 wave tiles,
+# one matrix of whole tiles) run the LDS-staged kernel, whose weights reach
+# the lanes through global -> LDS copies; short launches run the register
+# kernel.  Each row's arithmetic is the same in both, so the long launch
+# equals short launches over row slices bit for bit, and both are within
+# rel-L2 1e-5 of the oracle's fp64 combine of the same integer dots.
+@pytest.mark.parametrize("cols,rows,ntok", [(2048, 128256, 1), (2048, 32768, 2), (1024, 131072, 1)])
+def test_gemv_i8_split_long_launch(qk, torch_gpu, oracle, workloads, cols, rows, ntok):
+    t = torch_gpu
+    Q6_K_SPLIT = qk.Q6_K_SPLIT
+    w, x = workloads.gemv_case(Q6_K, cols, rows, seed=65, n_tokens=ntok)
+    x = x.reshape(ntok, cols)
+    xq = np.zeros((ntok, cols), dtype=np.int8)
+    xs = np.zeros((ntok, cols // 32), dtype=np.float32)
+    for k in range(ntok):
+        xq[k], xs[k] = oracle.quantize_x32(x[k])
+    split = qk.split_q6k(qk.Tensor((cols, rows), Q6_K, to_dev(t, w)))
+    xq_d, xs_d = to_dev(t, xq), to_dev(t, xs)
+    y = t.full((ntok, rows), float("nan"), device="cuda")
+    qk.matvec_i8(split, xq_d, xs_d, y, cols, rows, n_tokens=ntok, ldxq=cols, ldscale=cols // 32, ldy=rows)
+    t.cuda.synchronize()
+    got = y.cpu().numpy()
+    for k in range(ntok):
+        assert rel_l2(got[k], oracle.gemv_i8_f64(Q6_K, w, xq[k], xs[k], cols, rows)) < 1e-5
+    rb = qk.tensor_bytes(Q6_K_SPLIT, cols, 1)
+    n = 4096
+    for r0 in (0, rows // 2 - 7 * 16, rows - n):
+        part = qk.Tensor((cols, n), Q6_K_SPLIT, split.data[r0 * rb:(r0 + n) * rb])
+        ys = t.full((ntok, n), float("nan"), device="cuda")
+        qk.matvec_i8(part, xq_d, xs_d, ys, cols, n, n_tokens=ntok, ldxq=cols, ldscale=cols // 32, ldy=n)
+        t.cuda.synchronize()
+        assert np.array_equal(ys.cpu().numpy().view(np.uint32), got[:, r0:r0 + n].view(np.uint32)), r0
