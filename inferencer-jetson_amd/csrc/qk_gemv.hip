@@ -564,6 +564,121 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     arg_epilogue<Policy>(p, bv, bi);
 }
 
+// ------------------------------------- C == 1 over one whole-tile matrix --
+//
+// gemv_wave's work for a launch over one matrix whose rows fill whole tiles:
+// tile t is the span w + t * TR * row_bytes, so its base is wave-uniform
+// (scalar registers) and a lane's five field offsets inside a tile never
+// change.  The loads take the scalar base plus 32-bit lane offsets computed
+// once, so no per-tile vector address arithmetic is left (gemv_wave rebuilds
+// five 64-bit addresses per tile: 13 of its 177 VALU instructions).
+
+// Byte offsets of a lane's fields from the first byte of its tile (the
+// bytes fetch_typed loads).
+struct LaneFields {
+    uint32_t a, b, c, s, d;
+};
+
+template <int TYPE>
+__device__ __forceinline__ LaneFields lane_fields(int rit, int row_bytes, int nb, int b, int g, int h) {
+    const uint32_t r = static_cast<uint32_t>(rit * row_bytes);
+    LaneFields f;
+    if constexpr (TYPE == QK_TYPE_Q6_K_SPLIT) {
+        f.a = r + b * 128 + g * 64 + h * 16;
+        f.b = f.a + 32;
+        f.c = r + nb * 128 + b * 64 + g * 32 + h * 16;
+        f.s = r + nb * 192 + b * 16 + g * 8;
+        f.d = r + nb * 208 + b * 2;
+    } else if constexpr (TYPE == QK_TYPE_Q4_K) {
+        const uint32_t blk = r + b * 144;
+        f.a = blk;
+        f.b = blk + 16 + g * 64 + h * 16;
+        f.c = blk + 48 + g * 64 + h * 16;
+        f.s = f.d = 0;
+    } else {
+        const uint32_t blk = r + b * 210;
+        f.a = blk + g * 64 + h * 16;
+        f.b = blk + 32 + g * 64 + h * 16;
+        f.c = blk + 128 + g * 32 + h * 16;
+        f.s = blk + 192 + g * 8;
+        f.d = blk + 208;
+    }
+    return f;
+}
+
+// The tile as a raw buffer resource (scalar registers: base, no stride,
+// `bytes` records; the third descriptor word of gfx9-family chips), so every
+// field load is a buffer load at a 32-bit lane offset from a scalar base.
+// Offsets past `bytes` would read zero; every lane offset lies inside it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const uint8_t *base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(base), 0, bytes, 0x00020000);
+}
+
+template <int TYPE>
+__device__ __forceinline__ Raw fetch_whole(const uint8_t *tile, int tile_bytes, const LaneFields &f) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(tile, tile_bytes);
+    Raw r;
+    r.a = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, f.a, 0, 0));
+    r.b = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, f.b, 0, 0));
+    r.c = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, f.c, 0, 0));
+    if constexpr (TYPE == QK_TYPE_Q4_K) {
+        r.s = make_uint2(0, 0);
+        r.d = 0;
+    } else {
+        r.s = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rs, f.s, 0, 0));
+        r.d = __builtin_amdgcn_raw_buffer_load_b16(rs, f.d, 0, 0);
+    }
+    return r;
+}
+
+template <class Policy, int TYPE, int GROUP>
+__global__ __launch_bounds__(256) void gemv_whole(GemvParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_waves = blockDim.x >> 6;
+    const int token = blockIdx.y;
+    const int rit = lane / GROUP;
+    const int piece = lane & (GROUP - 1);
+    const int g = (piece >> 1) & 1, h = piece & 1;
+    const GemvMatrix &M = p.mat[0];
+    const int tile_bytes = p.tile_rows * M.row_bytes;
+    const LaneFields lf = lane_fields<TYPE>(rit, M.row_bytes, p.pieces >> 2, piece >> 2, g, h);
+    XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
+    const int stride = gridDim.x * n_waves;
+    const int first = blockIdx.x * n_waves + wave;
+    const int last = p.total_tiles - 1;
+    // Prefetch indexes clamp to the last tile: unconditional, in-bounds loads.
+    auto fetch = [&](int k) {
+        return fetch_whole<TYPE>(M.w + static_cast<size_t>(min(first + k * stride, last)) * tile_bytes, tile_bytes, lf);
+    };
+    Raw a = fetch(0);
+    Raw b = fetch(1);
+    if (Policy::kPrepLds) {
+        Policy::prep(p, token, p.pieces * 64, xg);
+        __syncthreads();
+    }
+    typename Policy::Lane L;
+    Policy::load(L, p, token, piece, xg);
+    float bv = -INFINITY;   // greedy-token epilogue: this lane's best row so far
+    int bi = 0x7FFFFFFF;
+    float *y = M.y + static_cast<int64_t>(token) * M.ldy + rit;
+    const int n_iter = first < p.total_tiles ? (last - first) / stride + 1 : 0;
+    int k = 0;
+    while (k < n_iter) {
+        int row0 = (first + k * stride) * p.tile_rows;
+        float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(TYPE, a, L, g, h));
+        if (piece == 0) keep_best<Policy>(bv, bi, store_y<Policy>(p, y + row0, v), row0 + rit);
+        a = fetch(k + 2);
+        if (++k == n_iter) break;
+        row0 = (first + k * stride) * p.tile_rows;
+        v = group_sum<GROUP>(piece_dot<Policy, TYPE>(TYPE, b, L, g, h));
+        if (piece == 0) keep_best<Policy>(bv, bi, store_y<Policy>(p, y + row0, v), row0 + rit);
+        b = fetch(k + 2);
+        ++k;
+    }
+    arg_epilogue<Policy>(p, bv, bi);
+}
+
 // ------------------------------------------- LDS-staged C == 1 variant --
 //
 // The INT8 kernel over the split Q6_K layout, for long launches over one
@@ -848,14 +963,20 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
                 return;
             }
         }
+        // One matrix of whole tiles: gemv_whole (scalar tile bases), else gemv_wave.
+        const bool whole = TYPE != 0 && p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0;
+        const void *fn = whole ? reinterpret_cast<const void *>(gemv_whole<Policy, TYPE, GROUP>) : k;
         const int per_cu = aligned && long_launch ? kWaveBlocksPerCuLong : kWaveBlocksPerCu;
-        const int cap = std::max(1, std::min(resident_blocks(k, block, x_lds), per_cu * cus) / n_tokens);
+        const int cap = std::max(1, std::min(resident_blocks(fn, block, x_lds), per_cu * cus) / n_tokens);
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
         // Grid-stride tiles: clamping keeps the argmax partials (one per wave)
         // in their buffer.
         const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / waves : grid_all);
         if (p.grid_out) *p.grid_out = grid * waves;
-        hipLaunchKernelGGL((gemv_wave<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
+        if (whole)
+            hipLaunchKernelGGL((gemv_whole<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
+        else
+            hipLaunchKernelGGL((gemv_wave<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), x_lds, stream, p);
     } else {
         const int wgroups = std::max(1, 4 / p.chunks);
         const int block = wgroups * p.chunks * 64;
