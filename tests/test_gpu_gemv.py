@@ -153,3 +153,32 @@ def test_wide_range_within_groups(qk, torch_gpu, oracle, workloads, qtype):
     small = oracle.gemv_f64(qtype, w, xs, cols, rows)
     print(f"rel-L2 {rel_l2(y, y64):.2e}; error / norm of the small values' share "
           f"{np.linalg.norm(y - y64) / np.linalg.norm(small):.2e}", flush=True)
+
+
+# One matrix whose rows fill whole wave tiles (tile = 64 / (4 * nb) rows for
+# nb <= 16 blocks per row) runs gemv_whole (scalar tile base, buffer loads);
+# one more row leaves a partial tile and runs gemv_wave.  Both compute every
+# row with the same arithmetic, so the shared rows agree bit for bit, and
+# both are within 1e-5 of the oracle.  Covers every tile height (16, 8, 4,
+# 2, 1 rows) and the three storage layouts.
+@pytest.mark.parametrize("layout", ["q4k", "q6k", "q6k_split"])
+@pytest.mark.parametrize("nb", [1, 2, 4, 8, 16])
+def test_whole_tiles_match_partial_tiles(qk, torch_gpu, oracle, workloads, layout, nb):
+    t = torch_gpu
+    qtype = Q4_K if layout == "q4k" else Q6_K
+    cols, rows = 256 * nb, 272
+    w, x = workloads.gemv_case(qtype, cols, rows + 1, seed=140 + nb, x_stream=3)
+    xd = to_dev(t, x)
+    full = qk.Tensor((cols, rows + 1), qtype, to_dev(t, w))
+    if layout == "q6k_split":
+        full = qk.split_q6k(full)
+    rb = qk.tensor_bytes(full.type, cols, 1)
+    whole = qk.Tensor((cols, rows), full.type, full.data[: rows * rb])
+    y_whole = t.full((rows,), float("nan"), device="cuda")
+    y_part = t.full((rows + 1,), float("nan"), device="cuda")
+    qk.matvec(whole, xd, y_whole, cols, rows)
+    qk.matvec(full, xd, y_part, cols, rows + 1)
+    t.cuda.synchronize()
+    a, b = y_whole.cpu().numpy(), y_part.cpu().numpy()
+    assert np.array_equal(a.view(np.uint32), b[:rows].view(np.uint32))
+    assert rel_l2(b, oracle.gemv_f64(qtype, w, x, cols, rows + 1)) < TOL
