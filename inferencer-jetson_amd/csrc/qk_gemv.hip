@@ -53,11 +53,14 @@ constexpr int kMaxChunks = 16;
 //     launch): 9.6 us at 2, 10.2 at 4.
 //   gemv_split, split Q6_K 2048 x 8192: 9.6 us at 2 / CU, 8.6 at 1; Q4_K
 //     3072 x 3072: 6.6 / 6.1; Q4_K 8192 x 3072: 8.7 / 10.1; split Q6_K
-//     128256 x 3072: 73.5 / 111.
+//     128256 x 3072 (3-wave workgroups, a long launch): 111 at 1, 72.8 at
+//     2, 60.8 at 4, 62.4 at 6 and 8 (INT8: 81.9 at 2, 56.2 at 4, 58.2 at
+//     6 and 8).
 constexpr int kWaveBlocksPerCu = 2;
 constexpr int kWaveBlocksPerCuLong = 5;
 constexpr int kWaveLongTiles = 16;      // tiles per wave at kWaveBlocksPerCu
 constexpr int kSplitBlocksPerCu = 2;
+constexpr int kSplitBlocksPerCuLong = 4;   // >= kWaveLongTiles tiles per wave-group at 2 / CU
 constexpr int kSplitShortTiles = 3;     // tiles per wave-group at kSplitBlocksPerCu
 // Activations staged per workgroup plus the split kernels' reduction slots.
 constexpr size_t kMaxLds = 64 * 1024;
@@ -988,7 +991,9 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int cus = device_info().cus;
         const bool short_launch = static_cast<int64_t>(p.total_tiles) * n_tokens <
                                   int64_t(kSplitShortTiles) * kSplitBlocksPerCu * wgroups * cus;
-        const int per_cu = short_launch ? 1 : kSplitBlocksPerCu;
+        const bool long_split = static_cast<int64_t>(p.total_tiles) * n_tokens >=
+                                int64_t(kWaveLongTiles) * kSplitBlocksPerCu * wgroups * cus;
+        const int per_cu = short_launch ? 1 : long_split ? kSplitBlocksPerCuLong : kSplitBlocksPerCu;
         const int cap = std::max(1, std::min(resident_blocks(k, block, lds), per_cu * cus) / n_tokens);
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
         const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / (block / 64) : grid_all);

@@ -182,3 +182,38 @@ def test_whole_tiles_match_partial_tiles(qk, torch_gpu, oracle, workloads, layou
     a, b = y_whole.cpu().numpy(), y_part.cpu().numpy()
     assert np.array_equal(a.view(np.uint32), b[:rows].view(np.uint32))
     assert rel_l2(b, oracle.gemv_f64(qtype, w, x, cols, rows + 1)) < TOL
+
+
+# Long launches of the multi-wave-tile kernel (cols 3072: three waves share a
+# four-row tile; at least 16 tiles per wave-group at two workgroups per CU)
+# run four workgroups per CU.  FP32 and INT8 against the oracle, and bit for
+# bit against a short launch over a row slice.
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
+def test_split_long_launch(qk, torch_gpu, oracle, workloads, qtype):
+    t = torch_gpu
+    cols, rows, n = 3072, 32768, 2048
+    w, x = workloads.gemv_case(qtype, cols, rows, seed=150, x_stream=4)
+    mat = qk.Tensor((cols, rows), qtype, to_dev(t, w))
+    if qtype == Q6_K:
+        mat = qk.split_q6k(mat)
+    xd = to_dev(t, x)
+    xq, xs = oracle.quantize_x32(x)
+    xq_d, xs_d = to_dev(t, xq), to_dev(t, xs)
+    y = t.full((rows,), float("nan"), device="cuda")
+    yi = t.full((rows,), float("nan"), device="cuda")
+    qk.matvec(mat, xd, y, cols, rows)
+    qk.matvec_i8(mat, xq_d, xs_d, yi, cols, rows)
+    t.cuda.synchronize()
+    got, goti = y.cpu().numpy(), yi.cpu().numpy()
+    assert rel_l2(got, oracle.gemv_f64(qtype, w, x, cols, rows)) < TOL
+    assert rel_l2(goti, oracle.gemv_i8_f64(qtype, w, xq, xs, cols, rows)) < TOL
+    rb = qk.tensor_bytes(mat.type, cols, 1)
+    r0 = rows // 2 + 4 * 37
+    part = qk.Tensor((cols, n), mat.type, mat.data[r0 * rb:(r0 + n) * rb])
+    ys = t.full((n,), float("nan"), device="cuda")
+    ysi = t.full((n,), float("nan"), device="cuda")
+    qk.matvec(part, xd, ys, cols, n)
+    qk.matvec_i8(part, xq_d, xs_d, ysi, cols, n)
+    t.cuda.synchronize()
+    assert np.array_equal(ys.cpu().numpy().view(np.uint32), got[r0:r0 + n].view(np.uint32))
+    assert np.array_equal(ysi.cpu().numpy().view(np.uint32), goti[r0:r0 + n].view(np.uint32))
