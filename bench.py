@@ -168,6 +168,34 @@ def bench_q4k_lm_shape(torch, qk, wl, stream, copies: int) -> dict:
                      "frac_of_peak": round(bi / (ki * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
 
 
+def bench_lm_head_3b(torch, qk, wl, stream, copies: int) -> dict:
+    """The Llama-3.2-3B tied LM head: split Q6_K 128256 x 3072 (323 MB of
+    super-blocks, rotating copies), batch 1, FP32 and INT8 (x quantized once
+    outside the timed launches).  Three waves share each four-row tile here
+    (the multi-wave-tile GEMV kernel)."""
+    cols, rows = 3072, 128256
+    ts = []
+    for c in range(copies):
+        g = qk.Tensor((cols, rows), qk.Q6_K,
+                      torch.from_numpy(wl.synth.quant_matrix(qk.Q6_K, cols, rows, 9, 1 + 16 * c, 0.02)).to("cuda"))
+        ts.append(qk.split_q6k(g, stream))
+        del g
+    x = torch.from_numpy(wl.synth.normal_f32(cols, 9, 2)).to("cuda")
+    y = torch.empty(rows, device="cuda")
+    _, k = time_launches(torch, lambda i: qk.matvec(ts[i % copies], x, y, cols, rows, stream), 1000, 500, stream)
+    b = qk.tensor_bytes(qk.Q6_K_SPLIT, cols, rows) + cols * 4 + rows * 4
+    xq = torch.empty(cols, dtype=torch.int8, device="cuda")
+    xs = torch.empty(cols // 32, dtype=torch.float32, device="cuda")
+    qk.quantize(x, xq, xs, cols, stream=stream)
+    _, ki = time_launches(torch, lambda i: qk.matvec_i8(ts[i % copies], xq, xs, y, cols, rows, stream=stream),
+                          1000, 500, stream)
+    bi = qk.tensor_bytes(qk.Q6_K_SPLIT, cols, rows) + cols + cols // 32 * 4 + rows * 4
+    return {"kernel_us": round(k * 1e3, 2), "bytes_per_launch": b,
+            "frac_of_peak": round(b / (k * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "int8": {"kernel_us": round(ki * 1e3, 2), "bytes_per_launch": bi,
+                     "frac_of_peak": round(bi / (ki * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
+
+
 def _workspace(torch, qk, cols, rows, ntok):
     n = qk.batch_workspace_bytes(cols, rows, ntok)
     return torch.empty(max(n, 256), dtype=torch.uint8, device="cuda"), n
@@ -638,7 +666,9 @@ def main() -> int:
                                       "lm_head_q6k_frac_of_ceiling": round(achieved / sr_gbps, 4)}
         log(f"[bench] stream_read_ceiling: {json.dumps(sec['stream_read_ceiling'])}")
         sec["gemv_q4k_128256x2048"] = bench_q4k_lm_shape(torch, qk, wl, stream, args.copies)
+        sec["lm_head_q6k_3b_128256x3072"] = bench_lm_head_3b(torch, qk, wl, stream, args.copies)
         log(f"[bench] gemv_q4k_128256x2048: {json.dumps(sec['gemv_q4k_128256x2048'])}")
+        log(f"[bench] lm_head_q6k_3b_128256x3072: {json.dumps(sec['lm_head_q6k_3b_128256x3072'])}")
         sec.update(bench_small_gemvs(torch, qk, wl, stream))
         sec["ffn_3b_ragged_t32"] = bench_ffn_3b_ragged(torch, qk, wl, stream)
         log(f"[bench] ffn_3b_ragged_t32: {json.dumps(sec['ffn_3b_ragged_t32'])}")
