@@ -834,7 +834,9 @@ __device__ __forceinline__ void split_step(const GemvParams &p, const Slot &s, c
     }
 }
 
-template <class Policy, int TYPE, int GROUP>
+// WHOLE: one matrix of whole tiles, read like gemv_whole (a raw buffer
+// resource per tile in scalar registers, 32-bit lane offsets computed once).
+template <class Policy, int TYPE, int GROUP, bool WHOLE = false>
 __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
     XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
     float *red = reinterpret_cast<float *>(qk_smem + Policy::lds_bytes(p.pieces * 64));
@@ -852,8 +854,22 @@ __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
     const int iters = (p.total_tiles + per_iter - 1) / per_iter;   // same for every wave of the block
     const int first = blockIdx.x * n_wgroups + wgroup;
     const int last = p.total_tiles - 1;
-    Slot a = prep<TYPE>(p, min(first, last), rit, piece, token, g, h);
-    Slot b = prep<TYPE>(p, min(first + per_iter, last), rit, piece, token, g, h);
+    const GemvMatrix &M = p.mat[0];
+    const int tile_bytes = p.tile_rows * M.row_bytes;
+    LaneFields lf{};
+    if constexpr (WHOLE) lf = lane_fields<TYPE>(rit, M.row_bytes, p.pieces >> 2, piece >> 2, g, h);
+    auto fetch = [&](int tile) -> Slot {
+        if constexpr (WHOLE) {
+            Slot sl;
+            sl.t.type = TYPE;
+            sl.r = fetch_whole<TYPE>(M.w + static_cast<size_t>(tile) * tile_bytes, tile_bytes, lf);
+            return sl;
+        } else {
+            return prep<TYPE>(p, tile, rit, piece, token, g, h);
+        }
+    };
+    Slot a = fetch(min(first, last));
+    Slot b = fetch(min(first + per_iter, last));
     if (Policy::kPrepLds) {
         Policy::prep(p, token, p.pieces * 64, xg);
         __syncthreads();
@@ -866,11 +882,11 @@ __global__ __launch_bounds__(1024) void gemv_split(GemvParams p) {
     while (true) {
         split_step<Policy, TYPE, GROUP>(p, a, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token,
                                         bv, bi);
-        a = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
+        a = fetch(min(first + (k + 2) * per_iter, last));
         if (++k == iters) break;
         split_step<Policy, TYPE, GROUP>(p, b, L, red, k, first + k * per_iter, wgroup, chunk, lane, q, g, h, token,
                                         bv, bi);
-        b = prep<TYPE>(p, min(first + (k + 2) * per_iter, last), rit, piece, token, g, h);
+        b = fetch(min(first + (k + 2) * per_iter, last));
         if (++k == iters) break;
     }
     arg_epilogue<Policy>(p, bv, bi);
@@ -984,7 +1000,14 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int wgroups = std::max(1, 4 / p.chunks);
         const int block = wgroups * p.chunks * 64;
         const size_t lds = x_lds + static_cast<size_t>(wgroups) * 2 * p.tile_rows * p.chunks * sizeof(float);
+        bool whole = false;
         const void *k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP>);
+        // Whole-tile reads for the FP32 policies (3B LM head 60.3 against
+        // 60.9 us); the INT8 kernel measured slower with them (57.4 / 56.4).
+        if constexpr (TYPE != 0 && !std::is_same_v<Policy, I8Policy>) {
+            whole = p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0;
+            if (whole) k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP, true>);
+        }
         // Every block stages the whole activation row: two blocks per CU (one
         // when each wave-group would see fewer than kSplitShortTiles tiles)
         // keep that staging small next to the weights.
@@ -998,6 +1021,13 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
         const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / (block / 64) : grid_all);
         if (p.grid_out) *p.grid_out = grid * (block / 64);
+        if constexpr (TYPE != 0 && !std::is_same_v<Policy, I8Policy>) {
+            if (whole) {
+                hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP, true>), dim3(grid, n_tokens), dim3(block), lds,
+                                   stream, p);
+                return;
+            }
+        }
         hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP>), dim3(grid, n_tokens), dim3(block), lds, stream, p);
     }
 }

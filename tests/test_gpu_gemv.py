@@ -155,14 +155,16 @@ def test_wide_range_within_groups(qk, torch_gpu, oracle, workloads, qtype):
           f"{np.linalg.norm(y - y64) / np.linalg.norm(small):.2e}", flush=True)
 
 
-# One matrix whose rows fill whole wave tiles (tile = 64 / (4 * nb) rows for
-# nb <= 16 blocks per row) runs gemv_whole (scalar tile base, buffer loads);
-# one more row leaves a partial tile and runs gemv_wave.  Both compute every
-# row with the same arithmetic, so the shared rows agree bit for bit, and
-# both are within 1e-5 of the oracle.  Covers every tile height (16, 8, 4,
-# 2, 1 rows) and the three storage layouts.
+# One matrix whose rows fill whole tiles (64 / gcd(4 * nb, 64) rows) is read
+# through a scalar tile base with buffer loads: gemv_whole for nb <= 16
+# blocks per row, gemv_split's whole-tile form for the multi-wave tiles of
+# nb = 3, 12 or 32.  One more row leaves a partial tile and runs the
+# per-lane-address kernels.  Both compute every row with the same
+# arithmetic, so the shared rows agree bit for bit, and both are within
+# 1e-5 of the oracle.  Covers every single-wave tile height (16, 8, 4, 2,
+# 1 rows), three multi-wave tiles and the three storage layouts.
 @pytest.mark.parametrize("layout", ["q4k", "q6k", "q6k_split"])
-@pytest.mark.parametrize("nb", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("nb", [1, 2, 3, 4, 8, 12, 16, 32])
 def test_whole_tiles_match_partial_tiles(qk, torch_gpu, oracle, workloads, layout, nb):
     t = torch_gpu
     qtype = Q4_K if layout == "q4k" else Q6_K
