@@ -475,18 +475,13 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
     ragged descriptor of the 3B FFN workload, seed 3), its KV rows packed in
     one cache and filled with N(0,1) on the device.  Timed: `steps` steps,
     each ending in the 32 greedy tokens' download; positions advance."""
-    cfg = dict(wl.LLAMA_1B, context=2048 + steps + warmup)
-    W = wl.llama_weights(cfg, 2)
-    desc = wl.ffn_3b_ragged()["desc"]
-    n = desc.n_tokens
-    cap = desc.ctx_len.astype(int) + steps + warmup
-    kv_row = [int(x) for x in (wl.np.concatenate([[0], wl.np.cumsum(cap[:-1])]))]
-    rows = int(cap.sum())
+    case = wl.batch_decode_1b(extra_rows=steps + warmup)
+    cfg, n, kv_row, rows = case["cfg"], case["n"], case["kv_row"], case["rows"]
+    W = wl.llama_weights(cfg, case["weights_seed"])
     runner = qk.BatchRunner(cfg, W, max_tokens=n, cache_rows=rows)
     kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
     _fill_caches(torch, runner, cfg, rows, 2)
-    tokens = [int(x) for x in wl.synth.uniform_i32(n, 3, 6, 0, cfg["vocab"] - 1)]
-    pos = [int(c) - 1 for c in desc.ctx_len]
+    tokens, pos = list(case["tokens"]), list(case["pos"])
     for _ in range(warmup):
         tokens = runner.forward(tokens, pos, kv_row, True)
         pos = [p + 1 for p in pos]

@@ -372,8 +372,9 @@ typedef struct qk_llama qk_llama;
    caller's Q6_K buffers may be released then.  Q4_K, split Q6_K and norm
    tensors are read in place at every step and stay owned by the caller.
    Like the reference's upload (inferencer.cu:329-333), create first checks
-   that the caches and split copies fit in free device memory with a 64 MiB
-   margin (QK_ERR_DEVICE otherwise). */
+   that everything it allocates (caches, split copies, activation buffers,
+   logits, workspaces) fits in free device memory with a 64 MiB margin
+   (QK_ERR_DEVICE otherwise). */
 int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_stream stream,
                     qk_llama **out);
 
@@ -409,6 +410,11 @@ int qk_llama_logits(qk_llama *m, const float **logits);
    step: the state --compare-prefill downloads from FastGPU::x
    (inferencer.cu:1744). */
 int qk_llama_residual(qk_llama *m, const float **x);
+/* Quantized matrix products the handle has issued since create: seven per
+   layer and step (q, k, v, o, gate, up, down) plus one per LM head, the
+   count FastGPU::calls keeps for the --stats line "GPU pipeline ... across
+   N quantized matrix calls" (inferencer.cu:1170, 1457, 1500, 1909-1910). */
+int qk_llama_matrix_calls(const qk_llama *m, uint64_t *calls);
 /* One decode step at position pos (FastRunner::forward, inferencer.cu:1424-1531).
    With need_logits, *next_token receives the greedy token (synchronises the
    stream like the reference's 4-byte copy, inferencer.cu:1529); otherwise
@@ -443,6 +449,10 @@ int qk_llama_batch_logits(qk_llama_batch *m, const float **logits);
 /* Device pointer to the fp32 residual streams after the last step,
    [n_tokens][dim] in the step's token order (inferencer.cu:1744). */
 int qk_llama_batch_residual(qk_llama_batch *m, const float **x);
+/* Quantized matrix products issued since create: seven per layer and token,
+   one per logit row (FastRunner::prefill's counts, inferencer.cu:1277, 1321,
+   1368). */
+int qk_llama_batch_matrix_calls(const qk_llama_batch *m, uint64_t *calls);
 /* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  Every
    token writes its key / value row kv_row + pos before any token's
    attention reads the cache, so a token sees the rows of earlier positions

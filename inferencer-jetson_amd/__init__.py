@@ -123,6 +123,7 @@ SIGNATURES = {
     "qk_llama_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_matrix_calls": (_i, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
     "qk_llama_forward": (_i, [_vp, _i, _i, _i, ctypes.POINTER(ctypes.c_int)]),
     "qk_rope_kv_write_batched": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, ctypes.c_int64, _vp, _i, _i, _i, _i, _i,
                                       _vp]),
@@ -143,6 +144,7 @@ SIGNATURES = {
     "qk_llama_batch_kv_cache": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
+    "qk_llama_batch_matrix_calls": (_i, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
     "qk_llama_batch_forward_rows": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i,
@@ -548,6 +550,12 @@ class Runner:
         check(lib().qk_llama_residual(self.handle, ctypes.byref(p)), "residual")
         return copy_to_host(p.value, self.cfg["dim"], np.float32)
 
+    def matrix_calls(self) -> int:
+        """Quantized matrix products issued since create (qk_llama_matrix_calls)."""
+        n = ctypes.c_uint64()
+        check(lib().qk_llama_matrix_calls(self.handle, ctypes.byref(n)), "matrix_calls")
+        return n.value
+
     def forward(self, token: int, pos: int, need_logits: bool = True) -> int:
         nxt = ctypes.c_int(-1)
         check(lib().qk_llama_forward(self.handle, token, pos, int(need_logits), ctypes.byref(nxt)), "forward")
@@ -638,6 +646,12 @@ class BatchRunner:
         check(lib().qk_llama_batch_residual(self.handle, ctypes.byref(p)), "residual")
         return copy_to_host(p.value, n_tokens * self.cfg["dim"], np.float32).reshape(n_tokens, self.cfg["dim"])
 
+    def matrix_calls(self) -> int:
+        """Quantized matrix products issued since create (qk_llama_batch_matrix_calls)."""
+        n = ctypes.c_uint64()
+        check(lib().qk_llama_batch_matrix_calls(self.handle, ctypes.byref(n)), "matrix_calls")
+        return n.value
+
     def load_kv(self, key_cache, value_cache) -> None:
         """Copy fp32 caches laid out [layer][cache_rows][kv_dim] (the
         reference's layout) into the driver's head-major caches."""
@@ -647,6 +661,11 @@ class BatchRunner:
         """Rows 0..n-1 of every layer of both caches, as host arrays
         [layer][n][kv_dim] (the reference's layout)."""
         return _kv_rows(self.kv_cache(), self.cfg, self.cache_rows, n)
+
+    def load_kv_rows(self, row0: int, key_rows, value_rows) -> None:
+        """Write host rows [layer][n][kv_dim] (one sequence's rows) at cache
+        rows row0 .. row0 + n - 1 of every layer."""
+        _load_kv_rows(self.kv_cache(), self.cfg, self.cache_rows, row0, key_rows, value_rows)
 
 
 _HIP = None
@@ -659,10 +678,52 @@ def _hip() -> ctypes.CDLL:
         h = ctypes.CDLL("libamdhip64.so")
         h.hipMemcpy.argtypes = [_vp, _vp, ctypes.c_size_t, _i]
         h.hipMemcpy.restype = _i
+        h.hipMemcpy2D.argtypes = [_vp, ctypes.c_size_t, _vp, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _i]
+        h.hipMemcpy2D.restype = _i
         h.hipDeviceSynchronize.argtypes = []
         h.hipDeviceSynchronize.restype = _i
+        h.hipEventCreate.argtypes, h.hipEventCreate.restype = [ctypes.POINTER(_vp)], _i
+        h.hipEventDestroy.argtypes, h.hipEventDestroy.restype = [_vp], _i
+        h.hipEventRecord.argtypes, h.hipEventRecord.restype = [_vp, _vp], _i
+        h.hipEventSynchronize.argtypes, h.hipEventSynchronize.restype = [_vp], _i
+        h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), _vp, _vp]
+        h.hipEventElapsedTime.restype = _i
         _HIP = h
     return _HIP
+
+
+class GpuTimer:
+    """Device time from start() to stop() on one stream, summed over every
+    interval (FastGPU's start_timer / stop_timer, inferencer.cu:1172-1179):
+    two HIP events recorded on the stream; stop() waits for the second."""
+
+    def __init__(self, stream=None):
+        h = _hip()
+        self._stream = stream_handle(stream)
+        self._start, self._end = _vp(), _vp()
+        if h.hipEventCreate(ctypes.byref(self._start)) != 0 or h.hipEventCreate(ctypes.byref(self._end)) != 0:
+            raise QKError("GpuTimer", QK_ERR_DEVICE, "hipEventCreate failed")
+        self.seconds = 0.0
+
+    def start(self) -> None:
+        if _hip().hipEventRecord(self._start, self._stream) != 0:
+            raise QKError("GpuTimer", QK_ERR_DEVICE, "hipEventRecord failed")
+
+    def stop(self) -> None:
+        h = _hip()
+        ms = ctypes.c_float()
+        if h.hipEventRecord(self._end, self._stream) != 0 or h.hipEventSynchronize(self._end) != 0 or \
+                h.hipEventElapsedTime(ctypes.byref(ms), self._start, self._end) != 0:
+            raise QKError("GpuTimer", QK_ERR_DEVICE, "GPU timer failed")
+        self.seconds += ms.value / 1e3
+
+    def close(self) -> None:
+        if getattr(self, "_start", None) and _HIP is not None:
+            _HIP.hipEventDestroy(self._start)
+            _HIP.hipEventDestroy(self._end)
+        self._start = self._end = None
+
+    __del__ = close
 
 
 def _kv_shape(cfg) -> tuple[int, int, int]:
@@ -683,34 +744,58 @@ def _load_kv(ptrs, cfg, rows: int, key_cache, value_cache) -> None:
 
 def _kv_rows(ptrs, cfg, rows: int, n: int):
     """Rows 0..n-1 of a driver's head-major caches as two host arrays
-    [layer][n][kv_heads * head_dim]."""
+    [layer][n][kv_heads * head_dim] (one strided copy per cache)."""
     import numpy as np
     layers, kvh, hd = _kv_shape(cfg)
     if not 0 <= n <= rows:
         raise QKError("kv_rows", QK_ERR_INVALID_ARG, f"{n} rows of a {rows}-row cache")
     out = []
     for src in ptrs:
-        a = np.empty((layers, n, kvh * hd), dtype=np.float32)
-        for layer in range(layers):
-            for h in range(kvh):
-                off = (layer * kvh + h) * rows * hd * 4
-                a[layer, :, h * hd:(h + 1) * hd] = copy_to_host(src + off, n * hd, np.float32).reshape(n, hd)
-        out.append(a)
+        a = np.empty((layers, kvh, n, hd), dtype=np.float32)
+        if n:
+            _copy_2d(a.ctypes.data, n * hd * 4, src, rows * hd * 4, n * hd * 4, layers * kvh, 2)
+        out.append(np.ascontiguousarray(a.transpose(0, 2, 1, 3)).reshape(layers, n, kvh * hd))
     return out[0], out[1]
+
+
+def _load_kv_rows(ptrs, cfg, rows: int, row0: int, key_rows, value_rows) -> None:
+    """Host rows [layer][n][kv_heads * head_dim] into rows row0 .. row0+n-1 of
+    a driver's head-major caches (one strided copy per cache)."""
+    import numpy as np
+    layers, kvh, hd = _kv_shape(cfg)
+    k = np.asarray(key_rows)
+    n = k.shape[1] if k.ndim == 3 else -1
+    if n < 0 or not 0 <= row0 <= rows - n:
+        raise QKError("load_kv_rows", QK_ERR_INVALID_ARG, f"rows {row0}..{row0 + n - 1} of a {rows}-row cache")
+    for dst, a in zip(ptrs, (key_rows, value_rows)):
+        a = _cache_array(a, layers * n * kvh * hd).reshape(layers, n, kvh, hd)
+        a = np.ascontiguousarray(a.transpose(0, 2, 1, 3))
+        if n:
+            _copy_2d(dst + row0 * hd * 4, rows * hd * 4, a.ctypes.data, n * hd * 4, n * hd * 4, layers * kvh, 1)
 
 
 def copy_kv_rows(dst, src, n: int) -> None:
     """Rows 0..n-1 of every layer and KV head of src's caches into dst's (a
-    Runner or BatchRunner each; same model), device to device."""
+    Runner or BatchRunner each; same model), device to device: one strided
+    copy per cache."""
     layers, kvh, hd = _kv_shape(dst.cfg)
     rows_of = lambda r: r.cache_rows if hasattr(r, "cache_rows") else r.cfg["context"]
     dr, sr = rows_of(dst), rows_of(src)
     if not 0 <= n <= min(dr, sr):
         raise QKError("copy_kv_rows", QK_ERR_INVALID_ARG, f"{n} rows between caches of {sr} and {dr} rows")
+    if n == 0:
+        return
     for d, s_ in zip(dst.kv_cache(), src.kv_cache()):
-        for layer in range(layers):
-            for h in range(kvh):
-                copy_device(d + (layer * kvh + h) * dr * hd * 4, s_ + (layer * kvh + h) * sr * hd * 4, n * hd * 4)
+        _copy_2d(d, dr * hd * 4, s_, sr * hd * 4, n * hd * 4, layers * kvh, 3)
+
+
+def _copy_2d(dst: int, dpitch: int, src: int, spitch: int, width: int, height: int, kind: int) -> None:
+    """height rows of width bytes between pitched buffers (hipMemcpy2D; kind
+    1 host->device, 2 device->host, 3 device->device), after a device-wide
+    synchronisation so no queued step still uses either buffer."""
+    h = _hip()
+    if h.hipDeviceSynchronize() != 0 or h.hipMemcpy2D(dst, dpitch, src, spitch, width, height, kind) != 0:
+        raise QKError("copy_2d", QK_ERR_DEVICE, "hipMemcpy2D failed")
 
 
 def _cache_array(a, count: int):

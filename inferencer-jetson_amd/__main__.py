@@ -29,25 +29,26 @@ import time
 _HERE = pathlib.Path(__file__).resolve().parent
 _PKG = "inferencer_jetson_amd"
 
-OPTIONS_HELP = """Supported options:
-  --model path.gguf          GGUF file (default: llama3.2-3b/model.gguf)
-  --max-tokens N             Maximum response tokens (default: 128)
-  --context N                Context capacity, at least 128 (default: 1024)
-  --prompts-file path        Read one prompt per nonempty line
-  --stats                    Print per-prompt and average timing statistics
-  --q6-dp4a                  Use INT8 activations for Q6_K (default)
-  --float-q6                 Use FP32 computation for Q6_K
-  --float-gemv               Use FP32 computation for Q4_K and Q6_K
-  --fused-norm-quant         Accepted (the decode step always runs fused)
-  --fused-rope-cache         Accepted (the decode step always runs fused)
-  --fused-small-kernels      Accepted (both of the above)
-  --gate-warps N             2, 4, 8 or 16; accepted, launches are sized per shape
-  --q6-warps N               2, 4, 8 or 16; accepted, launches are sized per shape
-  --prefill-batch N          Prompt tokens per batched prefill step: 1..32 (default: 1)
-  --tokenize-only            Print token IDs without running GPU inference
-  --compare-prefill          Compare sequential and batched prefill (requires N>1)
-  --help                     Show usage and supported options
-  prompt ...                 Positional prompts; stdin is used if none are given
+OPTIONS_HELP = """Options:
+  --model FILE         Llama GGUF to load (llama3.2-3b/model.gguf when omitted)
+  --max-tokens N       end a response after N generated tokens (128)
+  --context N          KV rows per sequence, 128 or more (1024)
+  --prompts-file FILE  take the prompts from FILE, one per non-empty line
+  --stats              report timings for each prompt and for the whole run
+  --q6-dp4a            Q6_K matrices take INT8 activations (on by default)
+  --float-q6           Q6_K matrices take FP32 activations
+  --float-gemv         every quantized matrix takes FP32 activations
+  --fused-norm-quant, --fused-rope-cache, --fused-small-kernels
+                       kept for old scripts; no effect, the step is always fused
+  --gate-warps N, --q6-warps N
+                       checked for 2, 4, 8 or 16, then ignored: this library
+                       chooses each launch's shape from the matrix
+  --prefill-batch N    feed the prompt N tokens per step, 1 to 32 (1)
+  --tokenize-only      print the prompt's token ids; the GPU is not used
+  --compare-prefill    run the prompt token by token and in batches and print
+                       where the two differ (needs --prefill-batch 2 or more)
+  --help               this text
+Prompts are the remaining arguments; without any, stdin is read as one prompt.
 """
 
 
@@ -158,6 +159,33 @@ def _prefill_batched(qk, runner, batch, ids: list[int]) -> int:
     return nxt
 
 
+STORAGE_NAMES = {0: "FP32", 1: "FP16", 12: "Q4_K", 14: "Q6_K"}
+
+
+def storage_summary(model, q4k_int8: bool, q6k_int8: bool) -> str:
+    """One line on the model's tensors: parameter count, each storage type's
+    share of the parameters (in type-id order), bits per parameter and
+    tensor bytes, and the arithmetic each quantized type runs in -- the facts
+    the reference prints at load (GGUF::print_storage, inferencer.cu:296-315)."""
+    params: dict[int, int] = {}
+    nbytes = 0
+    for t in model.tensors():
+        n = 1
+        for d in range(t.n_dims):
+            n *= int(t.dims[d])
+        params[t.type] = params.get(t.type, 0) + n
+        nbytes += int(t.bytes)
+    total = max(sum(params.values()), 1)
+    shares = []
+    for ty in sorted(params):
+        pct = 100.0 * params[ty] / total
+        shares.append(f"{STORAGE_NAMES.get(ty, 'unknown')} {'<0.1' if pct < 0.05 else f'{pct:.1f}'}%")
+    mode = lambda on: "INT8" if on else "FP32"
+    return (f"Model: {total / 1e9:.3f}B parameters ({', '.join(shares)}), {8.0 * nbytes / total:.2f} bits per "
+            f"parameter, {nbytes / 2**30:.2f} GiB of tensor data; Q4_K products in {mode(q4k_int8)}, Q6_K "
+            f"products in {mode(q6k_int8)}, accumulation in FP32\n")
+
+
 def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
     stdout = stdout or sys.stdout.buffer
     stderr = stderr or sys.stderr
@@ -175,7 +203,8 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
         t_loaded = time.perf_counter()
         tok = tk.Tokenizer.from_gguf(model)
         t_tok = time.perf_counter()
-        runner = batch = None
+        stderr.write(storage_summary(model, o.use_dp4a, o.use_q6_dp4a))
+        runner = batch = timer = None
         t_up0 = t_up1 = t_ready = t_tok
         if not o.tokenize_only:
             t_up0 = time.perf_counter()
@@ -188,6 +217,7 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                 runner.set_int8(o.use_dp4a, o.use_q6_dp4a)
                 if o.prefill_batch > 1:
                     batch = qk.BatchRunner.from_gguf(model, o.context, o.prefill_batch, o.context)
+                timer = qk.GpuTimer()
             t_ready = time.perf_counter()
             stderr.write(f"Q4_K matrix path: {'INT8' if o.use_dp4a else 'FP32'}; Q6_K matrix path: "
                          f"{'INT8' if o.use_q6_dp4a else 'FP32'}\n")
@@ -211,7 +241,8 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
             return 0
 
         stop = tok.stop_ids()
-        sums = dict(tokenize=0.0, prefill=0.0, decode=0.0, prompt=0.0, compute=0.0)
+        sums = dict(tokenize=0.0, prefill=0.0, decode=0.0, prompt=0.0, compute=0.0, gpu=0.0)
+        calls = lambda: runner.matrix_calls() + (batch.matrix_calls() if batch is not None else 0)
         n_in = n_out = n_steps = 0
         for p, prompt in enumerate(o.prompts):
             t0 = time.perf_counter()
@@ -228,13 +259,16 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                 stdout.write((" ".join(str(i) for i in ids) + " \n").encode())
                 sums["prompt"] += time.perf_counter() - t0
                 continue
+            gpu_before, calls_before = timer.seconds, calls()
             tp = time.perf_counter()
+            timer.start()
             if batch is not None:
                 nxt = _prefill_batched(qk, runner, batch, ids)
             else:
                 nxt = 0
                 for i, t in enumerate(ids):
                     nxt = runner.forward(t, i, i + 1 == len(ids))
+            timer.stop()
             td = time.perf_counter()
             generated = steps = 0
             compute = 0.0
@@ -247,7 +281,9 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                 if i + 1 == o.max_tokens or len(ids) + i >= o.context:
                     break
                 ts = time.perf_counter()
+                timer.start()
                 nxt = runner.forward(nxt, len(ids) + i, True)
+                timer.stop()
                 compute += time.perf_counter() - ts
                 steps += 1
             stdout.write(b"\n")
@@ -257,6 +293,8 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
             sums["decode"] += tf - td
             sums["prompt"] += tf - t0
             sums["compute"] += compute
+            gpu = timer.seconds - gpu_before
+            sums["gpu"] += gpu
             n_out += generated
             n_steps += steps
             if o.stats:
@@ -264,7 +302,8 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                              f"  tokenization {t1 - t0:.3f} s; prompt computation {td - tp:.3f} s; response "
                              f"generation {tf - td:.3f} s; total {tf - t0:.3f} s\n"
                              f"  output throughput {generated / max(tf - t0, 1e-9):.3f} tokens/s; steady decode "
-                             f"{steps / max(compute, 1e-9):.3f} tokens/s\n")
+                             f"{steps / max(compute, 1e-9):.3f} tokens/s\n"
+                             f"  GPU pipeline {gpu:.3f} s across {calls() - calls_before} quantized matrix calls\n")
         if o.stats:
             t_end = time.perf_counter()
             n = len(o.prompts)
@@ -280,7 +319,8 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                              f"  inference per prompt (including tokenization): {sums['prompt'] / n:.3f} s\n"
                              f"  input processing: {n_in / max(sums['prefill'], 1e-9):.3f} tokens/s\n"
                              f"  output throughput: {n_out / max(sums['prompt'], 1e-9):.3f} tokens/s\n"
-                             f"  steady decode: {n_steps / max(sums['compute'], 1e-9):.3f} tokens/s\n")
+                             f"  steady decode: {n_steps / max(sums['compute'], 1e-9):.3f} tokens/s\n"
+                             f"  GPU pipeline: {sums['gpu'] / n:.3f} s\n")
             stderr.write(f"Total: {n_in} input tokens, {n_out} output tokens, {t_end - t_start:.3f} s elapsed\n")
         stdout.flush()
         return 0

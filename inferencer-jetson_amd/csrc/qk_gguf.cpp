@@ -62,7 +62,7 @@ class Cursor {
 
     template <class T>
     T number() {
-        need(sizeof(T), "truncated GGUF metadata");
+        need(sizeof(T), "header ends before its metadata does");
         T v;
         std::memcpy(&v, base_ + pos_, sizeof(T));
         pos_ += sizeof(T);
@@ -70,8 +70,8 @@ class Cursor {
     }
     std::string str() {
         const uint64_t n = number<uint64_t>();
-        if (n > kMaxString) throw FormatError{"invalid GGUF string length"};
-        need(n, "truncated GGUF string");
+        if (n > kMaxString) throw FormatError{"metadata string over the 1e8-byte limit"};
+        need(n, "metadata string runs past the end of the file");
         std::string s(reinterpret_cast<const char *>(base_ + pos_), n);
         pos_ += n;
         return s;
@@ -99,7 +99,7 @@ class Cursor {
             if (depth > 8) throw FormatError{"GGUF arrays nested too deeply"};
             const uint32_t element = number<uint32_t>();
             const uint64_t count = number<uint64_t>();
-            if (count > kMaxArray) throw FormatError{"invalid GGUF array length"};
+            if (count > kMaxArray) throw FormatError{"metadata array over the 1e7-entry limit"};
             for (uint64_t i = 0; i < count; ++i) skip(element, depth + 1);
         } else {
             scalar(type);
@@ -122,7 +122,7 @@ uint64_t storage_bytes(uint32_t type, uint64_t elements, const std::string &name
         case 1: return elements * 2;
         case QK_TYPE_Q4_K:
         case QK_TYPE_Q6_K:
-            if (elements % 256) throw FormatError{"invalid quantized tensor shape: " + name};
+            if (elements % 256) throw FormatError{"block-quantized tensor whose size is not a multiple of 256: " + name};
             return elements / 256 * (type == QK_TYPE_Q4_K ? 144 : 210);
         default: throw FormatError{"unsupported tensor storage type " + std::to_string(type) + ": " + name};
     }
@@ -131,9 +131,9 @@ uint64_t storage_bytes(uint32_t type, uint64_t elements, const std::string &name
 void parse(qk_gguf &g) {
     Cursor r(static_cast<const uint8_t *>(g.mapping), g.file_size);
     const uint32_t magic = r.number<uint32_t>();
-    if (std::memcmp(&magic, "GGUF", 4)) throw FormatError{"file is not GGUF"};
+    if (std::memcmp(&magic, "GGUF", 4)) throw FormatError{"bad magic: no GGUF header"};
     const uint32_t version = r.number<uint32_t>();
-    if (version != 3) throw FormatError{"only GGUF v3 is supported (file has v" + std::to_string(version) + ")"};
+    if (version != 3) throw FormatError{"GGUF version " + std::to_string(version) + " found; this reader takes version 3"};
     const uint64_t n_tensors = r.number<uint64_t>(), n_meta = r.number<uint64_t>();
     // Every entry takes at least 8 + 4 bytes of the file, which bounds both
     // counts before anything is reserved.
@@ -143,11 +143,12 @@ void parse(qk_gguf &g) {
         const uint32_t type = r.number<uint32_t>();
         if (key == "tokenizer.ggml.tokens" || key == "tokenizer.ggml.merges") {
             if (type != kArray || r.number<uint32_t>() != kString)
-                throw FormatError{"expected string array: " + key};
+                throw FormatError{"token or merge list with non-string entries: " + key};
             const uint64_t count = r.number<uint64_t>();
             // Each entry needs at least its 8-byte length, which bounds the
             // reservation by the bytes left in the file.
-            if (count > kMaxArray || count > r.left() / 8) throw FormatError{"invalid GGUF array length"};
+            if (count > kMaxArray || count > r.left() / 8)
+                throw FormatError{"metadata array over the 1e7-entry limit or past the end of the file"};
             auto &target = key == "tokenizer.ggml.tokens" ? g.tokens : g.merges;
             target.clear();
             target.reserve(count);
@@ -190,10 +191,10 @@ void parse(qk_gguf &g) {
     if (al != g.params.end()) {
         const double a = al->second;
         if (!(a >= 1.0 && a <= 1073741824.0) || a != static_cast<double>(static_cast<uint64_t>(a)))
-            throw FormatError{"invalid GGUF alignment"};
+            throw FormatError{"general.alignment must be a positive power of two"};
         g.alignment = static_cast<uint64_t>(a);
     }
-    if (g.alignment & (g.alignment - 1)) throw FormatError{"invalid GGUF alignment"};
+    if (g.alignment & (g.alignment - 1)) throw FormatError{"general.alignment must be a positive power of two"};
     g.data_start = (r.pos() + g.alignment - 1) & ~(g.alignment - 1);
     if (g.file_size <= g.data_start) throw FormatError{"invalid GGUF file size: no tensor data"};
     const uint64_t data_bytes = g.file_size - g.data_start;
@@ -262,7 +263,7 @@ int qk_gguf_close(qk_gguf *g) {
 int qk_gguf_param(const qk_gguf *g, const char *key, double *value) {
     if (!g || !key || !value) return qk::fail(QK_ERR_INVALID_ARG, "qk_gguf_param: null argument");
     auto it = g->params.find(key);
-    if (it == g->params.end()) return qk::fail(QK_ERR_INVALID_ARG, std::string("missing GGUF parameter: ") + key);
+    if (it == g->params.end()) return qk::fail(QK_ERR_INVALID_ARG, std::string("no metadata key ") + key);
     *value = it->second;
     return qk::ok();
 }
@@ -285,7 +286,7 @@ int qk_gguf_tensor_at(const qk_gguf *g, int64_t i, qk_gguf_tensor *out) {
 int qk_gguf_find_tensor(const qk_gguf *g, const char *name, qk_gguf_tensor *out) {
     if (!g || !name || !out) return qk::fail(QK_ERR_INVALID_ARG, "qk_gguf_find_tensor: null argument");
     auto it = g->index.find(name);
-    if (it == g->index.end()) return qk::fail(QK_ERR_INVALID_ARG, std::string("missing tensor: ") + name);
+    if (it == g->index.end()) return qk::fail(QK_ERR_INVALID_ARG, std::string("no tensor named ") + name);
     *out = g->tensors[it->second];
     return qk::ok();
 }

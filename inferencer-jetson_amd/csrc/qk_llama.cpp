@@ -50,6 +50,7 @@ struct qk_llama {
     float *ss_norm = nullptr, *ss_ffn = nullptr;
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
     qk_llama_memory mem{};        // device bytes the handle holds
+    uint64_t matrix_calls = 0;    // quantized matrix products issued (FastGPU::calls)
 };
 
 namespace {
@@ -393,7 +394,16 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
     m->kv_dim = head_dim * c.kv_heads;
     const size_t cache = static_cast<size_t>(c.layers) * c.context * m->kv_dim;
     const int half = head_dim / 2;
-    int st = check_free_memory("qk_llama_create", 2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim));
+    m->attn_ws_bytes = qk::split_attention_workspace_bytes(1, c.heads, c.kv_heads, head_dim, c.context);
+    // Everything create allocates: caches, split Q6_K copies, activation
+    // buffers, RoPE tables, workspaces and the activation records.
+    const size_t argmax_bytes = std::max(2 * qk::kArgPartsMax * sizeof(float), qk_argmax_workspace_bytes(c.vocab));
+    const uint64_t buffer_bytes =
+        sizeof(float) * (5ull * c.dim + 2ull * m->kv_dim + 2ull * c.hidden + c.vocab + 2ull * c.context * half) +
+        argmax_bytes + 2 * sizeof(int32_t) + std::max(c.dim, c.hidden) / 32 * (32 + sizeof(float)) + m->attn_ws_bytes +
+        (4ull * c.dim / 16 + c.hidden / 16) * sizeof(qk::XGroup) + 2ull * c.dim / 16 * sizeof(float);
+    int st = check_free_memory("qk_llama_create",
+                               2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim) + buffer_bytes);
     if (st) {
         delete m;
         return st;
@@ -409,8 +419,7 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         (st = dev_alloc(m->mem.buffers, &m->sine, static_cast<size_t>(c.context) * half, "RoPE sine")) ||
         // The FP32 step's LM-head partials, or the INT8 step's qk_argmax_f32
         // workspace, whichever is larger (the latter grows with vocab).
-        (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->argmax_ws),
-                        std::max(2 * qk::kArgPartsMax * sizeof(float), qk_argmax_workspace_bytes(c.vocab)),
+        (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->argmax_ws), argmax_bytes,
                         "argmax partials")) ||
         (st = dev_alloc(m->mem.buffers, &m->d_next, 1, "next token")) || (st = dev_alloc(m->mem.buffers, &m->d_token, 1, "input token")) ||
         (st = dev_alloc(m->mem.buffers, &m->xq, std::max(c.dim, c.hidden), "quantized activations")) ||
@@ -418,7 +427,6 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         release(m);
         return st;
     }
-    m->attn_ws_bytes = qk::split_attention_workspace_bytes(1, c.heads, c.kv_heads, head_dim, c.context);
     if (m->attn_ws_bytes &&
         (st = dev_alloc(m->mem.buffers, reinterpret_cast<uint8_t **>(&m->attn_ws), m->attn_ws_bytes, "attention workspace"))) {
         release(m);
@@ -497,6 +505,12 @@ int qk_llama_logits(qk_llama *m, const float **logits) {
     return qk::ok();
 }
 
+int qk_llama_matrix_calls(const qk_llama *m, uint64_t *calls) {
+    if (!m || !calls) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_matrix_calls: null argument");
+    *calls = m->matrix_calls;
+    return qk::ok();
+}
+
 int qk_llama_residual(qk_llama *m, const float **x) {
     if (!m || !x) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_residual: null argument");
     *x = m->x;
@@ -525,6 +539,10 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         tok = m->d_token;
     }
     m->last_next = -1;
+    // Seven matrix products per layer (q, k, v, o, gate, up, down) and the
+    // LM head, counted as the reference counts FastGPU::matvec and its fused
+    // qkv / gate-up launches (inferencer.cu:1170, 1457, 1500).
+    m->matrix_calls += 7ull * c.layers + (need_logits ? 1 : 0);
     if (m->int8_q4k || m->int8_q6k) {
         if ((st = forward_int8(m, tok, pos, need_logits != 0, s))) return st;
         if (!need_logits) {
@@ -634,6 +652,7 @@ struct qk_llama_batch {
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
     std::vector<int64_t> kv_writes;   // host scratch of the KV-row check
     qk_llama_memory mem{};        // device bytes the handle holds
+    uint64_t matrix_calls = 0;    // quantized matrix products issued (FastGPU::calls)
 };
 
 namespace {
@@ -724,11 +743,6 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     m->cache_rows = cache_rows;
     const size_t T = static_cast<size_t>(max_tokens);
     const size_t cache = static_cast<size_t>(c.layers) * cache_rows * m->kv_dim;
-    if (int st0 = check_free_memory("qk_llama_batch_create",
-                                    2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim))) {
-        delete m;
-        return st0;
-    }
     const int half = head_dim / 2;
     size_t ws = 0;
     const int kv = m->kv_dim;
@@ -746,6 +760,18 @@ int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w,
     m->gemm_ws_bytes = ws;
     const size_t rec_bytes = qk::batched_records_bytes(std::max(c.dim, c.hidden), max_tokens);
     m->attn_ws_bytes = qk::split_attention_workspace_bytes(max_tokens, c.heads, c.kv_heads, head_dim, c.context);
+    // Everything create allocates: caches, split Q6_K copies, activation
+    // buffers and logits, RoPE tables, workspaces and chained records.
+    const uint64_t buffer_bytes =
+        sizeof(float) * (T * (5ull * c.dim + 2ull * kv + 2ull * c.hidden + c.vocab) + 2ull * c.context * half +
+                         T * (c.dim / 256)) +
+        ws + m->attn_ws_bytes + qk_argmax_rows_workspace_bytes(c.vocab, max_tokens) + 2 * rec_bytes +
+        T * (3 * sizeof(int32_t) + sizeof(qk_batch_token));
+    if (int st0 = check_free_memory("qk_llama_batch_create",
+                                    2 * cache * sizeof(float) + split_copy_bytes(*w, c, m->kv_dim) + buffer_bytes)) {
+        delete m;
+        return st0;
+    }
     int st = QK_OK;
     if ((st = dev_alloc(m->mem.buffers, &m->x, T * c.dim, "residual")) || (st = dev_alloc(m->mem.buffers, &m->xn, T * c.dim, "normalized state")) ||
         (st = dev_alloc(m->mem.buffers, &m->q, T * c.dim, "query")) || (st = dev_alloc(m->mem.buffers, &m->k, T * kv, "key")) ||
@@ -826,6 +852,12 @@ int qk_llama_batch_logits(qk_llama_batch *m, const float **logits) {
     return qk::ok();
 }
 
+int qk_llama_batch_matrix_calls(const qk_llama_batch *m, uint64_t *calls) {
+    if (!m || !calls) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_matrix_calls: null argument");
+    *calls = m->matrix_calls;
+    return qk::ok();
+}
+
 int qk_llama_batch_residual(qk_llama_batch *m, const float **x) {
     if (!m || !x) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_residual: null argument");
     *x = m->x;
@@ -880,6 +912,10 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         return qk::fail(QK_ERR_DEVICE, "qk_llama_batch_forward: batch upload failed");
     void *ws = m->gemm_ws;
     const size_t wsb = m->gemm_ws_bytes;
+    // Seven products per layer and token, one LM-head product per logit row
+    // (the reference's batched prefill counts 3, 1, 2 and 1 per token and
+    // layer, inferencer.cu:1321, 1368, 1277).
+    m->matrix_calls += 7ull * c.layers * T + n_rows;
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, m->d_tokens, T, m->x, dim, c.vocab, s))) return st;
     // Per layer: fused QKV (RMSNorm staged), RoPE + KV write + attention,
     // o (+ residual), fused gate/up (RMSNorm staged), down (SiLU * up staged,

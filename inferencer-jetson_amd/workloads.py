@@ -168,3 +168,19 @@ def mixed_1b_256(seed: int = 4):
     x = synth.normal_f32(256 * cfg["dim"], seed, 8).reshape(256, cfg["dim"])
     x_ffn = synth.normal_f32(256 * cfg["hidden"], seed, 9).reshape(256, cfg["hidden"])
     return dict(weights=weights, x=x, x_ffn=x_ffn, desc=desc, cfg=cfg)
+
+
+def batch_decode_1b(extra_rows: int, seed: int = 3):
+    """The 32-sequence decode batch on the random-init Llama-3.2-1B (weights
+    seed 2): sequence s decodes at position ctx_s - 1, ctx_s ~ U[64, 2048]
+    from the 3B FFN workload's descriptor (seed 3), its KV rows packed after
+    the previous sequence's with extra_rows rows to spare (the steps that
+    follow).  First tokens uniform in the vocabulary (seed 3, stream 6)."""
+    desc = ffn_3b_ragged(seed)["desc"]
+    n = desc.n_tokens
+    cap = desc.ctx_len.astype(np.int64) + extra_rows
+    kv_row = np.concatenate([[0], np.cumsum(cap[:-1])]).astype(np.int64)
+    cfg = dict(LLAMA_1B, context=2048 + extra_rows)
+    tokens = [int(x) for x in synth.uniform_i32(n, seed, 6, 0, cfg["vocab"] - 1)]
+    return dict(cfg=cfg, weights_seed=2, n=n, cap=cap, kv_row=[int(r) for r in kv_row], rows=int(cap.sum()),
+                pos=[int(c) - 1 for c in desc.ctx_len], tokens=tokens)

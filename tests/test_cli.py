@@ -73,8 +73,11 @@ def test_missing_model_is_an_error(tmp_path):
 
 def test_tokenize_only_prints_chat_prompt_ids(vocab_gguf, tmp_path):
     path, tok = vocab_gguf
-    rc, out, _ = run(["--model", str(path), "--tokenize-only", "hello world"])
+    rc, out, err = run(["--model", str(path), "--tokenize-only", "hello world"])
     assert rc == 0
+    # The load-time storage line: the file's one FP32 tensor of 256 values.
+    assert err.startswith("Model: 0.000B parameters (FP32 100.0%), 32.00 bits per parameter") and \
+        "Q4_K products in INT8, Q6_K products in INT8" in err, err
     want = T.chat_prompt(tok, "hello world")
     assert out == (" ".join(map(str, want)) + " \n").encode()
     # Several prompts from a file (CRLF lines, blank lines skipped): numbered.

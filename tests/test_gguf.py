@@ -116,21 +116,21 @@ def test_missing_file_is_io_error(qk, tmp_path):
 
 
 @pytest.mark.parametrize("case,needle", [
-    ("magic", "not GGUF"),
-    ("version", "v3"),
+    ("magic", "no GGUF header"),
+    ("version", "takes version 3"),
     ("ndims0", "dimensions"),
     ("ndims5", "dimensions"),
     ("dim0", "dimensions"),
     ("type", "storage type"),
-    ("quant_shape", "quantized tensor shape"),
+    ("quant_shape", "not a multiple of 256"),
     ("past_end", "outside the file"),
     ("offset_unaligned", "not aligned"),
     ("alignment0", "alignment"),
     ("alignment3", "alignment"),
-    ("string_len", "string length"),
-    ("array_len", "array length"),
+    ("string_len", "1e8-byte limit"),
+    ("array_len", "1e7-entry limit"),
     ("meta_type", "metadata type"),
-    ("tokens_not_strings", "string array"),
+    ("tokens_not_strings", "non-string entries"),
     ("duplicate", "duplicate"),
     ("no_data", "file size"),
     ("counts", "entry counts"),

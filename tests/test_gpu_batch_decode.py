@@ -279,3 +279,57 @@ def test_driver_cache_layout_round_trip(qk, torch_gpu, workloads, synth):
         qk.copy_kv_rows(r, br, cfg["context"] + 1)
     r.close()
     br.close()
+
+
+def test_llama_1b_32_sequences_bench_shape(qk, torch_gpu, oracle, workloads, synth):
+    """The batch bench.py times: 32 sequences of the random-init Llama-3.2-1B
+    decoding at positions ctx - 1, ctx ~ U[64, 2048] (seed-3 descriptor), each
+    sequence's rows packed in one cache (the timed step's multi-split
+    attention, its merge writing the o projection's records, and the
+    32-token matrix-core chain).  Every cache row holds N(0,1) values; the
+    checked sequences' rows come from the workload generator and feed one
+    fp64 oracle model each: the 8 longest contexts and 4 others, greedy
+    tokens identical, logits rel-L2 and top-2 margin printed per sequence
+    (--compare-prefill's report, inferencer.cu:1814-1825)."""
+    t = torch_gpu
+    case = workloads.batch_decode_1b(extra_rows=1)
+    cfg, n, rows = case["cfg"], case["n"], case["rows"]
+    W = workloads.llama_weights(cfg, case["weights_seed"])
+    br = qk.BatchRunner(cfg, W, max_tokens=n, cache_rows=rows)
+    layers, kv = cfg["layers"], cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
+    g = t.Generator(device="cuda")
+    g.manual_seed(2)
+    for dst in br.kv_cache():
+        for layer in range(layers):
+            blk = t.randn(rows * kv, device="cuda", generator=g)
+            qk.copy_device(dst + layer * rows * kv * 4, blk.data_ptr(), rows * kv * 4)
+            del blk
+    pos, kv_row = case["pos"], case["kv_row"]
+    order = [int(i) for i in np.argsort(pos, kind="stable")]
+    checked = order[-8:] + order[0:24:6]
+    host = {}
+    for s in checked:
+        p = pos[s]
+        k = synth.normal_f32(layers * p * kv, 80, 10 + 2 * s).reshape(layers, p, kv)
+        v = synth.normal_f32(layers * p * kv, 80, 11 + 2 * s).reshape(layers, p, kv)
+        br.load_kv_rows(kv_row[s], k, v)
+        host[s] = (k, v)
+    print(f"32 sequences, positions {min(pos)}..{max(pos)}, checking {sorted(checked)}", flush=True)
+    got = br.forward(case["tokens"], pos, kv_row, True)
+    lg = br.logits(n)
+    br.close()
+    for s in checked:
+        p = pos[s]
+        kc = np.zeros((layers, cfg["context"], kv), dtype=np.float32)
+        vc = np.zeros_like(kc)
+        kc[:, :p], vc[:, :p] = host[s]
+        om = oracle.Llama(cfg, W)
+        om.load_cache(kc, vc, p)
+        o, ref = om.forward(case["tokens"][s], p, True)
+        del om
+        top = np.sort(ref)[-2:]
+        err = rel_l2(lg[s], ref)
+        print(f"seq {s} pos {p}: gpu {got[s]} ref {o} top2 margin {top[1] - top[0]:.4f} logits rel-L2 {err:.2e}",
+              flush=True)
+        assert got[s] == o, s
+        assert err < 1e-2, s

@@ -245,3 +245,23 @@ def test_ffn_entry_residual_and_types(qk, torch_gpu, oracle, workloads, synth, n
         y = run_ffn(qk, t, (gw, uw, dwk), types, x, dim, hidden, accumulate=True, alias=True)
         for k in range(ntok):
             assert rel_l2(y[k] - x[k], want[k]) < TOL, (types, k)
+
+
+@pytest.mark.parametrize("down_layout", ["gguf", "split"])
+def test_ffn_entry_3b_shape(qk, torch_gpu, oracle, workloads, down_layout):
+    """The FFN call bench.py times: Llama-3.2-3B shapes (gate / up 8192 x 3072,
+    12 blocks a row; down 3072 x 8192, 32 blocks a row) on the seed-3
+    workload's 32 decode tokens, down in the GGUF and in the split Q6_K
+    layout, against gate / up / SiLU / down in fp64."""
+    t = torch_gpu
+    c = workloads.ffn_3b_ragged()
+    dim, hidden = c["cfg"]["dim"], c["cfg"]["hidden"]
+    dw, dtype = c["down"], Q6_K
+    if down_layout == "split":
+        dw = qk.split_q6k(qk.Tensor((hidden, dim), Q6_K, to_dev(t, c["down"]))).data.cpu().numpy()
+        dtype = qk.Q6_K_SPLIT
+    want = ffn_f64(oracle, (c["gate"], c["up"], c["down"]), (Q4_K, Q4_K, Q6_K), c["x"], dim, hidden)
+    y = run_ffn(qk, t, (c["gate"], c["up"], dw), (Q4_K, Q4_K, dtype), c["x"], dim, hidden)
+    errs = [rel_l2(y[k], want[k]) for k in range(c["x"].shape[0])]
+    print(f"3B FFN, 32 tokens, {down_layout} down: worst rel-L2 {max(errs):.2e}", flush=True)
+    assert max(errs) < TOL

@@ -133,6 +133,16 @@ def test_cli_generates_the_drivers_tokens(qk, torch_gpu, model, prefill):
     assert rc == 0, err
     assert out == text + b"\n", (out, text)
     assert "steady decode" in err and "Total:" in err
+    # Matrix products counted as FastGPU::calls counts them: seven per layer
+    # and token of the prompt plus its one LM head, then seven per layer and
+    # one LM head per decode step (a stop token ends the loop after its step).
+    shown = 0
+    while shown < n and want[shown] not in stop:
+        shown += 1
+    steps = n - 1 if shown == n else shown
+    calls = 7 * CFG["layers"] * len(ids) + 1 + steps * (7 * CFG["layers"] + 1)
+    assert f"s across {calls} quantized matrix calls" in err, err
+    assert "  GPU pipeline: " in err and "Model: " in err
 
 
 def test_cli_int8_default_and_compare_output(qk, torch_gpu, model):
