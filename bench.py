@@ -209,9 +209,8 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
     3072 x 8192).  `copies` weight sets rotate so the last-level cache cannot
     hold them (8 x 49 MB).  With int8, the reference's INT8 mode
     (FastRunner's batched INT8 FFN, inferencer.cu:1362-1380): x quantized
-    per 32, gate and up by the INT8 batched GEMM, SiLU * up, the product
-    quantized, down by the INT8 batched GEMM (5 launches, quantization
-    included in the timed step)."""
+    per 32, then qk_ffn_batched_i8 (3 launches, quantization included in
+    the timed step)."""
     dim, hidden, ntok = 3072, 8192, 32
     sets = []
     x_host = None
@@ -227,34 +226,35 @@ def bench_ffn_3b_ragged(torch, qk, wl, stream, copies: int = 8, steps: int = 200
     s = qk.stream_handle(stream)
 
     if int8:
-        xq = torch.empty((ntok, hidden), dtype=torch.int8, device="cuda")
-        xs = torch.empty((ntok, hidden // 32), dtype=torch.float32, device="cuda")
-        ws_i, n_i = _workspace(torch, qk, hidden, hidden, ntok)
+        # x quantized per 32 (quantize_batch_cuda), then one call
+        # (qk_ffn_batched_i8): gate / up on the integer matrix cores with
+        # SiLU(gate) * up quantized in their epilogue, and down.
+        xq = torch.empty((ntok, dim), dtype=torch.int8, device="cuda")
+        xs = torch.empty((ntok, dim // 32), dtype=torch.float32, device="cuda")
+        n_i = L.qk_ffn_batched_i8_workspace_bytes(dim, hidden, ntok)
+        ws_i = torch.empty(n_i, dtype=torch.uint8, device="cuda")
+        split_down = [qk.split_q6k(qk.Tensor((hidden, dim), qk.Q6_K, wd), stream).data for _, _, wd in sets]
 
-        def step(i):
-            wg, wu, wd = sets[i % copies]
-            qk.quantize(x, xq, xs, dim, n_tokens=ntok, ldxq=hidden, ldscale=hidden // 32, stream=stream)
-            for w, out in ((wg, gate), (wu, up)):
-                qk.check(L.qk_gemv_batched_i8(qk.Q4_K, w.data_ptr(), xq.data_ptr(), hidden, xs.data_ptr(),
-                                              hidden // 32, out.data_ptr(), hidden, dim, hidden, ntok,
-                                              ws_i.data_ptr(), n_i, s), "INT8 gate/up")
-            qk.check(L.qk_silu_mul_f32(gate.data_ptr(), up.data_ptr(), ntok * hidden, s), "silu")
-            qk.quantize(gate, xq, xs, hidden, n_tokens=ntok, stream=stream)
-            qk.check(L.qk_gemv_batched_i8(qk.Q6_K, wd.data_ptr(), xq.data_ptr(), hidden, xs.data_ptr(), hidden // 32,
-                                          y.data_ptr(), dim, hidden, dim, ntok, ws_i.data_ptr(), n_i, s), "INT8 down")
+        def run(i, down_type, downs):
+            wg, wu, _ = sets[i % copies]
+            qk.quantize(x, xq, xs, dim, n_tokens=ntok, stream=stream)
+            qk.check(L.qk_ffn_batched_i8(qk.Q4_K, wg.data_ptr(), qk.Q4_K, wu.data_ptr(), down_type,
+                                         downs[i % copies].data_ptr(), xq.data_ptr(), dim, xs.data_ptr(), dim // 32,
+                                         y.data_ptr(), dim, dim, hidden, ntok, 0, ws_i.data_ptr(), n_i, s), "INT8 FFN")
 
-        wall, ms = time_launches(torch, step, steps, warmup, stream)
+        wall, ms = time_launches(torch, lambda i: run(i, qk.Q6_K, [d for _, _, d in sets]), steps, warmup, stream)
+        _, ms_split = time_launches(torch, lambda i: run(i, qk.Q6_K_SPLIT, split_down), steps, warmup, stream)
         weights = 2 * qk.tensor_bytes(qk.Q4_K, dim, hidden) + qk.tensor_bytes(qk.Q6_K, hidden, dim)
-        # Per token: quantize x (4 dim in, dim + dim/8 out), gate and up
-        # (codes + scales in, 4 hidden out each), SiLU * up (8 hidden in,
-        # 4 hidden out), quantize h (4 hidden in, hidden + hidden/8 out),
-        # down (hidden + hidden/8 in, 4 dim out).
-        act = ntok * (4 * dim + 3 * (dim + dim // 8) + 8 * hidden + 12 * hidden + 4 * hidden
-                      + 2 * (hidden + hidden // 8) + 4 * dim)
+        # Per token: x in (4 dim), its codes and scales out and in again
+        # (dim + dim/8 each way), the hidden codes and scales out and in
+        # again (hidden + hidden/8 each way), y out (4 dim).
+        act = ntok * (4 * dim + 2 * (dim + dim // 8) + 2 * (hidden + hidden // 8) + 4 * dim)
         return {"tokens": ntok, "ms_per_step": round(ms, 4), "tokens_per_s": round(ntok / (ms * 1e-3), 1),
                 "bytes_per_step": weights + act, "GBps": round((weights + act) / (ms * 1e-3) / 1e9, 1),
                 "frac_of_peak": round((weights + act) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                "weight_copies": copies, "calls_per_step": 6}
+                "weight_copies": copies, "calls_per_step": 2, "launches_per_step": 3,
+                "split_q6k_down": {"ms_per_step": round(ms_split, 4),
+                                   "frac_of_peak": round((weights + act) / (ms_split * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}}
 
     # One call (qk_ffn_batched_f32): x packed once, gate / up on the matrix
     # cores with SiLU(gate) * up packed by their reduction straight into the

@@ -219,19 +219,24 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
                int ldscale, float *y, int ldy, int cols, int rows, int n_tokens,
                qk_stream stream);
 
-/* qk_gemv_i8 for a batch of tokens on the matrix cores: y[t*ldy + r] for
-   t < n_tokens, the reference's INT8 multi-token semantics (gemv_batch_dp4a,
-   qkv_batch_cuda, gate_up_batch_cuda, inferencer.cu:678-751; its default
-   batched mode, inferencer.cu:1611) without the 32-token cap and without
-   re-reading the weights per token.  From 8 tokens on, each token's codes
-   are multiplied by their per-32 scale while the activations are packed
-   (one fp32 rounding per value; exact when the scale is a power of two) and
-   the products with the exact integer weights d*sc*q - dmin*m (Q4_K) /
-   d*scale*(code - 32) (Q6_K) are summed by the FP32 matrix-core GEMM
-   (v_mfma_f32_32x32x16_f16 over fp16 integer weights and hi / lo halves of
-   the activations); below 8 tokens it is qk_gemv_i8.  workspace as for
-   qk_gemv_batched_f32 (qk_gemv_batched_workspace_bytes(cols, rows,
-   n_tokens)). */
+/* qk_gemv_i8 for a batch of tokens: y[t*ldy + r] for t < n_tokens, the
+   reference's INT8 multi-token semantics (gemv_batch_dp4a, inferencer.cu:
+   678-699; its default batched mode, inferencer.cu:1611) without the
+   32-token cap and without re-reading the weights per token.  From 8 tokens
+   on the exact integer sub-block dots run on the integer matrix cores
+   (v_mfma_i32_32x32x32_i8 per Q4_K sub-block of 32 columns,
+   v_mfma_i32_32x32x16_i8 per Q6_K sub-block of 16) for 32 tokens x 32 rows
+   at a time, and each sub-block is combined in fp32 as the reference does:
+   (d*sc*dot - dmin*m*sum(xq)) * xscale (Q4_K, inferencer.cu:520-542) and
+   d*scale*dot*xscale (Q6_K, 613-643; two sub-blocks sharing an xscale are
+   added in integers first); below 8 tokens it is qk_gemv_i8.  A workgroup
+   takes 32 rows x 32 tokens x up to 8 blocks of the row; rows longer than
+   2048 columns are split over workgroups and a second launch adds their
+   sums in order, which needs the workspace
+   (qk_gemv_batched_i8_workspace_bytes(cols, rows, n_tokens), 16-byte
+   aligned; 0 bytes, and NULL allowed, up to 2048 columns or below 8
+   tokens). */
+size_t qk_gemv_batched_i8_workspace_bytes(int cols, int rows, int n_tokens);
 int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                        float *y, int ldy, int cols, int rows, int n_tokens, void *workspace, size_t workspace_bytes,
                        qk_stream stream);
@@ -242,6 +247,33 @@ int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, cons
    Q6_K (either layout).  Each matrix's rows go to its own y. */
 int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const float *xscale, int cols,
                      qk_stream stream);
+
+/* The fused form of qk_gemv_batched_i8 (qkv_batch_cuda, gate_up_batch_cuda,
+   inferencer.cu:701-751): 1..QK_MAX_FUSED matrices (any mix of Q4_K, Q6_K
+   and split Q6_K) of cols columns read the same n_tokens quantized rows (xq
+   + t*ldxq, xscale + t*ldscale); mats[m].y receives [n_tokens][rows_m].
+   One launch from 8 tokens on (two above 2048 columns); workspace
+   qk_gemv_batched_i8_workspace_bytes(cols, sum of the rows, n_tokens). */
+int qk_gemv_multi_batched_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale,
+                             int ldscale, int cols, int n_tokens, void *workspace, size_t workspace_bytes,
+                             qk_stream stream);
+
+/* The feed-forward block in the reference's INT8 batched arithmetic for
+   n_tokens quantized rows of dim values: gate / up (gate_up_batch_cuda,
+   inferencer.cu:733-751), SiLU(gate) * up (silu_batch_cuda) quantized per 32
+   values (quantize_batch_cuda, 891-904), down (gemv_batch_dp4a), into
+   y[t*ldy + c] (overwritten, or added with accumulate: add_batch_cuda).
+   From 8 tokens on, the gate / up product forms SiLU * up and its
+   quantization in its own epilogue (or its reduction launch, above 2048
+   columns), then down.  gate and up have one storage type.  The workspace
+   holds the quantized hidden rows and the split sums:
+   qk_ffn_batched_i8_workspace_bytes(dim, hidden, n_tokens), 256-byte
+   aligned. */
+size_t qk_ffn_batched_i8_workspace_bytes(int dim, int hidden, int n_tokens);
+int qk_ffn_batched_i8(int gate_type, const void *gate, int up_type, const void *up, int down_type, const void *down,
+                      const int8_t *xq, int ldxq, const float *xscale, int ldscale, float *y, int ldy, int dim,
+                      int hidden, int n_tokens, int accumulate, void *workspace, size_t workspace_bytes,
+                      qk_stream stream);
 
 /* -------------------------------------------------------- step kernels -- */
 

@@ -110,6 +110,12 @@ SIGNATURES = {
     "qk_rmsnorm_quantize_x32": (_i, [_vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, ctypes.c_float, _vp]),
     "qk_gemv_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp]),
     "qk_gemv_batched_i8": (_i, [_i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _vp, ctypes.c_size_t, _vp]),
+    "qk_gemv_batched_i8_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i]),
+    "qk_gemv_multi_batched_i8": (_i, [ctypes.POINTER(qk_matrix), _i, _vp, _i, _vp, _i, _i, _i, _vp, ctypes.c_size_t,
+                                      _vp]),
+    "qk_ffn_batched_i8_workspace_bytes": (ctypes.c_size_t, [_i, _i, _i]),
+    "qk_ffn_batched_i8": (_i, [_i, _vp, _i, _vp, _i, _vp, _vp, _i, _vp, _i, _vp, _i, _i, _i, _i, _i, _vp,
+                               ctypes.c_size_t, _vp]),
     "qk_rmsnorm_f32": (_i, [_vp, _vp, _vp, _i, _i, _f, _vp]),
     "qk_rope_kv_write": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),
     "qk_attention_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp]),

@@ -98,11 +98,6 @@ struct BatchParams {
     float norm_eps;
     const float *up;        // stage x / (1 + exp(-x)) * up (up has x's layout)
     int accumulate;         // y += W x
-    // INT8 mode (x unused): activations xq[t*ldxq + c] * xscale[t*ldscale + c/32],
-    // the reference's per-32 quantized inputs.
-    const int8_t *xq;
-    const float *xscale;
-    int ldxq, ldscale;
     // Decode-driver chain (zero: none).  in_ss: per (token, input block) sums
     // of squares of the unnormalised input, whose RMSNorm is applied as an
     // output scale (W (s x * g) = s W (x * g)) where the outputs are final.
@@ -148,19 +143,10 @@ __device__ __forceinline__ float stage_norm_scale(const BatchParams &p, int t, i
 
 // The lane's four values of column c = b*256 + q*32 + 4j: x (times the
 // token's RMSNorm scale and the gain with norm_w; x / (1 + exp(-x)) * up
-// with up, silu_cuda, inferencer.cu:1053-1056), or in INT8 mode the codes
-// times their per-32 scale (exact products, rounded once); zero past the
-// last token.
+// with up, silu_cuda, inferencer.cu:1053-1056); zero past the last token.
 __device__ __forceinline__ void stage_load4(const BatchParams &p, int t, int c, float scale, float (&v)[4]) {
     v[0] = v[1] = v[2] = v[3] = 0.f;
     if (t >= p.n_tokens) return;
-    if (p.xq) {
-        const uint32_t w = *reinterpret_cast<const uint32_t *>(p.xq + static_cast<int64_t>(t) * p.ldxq + c);
-        const float xs = p.xscale[static_cast<int64_t>(t) * p.ldscale + c / 32];
-        #pragma unroll
-        for (int k = 0; k < 4; ++k) v[k] = static_cast<float>(static_cast<int8_t>((w >> (8 * k)) & 0xFFu)) * xs;
-        return;
-    }
     const int64_t at = static_cast<int64_t>(t) * p.ldx + c;
     const float4 u = *reinterpret_cast<const float4 *>(p.x + at);
     v[0] = u.x;
@@ -840,16 +826,9 @@ void launch_gemm(int type, const dim3 &grid, size_t lds, hipStream_t stream, con
         hipLaunchKernelGGL((batch_gemm<0, TT>), grid, dim3(256), lds, stream, p);
 }
 
-// INT8 activations of the matrix-core path (xq / xscale of n_tokens tokens).
-struct I8Input {
-    const int8_t *xq;
-    const float *xscale;
-    int ldxq, ldscale;
-};
-
 int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *x, int ldx, int cols, int n_tokens,
                 void *workspace, size_t workspace_size, hipStream_t stream, const char *where,
-                const GemvFusion *fusion = nullptr, const I8Input *i8 = nullptr) {
+                const GemvFusion *fusion = nullptr) {
     const int nb = cols / 256;
     const int tiles = tile_count(n_tokens);
     const int tt = token_tiles_per_group(tiles);
@@ -889,7 +868,7 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
     if (chain_out) {
         const bool pair = fusion->pair != 0;
         if ((pair && (n_mats != 2 || rows[0] != rows[1])) || (!pair && n_mats != 1) || rows[0] % 256 ||
-            (!pair && !fusion->out_gain) || (fusion->out_gain && !fusion->out_ss) || i8)
+            (!pair && !fusion->out_gain) || (fusion->out_gain && !fusion->out_ss))
             return fail(QK_ERR_INVALID_ARG, std::string(where) + ": unsupported chained reduction");
     }
     const size_t need = workspace_bytes(cols, rows, n_mats, n_tokens, need_partials);
@@ -913,12 +892,6 @@ int launch_mfma(const qk_matrix *mats, int n_mats, const int *ldy, const float *
         p.out_gain = fusion->out_gain;
         p.out_ss = fusion->out_ss;
         p.pair = fusion->pair;
-    }
-    if (i8) {
-        p.xq = i8->xq;
-        p.xscale = i8->xscale;
-        p.ldxq = i8->ldxq;
-        p.ldscale = i8->ldscale;
     }
     if (!(fusion && fusion->in_records))
         hipLaunchKernelGGL(pack_activations, dim3(nb, tiles * (kTokTile / kPackTokens)), dim3(256), 0, stream, p, ws);
@@ -1006,28 +979,6 @@ int qk_gemv_batched_f32(int type, const void *w, const float *x, int ldx, float 
         return qk::launch_mfma(&m, 1, &ldy, x, ldx, cols, n_tokens, workspace, workspace_bytes,
                                static_cast<hipStream_t>(stream), "qk_gemv_batched_f32");
     return qk::launch_gemv_f32(&m, 1, x, ldx, cols, n_tokens, &ldy, static_cast<hipStream_t>(stream));
-}
-
-int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
-                       float *y, int ldy, int cols, int rows, int n_tokens, void *workspace, size_t workspace_bytes,
-                       qk_stream stream) {
-    int st = qk::check_weights("qk_gemv_batched_i8", type, w, cols, rows);
-    if (st) return st;
-    if (!xq || !xscale || !y || n_tokens < 0)
-        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_batched_i8: null pointer or negative token count");
-    if (n_tokens == 0) return qk::ok();
-    if (ldxq < cols || ldscale < cols / 32 || ldy < rows)
-        return qk::fail(QK_ERR_INVALID_ARG, "qk_gemv_batched_i8: leading dimension smaller than the row");
-    if (!qk::aligned(xq, 16) || ldxq % 16 || !qk::aligned(xscale, 4) || !qk::aligned(y, 4))
-        return qk::fail(QK_ERR_ALIGN, "qk_gemv_batched_i8: xq and ldxq must keep 16-byte alignment");
-    const hipStream_t s = static_cast<hipStream_t>(stream);
-    const qk_matrix m{type, rows, w, y};
-    if (n_tokens < qk::kMfmaMinTokens)
-        return qk::launch_gemv_i8(&m, 1, xq, ldxq, xscale, ldscale, cols, n_tokens, &ldy, 0, s);
-    const qk::I8Input in{xq, xscale, ldxq, ldscale};
-    // x is unused in INT8 mode; any 16-byte aligned pointer passes the packer's checks.
-    return qk::launch_mfma(&m, 1, &ldy, reinterpret_cast<const float *>(xq), cols, cols, n_tokens, workspace,
-                           workspace_bytes, s, "qk_gemv_batched_i8", nullptr, &in);
 }
 
 size_t qk_ffn_batched_workspace_bytes(int dim, int hidden, int n_tokens) {

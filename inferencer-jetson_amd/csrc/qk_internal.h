@@ -104,6 +104,19 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
 // adds W x into y instead of overwriting it.
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                    int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
+// INT8 product of n_tokens per-32 quantized rows with n_mats matrices on
+// the integer matrix cores (csrc/qk_skinny.hip), arguments already
+// validated: y_m[t*ldy[m] + r] overwritten (or added with accumulate); with
+// out_xq, matrices 0 and 1 are a gate / up pair and SiLU(gate) * up is
+// quantized per 32 values into out_xq / out_xs (ldy and y unused).  Rows
+// longer than 2048 columns are split over workgroups whose sums a second
+// launch adds: the workspace holds them (skinny_i8_workspace_bytes of the
+// launch's row tiles: sum of ceil(rows / 32), or rows / 32 for a pair).
+size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair);
+int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
+                     const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
+                     float *out_xs, int out_ldxq, int out_ldxs, void *workspace, size_t workspace_size,
+                     hipStream_t stream, const char *where);
 // SiLU(gate) * up quantized per 32 values straight into xq / xscale (n a
 // multiple of 32): bit-identical to qk_silu_mul_f32 then qk_quantize_x32,
 // without the fp32 product written.  Arguments already validated.

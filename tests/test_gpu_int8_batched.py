@@ -40,7 +40,7 @@ def _run(qk, t, qtype, w, xq, xs, cols, rows, ntok):
     L = qk.lib()
     wd, xqd, xsd = to_dev(t, w), to_dev(t, xq), to_dev(t, xs)
     y = t.full((ntok, rows), float("nan"), device="cuda")
-    nws = L.qk_gemv_batched_workspace_bytes(cols, rows, ntok)
+    nws = L.qk_gemv_batched_i8_workspace_bytes(cols, rows, ntok)
     ws = t.empty(max(nws, 256), dtype=t.uint8, device="cuda")
     qk.check(L.qk_gemv_batched_i8(qtype, wd.data_ptr(), xqd.data_ptr(), LDXQ, xsd.data_ptr(), LDSCALE, y.data_ptr(),
                                   rows, cols, rows, ntok, ws.data_ptr(), nws, None), "batched INT8 GEMV")

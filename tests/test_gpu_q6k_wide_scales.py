@@ -121,7 +121,7 @@ def test_batched_int8_wide_scales(qk, torch_gpu, oracle, synth, ntok):
     for name, tensor in layouts(qk, t, w, cols, rows).items():
         xqd, xsd = to_dev(t, xq), to_dev(t, xs)
         y = t.full((ntok, rows), float("nan"), device="cuda")
-        nws = L.qk_gemv_batched_workspace_bytes(cols, rows, ntok)
+        nws = L.qk_gemv_batched_i8_workspace_bytes(cols, rows, ntok)
         ws = t.empty(max(nws, 256), dtype=t.uint8, device="cuda")
         qk.check(L.qk_gemv_batched_i8(tensor.type, tensor.gpu, xqd.data_ptr(), LDXQ, xsd.data_ptr(), LDSCALE,
                                       y.data_ptr(), rows, cols, rows, ntok, ws.data_ptr(), nws, None),
