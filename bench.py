@@ -469,7 +469,7 @@ def bench_mixed_1b_step(torch, qk, wl, steps: int = 10, warmup: int = 3) -> dict
             "mfma_ops_per_useful_product": 2}
 
 
-def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dict:
+def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2, int8: bool = False) -> dict:
     """Random-init Llama-3.2-1B decode step for 32 ragged sequences at once:
     sequence s decodes at position ctx_s - 1 with ctx_s ~ U[64, 2048] (the
     ragged descriptor of the 3B FFN workload, seed 3), its KV rows packed in
@@ -479,6 +479,8 @@ def bench_batch_decode_1b(torch, qk, wl, steps: int = 8, warmup: int = 2) -> dic
     cfg, n, kv_row, rows = case["cfg"], case["n"], case["kv_row"], case["rows"]
     W = wl.llama_weights(cfg, case["weights_seed"])
     runner = qk.BatchRunner(cfg, W, max_tokens=n, cache_rows=rows)
+    if int8:
+        runner.set_int8(True, True)
     kv_dim = cfg["dim"] // cfg["heads"] * cfg["kv_heads"]
     _fill_caches(torch, runner, cfg, rows, 2)
     tokens, pos = list(case["tokens"]), list(case["pos"])
@@ -551,7 +553,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--secondary", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--only", choices=["gemv", "copy", "stream", "ffn", "ffn_int8", "mixed", "mixed_step", "decode",
-                                       "decode_int8", "batch_decode"],
+                                       "decode_int8", "batch_decode", "batch_decode_int8"],
                     default="gemv",
                     help="copy / stream: time the reference bandwidth kernels of libqkbench.so instead "
                          "(a plain 256 MiB copy calibrates FETCH_SIZE / WRITE_SIZE; a streaming read gives "
@@ -579,7 +581,8 @@ def main() -> int:
                "mixed_step": lambda: bench_mixed_1b_step(torch, qk, wl),
                "decode": lambda: bench_decode_1b(torch, qk, wl),
                "decode_int8": lambda: bench_decode_1b(torch, qk, wl, int8=True),
-               "batch_decode": lambda: bench_batch_decode_1b(torch, qk, wl)}[args.only]
+               "batch_decode": lambda: bench_batch_decode_1b(torch, qk, wl),
+               "batch_decode_int8": lambda: bench_batch_decode_1b(torch, qk, wl, int8=True)}[args.only]
         print(json.dumps({args.only: run()}), flush=True)
         return 0
     stream = torch.cuda.current_stream()
@@ -679,6 +682,8 @@ def main() -> int:
         log(f"[bench] llama_1b_decode_int8: {json.dumps(sec['llama_1b_decode_int8'])}")
         sec["llama_1b_batch_decode_32"] = bench_batch_decode_1b(torch, qk, wl)
         log(f"[bench] llama_1b_batch_decode_32: {json.dumps(sec['llama_1b_batch_decode_32'])}")
+        sec["llama_1b_batch_decode_32_int8"] = bench_batch_decode_1b(torch, qk, wl, int8=True)
+        log(f"[bench] llama_1b_batch_decode_32_int8: {json.dumps(sec['llama_1b_batch_decode_32_int8'])}")
         result["secondary"] = sec
 
     if not args.no_cpu_baseline:

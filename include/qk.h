@@ -485,6 +485,17 @@ int qk_llama_batch_residual(qk_llama_batch *m, const float **x);
    one per logit row (FastRunner::prefill's counts, inferencer.cu:1277, 1321,
    1368). */
 int qk_llama_batch_matrix_calls(const qk_llama_batch *m, uint64_t *calls);
+/* The reference's INT8 batched arithmetic for the steps that follow
+   (FastRunner::prefill with use_dp4a and use_q6_dp4a, inferencer.cu:
+   1279-1423; its batched prefill requires both, 1662-1663): per layer
+   RMSNorm and per-32 quantization of x, the fused QKV product, attention,
+   the attention output quantized, o added into x, RMSNorm and quantization,
+   gate / up with SiLU(gate) * up quantized, down added into x; the LM head
+   over the RMSNorm of x quantized.  Products run as qk_gemv_multi_batched_i8
+   (exact integer sub-block dots).  q4k_int8 and q6k_int8 must be equal
+   (QK_ERR_INVALID_ARG otherwise); the first enable allocates the quantized
+   activation buffers (QK_ERR_DEVICE when they do not fit). */
+int qk_llama_batch_set_int8(qk_llama_batch *m, int q4k_int8, int q6k_int8);
 /* One step for n_tokens tokens: tokens[t] (host) at desc[t] (host).  Every
    token writes its key / value row kv_row + pos before any token's
    attention reads the cache, so a token sees the rows of earlier positions

@@ -151,6 +151,7 @@ SIGNATURES = {
     "qk_llama_batch_logits": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_matrix_calls": (_i, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
+    "qk_llama_batch_set_int8": (_i, [_vp, _i, _i]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
     "qk_llama_batch_forward_rows": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i,
@@ -651,6 +652,11 @@ class BatchRunner:
         p = ctypes.c_void_p()
         check(lib().qk_llama_batch_residual(self.handle, ctypes.byref(p)), "residual")
         return copy_to_host(p.value, n_tokens * self.cfg["dim"], np.float32).reshape(n_tokens, self.cfg["dim"])
+
+    def set_int8(self, q4k: bool = True, q6k: bool = True) -> None:
+        """The reference's INT8 batched arithmetic (both types or neither;
+        qk_llama_batch_set_int8)."""
+        check(lib().qk_llama_batch_set_int8(self.handle, int(q4k), int(q6k)), "set_int8")
 
     def matrix_calls(self) -> int:
         """Quantized matrix products issued since create (qk_llama_batch_matrix_calls)."""

@@ -653,6 +653,14 @@ struct qk_llama_batch {
     std::vector<int64_t> kv_writes;   // host scratch of the KV-row check
     qk_llama_memory mem{};        // device bytes the handle holds
     uint64_t matrix_calls = 0;    // quantized matrix products issued (FastGPU::calls)
+    // INT8 mode (qk_llama_batch_set_int8; buffers made at its first enable):
+    // quantized inputs of dim (xq / xs) and hidden (hq / hs) columns per
+    // token, and the split sums of the matrix-core products.
+    int int8 = 0;
+    int8_t *xq = nullptr, *hq = nullptr;
+    float *xs = nullptr, *hs = nullptr;
+    void *i8_ws = nullptr;
+    size_t i8_ws_bytes = 0;
 };
 
 namespace {
@@ -660,7 +668,7 @@ namespace {
 void release_batch(qk_llama_batch *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->attn_ws, m->d_tokens, m->d_next,
-                    m->d_rows, m->d_desc, m->rec_a, m->rec_b, m->ss};
+                    m->d_rows, m->d_desc, m->rec_a, m->rec_b, m->ss, m->xq, m->hq, m->xs, m->hs, m->i8_ws};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
@@ -697,9 +705,106 @@ int check_kv_rows(const qk_batch_token *desc, int n, std::vector<int64_t> &write
     return QK_OK;
 }
 
+// INT8 products of T tokens (the reference's dp4a paths): the GEMV kernels
+// below 8 tokens, the integer matrix cores from 8 on.
+int batch_gemm_i8(qk_llama_batch *m, const qk_matrix *mats, int n, const int8_t *xq, const float *xs, int cols, int T,
+                  bool accumulate, hipStream_t s) {
+    int ldy[QK_MAX_FUSED];
+    for (int i = 0; i < n; ++i) ldy[i] = mats[i].rows;
+    if (T < 8) return qk::launch_gemv_i8(mats, n, xq, cols, xs, cols / 32, cols, T, ldy, accumulate, s);
+    return qk::launch_skinny_i8(mats, n, ldy, xq, cols, xs, cols / 32, cols, T, accumulate, nullptr, nullptr, 0, 0,
+                                m->i8_ws, m->i8_ws_bytes, s, "qk_llama_batch_forward");
+}
+
+// The layers of an INT8 step, the reference's batched INT8 arithmetic
+// (FastRunner::prefill, inferencer.cu:1279-1423) for any ragged batch: per
+// layer RMSNorm and quantization of x (rmsnorm_quantize_batch_cuda), the
+// fused QKV product (qkv_batch_cuda), RoPE + KV write + attention, the
+// attention output quantized and o added into x (batch_matvec +
+// add_batch_cuda), RMSNorm and quantization, gate / up with SiLU(gate) * up
+// quantized (gate_up_batch_cuda, silu_batch_cuda, and down's quantization),
+// down added into x.
+int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention &attn, hipStream_t s) {
+    const qk_llama_config &c = m->cfg;
+    const int dim = c.dim, hidden = c.hidden, kv = m->kv_dim, hd = m->head_dim;
+    int st;
+    auto norm_quant = [&](const float *w) {
+        return qk_rmsnorm_quantize_x32(m->x, dim, w, nullptr, 0, m->xq, dim, m->xs, dim / 32, dim, T, c.eps, s);
+    };
+    for (int l = 0; l < c.layers; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = norm_quant(L.attn_norm)) || (st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s)))
+            return st;
+        if (chained &&
+            (st = qk::launch_rope_kv_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
+                                             m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, 1, s)))
+            return st;
+        attn.layer = l;
+        attn.gemm_rec = nullptr;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->x};
+        if ((st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xs, dim / 32, dim, T, s)) ||
+            (st = batch_gemm_i8(m, &o, 1, m->xq, m->xs, dim, T, true, s)) || (st = norm_quant(L.ffn_norm)))
+            return st;
+        const qk_matrix gu[2] = {{L.gate_type, hidden, L.gate, m->gate}, {L.up_type, hidden, L.up, m->up}};
+        if (T >= 8 && L.gate_type == L.up_type) {
+            // SiLU(gate) * up quantized in the product's own epilogue.
+            if ((st = qk::launch_skinny_i8(gu, 2, nullptr, m->xq, dim, m->xs, dim / 32, dim, T, 0, m->hq, m->hs, hidden,
+                                           hidden / 32, m->i8_ws, m->i8_ws_bytes, s, "qk_llama_batch_forward")))
+                return st;
+        } else if ((st = batch_gemm_i8(m, gu, 2, m->xq, m->xs, dim, T, false, s)) ||
+                   (st = qk::launch_silu_mul_quantize(m->gate, m->up, m->hq, m->hs, T * hidden, s))) {
+            return st;
+        }
+        const qk_matrix down{L.down_type, dim, L.down, m->x};
+        if ((st = batch_gemm_i8(m, &down, 1, m->hq, m->hs, hidden, T, true, s))) return st;
+    }
+    return QK_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int qk_llama_batch_set_int8(qk_llama_batch *m, int q4k_int8, int q6k_int8) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_set_int8: null handle");
+    if ((q4k_int8 != 0) != (q6k_int8 != 0))
+        return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_set_int8: the batched step runs INT8 for both Q4_K and "
+                                            "Q6_K or for neither");
+    if (q4k_int8 && !m->xq) {
+        const qk_llama_config &c = m->cfg;
+        const size_t T = static_cast<size_t>(m->max_tokens);
+        const int kv = m->kv_dim;
+        auto tiles = [](int rows) { return (rows + 31) / 32; };
+        size_t ws = 0;
+        ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.dim, tiles(c.dim) + 2 * tiles(kv), m->max_tokens, false));
+        ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.dim, tiles(c.hidden), m->max_tokens, true));
+        ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.hidden, tiles(c.dim), m->max_tokens, false));
+        ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.dim, tiles(c.vocab), m->max_tokens, false));
+        const uint64_t need = T * (c.dim + c.hidden) * (1 + sizeof(float) / 32.0) + ws + 1024;
+        int st;
+        if ((st = check_free_memory("qk_llama_batch_set_int8", need))) return st;
+        uint64_t bytes = 0;
+        if ((st = dev_alloc(bytes, &m->xq, T * c.dim, "quantized activations")) ||
+            (st = dev_alloc(bytes, &m->xs, T * (c.dim / 32), "activation scales")) ||
+            (st = dev_alloc(bytes, &m->hq, T * c.hidden, "quantized hidden activations")) ||
+            (st = dev_alloc(bytes, &m->hs, T * (c.hidden / 32), "hidden activation scales")) ||
+            (ws && (st = dev_alloc(bytes, reinterpret_cast<uint8_t **>(&m->i8_ws), ws, "split sums")))) {
+            for (void *b : {static_cast<void *>(m->xq), static_cast<void *>(m->xs), static_cast<void *>(m->hq),
+                            static_cast<void *>(m->hs), m->i8_ws})
+                (void)hipFree(b);
+            m->xq = m->hq = nullptr;
+            m->xs = m->hs = nullptr;
+            m->i8_ws = nullptr;
+            return st;
+        }
+        m->i8_ws_bytes = ws;
+        m->mem.buffers += bytes;
+    }
+    m->int8 = q4k_int8 != 0;
+    return qk::ok();
+}
 
 int qk_llama_batch_create(const qk_llama_config *cfg, const qk_llama_weights *w, int max_tokens, int64_t cache_rows,
                           qk_stream stream, qk_llama_batch **out) {
@@ -954,7 +1059,8 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     // layer (one more with split attention) instead of thirteen.
     const bool chain = qk::batched_chain_supported(T) && m->rec_a;
     const bool attn_records = chain && qk::attention_gemm_records(attn);
-    for (int l = 0; l < c.layers; ++l) {
+    if (m->int8 && (st = batch_layers_int8(m, T, chained, attn, s))) return st;
+    for (int l = 0; l < c.layers && !m->int8; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
         ffn_in.norm_w = L.ffn_norm;
@@ -1023,7 +1129,16 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
-    if ((st = qk::launch_batched_fused(&head, 1, head_x, dim, dim, n_rows, out_in, ws, wsb, s))) return st;
+    if (m->int8) {
+        // rmsnorm_cuda, then gpu.matvec's quantization and INT8 product
+        // (inferencer.cu:1408-1414) for the selected rows.
+        if ((st = qk_rmsnorm_quantize_x32(head_x, dim, m->w.output_norm, nullptr, 0, m->xq, dim, m->xs, dim / 32, dim,
+                                          n_rows, c.eps, s)) ||
+            (st = batch_gemm_i8(m, &head, 1, m->xq, m->xs, dim, n_rows, false, s)))
+            return st;
+    } else if ((st = qk::launch_batched_fused(&head, 1, head_x, dim, dim, n_rows, out_in, ws, wsb, s))) {
+        return st;
+    }
     if ((st = qk_argmax_rows_f32(m->logits, c.vocab, c.vocab, n_rows, m->d_next, m->argmax_ws, s))) return st;
     if (hipMemcpyAsync(h_next, m->d_next, n_rows * sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
         hipStreamSynchronize(s) != hipSuccess)
