@@ -447,6 +447,15 @@ int qk_llama_residual(qk_llama *m, const float **x);
    count FastGPU::calls keeps for the --stats line "GPU pipeline ... across
    N quantized matrix calls" (inferencer.cu:1170, 1457, 1500, 1909-1910). */
 int qk_llama_matrix_calls(const qk_llama *m, uint64_t *calls);
+/* The per-layer state --compare-prefill reads (FastRunner::forward's
+   layer_trace and quant_trace, inferencer.cu:1424-1531): while set, every
+   step copies the residual stream after each layer to residuals
+   [layer][dim] and, for the products that run in an INT8 mode, their
+   quantized inputs to quantized [layer][4][max(dim, hidden)] -- QKV,
+   attention output (o), gate / up, down; the first dim (down: hidden)
+   bytes of each slot.  Both are device buffers the caller owns (either may
+   be NULL); the copies run on the handle's stream. */
+int qk_llama_set_trace(qk_llama *m, float *residuals, int8_t *quantized);
 /* One decode step at position pos (FastRunner::forward, inferencer.cu:1424-1531).
    With need_logits, *next_token receives the greedy token (synchronises the
    stream like the reference's 4-byte copy, inferencer.cu:1529); otherwise
@@ -485,6 +494,11 @@ int qk_llama_batch_residual(qk_llama_batch *m, const float **x);
    one per logit row (FastRunner::prefill's counts, inferencer.cu:1277, 1321,
    1368). */
 int qk_llama_batch_matrix_calls(const qk_llama_batch *m, uint64_t *calls);
+/* qk_llama_set_trace for the batched driver (FastRunner::prefill's
+   all_layer_trace and quant_trace, inferencer.cu:1279-1423): per token of
+   the step, residuals [token][layer][dim] and, in the INT8 mode, quantized
+   [token][layer][4][max(dim, hidden)]; sized for the step's n_tokens. */
+int qk_llama_batch_set_trace(qk_llama_batch *m, float *residuals, int8_t *quantized);
 /* The reference's INT8 batched arithmetic for the steps that follow
    (FastRunner::prefill with use_dp4a and use_q6_dp4a, inferencer.cu:
    1279-1423; its batched prefill requires both, 1662-1663): per layer

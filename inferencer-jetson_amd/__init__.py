@@ -152,6 +152,8 @@ SIGNATURES = {
     "qk_llama_batch_residual": (_i, [_vp, ctypes.POINTER(ctypes.c_void_p)]),
     "qk_llama_batch_matrix_calls": (_i, [_vp, ctypes.POINTER(ctypes.c_uint64)]),
     "qk_llama_batch_set_int8": (_i, [_vp, _i, _i]),
+    "qk_llama_set_trace": (_i, [_vp, _vp, _vp]),
+    "qk_llama_batch_set_trace": (_i, [_vp, _vp, _vp]),
     "qk_llama_batch_forward": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i, _i,
                                     ctypes.POINTER(ctypes.c_int32)]),
     "qk_llama_batch_forward_rows": (_i, [_vp, ctypes.POINTER(ctypes.c_int32), ctypes.POINTER(qk_batch_token), _i,
@@ -557,6 +559,13 @@ class Runner:
         check(lib().qk_llama_residual(self.handle, ctypes.byref(p)), "residual")
         return copy_to_host(p.value, self.cfg["dim"], np.float32)
 
+    def set_trace(self, residuals: "DeviceBuffer | None", quantized: "DeviceBuffer | None" = None) -> None:
+        """Per-layer residuals [layer][dim] and INT8 inputs [layer][4][max(dim,
+        hidden)] of every following step (qk_llama_set_trace); None stops."""
+        self._trace = (residuals, quantized)
+        check(lib().qk_llama_set_trace(self.handle, residuals.ptr if residuals else None,
+                                       quantized.ptr if quantized else None), "set_trace")
+
     def matrix_calls(self) -> int:
         """Quantized matrix products issued since create (qk_llama_matrix_calls)."""
         n = ctypes.c_uint64()
@@ -653,6 +662,14 @@ class BatchRunner:
         check(lib().qk_llama_batch_residual(self.handle, ctypes.byref(p)), "residual")
         return copy_to_host(p.value, n_tokens * self.cfg["dim"], np.float32).reshape(n_tokens, self.cfg["dim"])
 
+    def set_trace(self, residuals: "DeviceBuffer | None", quantized: "DeviceBuffer | None" = None) -> None:
+        """Per token of each following step, residuals [token][layer][dim] and
+        INT8 inputs [token][layer][4][max(dim, hidden)]
+        (qk_llama_batch_set_trace); None stops."""
+        self._trace = (residuals, quantized)
+        check(lib().qk_llama_batch_set_trace(self.handle, residuals.ptr if residuals else None,
+                                             quantized.ptr if quantized else None), "set_trace")
+
     def set_int8(self, q4k: bool = True, q6k: bool = True) -> None:
         """The reference's INT8 batched arithmetic (both types or neither;
         qk_llama_batch_set_int8)."""
@@ -694,6 +711,8 @@ def _hip() -> ctypes.CDLL:
         h.hipMemcpy2D.restype = _i
         h.hipDeviceSynchronize.argtypes = []
         h.hipDeviceSynchronize.restype = _i
+        h.hipMalloc.argtypes, h.hipMalloc.restype = [ctypes.POINTER(_vp), ctypes.c_size_t], _i
+        h.hipFree.argtypes, h.hipFree.restype = [_vp], _i
         h.hipEventCreate.argtypes, h.hipEventCreate.restype = [ctypes.POINTER(_vp)], _i
         h.hipEventDestroy.argtypes, h.hipEventDestroy.restype = [_vp], _i
         h.hipEventRecord.argtypes, h.hipEventRecord.restype = [_vp, _vp], _i
@@ -702,6 +721,32 @@ def _hip() -> ctypes.CDLL:
         h.hipEventElapsedTime.restype = _i
         _HIP = h
     return _HIP
+
+
+class DeviceBuffer:
+    """nbytes of device memory owned by this object (hipMalloc / hipFree),
+    for buffers the C ABI fills, such as the drivers' traces."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _vp()
+        if _hip().hipMalloc(ctypes.byref(p), max(self.nbytes, 1)) != 0:
+            raise QKError("DeviceBuffer", QK_ERR_DEVICE, f"hipMalloc of {self.nbytes} bytes failed")
+        self.ptr = p.value
+
+    def host(self, dtype, count: int | None = None):
+        """The first count values (all by default) as a host array."""
+        import numpy as np
+        size = np.dtype(dtype).itemsize
+        return copy_to_host(self.ptr, self.nbytes // size if count is None else count, dtype)
+
+    def close(self) -> None:
+        if getattr(self, "ptr", None) and _HIP is not None:
+            _HIP.hipDeviceSynchronize()
+            _HIP.hipFree(self.ptr)
+        self.ptr = None
+
+    __del__ = close
 
 
 class GpuTimer:

@@ -13,9 +13,11 @@ Differences from the reference, each because the kernels here differ:
   no effect: every launch here is sized per shape by the library.
 * --fused-norm-quant, --fused-rope-cache and --fused-small-kernels are
   accepted; the decode step here always runs fused.
-* --prefill-batch N > 1 does not require the INT8 paths: the batched driver
-  computes in FP32 whatever the decode mode, and the prompt's cache rows are
-  handed to the one-sequence driver for decoding.
+* --prefill-batch N > 1 runs the batched driver in the decode mode: INT8
+  for both types (the default; the reference's only batched mode) or, with
+  --float-gemv, FP32 for both (an addition).  Like the reference, a mixed
+  mode (--float-q6) is rejected with batched prefill.  The prompt's cache
+  rows are then handed to the one-sequence driver for decoding.
 * There is no board power meter (the reference reads Jetson's VDD_IN), so
   no energy figures are printed.
 """
@@ -136,6 +138,8 @@ def parse(argv: list[str], stdin) -> Options | None:
         raise ValueError("--gate-warps and --q6-warps must be 2, 4, 8, or 16")
     if not 1 <= o.prefill_batch <= 32:
         raise ValueError("--prefill-batch must be in 1..32")
+    if o.prefill_batch > 1 and o.use_dp4a != o.use_q6_dp4a:
+        raise ValueError("Batched prefill runs Q4_K and Q6_K in one mode: INT8 (the default) or FP32 (--float-gemv)")
     if o.compare_prefill and (o.tokenize_only or o.prefill_batch == 1):
         raise ValueError("--compare-prefill requires --prefill-batch 2..32 and GPU inference")
     if len(o.prompts) > 1:
@@ -217,6 +221,7 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                 runner.set_int8(o.use_dp4a, o.use_q6_dp4a)
                 if o.prefill_batch > 1:
                     batch = qk.BatchRunner.from_gguf(model, o.context, o.prefill_batch, o.context)
+                    batch.set_int8(o.use_dp4a, o.use_q6_dp4a)
                 timer = qk.GpuTimer()
             t_ready = time.perf_counter()
             stderr.write(f"Q4_K matrix path: {'INT8' if o.use_dp4a else 'FP32'}; Q6_K matrix path: "
@@ -233,7 +238,7 @@ def run(argv: list[str], stdout=None, stderr=None, stdin=None) -> int:
                 # runner->reset() does.
                 r = qk.Runner.from_gguf(model, o.context)
                 b = qk.BatchRunner.from_gguf(model, o.context, o.prefill_batch, o.context)
-                rep = cmp.compare_prefill(qk, r, b, ids, steps, o.prefill_batch)
+                rep = cmp.compare_prefill(qk, r, b, ids, steps, o.prefill_batch, int8=o.use_dp4a)
                 r.close()
                 b.close()
                 stdout.write(("\n".join(cmp.format_report(p + 1, rep)) + "\n").encode())

@@ -4,25 +4,30 @@
 The baseline runs the prompt one token per step through the one-sequence
 driver (Runner, FastRunner::forward), the batched run feeds it as prefill
 chunks of `chunk` tokens through the batched driver (BatchRunner; several
-tokens of one sequence per step, causal within the chunk), and both then
-decode `steps` greedy tokens.  Reported, as the reference does:
+tokens of one sequence per step, causal within the chunk), both in one
+arithmetic mode (the reference's INT8 modes, or FP32), and both then decode
+`steps` greedy tokens.  Both drivers trace every prompt token's residual
+after each layer, and in the INT8 mode the quantized inputs of each layer's
+four products (qk_llama_set_trace, qk_llama_batch_set_trace).  Reported, as
+the reference does:
 
 * the residual stream after the prompt (max abs and RMS difference,
   inferencer.cu:1764-1767);
-* per layer, the prompt's key and value cache rows (the reference traces the
-  per-layer residuals of every prompt token and names the first layer
-  differing by more than 1e-6, inferencer.cu:1768-1782; the cache rows are
-  what both drivers keep per layer);
+* per prompt token, the first layer whose residual differs by more than
+  1e-6 (1768-1782);
+* INT8: the first layer where the first token's quantized inputs differ,
+  with the mismatch counts [QKV, attention output, gate/up, down]
+  (1783-1797);
+* per layer, the last token's residual difference and, INT8, its mismatch
+  counts (1798-1813);
 * per decode step, both greedy tokens, the baseline's top-2 logit margin
-  and the logits' max abs / RMS difference (inferencer.cu:1814-1825).
-
-The reference's INT8 mismatch counts (inferencer.cu:1783-1813) have no
-counterpart: the batched driver computes in FP32 (block fixed point), so the
-comparison is run with the one-sequence driver in its FP32 mode.
+  and the logits' max abs / RMS difference (1814-1825).
 """
 from __future__ import annotations
 
 import numpy as np
+
+STAGES = "[QKV, attention output, gate/up, down]"
 
 
 def _diff(a, b) -> tuple[float, float]:
@@ -37,24 +42,44 @@ def _rms(a) -> float:
     return float(np.sqrt(np.mean(a * a))) if a.size else 0.0
 
 
-def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dict:
+def _counts(a, b, dim: int, hidden: int) -> list[int]:
+    """Mismatching codes per stage; a, b: [4][max(dim, hidden)] int8."""
+    widths = (dim, dim, dim, hidden)
+    return [int(np.count_nonzero(a[s, :w] != b[s, :w])) for s, w in enumerate(widths)]
+
+
+def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int, int8: bool = False) -> dict:
     """Run both prefills of input_ids and `steps` greedy steps each.
 
-    runner: a Runner (FP32 mode) with context >= len(input_ids) + steps;
-    batch: a BatchRunner with max_tokens >= chunk and cache_rows >=
-    len(input_ids) + steps (the sequence's rows start at row 0)."""
+    runner: a Runner with context >= len(input_ids) + steps; batch: a
+    BatchRunner with max_tokens >= chunk and cache_rows >= len(input_ids) +
+    steps (the sequence's rows start at row 0); int8: both run the
+    reference's INT8 modes (set_int8), else FP32."""
     ids = [int(t) for t in input_ids]
     n = len(ids)
     if n < 1 or steps < 1 or chunk < 1:
         raise ValueError("compare_prefill needs a prompt, steps >= 1 and chunk >= 1")
     c = runner.cfg
+    layers, dim, hidden = c["layers"], c["dim"], c["hidden"]
+    qs = max(dim, hidden)
+    runner.set_int8(int8, int8)
+    batch.set_int8(int8, int8)
 
-    # Baseline: one token per step (inferencer.cu:1731-1740).
+    # Baseline: one token per step (inferencer.cu:1731-1740), each step's
+    # per-layer residuals and quantized inputs traced.
+    tx = qk.DeviceBuffer(layers * dim * 4)
+    tq = qk.DeviceBuffer(layers * 4 * qs)
+    runner.set_trace(tx, tq)
+    base_layers = np.empty((n, layers, dim), dtype=np.float32)
+    base_q = {}
     nxt = 0
     for i, t in enumerate(ids):
         nxt = runner.forward(t, i, i + 1 == n)
+        base_layers[i] = tx.host(np.float32).reshape(layers, dim)
+        if int8 and i in (0, n - 1):
+            base_q[i] = tq.host(np.int8).reshape(layers, 4, qs)
+    runner.set_trace(None, None)
     base_res = runner.residual()
-    base_k, base_v = runner.kv_rows(n)
     base_ids, base_logits = [], []
     for i in range(steps):
         base_ids.append(nxt)
@@ -63,17 +88,27 @@ def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dic
             nxt = runner.forward(nxt, n + i, True)
 
     # Batched: prefill chunks of one sequence (kv_row 0), logits for the
-    # prompt's last token only.
+    # prompt's last token only, every chunk's tokens traced.
+    bx = qk.DeviceBuffer(chunk * layers * dim * 4)
+    bq = qk.DeviceBuffer(chunk * layers * 4 * qs)
+    batch.set_trace(bx, bq)
+    bat_layers = np.empty((n, layers, dim), dtype=np.float32)
+    bat_q = {}
     for c0 in range(0, n, chunk):
         part = ids[c0:c0 + chunk]
         m = len(part)
-        last = c0 + m == n
-        if last:
+        if c0 + m == n:
             nxt = batch.forward(part, list(range(c0, c0 + m)), [0] * m, seq=[0] * m, logit_rows=[m - 1])[0]
         else:
             batch.forward(part, list(range(c0, c0 + m)), [0] * m, False, seq=[0] * m)
+        bat_layers[c0:c0 + m] = bx.host(np.float32, m * layers * dim).reshape(m, layers, dim)
+        if int8:
+            q = bq.host(np.int8, m * layers * 4 * qs).reshape(m, layers, 4, qs)
+            for i in (0, n - 1):
+                if c0 <= i < c0 + m:
+                    bat_q[i] = q[i - c0]
+    batch.set_trace(None, None)
     bat_res = batch.residual(len(ids[(n - 1) // chunk * chunk:]))[-1]
-    bat_k, bat_v = batch.kv_rows(n)
     bat_ids, bat_logits = [], []
     for i in range(steps):
         bat_ids.append(nxt)
@@ -81,15 +116,28 @@ def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dic
         if i + 1 < steps:
             nxt = batch.forward([nxt], [n + i], [0], True, seq=[0])[0]
 
-    layers = []
-    first = None
-    for layer in range(c["layers"]):
-        km, kr = _diff(base_k[layer], bat_k[layer])
-        vm, vr = _diff(base_v[layer], bat_v[layer])
-        layers.append({"layer": layer, "key_max": km, "key_rms": kr, "value_max": vm, "value_rms": vr,
-                       "key_ref_rms": _rms(base_k[layer]), "value_ref_rms": _rms(base_v[layer])})
-        if first is None and max(km, vm) > 1e-6:
-            first = layer
+    token_first = []
+    for t in range(n):
+        for layer in range(layers):
+            mx, rms = _diff(base_layers[t, layer], bat_layers[t, layer])
+            if mx > 1e-6:
+                token_first.append({"token": t, "id": ids[t], "layer": layer, "max": mx, "rms": rms})
+                break
+    first_int8 = None
+    if int8:
+        for layer in range(layers):
+            cnt = _counts(base_q[0][layer], bat_q[0][layer], dim, hidden)
+            if any(cnt):
+                first_int8 = {"layer": layer, "counts": cnt}
+                break
+    layer_rows = []
+    for layer in range(layers):
+        mx, rms = _diff(base_layers[n - 1, layer], bat_layers[n - 1, layer])
+        row = {"layer": layer, "residual_max": mx, "residual_rms": rms,
+               "residual_ref_rms": _rms(base_layers[n - 1, layer])}
+        if int8:
+            row["int8_mismatches"] = _counts(base_q[n - 1][layer], bat_q[n - 1][layer], dim, hidden)
+        layer_rows.append(row)
     step_rows = []
     for i in range(steps):
         lg = base_logits[i]
@@ -99,21 +147,28 @@ def compare_prefill(qk, runner, batch, input_ids, steps: int, chunk: int) -> dic
         step_rows.append({"step": i + 1, "baseline_token": tid, "batched_token": bat_ids[i],
                           "top2_margin": float(lg[tid]) - second, "logit_max": mx, "logit_rms": rms})
     rm, rr = _diff(base_res, bat_res)
-    return {"tokens": n, "chunk": chunk, "residual_max": rm, "residual_rms": rr, "residual_ref_rms": _rms(base_res),
-            "layers": layers,
-            "first_layer_over_1e-6": first, "steps": step_rows}
+    return {"tokens": n, "chunk": chunk, "int8": int8, "residual_max": rm, "residual_rms": rr,
+            "residual_ref_rms": _rms(base_res), "token_first_over_1e-6": token_first,
+            "first_int8_difference": first_int8, "layers": layer_rows, "steps": step_rows}
 
 
 def format_report(index: int, rep: dict) -> list[str]:
-    """The report as text lines in the reference's wording (inferencer.cu:1766-1825)."""
+    """The report as text lines in the reference's format (inferencer.cu:1766-1825)."""
     out = [f"Prompt {index}: residual max abs difference {rep['residual_max']:.9g}, "
            f"RMS difference {rep['residual_rms']:.9g}"]
-    if rep["first_layer_over_1e-6"] is not None:
-        out.append(f"  first key/value cache difference >1e-6 at layer {rep['first_layer_over_1e-6']}")
+    for t in rep["token_first_over_1e-6"]:
+        out.append(f"  input token {t['token']} (id {t['id']}): first residual difference >1e-6 at layer "
+                   f"{t['layer']}, max {t['max']:.9g}, RMS {t['rms']:.9g}")
+    f = rep["first_int8_difference"]
+    if f is not None:
+        out.append(f"  input token 0 first INT8 differences at layer {f['layer']} {STAGES} "
+                   + "/".join(str(x) for x in f["counts"]))
     for L in rep["layers"]:
-        out.append(f"  layer {L['layer']}: key cache max abs difference {L['key_max']:.9g}, RMS difference "
-                   f"{L['key_rms']:.9g}; value cache max abs difference {L['value_max']:.9g}, RMS difference "
-                   f"{L['value_rms']:.9g}")
+        line = (f"  layer {L['layer']}: residual max abs difference {L['residual_max']:.9g}, RMS difference "
+                f"{L['residual_rms']:.9g}")
+        if "int8_mismatches" in L:
+            line += f", INT8 differences {STAGES} " + "/".join(str(x) for x in L["int8_mismatches"])
+        out.append(line)
     for s in rep["steps"]:
         out.append(f"  step {s['step']}: baseline token {s['baseline_token']}, batched token {s['batched_token']}, "
                    f"baseline top-2 margin {s['top2_margin']:.9g}, logit max abs difference {s['logit_max']:.9g}, "

@@ -51,9 +51,30 @@ struct qk_llama {
     std::vector<void *> owned;    // split-layout copies of the Q6_K weights
     qk_llama_memory mem{};        // device bytes the handle holds
     uint64_t matrix_calls = 0;    // quantized matrix products issued (FastGPU::calls)
+    // qk_llama_set_trace: the residual after each layer [layer][dim] and the
+    // INT8 inputs of each layer's products [layer][4][max(dim, hidden)].
+    float *trace_x = nullptr;
+    int8_t *trace_q = nullptr;
 };
 
 namespace {
+
+// Trace copies of a step (device to device, on the step's stream).
+int trace_copy(void *dst, const void *src, size_t bytes, hipStream_t s) {
+    if (!dst) return QK_OK;
+    if (hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, s) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "trace copy failed");
+    return QK_OK;
+}
+
+// The same for the rows of a batch: rows of `width` bytes `spitch` apart
+// into rows `dpitch` apart.
+int trace_copy_2d(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width, int rows, hipStream_t s) {
+    if (!dst) return QK_OK;
+    if (hipMemcpy2DAsync(dst, dpitch, src, spitch, width, rows, hipMemcpyDeviceToDevice, s) != hipSuccess)
+        return qk::fail(QK_ERR_DEVICE, "trace copy failed");
+    return QK_OK;
+}
 
 template <class T>
 int dev_alloc(uint64_t &total, T **p, size_t count, const char *what) {
@@ -216,25 +237,34 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     auto norm_quant = [&](const float *w) {
         return qk_rmsnorm_quantize_x32(m->x, dim, w, m->xn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, c.eps, s);
     };
+    const size_t qstride = std::max(dim, c.hidden);
+    auto trace_q = [&](int l, int stage, int cols) {
+        return trace_copy(m->trace_q ? m->trace_q + (l * 4 + stage) * qstride : nullptr, m->xq, cols, s);
+    };
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
-        if ((st = norm_quant(L.attn_norm))) return st;
+        if ((st = norm_quant(L.attn_norm)) || (st = trace_q(l, 0, dim))) return st;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
         if ((st = gemv_by_mode(m, qkv, 3, m->xn, dim, s))) return st;
         attn.layer = l;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         if (int8_type(m, L.o_type) &&
-            (st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, s)))
+            ((st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xscale, dim / 32, dim, 1, s)) ||
+             (st = trace_q(l, 1, dim))))
             return st;
         if ((st = residual_by_mode(m, L.o_type, dim, L.o, m->attn, dim, s))) return st;
-        if ((st = norm_quant(L.ffn_norm))) return st;
+        if ((st = norm_quant(L.ffn_norm)) || (st = trace_q(l, 2, dim))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
         if ((st = gemv_by_mode(m, gu, 2, m->xn, dim, s))) return st;
         if (int8_type(m, L.down_type))
             st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s);
         else
             st = qk_silu_mul_f32(m->gate, m->up, c.hidden, s);
-        if (st || (st = residual_by_mode(m, L.down_type, dim, L.down, m->gate, c.hidden, s))) return st;
+        if (st || (int8_type(m, L.down_type) && (st = trace_q(l, 3, c.hidden))) ||
+            (st = residual_by_mode(m, L.down_type, dim, L.down, m->gate, c.hidden, s)) ||
+            (st = trace_copy(m->trace_x ? m->trace_x + static_cast<size_t>(l) * dim : nullptr, m->x,
+                             dim * sizeof(float), s)))
+            return st;
     }
     if (!need_logits) return QK_OK;
     if ((st = norm_quant(m->w.output_norm))) return st;
@@ -325,7 +355,10 @@ int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, 
         if ((st = qk::launch_rec_gemv(gu, 2, dim, gu_io, s))) return st;
         const qk_matrix down{L.down_type, dim, L.down, m->x};
         down_out.gain = l + 1 < c.layers ? m->layers[l + 1].attn_norm : m->w.output_norm;
-        if ((st = qk::launch_rec_gemv(&down, 1, c.hidden, down_out, s))) return st;
+        if ((st = qk::launch_rec_gemv(&down, 1, c.hidden, down_out, s)) ||
+            (st = trace_copy(m->trace_x ? m->trace_x + static_cast<size_t>(l) * dim : nullptr, m->x,
+                             dim * sizeof(float), s)))
+            return st;
     }
     if (!need_logits) return QK_OK;
     qk::RecGemv head_in;
@@ -505,6 +538,15 @@ int qk_llama_logits(qk_llama *m, const float **logits) {
     return qk::ok();
 }
 
+int qk_llama_set_trace(qk_llama *m, float *residuals, int8_t *quantized) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_set_trace: null handle");
+    if ((residuals && !qk::aligned(residuals, 4)))
+        return qk::fail(QK_ERR_ALIGN, "qk_llama_set_trace: residuals must be 4-byte aligned");
+    m->trace_x = residuals;
+    m->trace_q = quantized;
+    return qk::ok();
+}
+
 int qk_llama_matrix_calls(const qk_llama *m, uint64_t *calls) {
     if (!m || !calls) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_matrix_calls: null argument");
     *calls = m->matrix_calls;
@@ -594,7 +636,10 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
             const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
             if ((st = qk::launch_gemv_fused(gu, 2, m->x, dim, dim, 1, nullptr, ffn_in, s))) return st;
             const qk_matrix down{L.down_type, dim, L.down, m->x};
-            if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, c.hidden, 1, nullptr, down_in, s))) return st;
+            if ((st = qk::launch_gemv_fused(&down, 1, m->gate, c.hidden, c.hidden, 1, nullptr, down_in, s)) ||
+                (st = trace_copy(m->trace_x ? m->trace_x + static_cast<size_t>(l) * dim : nullptr, m->x,
+                                 dim * sizeof(float), s)))
+                return st;
         }
         if (!need_logits) {
             if (next_token) *next_token = -1;
@@ -661,6 +706,11 @@ struct qk_llama_batch {
     float *xs = nullptr, *hs = nullptr;
     void *i8_ws = nullptr;
     size_t i8_ws_bytes = 0;
+    // qk_llama_batch_set_trace: per token the residual after each layer
+    // [token][layer][dim] and the INT8 inputs of each layer's products
+    // [token][layer][4][max(dim, hidden)].
+    float *trace_x = nullptr;
+    int8_t *trace_q = nullptr;
 };
 
 namespace {
@@ -705,6 +755,13 @@ int check_kv_rows(const qk_batch_token *desc, int n, std::vector<int64_t> &write
     return QK_OK;
 }
 
+// The residual of the step's T tokens after layer l into the trace.
+int batch_trace_x(qk_llama_batch *m, int l, int T, hipStream_t s) {
+    const size_t row = static_cast<size_t>(m->cfg.dim) * sizeof(float);
+    return trace_copy_2d(m->trace_x ? m->trace_x + static_cast<size_t>(l) * m->cfg.dim : nullptr, m->cfg.layers * row,
+                         m->x, row, row, T, s);
+}
+
 // INT8 products of T tokens (the reference's dp4a paths): the GEMV kernels
 // below 8 tokens, the integer matrix cores from 8 on.
 int batch_gemm_i8(qk_llama_batch *m, const qk_matrix *mats, int n, const int8_t *xq, const float *xs, int cols, int T,
@@ -731,10 +788,16 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
     auto norm_quant = [&](const float *w) {
         return qk_rmsnorm_quantize_x32(m->x, dim, w, nullptr, 0, m->xq, dim, m->xs, dim / 32, dim, T, c.eps, s);
     };
+    const size_t qstride = std::max(dim, hidden);
+    auto trace_q = [&](int l, int stage, const int8_t *src, int cols) {
+        return trace_copy_2d(m->trace_q ? m->trace_q + (l * 4 + stage) * qstride : nullptr, c.layers * 4 * qstride,
+                             src, cols, cols, T, s);
+    };
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = norm_quant(L.attn_norm)) || (st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s)))
+        if ((st = norm_quant(L.attn_norm)) || (st = trace_q(l, 0, m->xq, dim)) ||
+            (st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s)))
             return st;
         if (chained &&
             (st = qk::launch_rope_kv_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
@@ -745,7 +808,8 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         if ((st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xs, dim / 32, dim, T, s)) ||
-            (st = batch_gemm_i8(m, &o, 1, m->xq, m->xs, dim, T, true, s)) || (st = norm_quant(L.ffn_norm)))
+            (st = trace_q(l, 1, m->xq, dim)) || (st = batch_gemm_i8(m, &o, 1, m->xq, m->xs, dim, T, true, s)) ||
+            (st = norm_quant(L.ffn_norm)) || (st = trace_q(l, 2, m->xq, dim)))
             return st;
         const qk_matrix gu[2] = {{L.gate_type, hidden, L.gate, m->gate}, {L.up_type, hidden, L.up, m->up}};
         if (T >= 8 && L.gate_type == L.up_type) {
@@ -758,7 +822,9 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
             return st;
         }
         const qk_matrix down{L.down_type, dim, L.down, m->x};
-        if ((st = batch_gemm_i8(m, &down, 1, m->hq, m->hs, hidden, T, true, s))) return st;
+        if ((st = trace_q(l, 3, m->hq, hidden)) || (st = batch_gemm_i8(m, &down, 1, m->hq, m->hs, hidden, T, true, s)) ||
+            (st = batch_trace_x(m, l, T, s)))
+            return st;
     }
     return QK_OK;
 }
@@ -957,6 +1023,15 @@ int qk_llama_batch_logits(qk_llama_batch *m, const float **logits) {
     return qk::ok();
 }
 
+int qk_llama_batch_set_trace(qk_llama_batch *m, float *residuals, int8_t *quantized) {
+    if (!m) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_set_trace: null handle");
+    if ((residuals && !qk::aligned(residuals, 4)))
+        return qk::fail(QK_ERR_ALIGN, "qk_llama_batch_set_trace: residuals must be 4-byte aligned");
+    m->trace_x = residuals;
+    m->trace_q = quantized;
+    return qk::ok();
+}
+
 int qk_llama_batch_matrix_calls(const qk_llama_batch *m, uint64_t *calls) {
     if (!m || !calls) return qk::fail(QK_ERR_INVALID_ARG, "qk_llama_batch_matrix_calls: null argument");
     *calls = m->matrix_calls;
@@ -1088,7 +1163,8 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         if (!chain) {
             if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, residual, ws, wsb, s)) ||
                 (st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, ffn_in, ws, wsb, s)) ||
-                (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s)))
+                (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_in, ws, wsb, s)) ||
+                (st = batch_trace_x(m, l, T, s)))
                 return st;
             continue;
         }
@@ -1111,7 +1187,8 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         }
         if ((st = qk::launch_batched_fused(&o, 1, m->attn, dim, dim, T, o_f, ws, wsb, s)) ||
             (st = qk::launch_batched_fused(gu, 2, m->x, dim, dim, T, gu_f, ws, wsb, s)) ||
-            (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_f, ws, wsb, s)))
+            (st = qk::launch_batched_fused(&down, 1, m->gate, c.hidden, c.hidden, T, down_f, ws, wsb, s)) ||
+            (st = batch_trace_x(m, l, T, s)))
             return st;
     }
     if (!n_rows) return qk::ok();

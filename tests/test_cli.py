@@ -56,6 +56,7 @@ def test_help():
     (["--q6-warps", "32", "x"], "must be 2, 4, 8, or 16"),
     (["--prefill-batch", "33", "x"], "must be in 1..32"),
     (["--prefill-batch", "0", "x"], "must be in 1..32"),
+    (["--prefill-batch", "4", "--float-q6", "x"], "one mode"),
     (["--compare-prefill", "x"], "requires --prefill-batch 2..32"),
     (["--compare-prefill", "--prefill-batch", "4", "--tokenize-only", "x"], "requires --prefill-batch 2..32"),
     (["--prompts-file", "/nonexistent/prompts.txt"], "Cannot open prompts file"),

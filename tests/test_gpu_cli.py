@@ -58,31 +58,40 @@ def _greedy(qk, g, ids, n, int8=False):
     return out
 
 
-@pytest.mark.parametrize("chunk", [4, 8, 32])
-def test_compare_prefill(qk, torch_gpu, model, chunk):
+@pytest.mark.parametrize("chunk,int8", [(4, False), (8, False), (32, False), (8, True), (32, True)])
+def test_compare_prefill(qk, torch_gpu, model, chunk, int8):
     import inferencer_jetson_amd.compare as cmp
     _, g, tok, T = model
     ids = T.chat_prompt(tok, PROMPT)
     assert len(ids) > 8
     r = qk.Runner.from_gguf(g, CFG["context"])
     b = qk.BatchRunner.from_gguf(g, CFG["context"], chunk, CFG["context"])
-    rep = cmp.compare_prefill(qk, r, b, ids, 6, chunk)
+    rep = cmp.compare_prefill(qk, r, b, ids, 6, chunk, int8=int8)
     r.close()
     b.close()
     assert rep["tokens"] == len(ids) and len(rep["layers"]) == CFG["layers"]
     # Random-init weights make activations and attention scores large, so
-    # the two drivers' roundoff (different GEMV kernels, ~1e-7 relative) is
-    # amplified through the softmax from layer to layer: relative bars of
-    # 1e-3 on the diagnostics the reference prints, strict on the tokens.
-    assert rep["residual_rms"] < 1e-3 * rep["residual_ref_rms"]
+    # the two drivers' roundoff (different kernels, ~1e-7 relative) is
+    # amplified through the softmax from layer to layer; in the INT8 mode a
+    # code on a rounding midpoint can go either way as well.  Relative bars
+    # on the diagnostics the reference prints, strict on the tokens.
+    bar = 2e-2 if int8 else 1e-3
+    assert rep["residual_rms"] < bar * rep["residual_ref_rms"]
     for L in rep["layers"]:
-        assert L["key_rms"] < 1e-3 * L["key_ref_rms"] and L["value_rms"] < 1e-3 * L["value_ref_rms"], L
+        assert L["residual_rms"] < bar * L["residual_ref_rms"], L
+        if int8:
+            assert sum(L["int8_mismatches"]) <= 0.02 * (3 * CFG["dim"] + CFG["hidden"]), L
+        else:
+            assert "int8_mismatches" not in L
     for s in rep["steps"]:
         if s["top2_margin"] > 100 * s["logit_max"]:
             assert s["baseline_token"] == s["batched_token"], s
     assert rep["steps"][0]["baseline_token"] == rep["steps"][0]["batched_token"]
     lines = cmp.format_report(1, rep)
     assert lines[0].startswith("Prompt 1: residual max abs difference") and len(lines) >= 1 + CFG["layers"] + 6
+    layer_lines = [l for l in lines if l.startswith("  layer ")]
+    assert len(layer_lines) == CFG["layers"]
+    assert all(("INT8 differences [QKV, attention output, gate/up, down]" in l) == int8 for l in layer_lines)
 
 
 def test_compare_prefill_logits_close(qk, torch_gpu, model):
@@ -160,11 +169,18 @@ def test_cli_int8_default_and_compare_output(qk, torch_gpu, model):
     assert rc == 0, err
     assert out == text + b"\n"
     assert "Q4_K matrix path: INT8; Q6_K matrix path: INT8" in err
+    # INT8 batched prefill (the reference's only batched mode) runs and
+    # counts the prompt's products the same way.
+    rc, out2, err2 = _run(cli, ["--model", str(path), "--context", "128", "--max-tokens", "4", "--prefill-batch", "8",
+                                "--stats", PROMPT])
+    assert rc == 0, err2
+    assert out2.endswith(b"\n") and "quantized matrix calls" in err2
     rc, out, err = _run(cli, ["--model", str(path), "--context", "128", "--max-tokens", "5", "--prefill-batch", "6",
                               "--compare-prefill", PROMPT])
     assert rc == 0, err
     lines = out.decode().splitlines()
     assert lines[0].startswith("Prompt 1: residual max abs difference")
+    assert sum("INT8 differences [QKV, attention output, gate/up, down]" in l for l in lines) == CFG["layers"]
     steps = [l for l in lines if l.startswith("  step ")]
     assert len(steps) == 5
     assert all("baseline token" in l and "batched token" in l and "top-2 margin" in l for l in steps)
