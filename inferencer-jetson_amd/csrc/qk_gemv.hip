@@ -925,36 +925,6 @@ int gcd_int(int a, int b) {
     return a;
 }
 
-// Resident workgroups of a kernel on the current device, cached per
-// (device, kernel, block size, LDS bytes): the occupancy query costs
-// microseconds of host time, more than a small GEMV runs.
-int resident_blocks(const void *kernel, int block, size_t lds) {
-    struct Key {
-        int device;
-        const void *kernel;
-        int block;
-        size_t lds;
-        bool operator==(const Key &o) const {
-            return device == o.device && kernel == o.kernel && block == o.block && lds == o.lds;
-        }
-    };
-    static std::mutex mutex;
-    static std::vector<std::pair<Key, int>> cache;
-    const Key key{device_info().device, kernel, block, lds};
-    {
-        std::lock_guard<std::mutex> lock(mutex);
-        for (const auto &e : cache)
-            if (e.first == key) return e.second;
-    }
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1)
-        per_cu = 1;
-    const int total = per_cu * device_info().cus;
-    std::lock_guard<std::mutex> lock(mutex);
-    cache.emplace_back(key, total);
-    return total;
-}
-
 template <class Policy, int TYPE, int GROUP>
 void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
     const size_t x_lds = Policy::lds_bytes(p.pieces * 64);

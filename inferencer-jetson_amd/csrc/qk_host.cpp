@@ -52,12 +52,13 @@ int check_weights(const char *where, int type, const void *w, int cols, int rows
 }
 
 const DeviceInfo &device_info() {
+    // A fixed table: the references handed out stay valid.
+    constexpr int kDevicesMax = 64;
     static std::mutex mutex;
-    static std::vector<DeviceInfo> cache;
+    static DeviceInfo cache[kDevicesMax];
     int device = 0;
-    if (hipGetDevice(&device) != hipSuccess) device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kDevicesMax) device = 0;
     std::lock_guard<std::mutex> lock(mutex);
-    if (cache.size() <= static_cast<size_t>(device)) cache.resize(device + 1);
     DeviceInfo &info = cache[device];
     if (info.device < 0) {
         hipDeviceProp_t prop{};
@@ -70,6 +71,37 @@ const DeviceInfo &device_info() {
         info.device = device;
     }
     return info;
+}
+
+
+// Resident workgroups of a kernel on the current device, cached per
+// (device, kernel, block size, LDS bytes): the occupancy query costs
+// microseconds of host time, more than a small GEMV runs.
+int resident_blocks(const void *kernel, int block, size_t lds) {
+    struct Key {
+        int device;
+        const void *kernel;
+        int block;
+        size_t lds;
+        bool operator==(const Key &o) const {
+            return device == o.device && kernel == o.kernel && block == o.block && lds == o.lds;
+        }
+    };
+    static std::mutex mutex;
+    static std::vector<std::pair<Key, int>> cache;
+    const Key key{device_info().device, kernel, block, lds};
+    {
+        std::lock_guard<std::mutex> lock(mutex);
+        for (const auto &e : cache)
+            if (e.first == key) return e.second;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int total = per_cu * device_info().cus;
+    std::lock_guard<std::mutex> lock(mutex);
+    cache.emplace_back(key, total);
+    return total;
 }
 
 }  // namespace qk

@@ -353,6 +353,9 @@ struct DeviceInfo {
     int max_threads = 1024;
 };
 const DeviceInfo &device_info();
+// Workgroups of `block` threads and `lds` bytes of dynamic LDS the current
+// device holds at once (per CU times CUs), cached.
+int resident_blocks(const void *kernel, int block, size_t lds);
 
 // ---------------------------------------------------------------- device --
 

@@ -40,7 +40,10 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kRows = 32;      // weight rows per row tile (the MFMA's N)
 constexpr int kToks = 32;      // tokens per token tile (the MFMA's M)
-constexpr int kWavesMax = 8;   // waves splitting a row's blocks
+// Waves (one block each) a workgroup may spread a row over: 16 where the
+// kernel fits 128 VGPRs (Q4_K, one row tile), else 12 (at most 170 VGPRs).
+// A 3072-column row (12 blocks) then needs one workgroup.
+__host__ __device__ constexpr int waves_max(int type, int rt) { return type == QK_TYPE_Q4_K && rt == 1 ? 16 : 12; }
 
 enum Epilogue { kStore = 0, kAccumulate = 1, kPairQuant = 2 };
 
@@ -432,7 +435,7 @@ __device__ __forceinline__ void skinny_body(const SkParams &p, float *lds) {
 }
 
 template <int TYPE, int RT>
-__global__ __launch_bounds__(64 * kWavesMax) void skinny_i8(SkParams p) {
+__global__ __launch_bounds__(64 * waves_max(TYPE, RT)) void skinny_i8(SkParams p) {
     extern __shared__ __align__(16) float lds[];
     if constexpr (TYPE != 0) {
         skinny_body<TYPE, RT>(p, lds);
@@ -483,11 +486,64 @@ void launch_type(int type, const dim3 &grid, int threads, size_t lds, hipStream_
         hipLaunchKernelGGL((skinny_i8<0, 1>), grid, dim3(threads), lds, stream, p);
 }
 
-// Splits of a row of nb blocks: one block per wave, at most kWavesMax waves
-// a workgroup, the blocks spread evenly.
-void split_plan(int nb, int &splits, int &waves) {
-    splits = (nb + kWavesMax - 1) / kWavesMax;
-    waves = (nb + splits - 1) / splits;
+const void *skinny_kernel(int type, int rt) {
+    if (rt == 2)
+        return type == QK_TYPE_Q4_K   ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q4_K, 2>)
+               : type == QK_TYPE_Q6_K ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K, 2>)
+                                      : reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K_SPLIT, 2>);
+    return type == QK_TYPE_Q4_K         ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q4_K, 1>)
+           : type == QK_TYPE_Q6_K       ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K, 1>)
+           : type == QK_TYPE_Q6_K_SPLIT ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K_SPLIT, 1>)
+                                        : reinterpret_cast<const void *>(skinny_i8<0, 1>);
+}
+
+// LDS of a workgroup of `waves` waves: the waves' sums, then each wave's
+// activation transpose.
+size_t skinny_lds(int waves, int rt) {
+    return (static_cast<size_t>(waves) * rt * 1024 + static_cast<size_t>(waves) * 8 * kToks) * sizeof(float);
+}
+
+// Splits beyond the fewest a row needs are planned only while the split
+// sums of a launch stay within this many (row tile, token tile, split)
+// units, which bounds the workspace.
+constexpr int64_t kPartialUnitsMax = 2048;
+
+// Duration model of a plan, fitted to 3B-shaped launches: each round of
+// resident workgroups costs about kRoundUs plus kWaveUs per wave a SIMD
+// runs in it (one block of RT row tiles each), and the second launch that
+// adds split sums about kReduceUs.
+constexpr float kRoundUs = 10.f, kWaveUs = 1.f, kReduceUs = 4.7f;
+
+int fewest_splits(int nb, int wmax) { return (nb + wmax - 1) / wmax; }
+
+// Splits of a row of nb blocks (one block per wave, the blocks spread
+// evenly over a workgroup's waves) for a launch of `units` (row tile, token
+// tile) pairs on kernel (type, rt): the plan of least modelled duration,
+// from the fewest splits the widest workgroup allows up to kSplitsMax.
+// Wider workgroups hold fewer per CU, narrower ones need more splits.
+void split_plan(int nb, int64_t units, int type, int rt, int &splits, int &waves) {
+    const int s0 = fewest_splits(nb, waves_max(type, rt));
+    const int cus = std::max(1, device_info().cus);
+    const void *kernel = skinny_kernel(type, rt);
+    splits = s0;
+    waves = (nb + s0 - 1) / s0;
+    float best = 0.f;
+    for (int s = s0; s <= std::min(nb, kSplitsMax); ++s) {
+        const int w = (nb + s - 1) / s;
+        if (s > s0 && w == (nb + s - 2) / (s - 1)) continue;   // as wide as the previous plan: only more waves idle
+        const int64_t wgs = units * s;
+        if (s > s0 && wgs > kPartialUnitsMax) break;
+        const int per_cu = std::max(1, resident_blocks(kernel, 64 * w, skinny_lds(w, rt)) / cus);
+        const int64_t rounds = (wgs + static_cast<int64_t>(cus) * per_cu - 1) / (static_cast<int64_t>(cus) * per_cu);
+        const int load = static_cast<int>(std::min<int64_t>(per_cu, (wgs + cus - 1) / cus));   // busiest CU
+        const float cost = static_cast<float>(rounds) * (kRoundUs + kWaveUs * rt * ((load * w + 3) / 4)) +
+                           (s > 1 ? kReduceUs : 0.f);
+        if (s == s0 || cost < best - 1e-3f) {
+            best = cost;
+            splits = s;
+            waves = w;
+        }
+    }
 }
 
 int row_tiles(const qk_matrix *mats, int n_mats, bool pair) {
@@ -499,21 +555,24 @@ int row_tiles(const qk_matrix *mats, int n_mats, bool pair) {
 
 }  // namespace
 
-// Workspace of a launch: the splits' partial sums when a row takes more
-// than one split (zero otherwise).
+// Workspace bound of a launch, for any storage type: the split sums of
+// the fewest splits of the narrowest workgroups (12 waves), or of the
+// planner's extra splits (at most kPartialUnitsMax units).
 size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair) {
-    int splits, waves;
-    split_plan(cols / 256, splits, waves);
-    if (splits == 1 || n_tokens <= 0) return 0;
-    const size_t ttiles = (static_cast<size_t>(n_tokens) + kToks - 1) / kToks;
-    return static_cast<size_t>(tiles) * ttiles * splits * (pair ? 2 : 1) * 1024 * sizeof(float);
+    const int nb = cols / 256;
+    if (nb <= 1 || n_tokens <= 0 || tiles <= 0) return 0;
+    const int64_t units = static_cast<int64_t>(tiles) * ((n_tokens + kToks - 1) / kToks);
+    const int s0 = fewest_splits(nb, 12);
+    const int64_t sums = std::max<int64_t>(s0 > 1 ? units * s0 : 0,
+                                           std::min<int64_t>(units * std::min(nb, kSplitsMax), kPartialUnitsMax));
+    return static_cast<size_t>(sums) * (pair ? 2 : 1) * 1024 * sizeof(float);
 }
 
 // The INT8 product of n_tokens per-32 quantized activation rows with
 // n_mats matrices (arguments validated by the caller): y_m[t][r] (overwrite
 // or add), or with out_xq the pair's SiLU(y0) * y1 quantized per 32 values
 // (y unused; the two matrices of one type, rows equal and a multiple of 32).
-// Rows of more than kWavesMax blocks are split over workgroups, whose sums
+// Rows of more blocks than a workgroup's waves are split over workgroups, whose sums
 // a second launch adds (workspace: skinny_i8_workspace_bytes).
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
@@ -528,9 +587,8 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
     p.ldxs = ldscale;
     p.n_tokens = n_tokens;
     p.nb = nb;
-    if (nb > kSplitsMax * kWavesMax)
-        return fail(QK_ERR_LIMIT, std::string(where) + ": rows longer than 16384 columns are not supported");
-    split_plan(nb, p.splits, p.waves);
+    if (nb > kSplitsMax * 12)
+        return fail(QK_ERR_LIMIT, std::string(where) + ": rows longer than 24576 columns are not supported");
     const bool pair = out_xq != nullptr;
     p.epilogue = pair ? kPairQuant : accumulate ? kAccumulate : kStore;
     p.out_xq = out_xq;
@@ -555,9 +613,14 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
     }
     if (pair) tiles = mats[0].rows / kRows;
     const int token_tiles = (n_tokens + kToks - 1) / kToks;
-    if (token_tiles > 65535 || static_cast<int64_t>(tiles) * p.splits > (1 << 30))
+    if (token_tiles > 65535 || static_cast<int64_t>(tiles) * kSplitsMax > (1 << 30))
         return fail(QK_ERR_LIMIT, std::string(where) + ": launch too large");
-    const size_t need = skinny_i8_workspace_bytes(cols, tiles, n_tokens, pair);
+    const int rt = pair ? 2 : 1;
+    split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, type, rt, p.splits, p.waves);
+    // The plan's split sums; callers size the workspace by
+    // skinny_i8_workspace_bytes, which bounds every plan.
+    const size_t need = p.splits > 1 ? static_cast<size_t>(tiles) * token_tiles * p.splits * rt * 1024 * sizeof(float)
+                                     : 0;
     if (need) {
         if (!workspace || workspace_size < need)
             return fail(QK_ERR_INVALID_ARG, std::string(where) + ": workspace smaller than " + std::to_string(need) +
@@ -565,9 +628,7 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
         if (!aligned(workspace, 16)) return fail(QK_ERR_ALIGN, std::string(where) + ": workspace not 16-byte aligned");
         p.partials = static_cast<float *>(workspace);
     }
-    const int rt = pair ? 2 : 1;
-    const size_t lds = (static_cast<size_t>(p.waves) * rt * 1024 + static_cast<size_t>(p.waves) * 8 * kToks) *
-                       sizeof(float);
+    const size_t lds = skinny_lds(p.waves, rt);
     const dim3 grid(static_cast<unsigned>(tiles * p.splits), static_cast<unsigned>(token_tiles));
     if (pair)
         launch_type<2>(type, grid, 64 * p.waves, lds, stream, p);
