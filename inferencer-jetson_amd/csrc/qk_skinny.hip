@@ -61,6 +61,7 @@ struct SkParams {
     const float *xs;
     int ldxq, ldxs;
     int n_tokens, nb;
+    int tiles;           // row tiles of the launch
     int splits, waves;   // workgroups per row and blocks (= waves) per workgroup
     int epilogue;
     // kPairQuant: SiLU(y0) * y1 of matrices 0 and 1, quantized per 32 values
@@ -283,19 +284,18 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_wave_barrier();
 }
 
-// One block for every row tile of the workgroup: the block's per-32 scales
-// transposed through the wave's LDS slice (a wave's DS operations complete
-// in order), the Q4_K sums S per sub-block of the lane's token (both column
-// halves), then each row tile's dots and combine.
-template <int TYPE, int RT>
-__device__ __forceinline__ void block_tile(const Raw (&cur)[RT], const uint4 (&ca)[8], const float (&cx)[8],
-                                           float *xst, int col, int kh, v16f (&acc)[RT], v16f (&accmin)[RT]) {
+// The wave's activation block, prepared once for every row tile it meets:
+// the block's per-32 scales transposed through the wave's LDS slice (a
+// wave's DS operations complete in order) and the Q4_K sums S per
+// sub-block of the lane's token (both column halves).
+template <int TYPE>
+__device__ __forceinline__ void act_prep(const uint4 (&ca)[8], const float (&cx)[8], float *xst, int col, int kh,
+                                         float (&xss)[8]) {
     if (kh == 0) {
         #pragma unroll
         for (int c = 0; c < 8; ++c) xst[c * kToks + col] = cx[c];
     }
     wave_sync();
-    float xss[8];
     if (is_q4<TYPE>(TYPE)) {
         #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -310,9 +310,6 @@ __device__ __forceinline__ void block_tile(const Raw (&cur)[RT], const uint4 (&c
         #pragma unroll
         for (int s = 0; s < 8; ++s) xss[s] = 0.f;
     }
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) block_i8<TYPE>(cur[rt], TYPE, ca, xst, xss, kh, acc[rt], accmin[rt]);
-    wave_sync();
 }
 
 // The matrix of row tile `tile` in a launch over one tile column per 32
@@ -376,80 +373,125 @@ __device__ __forceinline__ void epilogue(const SkParams &p, const int (&mi)[RT],
     }
 }
 
-// One workgroup: row tile(s) x token tile x the `waves` blocks of its split
-// (one block per wave), for weights of storage type TYPE.
+// Block b of the raw weight rows of row tile `tile` (every row tile of the
+// workgroup: RT matrices' rows), the lane's row clamped into its matrix.
 template <int TYPE, int RT>
+__device__ __forceinline__ void load_tile(const SkParams &p, int tile, int b, int col, int kh, Raw (&r)[RT]) {
+    int mi[RT], row0[RT];
+    tile_rows<RT>(p, tile, mi, row0);
+    #pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+        const SkMatrix &M = p.mat[mi[rt]];
+        const uint8_t *wrow = M.w + static_cast<size_t>(min(row0[rt] + col, M.rows - 1)) * M.row_bytes;
+        load_raw<TYPE>(r[rt], wrow, b, p.nb, TYPE, kh);
+    }
+}
+
+// One workgroup: the row tiles tile0, tile0 + stride, ... (stride =
+// workgroups per split and token tile; one tile unless LOOP) x its token
+// tile x the `waves` blocks of its split, one block per wave.  The wave's
+// activations are loaded and prepared once; with LOOP the next tile's
+// weights load while this one computes (the last tile's reload is
+// redundant and in bounds).
+template <int TYPE, int RT, bool LOOP>
 __device__ __forceinline__ void skinny_body(const SkParams &p, float *lds) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kh = lane >> 5, col = lane & 31;
-    const int split = static_cast<int>(blockIdx.x) % p.splits, tile = static_cast<int>(blockIdx.x) / p.splits;
+    const int split = static_cast<int>(blockIdx.x) % p.splits;
+    const int stride = static_cast<int>(gridDim.x) / p.splits;
     const int ttile = blockIdx.y;
     const int t_a = min(ttile * kToks + col, p.n_tokens - 1);   // token of the lane's A operand (in bounds)
-    int mi[RT], row0[RT];
-    tile_rows<RT>(p, tile, mi, row0);
     float *red = lds;
     float *xst = lds + static_cast<size_t>(p.waves) * RT * 1024 + wave * (8 * kToks);
-
-    v16f acc[RT], accmin[RT];
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt)
-        #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[rt][i] = accmin[rt][i] = 0.f;
     const int b = split * p.waves + wave;
-    if (b < p.nb) {   // wave-uniform
-        Raw cur[RT];
-        uint4 ca[8];
-        float cx[8];
-        #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const SkMatrix &M = p.mat[mi[rt]];
-            const uint8_t *wrow = M.w + static_cast<size_t>(min(row0[rt] + col, M.rows - 1)) * M.row_bytes;
-            load_raw<TYPE>(cur[rt], wrow, b, p.nb, TYPE, kh);
-        }
-        load_act<TYPE>(ca, cx, p.xq + static_cast<int64_t>(t_a) * p.ldxq, p.xs + static_cast<int64_t>(t_a) * p.ldxs,
-                       b, TYPE, kh);
-        block_tile<TYPE, RT>(cur, ca, cx, xst, col, kh, acc, accmin);
-    }
-    #pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-        float *mine = red_slot(red, wave, rt, RT) + lane;
-        #pragma unroll
-        for (int i = 0; i < 16; ++i) mine[i * 64] = acc[rt][i] + accmin[rt][i];
-    }
-    __syncthreads();
+    const bool live = b < p.nb;   // wave-uniform
+    // Loads are unconditional (a wave past the row's end reloads the last
+    // block, in bounds), so every path has the same loads in flight and the
+    // waits before the first use of a tile stay partial.
+    const int bl = min(b, p.nb - 1);
+    int tile = static_cast<int>(blockIdx.x) / p.splits;
+
+    Raw cur[RT];
+    uint4 ca[8];
+    float cx[8], xss[8];
+    load_tile<TYPE, RT>(p, tile, bl, col, kh, cur);
+    load_act<TYPE>(ca, cx, p.xq + static_cast<int64_t>(t_a) * p.ldxq, p.xs + static_cast<int64_t>(t_a) * p.ldxs, bl,
+                   TYPE, kh);
+    act_prep<TYPE>(ca, cx, xst, col, kh, xss);
     const int nthreads = 64 * p.waves;
     auto wave_sum = [&](int e) {   // the waves' partial sums in wave order
         float v = red[e];
         for (int w = 1; w < p.waves; ++w) v += red[static_cast<size_t>(w) * RT * 1024 + e];
         return v;
     };
-    if (p.splits == 1) {
-        epilogue<RT>(p, mi, row0, ttile, nthreads, wave_sum);
-        return;
+    for (;;) {
+        Raw nxt[RT];
+        if constexpr (LOOP) load_tile<TYPE, RT>(p, min(tile + stride, p.tiles - 1), bl, col, kh, nxt);
+        v16f acc[RT], accmin[RT];
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+            #pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rt][i] = accmin[rt][i] = 0.f;
+        if (live) {
+            #pragma unroll
+            for (int rt = 0; rt < RT; ++rt) block_i8<TYPE>(cur[rt], TYPE, ca, xst, xss, kh, acc[rt], accmin[rt]);
+        }
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            float *mine = red_slot(red, wave, rt, RT) + lane;
+            #pragma unroll
+            for (int i = 0; i < 16; ++i) mine[i * 64] = acc[rt][i] + accmin[rt][i];
+        }
+        __syncthreads();
+        if (p.splits == 1) {
+            int mi[RT], row0[RT];
+            tile_rows<RT>(p, tile, mi, row0);
+            epilogue<RT>(p, mi, row0, ttile, nthreads, wave_sum);
+        } else {
+            // Several splits of the row: this one's sums to the workspace,
+            // [tile][token tile][split][RT * 1024]; skinny_reduce finishes.
+            float *dst =
+                p.partials + (static_cast<size_t>(tile * gridDim.y + ttile) * p.splits + split) * (RT * 1024);
+            for (int e = threadIdx.x; e < RT * 1024; e += nthreads) dst[e] = wave_sum(e);
+        }
+        if constexpr (!LOOP) return;
+        tile += stride;
+        if (tile >= p.tiles) return;
+        __syncthreads();   // every wave's sums read before the next tile's overwrite them
+        #pragma unroll
+        for (int rt = 0; rt < RT; ++rt) cur[rt] = nxt[rt];
     }
-    // Several splits of the row: this one's sums to the workspace,
-    // [tile][token tile][split][RT * 1024]; skinny_reduce finishes.
-    float *dst = p.partials + (static_cast<size_t>(tile * gridDim.y + ttile) * p.splits + split) * (RT * 1024);
-    for (int e = threadIdx.x; e < RT * 1024; e += nthreads) dst[e] = wave_sum(e);
 }
 
 template <int TYPE, int RT>
 __global__ __launch_bounds__(64 * waves_max(TYPE, RT)) void skinny_i8(SkParams p) {
     extern __shared__ __align__(16) float lds[];
     if constexpr (TYPE != 0) {
-        skinny_body<TYPE, RT>(p, lds);
+        skinny_body<TYPE, RT, false>(p, lds);
     } else {
         // A launch over matrices of several types (one row tile each): the
         // tile's matrix fixes the type, uniformly for the workgroup.
         const int type = p.mat[tile_matrix(p, static_cast<int>(blockIdx.x) / p.splits)].type;
         if (type == QK_TYPE_Q4_K)
-            skinny_body<QK_TYPE_Q4_K, RT>(p, lds);
+            skinny_body<QK_TYPE_Q4_K, RT, false>(p, lds);
         else if (type == QK_TYPE_Q6_K)
-            skinny_body<QK_TYPE_Q6_K, RT>(p, lds);
+            skinny_body<QK_TYPE_Q6_K, RT, false>(p, lds);
         else
-            skinny_body<QK_TYPE_Q6_K_SPLIT, RT>(p, lds);
+            skinny_body<QK_TYPE_Q6_K_SPLIT, RT, false>(p, lds);
     }
+}
+
+// Workgroups of the looping kernel hold at most kLoopWaves waves (room for
+// two tiles' weights in registers).
+constexpr int kLoopWaves = 8;
+
+// Launches of more (row tile, token tile) units than the chip holds at
+// once, over matrices of one type: resident workgroups walk the row tiles.
+template <int TYPE, int RT>
+__global__ __launch_bounds__(64 * kLoopWaves) void skinny_i8_loop(SkParams p) {
+    extern __shared__ __align__(16) float lds[];
+    skinny_body<TYPE, RT, true>(p, lds);
 }
 
 constexpr int kSplitsMax = 8;
@@ -474,27 +516,27 @@ __global__ __launch_bounds__(256) void skinny_reduce(SkParams p) {
     });
 }
 
-template <int RT>
-void launch_type(int type, const dim3 &grid, int threads, size_t lds, hipStream_t stream, const SkParams &p) {
-    if (type == QK_TYPE_Q4_K)
-        hipLaunchKernelGGL((skinny_i8<QK_TYPE_Q4_K, RT>), grid, dim3(threads), lds, stream, p);
-    else if (type == QK_TYPE_Q6_K)
-        hipLaunchKernelGGL((skinny_i8<QK_TYPE_Q6_K, RT>), grid, dim3(threads), lds, stream, p);
-    else if (type == QK_TYPE_Q6_K_SPLIT)
-        hipLaunchKernelGGL((skinny_i8<QK_TYPE_Q6_K_SPLIT, RT>), grid, dim3(threads), lds, stream, p);
-    else if constexpr (RT == 1)
-        hipLaunchKernelGGL((skinny_i8<0, 1>), grid, dim3(threads), lds, stream, p);
+template <int RT, bool LOOP>
+const void *kernel_of(int type) {
+    if constexpr (LOOP) {
+        return type == QK_TYPE_Q4_K   ? reinterpret_cast<const void *>(skinny_i8_loop<QK_TYPE_Q4_K, RT>)
+               : type == QK_TYPE_Q6_K ? reinterpret_cast<const void *>(skinny_i8_loop<QK_TYPE_Q6_K, RT>)
+                                      : reinterpret_cast<const void *>(skinny_i8_loop<QK_TYPE_Q6_K_SPLIT, RT>);
+    } else {
+        if (type == 0) {
+            if constexpr (RT == 1) return reinterpret_cast<const void *>(skinny_i8<0, 1>);
+            return nullptr;
+        }
+        return type == QK_TYPE_Q4_K   ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q4_K, RT>)
+               : type == QK_TYPE_Q6_K ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K, RT>)
+                                      : reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K_SPLIT, RT>);
+    }
 }
 
-const void *skinny_kernel(int type, int rt) {
-    if (rt == 2)
-        return type == QK_TYPE_Q4_K   ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q4_K, 2>)
-               : type == QK_TYPE_Q6_K ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K, 2>)
-                                      : reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K_SPLIT, 2>);
-    return type == QK_TYPE_Q4_K         ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q4_K, 1>)
-           : type == QK_TYPE_Q6_K       ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K, 1>)
-           : type == QK_TYPE_Q6_K_SPLIT ? reinterpret_cast<const void *>(skinny_i8<QK_TYPE_Q6_K_SPLIT, 1>)
-                                        : reinterpret_cast<const void *>(skinny_i8<0, 1>);
+// The kernel of a launch: type 0 (several types) has only the one-pass form.
+const void *skinny_kernel(int type, int rt, bool loop) {
+    if (rt == 2) return loop ? kernel_of<2, true>(type) : kernel_of<2, false>(type);
+    return loop ? kernel_of<1, true>(type) : kernel_of<1, false>(type);
 }
 
 // LDS of a workgroup of `waves` waves: the waves' sums, then each wave's
@@ -516,17 +558,26 @@ constexpr float kRoundUs = 10.f, kWaveUs = 1.f, kReduceUs = 4.7f;
 
 int fewest_splits(int nb, int wmax) { return (nb + wmax - 1) / wmax; }
 
+struct SkPlan {
+    int splits, waves;
+    int loop_groups;   // workgroups per (split, token tile) of the looping kernel; 0: one pass
+};
+
 // Splits of a row of nb blocks (one block per wave, the blocks spread
 // evenly over a workgroup's waves) for a launch of `units` (row tile, token
 // tile) pairs on kernel (type, rt): the plan of least modelled duration,
 // from the fewest splits the widest workgroup allows up to kSplitsMax.
-// Wider workgroups hold fewer per CU, narrower ones need more splits.
-void split_plan(int nb, int64_t units, int type, int rt, int &splits, int &waves) {
+// Wider workgroups hold fewer per CU, narrower ones need more splits.  A
+// launch of one type whose best plan needs more than one round of
+// workgroups instead runs the looping kernel: the fewest splits of
+// kLoopWaves-wave workgroups, as many as the chip holds, each walking its
+// share of the row tiles.
+SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt) {
     const int s0 = fewest_splits(nb, waves_max(type, rt));
     const int cus = std::max(1, device_info().cus);
-    const void *kernel = skinny_kernel(type, rt);
-    splits = s0;
-    waves = (nb + s0 - 1) / s0;
+    const void *kernel = skinny_kernel(type, rt, false);
+    int splits = s0, waves = (nb + s0 - 1) / s0;
+    int64_t best_rounds = 0;
     float best = 0.f;
     for (int s = s0; s <= std::min(nb, kSplitsMax); ++s) {
         const int w = (nb + s - 1) / s;
@@ -540,10 +591,20 @@ void split_plan(int nb, int64_t units, int type, int rt, int &splits, int &waves
                            (s > 1 ? kReduceUs : 0.f);
         if (s == s0 || cost < best - 1e-3f) {
             best = cost;
+            best_rounds = rounds;
             splits = s;
             waves = w;
         }
     }
+    if (type == 0 || best_rounds <= 1) return SkPlan{splits, waves, 0};
+    SkPlan lp;
+    lp.splits = fewest_splits(nb, kLoopWaves);
+    lp.waves = (nb + lp.splits - 1) / lp.splits;
+    const int resident = resident_blocks(skinny_kernel(type, rt, true), 64 * lp.waves, skinny_lds(lp.waves, rt));
+    const int64_t tiles = units / ttiles;
+    lp.loop_groups =
+        static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(tiles, resident / (lp.splits * ttiles))));
+    return lp;
 }
 
 int row_tiles(const qk_matrix *mats, int n_mats, bool pair) {
@@ -556,13 +617,13 @@ int row_tiles(const qk_matrix *mats, int n_mats, bool pair) {
 }  // namespace
 
 // Workspace bound of a launch, for any storage type: the split sums of
-// the fewest splits of the narrowest workgroups (12 waves), or of the
-// planner's extra splits (at most kPartialUnitsMax units).
+// the fewest splits of the narrowest workgroups (the looping kernel's), or
+// of the planner's extra splits (at most kPartialUnitsMax units).
 size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair) {
     const int nb = cols / 256;
     if (nb <= 1 || n_tokens <= 0 || tiles <= 0) return 0;
     const int64_t units = static_cast<int64_t>(tiles) * ((n_tokens + kToks - 1) / kToks);
-    const int s0 = fewest_splits(nb, 12);
+    const int s0 = fewest_splits(nb, kLoopWaves);
     const int64_t sums = std::max<int64_t>(s0 > 1 ? units * s0 : 0,
                                            std::min<int64_t>(units * std::min(nb, kSplitsMax), kPartialUnitsMax));
     return static_cast<size_t>(sums) * (pair ? 2 : 1) * 1024 * sizeof(float);
@@ -616,7 +677,10 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
     if (token_tiles > 65535 || static_cast<int64_t>(tiles) * kSplitsMax > (1 << 30))
         return fail(QK_ERR_LIMIT, std::string(where) + ": launch too large");
     const int rt = pair ? 2 : 1;
-    split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, type, rt, p.splits, p.waves);
+    const SkPlan plan = split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, token_tiles, type, rt);
+    p.splits = plan.splits;
+    p.waves = plan.waves;
+    p.tiles = tiles;
     // The plan's split sums; callers size the workspace by
     // skinny_i8_workspace_bytes, which bounds every plan.
     const size_t need = p.splits > 1 ? static_cast<size_t>(tiles) * token_tiles * p.splits * rt * 1024 * sizeof(float)
@@ -629,11 +693,12 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
         p.partials = static_cast<float *>(workspace);
     }
     const size_t lds = skinny_lds(p.waves, rt);
-    const dim3 grid(static_cast<unsigned>(tiles * p.splits), static_cast<unsigned>(token_tiles));
-    if (pair)
-        launch_type<2>(type, grid, 64 * p.waves, lds, stream, p);
-    else
-        launch_type<1>(type, grid, 64 * p.waves, lds, stream, p);
+    const int groups = plan.loop_groups ? plan.loop_groups : tiles;   // workgroups per (split, token tile)
+    void *args[] = {&p};
+    if (hipLaunchKernel(skinny_kernel(type, rt, plan.loop_groups > 0),
+                        dim3(static_cast<unsigned>(groups * p.splits), static_cast<unsigned>(token_tiles)),
+                        dim3(64 * p.waves), args, lds, stream) != hipSuccess)
+        return launch_status(where);
     if (p.splits > 1) {
         const dim3 rgrid(static_cast<unsigned>(tiles), static_cast<unsigned>(token_tiles));
         if (pair)

@@ -13,7 +13,10 @@ dot_q4_block_dp4a / dot_q6_block_dp4a, 520-542, 613-643).
   block: within rel-L2 1e-5 of the oracle's fp64 combine (gemv_i8_f64).
 * Fused matrices of mixed types, the split Q6_K layout, and the FFN call
   (SiLU(gate) * up quantized in the gate / up product's epilogue) against
-  the oracle's quantizer and fp64 products."""
+  the oracle's quantizer and fp64 products.
+* Launches larger than one round of workgroups (20010 rows, or the FFN at
+  520 tokens), which walk their row tiles with the next tile's weights in
+  flight, against the same fp64 bars."""
 import numpy as np
 import pytest
 
@@ -147,7 +150,32 @@ def test_fused_qkv_mixed_types(qk, torch_gpu, oracle, workloads, ntok, split_v, 
             assert rel_l2(got[k], want) < 1e-5, (i, k)
 
 
-@pytest.mark.parametrize("ntok", [4, 8, 32, 40])
+@pytest.mark.parametrize("qtype", [Q4_K, Q6_K, 114])
+@pytest.mark.parametrize("cols,ntok", [(2048, 32), (3072, 70)])
+def test_tile_walking_launch(qk, torch_gpu, oracle, workloads, synth, qtype, cols, ntok):
+    """More (row tile, token tile) units than the chip holds at once: the
+    workgroups walk the row tiles with the next tile's weights in flight
+    (3072 columns: two splits and the reduction too).  20010 rows, so the
+    last row tile is partial; three tokens of every token tile against the
+    fp64 oracle at rel-L2 1e-5."""
+    t = torch_gpu
+    base = Q6_K if qtype == 114 else qtype
+    rows = 20010
+    w, x = workloads.gemv_case(base, cols, rows, seed=140, n_tokens=ntok)
+    xq = np.zeros((ntok, LDXQ), dtype=np.int8)
+    xs = np.zeros((ntok, LDSCALE), dtype=np.float32)
+    for k in range(ntok):
+        xq[k, :cols], xs[k, : cols // 32] = oracle.quantize_x32(x[k])
+    wk = w
+    if qtype == 114:
+        wk = qk.split_q6k(qk.Tensor((cols, rows), Q6_K, to_dev(t, w))).data.cpu().numpy()
+    got = _run(qk, t, qtype, wk, xq, xs, cols, rows, ntok)
+    for k in sorted({0, 31, ntok // 2, ntok - 1}):
+        want = oracle.gemv_i8_f64(base, w, xq[k, :cols], xs[k, : cols // 32], cols, rows)
+        assert rel_l2(got[k], want) < 1e-5, k
+
+
+@pytest.mark.parametrize("ntok", [4, 8, 32, 40, 520])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_ffn_int8(qk, torch_gpu, oracle, workloads, synth, ntok, accumulate):
     """gate / up, SiLU(gate) * up quantized per 32, down: the hidden rows the
@@ -185,7 +213,11 @@ def test_ffn_int8(qk, torch_gpu, oracle, workloads, synth, ntok, accumulate):
     for k in range(ntok):
         g = oracle.gemv_i8_f64(Q4_K, gw, xq[k], xs[k], dim, hidden)
         u = oracle.gemv_i8_f64(Q4_K, uw, xq[k], xs[k], dim, hidden)
-        h = (g / (1.0 + np.exp(-np.clip(g, -80, 80))) * u).astype(np.float32)
+        # silu_cuda's fp32 arithmetic: exp(-g) overflows to inf below g = -88.7
+        # and the product is then 0 (at 520 tokens whole groups of 32 lie there).
+        g32, u32 = g.astype(np.float32), u.astype(np.float32)
+        with np.errstate(over="ignore"):
+            h = g32 / (np.float32(1.0) + np.exp(-g32)) * u32
         wq, wsc = oracle.quantize_x32(h)
         assert np.max(np.abs(hq[k].astype(int) - wq.astype(int))) <= 1, k
         flips += int(np.count_nonzero(hq[k] != wq))
