@@ -401,7 +401,7 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             # pick.  INT8, per layer: norm+quantize, QKV, attention, quantize,
             # o (+add), norm+quantize, gate/up, SiLU*up+quantize, down (+add);
             # then embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (9 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
+            "kernels_per_token": (6 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
             "device_bytes": mem}
 
 

@@ -185,6 +185,8 @@ __device__ __forceinline__ float limb_dot(const uint32_t *codes, const int *limb
 
 struct F32Policy {
     static constexpr bool kPrepLds = true;
+    static constexpr bool kInt8 = false;
+    static constexpr bool kDirect = true;   // load_direct exists (rows too long to stage)
 
     struct Lane {
         int limb[4][12];
@@ -341,6 +343,8 @@ struct F32ArgPolicy : F32FusedPolicy {
 
 struct I8Policy {
     static constexpr bool kPrepLds = false;
+    static constexpr bool kInt8 = true;
+    static constexpr bool kDirect = true;
     static constexpr bool kAccumulate = true;   // the INT8 step's residual adds
     static constexpr bool kArgmax = false;
     __host__ __device__ static size_t lds_bytes(int) { return 0; }
@@ -425,6 +429,155 @@ struct I8Policy {
             acc = fmaf(d * sc[part] * static_cast<float>(D[part] - 32 * L.xs[part]), L.scale[part], acc);
         return acc;
     }
+};
+
+// The INT8 step's activations quantized by the GEMV itself: every block
+// quantizes its token's fp32 row into LDS (codes, then per-32 scales, then
+// 64 bytes of reduction scratch) and the lanes read their pieces from
+// there.  The row is RMSNorm(x) * norm_w (norm_w set), SiLU(x) * up (up
+// set) or x, quantized per 32 values -- the arithmetic of
+// rmsnorm_quantize_kernel, silu_mul_quantize_kernel and quantize_x32_kernel
+// (rmsnorm_quantize_cuda, silu_cuda + quantize_x32_cuda, quantize_x32_cuda;
+// inferencer.cu:839-889, 1053-1056, 544-556).  With 256-thread blocks the
+// sum of squares runs in rmsnorm_quantize_kernel's order, so the codes and
+// scales are those kernels' bit for bit; other block sizes (3072 columns)
+// sum in their own order.
+struct I8FusedPolicy : I8Policy {
+    static constexpr bool kPrepLds = true;
+    static constexpr bool kDirect = false;
+
+    __host__ __device__ static size_t lds_bytes(int cols) {
+        return static_cast<size_t>(cols) + static_cast<size_t>(cols / 32) * sizeof(float) + 64;
+    }
+
+    // A group of 32 values is eight float4 of eight adjacent lanes (n4 is a
+    // multiple of 8 and blocks hold whole waves): amax in three xor
+    // shuffles, scale and codes as quantize_x32_kernel's.
+    __device__ static void quantize4(const float4 &o, int i, uint32_t *q4, float *st) {
+        float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+        amax = fmaxf(amax, __shfl_xor(amax, 1));
+        amax = fmaxf(amax, __shfl_xor(amax, 2));
+        amax = fmaxf(amax, __shfl_xor(amax, 4));
+        const float gs = amax > 0.f ? amax / 127.f : 1.f;
+        if ((i & 7) == 0) st[i >> 3] = gs;
+        auto q8 = [gs](float val) {
+            int q = static_cast<int>(rintf(val / gs));
+            q = q < -127 ? -127 : (q > 127 ? 127 : q);
+            return static_cast<uint32_t>(q) & 0xFFu;
+        };
+        q4[i] = q8(o.x) | (q8(o.y) << 8) | (q8(o.z) << 16) | (q8(o.w) << 24);
+    }
+
+    // Rows of up to kHeld float4 per thread are read once, x and the gains
+    // together, and held in registers across the sum of squares; longer rows
+    // read x twice.
+    static constexpr int kHeld = 4;
+
+    __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
+        uint32_t *q4 = reinterpret_cast<uint32_t *>(lds);
+        float *st = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + cols);
+        float *scratch = st + cols / 32;
+        const float4 *x4 = reinterpret_cast<const float4 *>(static_cast<const float *>(p.x) +
+                                                            static_cast<int64_t>(token) * p.ldx);
+        const float4 *w4 = reinterpret_cast<const float4 *>(p.norm_w);
+        const float4 *u4 = reinterpret_cast<const float4 *>(p.up + (p.up ? static_cast<int64_t>(token) * p.ldx : 0));
+        const int n4 = cols >> 2;
+        const int nt = blockDim.x;
+        const int tid = threadIdx.x;
+        if (p.norm_w && n4 <= kHeld * nt) {
+            float4 v[kHeld], w[kHeld];
+            #pragma unroll
+            for (int k = 0; k < kHeld; ++k) {
+                const int i = tid + k * nt;
+                if (i < n4) {
+                    v[k] = x4[i];
+                    w[k] = w4[i];
+                }
+            }
+            float ss = 0.f;
+            #pragma unroll
+            for (int k = 0; k < kHeld; ++k) {
+                if (tid + k * nt < n4) {
+                    ss = fmaf(v[k].x, v[k].x, ss);
+                    ss = fmaf(v[k].y, v[k].y, ss);
+                    ss = fmaf(v[k].z, v[k].z, ss);
+                    ss = fmaf(v[k].w, v[k].w, ss);
+                }
+            }
+            const float scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+            #pragma unroll
+            for (int k = 0; k < kHeld; ++k) {
+                const int i = tid + k * nt;
+                if (i < n4)
+                    quantize4(make_float4(v[k].x * scale * w[k].x, v[k].y * scale * w[k].y, v[k].z * scale * w[k].z,
+                                          v[k].w * scale * w[k].w),
+                              i, q4, st);
+            }
+            return;
+        }
+        float scale = 1.f;
+        if (p.norm_w) {
+            float ss = 0.f;
+            #pragma unroll 4
+            for (int i = tid; i < n4; i += nt) {
+                const float4 v = x4[i];
+                ss = fmaf(v.x, v.x, ss);
+                ss = fmaf(v.y, v.y, ss);
+                ss = fmaf(v.z, v.z, ss);
+                ss = fmaf(v.w, v.w, ss);
+            }
+            scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+        }
+        for (int i = tid; i < n4; i += nt) {
+            const float4 v = x4[i];
+            float4 o = v;
+            if (p.norm_w) {
+                const float4 w = w4[i];
+                o = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+            } else if (p.up) {
+                const float4 u = u4[i];
+                o = make_float4(silu_mul_value(v.x, u.x), silu_mul_value(v.y, u.y), silu_mul_value(v.z, u.z),
+                                silu_mul_value(v.w, u.w));
+            }
+            quantize4(o, i, q4, st);
+        }
+    }
+
+    // Block sum in rmsnorm_quantize_kernel's order for 256 threads (every
+    // wave's xor tree, then (w0 + w1) + (w2 + w3)); in wave order otherwise.
+    __device__ static float block_sum(float ss, float *scratch) {
+        #pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        if (blockDim.x == 256) return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+        ss = 0.f;
+        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) ss += scratch[w];
+        return ss;
+    }
+
+    // The lane's piece from LDS: I8Policy::load_direct's layout.
+    __device__ static void load(Lane &L, const GemvParams &p, int, int piece, const XGroup *lds) {
+        const int cols = p.pieces * 64;
+        const int b = piece >> 2, g = (piece >> 1) & 1, h = piece & 1;
+        const uint8_t *xq = reinterpret_cast<const uint8_t *>(lds) + b * 256 + g * 128 + h * 16;
+        const float *st = reinterpret_cast<const float *>(reinterpret_cast<const uint8_t *>(lds) + cols) + b * 8 + g * 4;
+        #pragma unroll
+        for (int part = 0; part < 4; ++part) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(xq + part * 32);
+            L.xq[part * 4 + 0] = static_cast<int>(v.x);
+            L.xq[part * 4 + 1] = static_cast<int>(v.y);
+            L.xq[part * 4 + 2] = static_cast<int>(v.z);
+            L.xq[part * 4 + 3] = static_cast<int>(v.w);
+            int sum = 0;
+            #pragma unroll
+            for (int k = 0; k < 4; ++k) sum = __builtin_amdgcn_sdot4(L.xq[part * 4 + k], 0x01010101, sum, false);
+            L.xs[part] = sum;
+            L.scale[part] = st[part];
+        }
+    }
+
+    __device__ static void load_direct(Lane &, const GemvParams &, int, int) {}
 };
 
 // Type dispatch of one piece: TYPE is the storage type when every matrix of
@@ -974,7 +1127,7 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const void *k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP>);
         // Whole-tile reads for the FP32 policies (3B LM head 60.3 against
         // 60.9 us); the INT8 kernel measured slower with them (57.4 / 56.4).
-        if constexpr (TYPE != 0 && !std::is_same_v<Policy, I8Policy>) {
+        if constexpr (TYPE != 0 && !Policy::kInt8) {
             whole = p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0;
             if (whole) k = reinterpret_cast<const void *>(gemv_split<Policy, TYPE, GROUP, true>);
         }
@@ -991,7 +1144,7 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + wgroups - 1) / wgroups, cap));
         const int grid = std::min(grid_all, p.arg_v ? kArgPartsMax / (block / 64) : grid_all);
         if (p.grid_out) *p.grid_out = grid * (block / 64);
-        if constexpr (TYPE != 0 && !std::is_same_v<Policy, I8Policy>) {
+        if constexpr (TYPE != 0 && !Policy::kInt8) {
             if (whole) {
                 hipLaunchKernelGGL((gemv_split<Policy, TYPE, GROUP, true>), dim3(grid, n_tokens), dim3(block), lds,
                                    stream, p);
@@ -1045,9 +1198,13 @@ int launch(GemvParams &p, const qk_matrix *mats, int n_mats, int cols, int n_tok
     p.total_tiles = static_cast<int>(tiles);
 
     if (long_rows) {
-        const int block = 256, waves = block / 64;
-        const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, device_info().cus * 8));
-        hipLaunchKernelGGL(gemv_long<Policy>, dim3(grid, n_tokens), dim3(block), 0, stream, p);
+        if constexpr (Policy::kDirect) {
+            const int block = 256, waves = block / 64;
+            const int grid = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, device_info().cus * 8));
+            hipLaunchKernelGGL(gemv_long<Policy>, dim3(grid, n_tokens), dim3(block), 0, stream, p);
+        } else {
+            return fail(QK_ERR_LIMIT, std::string(where) + ": rows too long to stage in LDS");
+        }
     } else if (type == QK_TYPE_Q4_K) {
         launch_group<Policy, QK_TYPE_Q4_K>(p, n_tokens, stream);
     } else if (type == QK_TYPE_Q6_K) {
@@ -1522,6 +1679,28 @@ int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq
     p.ldscale = ldscale;
     p.accumulate = accumulate;
     return launch<I8Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "INT8 GEMV launch");
+}
+
+// The INT8 GEMV quantizing its own input (I8FusedPolicy): fp32 rows x of
+// n_tokens tokens, RMSNorm'd with norm_w (eps) or multiplied by SiLU with up
+// (same strides as x) first when either is set.
+int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int ldx, const float *norm_w, float eps,
+                          const float *up, int cols, int n_tokens, const int *ldy, int accumulate,
+                          hipStream_t stream) {
+    GemvParams p{};
+    p.x = x;
+    p.ldx = ldx;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
+    p.up = up;
+    p.accumulate = accumulate;
+    return launch<I8FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "staged INT8 GEMV launch");
+}
+
+bool gemv_i8_stageable(int cols) {
+    if (cols <= 0 || cols % 256) return false;
+    const int pieces = cols / 64;
+    return pieces / gcd_int(pieces, 64) <= kMaxChunks && I8FusedPolicy::lds_bytes(cols) + 4096 <= kMaxLds;
 }
 
 bool gemv_fusable(int cols) {

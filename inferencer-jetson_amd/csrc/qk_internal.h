@@ -104,6 +104,13 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
 // adds W x into y instead of overwriting it.
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                    int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
+// The INT8 GEMV quantizing its own fp32 input per 32 values in LDS, after
+// RMSNorm with norm_w (eps) or SiLU(x) * up when given -- bit for bit the
+// separate quantization kernels' codes with 256-thread blocks.  Only for
+// rows gemv_i8_stageable accepts.
+int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int ldx, const float *norm_w, float eps,
+                          const float *up, int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
+bool gemv_i8_stageable(int cols);
 // INT8 product of n_tokens per-32 quantized rows with n_mats matrices on
 // the integer matrix cores (csrc/qk_skinny.hip), arguments already
 // validated: y_m[t*ldy[m] + r] overwritten (or added with accumulate); with

@@ -211,11 +211,15 @@ int residual_by_mode(qk_llama *m, int type, int rows, const void *w, const float
 // one launch before the QKV and gate/up GEMVs, the attention output quantized
 // before the o GEMV, SiLU * up and its quantization in one launch before the
 // down GEMV, and the residual adds in the INT8 GEMVs' epilogues (the same
-// fp32 sums as the reference's separate add launches).
+// fp32 sums as the reference's separate add launches).  With every matrix in
+// INT8 mode and no input traces, the QKV, o and gate/up GEMVs quantize their
+// own inputs instead (launch_gemv_i8_staged: the same codes, three launches
+// per layer fewer).
 int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
     const qk_llama_config &c = m->cfg;
     const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
     int st;
+    const bool staged = m->int8_q4k && m->int8_q6k && !m->trace_q && qk::gemv_i8_stageable(dim);
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
     qk::SplitAttention attn{};
     attn.q = m->q;
@@ -241,7 +245,27 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     auto trace_q = [&](int l, int stage, int cols) {
         return trace_copy(m->trace_q ? m->trace_q + (l * 4 + stage) * qstride : nullptr, m->xq, cols, s);
     };
-    for (int l = 0; l < c.layers; ++l) {
+    for (int l = 0; l < c.layers && staged; ++l) {
+        const qk_llama_layer &L = m->layers[l];
+        const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
+        if ((st = qk::launch_gemv_i8_staged(qkv, 3, m->x, dim, L.attn_norm, c.eps, nullptr, dim, 1, nullptr, 0, s)))
+            return st;
+        attn.layer = l;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        const qk_matrix o{L.o_type, dim, L.o, m->x};
+        const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
+        const qk_matrix down{L.down_type, dim, L.down, m->x};
+        // Down keeps the separate SiLU * up quantization: every GEMV block
+        // would otherwise read and activate the whole 4 x hidden bytes twice.
+        if ((st = qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1, s)) ||
+            (st = qk::launch_gemv_i8_staged(gu, 2, m->x, dim, L.ffn_norm, c.eps, nullptr, dim, 1, nullptr, 0, s)) ||
+            (st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s)) ||
+            (st = qk::launch_gemv_i8(&down, 1, m->xq, c.hidden, m->xscale, c.hidden / 32, c.hidden, 1, nullptr, 1, s)) ||
+            (st = trace_copy(m->trace_x ? m->trace_x + static_cast<size_t>(l) * dim : nullptr, m->x,
+                             dim * sizeof(float), s)))
+            return st;
+    }
+    for (int l = 0; l < c.layers && !staged; ++l) {
         const qk_llama_layer &L = m->layers[l];
         if ((st = norm_quant(L.attn_norm)) || (st = trace_q(l, 0, dim))) return st;
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};

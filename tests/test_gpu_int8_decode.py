@@ -64,6 +64,36 @@ def _weights(wl, synth, cfg, seed):
     return W
 
 
+@pytest.mark.parametrize("cfg", [SMALL, dict(SMALL, dim=2048, hidden=8192, heads=32, kv_heads=8)])
+def test_staged_quantization_matches_separate_launches(qk, torch_gpu, workloads, synth, cfg):
+    """Both types in INT8 mode: the step's four GEMVs quantize their own
+    inputs (RMSNorm, plain, SiLU * up) instead of the separate quantization
+    launches, which the step still runs while INT8 inputs are traced.  The
+    codes are the same bit for bit at these widths (256-thread blocks sum the
+    squares in the separate kernel's order), so 8 steps' logits and tokens
+    are identical between the two."""
+    W = _weights(workloads, synth, cfg, 17)
+    kc, vc = workloads.llama_kv_prefill(cfg, 17, 20)
+    outs = []
+    for traced in (False, True):
+        gm = qk.Runner(cfg, W)
+        gm.set_int8(True, True)
+        gm.load_kv(kc, vc)
+        if traced:
+            tx = qk.DeviceBuffer(cfg["layers"] * cfg["dim"] * 4)
+            tq = qk.DeviceBuffer(cfg["layers"] * 4 * max(cfg["dim"], cfg["hidden"]))
+            gm.set_trace(tx, tq)
+        tok, got = 5, []
+        for i in range(8):
+            tok = gm.forward(tok, 20 + i, True)
+            got.append((tok, gm.logits()))
+        gm.close()
+        outs.append(got)
+    for (ta, la), (tb, lb) in zip(*outs):
+        assert ta == tb
+        assert np.array_equal(la, lb)
+
+
 def run_int8_decode(qk, oracle, wl, synth, cfg, seed, n_prefill, prompt, n_greedy, q4k, q6k, unit_gains=False):
     W = wl.llama_weights(cfg, seed) if unit_gains else _weights(wl, synth, cfg, seed)
     kc, vc = wl.llama_kv_prefill(cfg, seed, n_prefill)
