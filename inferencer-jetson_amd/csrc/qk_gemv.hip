@@ -451,21 +451,9 @@ struct I8FusedPolicy : I8Policy {
     }
 
     // A group of 32 values is eight float4 of eight adjacent lanes (n4 is a
-    // multiple of 8 and blocks hold whole waves): amax in three xor
-    // shuffles, scale and codes as quantize_x32_kernel's.
+    // multiple of 8 and blocks hold whole waves).
     __device__ static void quantize4(const float4 &o, int i, uint32_t *q4, float *st) {
-        float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
-        amax = fmaxf(amax, __shfl_xor(amax, 1));
-        amax = fmaxf(amax, __shfl_xor(amax, 2));
-        amax = fmaxf(amax, __shfl_xor(amax, 4));
-        const float gs = amax > 0.f ? amax / 127.f : 1.f;
-        if ((i & 7) == 0) st[i >> 3] = gs;
-        auto q8 = [gs](float val) {
-            int q = static_cast<int>(rintf(val / gs));
-            q = q < -127 ? -127 : (q > 127 ? 127 : q);
-            return static_cast<uint32_t>(q) & 0xFFu;
-        };
-        q4[i] = q8(o.x) | (q8(o.y) << 8) | (q8(o.z) << 16) | (q8(o.w) << 24);
+        quantize_quad_store(o, (i & 7) == 0, q4 + i, st + (i >> 3));
     }
 
     // Rows of up to kHeld float4 per thread are read once, x and the gains

@@ -151,6 +151,25 @@ __device__ __forceinline__ void quantize_group_store(float value, bool in_row, i
         *q_out = static_cast<int8_t>(q);
     }
 }
+
+// The same for four values a lane holds: eight adjacent lanes form one
+// 32-value group (amax in three xor shuffles, so all eight must be active
+// together); the first of them stores the scale.  q: the four codes, lowest
+// column in the low byte.
+__device__ __forceinline__ void quantize_quad_store(const float4 &o, bool first, uint32_t *q, float *scale_out) {
+    float amax = fmaxf(fmaxf(fabsf(o.x), fabsf(o.y)), fmaxf(fabsf(o.z), fabsf(o.w)));
+    amax = fmaxf(amax, __shfl_xor(amax, 1));
+    amax = fmaxf(amax, __shfl_xor(amax, 2));
+    amax = fmaxf(amax, __shfl_xor(amax, 4));
+    const float gs = amax > 0.f ? amax / 127.f : 1.f;
+    if (first) *scale_out = gs;
+    auto q8 = [gs](float val) {
+        int c = static_cast<int>(rintf(val / gs));
+        c = c < -127 ? -127 : (c > 127 ? 127 : c);
+        return static_cast<uint32_t>(c) & 0xFFu;
+    };
+    *q = q8(o.x) | (q8(o.y) << 8) | (q8(o.z) << 16) | (q8(o.w) << 24);
+}
 // Whether a row of cols columns can stage its activations for the fusions.
 bool gemv_fusable(int cols);
 // n_tokens tokens (x + t*ldx; y + t*ldy[m], NULL: rows), arguments already
@@ -316,6 +335,11 @@ struct SplitAttention {
     uint8_t *gemm_rec;
     int64_t cache_rows;
     int64_t rows_hint;               // sum over tokens of pos + 1 (0: n_tokens * (max_pos + 1))
+    // The outputs quantized per 32 values as well ([n_tokens][heads *
+    // head_dim] codes, [n_tokens][heads * head_dim / 32] scales; head_dim % 32
+    // == 0), or NULL: the INT8 o projection's input.
+    int8_t *q8_out;
+    float *q8_scale;
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
     // Cache layout: 0 the reference's [layers][cache_rows][kv_heads][head_dim],
     // 1 [layers][kv_heads][cache_rows][head_dim] (the decode drivers' own: a

@@ -212,14 +212,15 @@ int residual_by_mode(qk_llama *m, int type, int rows, const void *w, const float
 // before the o GEMV, SiLU * up and its quantization in one launch before the
 // down GEMV, and the residual adds in the INT8 GEMVs' epilogues (the same
 // fp32 sums as the reference's separate add launches).  With every matrix in
-// INT8 mode and no input traces, the QKV, o and gate/up GEMVs quantize their
-// own inputs instead (launch_gemv_i8_staged: the same codes, three launches
-// per layer fewer).
+// INT8 mode and no input traces, the QKV and gate/up GEMVs quantize their
+// own inputs instead (launch_gemv_i8_staged) and the attention quantizes
+// o's: the same codes, three launches per layer fewer.
 int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
     const qk_llama_config &c = m->cfg;
     const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
     int st;
     const bool staged = m->int8_q4k && m->int8_q6k && !m->trace_q && qk::gemv_i8_stageable(dim);
+    const bool q8 = c.heads * hd == dim && hd % 32 == 0;   // the attention can quantize o's input
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
     qk::SplitAttention attn{};
     attn.q = m->q;
@@ -251,13 +252,18 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
         if ((st = qk::launch_gemv_i8_staged(qkv, 3, m->x, dim, L.attn_norm, c.eps, nullptr, dim, 1, nullptr, 0, s)))
             return st;
         attn.layer = l;
+        attn.q8_out = q8 ? m->xq : nullptr;
+        attn.q8_scale = q8 ? m->xscale : nullptr;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
         const qk_matrix down{L.down_type, dim, L.down, m->x};
-        // Down keeps the separate SiLU * up quantization: every GEMV block
-        // would otherwise read and activate the whole 4 x hidden bytes twice.
-        if ((st = qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1, s)) ||
+        // o reads the codes the attention wrote (or quantizes the attention's
+        // output itself); down keeps the separate SiLU * up quantization:
+        // every GEMV block would otherwise read and activate the whole
+        // 4 x hidden bytes twice.
+        if ((st = q8 ? qk::launch_gemv_i8(&o, 1, m->xq, dim, m->xscale, dim / 32, dim, 1, nullptr, 1, s)
+                     : qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1, s)) ||
             (st = qk::launch_gemv_i8_staged(gu, 2, m->x, dim, L.ffn_norm, c.eps, nullptr, dim, 1, nullptr, 0, s)) ||
             (st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s)) ||
             (st = qk::launch_gemv_i8(&down, 1, m->xq, c.hidden, m->xscale, c.hidden / 32, c.hidden, 1, nullptr, 1, s)) ||
@@ -829,9 +835,16 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
             return st;
         attn.layer = l;
         attn.gemm_rec = nullptr;
+        // The attention quantizes its own outputs for o (quantize_batch_cuda's
+        // codes) when its rows are the o projection's input rows.
+        const bool q8 = c.heads * hd == dim && hd % 32 == 0;
+        attn.q8_out = q8 ? m->xq : nullptr;
+        attn.q8_scale = q8 ? m->xs : nullptr;
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        attn.q8_out = nullptr;
+        attn.q8_scale = nullptr;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
-        if ((st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xs, dim / 32, dim, T, s)) ||
+        if ((!q8 && (st = qk_quantize_x32(m->attn, dim, m->xq, dim, m->xs, dim / 32, dim, T, s))) ||
             (st = trace_q(l, 1, m->xq, dim)) || (st = batch_gemm_i8(m, &o, 1, m->xq, m->xs, dim, T, true, s)) ||
             (st = norm_quant(L.ffn_norm)) || (st = trace_q(l, 2, m->xq, dim)))
             return st;

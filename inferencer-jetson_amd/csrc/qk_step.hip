@@ -571,6 +571,13 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
             const float4 r = scale4(x, 1.0f / lw);
             *reinterpret_cast<float4 *>(o + g * hd + 4 * e) = r;
             if (a.rec_out || a.gemm_rec) qs[g * HD / 4 + e] = r;   // the query rows are in registers by now
+            if (a.q8_out) {
+                // Column kvh * G * hd + 4 * i of the token's row; hv % 8 == 0, so
+                // the eight lanes of a group share g and are active together.
+                const int64_t c4 = (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 4 + i;
+                quantize_quad_store(r, (i & 7) == 0, reinterpret_cast<uint32_t *>(a.q8_out) + c4,
+                                    a.q8_scale + c4 / 8);
+            }
         } else {
             if (e == 0) {
                 mine[g] = mw;
@@ -629,6 +636,11 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
         }
         o[i] = num / den;
         if (a.rec_out || a.gemm_rec) mo[i] = num / den;
+        if (a.q8_out) {
+            // G * hd % 32 == 0: a half-wave holds one group, active together.
+            const int64_t c = static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd + i;
+            quantize_group_store(num / den, true, threadIdx.x & 31, a.q8_out + c, a.q8_scale + c / 32);
+        }
     }
     if (a.gemm_rec) {
         __syncthreads();
@@ -847,6 +859,8 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     if (!fn) return fail(QK_ERR_LIMIT, "split attention: unsupported head layout");
     if (a.n_tokens > 65535) return fail(QK_ERR_LIMIT, "split attention: too many tokens in one launch");
     if (a.rec_out && a.head_dim % 16) return fail(QK_ERR_LIMIT, "split attention: records need head_dim % 16 == 0");
+    if (a.q8_out && (a.head_dim % 32 || !a.q8_scale))
+        return fail(QK_ERR_LIMIT, "split attention: quantized outputs need head_dim % 32 == 0 and scales");
     const int max_rows = a.max_pos + 1;
     // Few (token, KV head) pairs over short rows: one wide workgroup each
     // reads all of its rows, and no merge kernel runs.  A CU alone streams
