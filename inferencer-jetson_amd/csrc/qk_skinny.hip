@@ -291,10 +291,10 @@ __device__ __forceinline__ void wave_sync() {
 template <int TYPE>
 __device__ __forceinline__ void act_prep(const uint4 (&ca)[8], const float (&cx)[8], float *xst, int col, int kh,
                                          float (&xss)[8]) {
-    if (kh == 0) {
-        #pragma unroll
-        for (int c = 0; c < 8; ++c) xst[c * kToks + col] = cx[c];
-    }
+    // Both column halves write the same values (no branch for the
+    // compiler to sink the scale loads into).
+    #pragma unroll
+    for (int c = 0; c < 8; ++c) xst[c * kToks + col] = cx[c];
     wave_sync();
     if (is_q4<TYPE>(TYPE)) {
         #pragma unroll
