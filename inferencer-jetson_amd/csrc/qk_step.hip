@@ -376,9 +376,16 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
     __shared__ float4 part[kSplitWaves][G * HD / 4];
     __shared__ float wm[kSplitWaves][G], wl[kSplitWaves][G];
     const SplitAttention &a = ka.a;
-    // Workgroup x serves query heads x*G .. x*G + G - 1 of KV head
-    // x / head_split; the first of a KV head's workgroups writes its row.
-    const int kvh = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
+    // Workgroup kvh serves query heads kvh*G .. kvh*G + G - 1 of KV head
+    // kvh / head_split; the first of a KV head's workgroups writes its row.
+    // With head_split > 1 the workgroups sharing a KV head are numbered
+    // kv_heads apart: workgroups are dealt to the XCDs round-robin, so they
+    // land on one XCD (kv_heads a multiple of 8) and read the rows through
+    // one L2 instead of fetching them head_split times.
+    const int kvh = ka.head_split > 1 ? static_cast<int>(blockIdx.x % a.kv_heads) * ka.head_split +
+                                            static_cast<int>(blockIdx.x / a.kv_heads)
+                                      : static_cast<int>(blockIdx.x);
+    const int b = blockIdx.y, split = blockIdx.z;
     const int cache_kvh = kvh / ka.head_split;
     const bool writer = kvh % ka.head_split == 0;
     const int tid = threadIdx.x, lane = tid & 63;
