@@ -75,6 +75,20 @@ int64_t qk_tensor_bytes(int type, int64_t cols, int64_t rows);
 
 /* ------------------------------------------------ FP32 dequant-GEMV -- */
 
+/* Precision of the FP32 entry points (this section, the FP32 step kernels
+   that feed them and the FP32 decode drivers): x is carried as 22-bit block
+   fixed point per 16 consecutive values, X = rint(x * 2^(21-e)) with e =
+   ilogb of the group's largest |x|, so each value is rounded to within
+   2^(e-22) -- relative 2^-22 for the group's largest value, coarser for
+   values far below it -- and the products and sums that follow are exact
+   integer dots plus fp32 combines.  An output therefore differs from the
+   reference's fp32 products by at most sum_c |W[r][c]| 2^(e_c - 22) plus
+   fp32 rounding (tests/test_gpu_gemv.py pins both terms); on N(0, 1)-like
+   activations that is within 1e-6 rel-L2 of an fp64 product.  The
+   multi-token forms carry the same 22 bits per 256-column block as fp16
+   high / low halves.  The INT8 entry points below follow the reference's
+   INT8 arithmetic instead. */
+
 /* y[r] = sum_c W[r][c] * x[c] for r < rows.
    Replaces FastGPU::matvec's FP32 branch (inferencer.cu:1156-1171) and the
    gemv_quant<12|14> kernel (inferencer.cu:645-661) it launches. */
@@ -108,8 +122,9 @@ int qk_gemv_multi_f32(const qk_matrix *mats, int n_mats, const float *x, int col
 size_t qk_gemv_batched_workspace_bytes(int cols, int rows, int n_tokens);
 
 /* Multi-token variant: y[t*ldy + r] = sum_c W[r][c] * x[t*ldx + c] for
-   t < n_tokens (token-major like inferencer.cu:698).  FP32 semantics of the
-   reference's INT8-only batched path FastRunner::batch_matvec +
+   t < n_tokens (token-major like inferencer.cu:698).  The FP32 arithmetic
+   above (22-bit block fixed point per 256-column block) applied to the
+   reference's batched path FastRunner::batch_matvec +
    gemv_batch_dp4a (inferencer.cu:1265-1278, 678-699), without its 32-token
    cap; n_tokens = 0 is a no-op.  workspace holds at least
    qk_gemv_batched_workspace_bytes(cols, rows, n_tokens) device bytes and
@@ -230,12 +245,15 @@ int qk_gemv_i8(int type, const void *w, const int8_t *xq, int ldxq, const float 
    (d*sc*dot - dmin*m*sum(xq)) * xscale (Q4_K, inferencer.cu:520-542) and
    d*scale*dot*xscale (Q6_K, 613-643; two sub-blocks sharing an xscale are
    added in integers first); below 8 tokens it is qk_gemv_i8.  A workgroup
-   takes 32 rows x 32 tokens x up to 8 blocks of the row; rows longer than
-   2048 columns are split over workgroups and a second launch adds their
-   sums in order, which needs the workspace
-   (qk_gemv_batched_i8_workspace_bytes(cols, rows, n_tokens), 16-byte
-   aligned; 0 bytes, and NULL allowed, up to 2048 columns or below 8
-   tokens). */
+   takes 32 rows x 32 tokens x up to 12 or 16 blocks of the row, one per
+   wave.  Each launch's plan, chosen from the kernels' occupancy on the
+   device, may split rows over workgroups, whose sums a second launch adds
+   in split order (deterministic), and a launch larger than the chip holds
+   at once lets resident workgroups walk the row tiles.  The workspace
+   holds the split sums of any plan:
+   qk_gemv_batched_i8_workspace_bytes(cols, rows, n_tokens) bytes, 16-byte
+   aligned (0, and NULL allowed, below 8 tokens or at 256 columns; a plan
+   without splits ignores it). */
 size_t qk_gemv_batched_i8_workspace_bytes(int cols, int rows, int n_tokens);
 int qk_gemv_batched_i8(int type, const void *w, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                        float *y, int ldy, int cols, int rows, int n_tokens, void *workspace, size_t workspace_bytes,
@@ -252,8 +270,9 @@ int qk_gemv_multi_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, const 
    inferencer.cu:701-751): 1..QK_MAX_FUSED matrices (any mix of Q4_K, Q6_K
    and split Q6_K) of cols columns read the same n_tokens quantized rows (xq
    + t*ldxq, xscale + t*ldscale); mats[m].y receives [n_tokens][rows_m].
-   One launch from 8 tokens on (two above 2048 columns); workspace
-   qk_gemv_batched_i8_workspace_bytes(cols, sum of the rows, n_tokens). */
+   One launch from 8 tokens on (two when the plan splits the rows);
+   workspace qk_gemv_batched_i8_workspace_bytes(cols, sum of the rows,
+   n_tokens). */
 int qk_gemv_multi_batched_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale,
                              int ldscale, int cols, int n_tokens, void *workspace, size_t workspace_bytes,
                              qk_stream stream);
@@ -264,11 +283,11 @@ int qk_gemv_multi_batched_i8(const qk_matrix *mats, int n_mats, const int8_t *xq
    values (quantize_batch_cuda, 891-904), down (gemv_batch_dp4a), into
    y[t*ldy + c] (overwritten, or added with accumulate: add_batch_cuda).
    From 8 tokens on, the gate / up product forms SiLU * up and its
-   quantization in its own epilogue (or its reduction launch, above 2048
-   columns), then down.  gate and up have one storage type.  The workspace
+   quantization in its own epilogue (or its reduction launch when the plan
+   splits its rows), then down.  gate and up have one storage type.  The workspace
    holds the quantized hidden rows and the split sums:
    qk_ffn_batched_i8_workspace_bytes(dim, hidden, n_tokens), 256-byte
-   aligned. */
+   aligned (also enough for fewer tokens). */
 size_t qk_ffn_batched_i8_workspace_bytes(int dim, int hidden, int n_tokens);
 int qk_ffn_batched_i8(int gate_type, const void *gate, int up_type, const void *up, int down_type, const void *down,
                       const int8_t *xq, int ldxq, const float *xscale, int ldscale, float *y, int ldy, int dim,

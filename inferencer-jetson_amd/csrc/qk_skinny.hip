@@ -795,7 +795,10 @@ int qk_gemv_multi_batched_i8(const qk_matrix *mats, int n_mats, const int8_t *xq
 
 size_t qk_ffn_batched_i8_workspace_bytes(int dim, int hidden, int n_tokens) {
     if (dim <= 0 || dim % 256 || hidden <= 0 || hidden % 256 || n_tokens <= 0) return 0;
-    return ffn_i8_bytes(dim, hidden, n_tokens);
+    // Enough for any token count up to n_tokens: each form's need grows
+    // with the count, so the larger of the two forms' needs covers both.
+    return std::max(ffn_i8_bytes(dim, hidden, n_tokens),
+                    ffn_i8_bytes(dim, hidden, std::min(n_tokens, kMatrixCoreTokens - 1)));
 }
 
 int qk_ffn_batched_i8(int gate_type, const void *gate, int up_type, const void *up, int down_type, const void *down,

@@ -133,12 +133,14 @@ def test_validation_errors(qk, torch_gpu):
 @pytest.mark.parametrize("qtype", [Q4_K, Q6_K])
 def test_wide_range_within_groups(qk, torch_gpu, oracle, workloads, qtype):
     """Every 16-column activation group holds one value ~1e3 and fifteen
-    ~1e-3 (10^6 apart).  The FP32 kernels carry each group as 22-bit
-    fixed point relative to its largest value, so the small values keep
-    only ~2 bits each; the output still meets the 1e-5 bar against fp64
-    because the large values dominate every row.  The error of the small
-    values' own share is printed, not bounded: it is the cost of the block
-    fixed point against true fp32 products."""
+    ~1e-3 (10^6 apart).  The FP32 kernels carry each group as 22-bit block
+    fixed point: X = rint(x * 2^(21-e)), e = ilogb(max|x|) of the group, so
+    each value is rounded to within 2^(e-22) and the small ones keep ~2
+    bits.  Pinned three ways: the device equals the fp64 product of that
+    rounded x to fp32 rounding (rel-L2 1e-6), the rounding moves each row by
+    at most sum_k |W_rk| 2^(e_k - 22) (the documented bound, computed from
+    the dequantized weights), and the whole output meets the 1e-5 bar
+    against the exact fp64 product because the large values dominate."""
     cols, rows = 2048, 515
     w, _ = workloads.gemv_case(qtype, cols, rows, seed=43)
     rng = np.random.default_rng(44)
@@ -148,11 +150,23 @@ def test_wide_range_within_groups(qk, torch_gpu, oracle, workloads, qtype):
     y = run_gemv(qk, torch_gpu, qtype, w, x, cols, rows)
     y64 = oracle.gemv_f64(qtype, w, x, cols, rows)
     assert rel_l2(y, y64) < TOL
+    # The block fixed point in fp64: e = ilogb of each group's max.
+    gmax = np.abs(x.astype(np.float64)).reshape(-1, 16).max(axis=1)
+    e = (np.frexp(gmax)[1] - 1).astype(np.float64)
+    step = np.repeat(np.exp2(e - 21), 16)
+    xf = np.rint(x.astype(np.float64) / step) * step
+    yf = oracle.gemv_f64(qtype, w, xf.astype(np.float32), cols, rows)
+    assert np.array_equal(xf.astype(np.float32).astype(np.float64), xf)   # the rounded x is exact in fp32
+    assert rel_l2(y, yf) < 1e-6
+    W = oracle.dequant(qtype, w, cols, rows).astype(np.float64).reshape(rows, cols)
+    bound = np.abs(W) @ (step / 2)
+    assert np.all(np.abs(yf - y64) <= bound * (1 + 1e-9))
     xs = x.copy()
     xs[big] = 0.0
     small = oracle.gemv_f64(qtype, w, xs, cols, rows)
-    print(f"rel-L2 {rel_l2(y, y64):.2e}; error / norm of the small values' share "
-          f"{np.linalg.norm(y - y64) / np.linalg.norm(small):.2e}", flush=True)
+    print(f"rel-L2 {rel_l2(y, y64):.2e}, against the rounded x {rel_l2(y, yf):.2e}; error / norm of the small "
+          f"values' share {np.linalg.norm(y - y64) / np.linalg.norm(small):.2e}; largest row error / bound "
+          f"{np.max(np.abs(yf - y64) / bound):.2f}", flush=True)
 
 
 # One matrix whose rows fill whole tiles (64 / gcd(4 * nb, 64) rows) is read
