@@ -9,7 +9,9 @@ Llama with Llama 3's 128256-token vocabulary written to a GGUF file.
   1e-3 relative.
 * The command line's text equals the one-sequence driver's greedy tokens
   decoded, with sequential and with batched prefill (the prompt's cache
-  rows handed from the batched to the one-sequence driver)."""
+  rows handed from the batched to the one-sequence driver), and the fp64
+  oracle's greedy tokens decoded, over the same weights (up to the first
+  step whose top-2 margin is within fp32 roundoff of a tie)."""
 import io
 import importlib.util
 
@@ -27,15 +29,20 @@ CFG = dict(dim=256, layers=2, heads=4, kv_heads=2, hidden=512, vocab=128256, con
 PROMPT = "the quantized matrix, naïve GPU cache: 12345 tokens"
 
 
+def _weights(workloads, synth):
+    W = workloads.llama_weights(CFG, 31)
+    for l, L in enumerate(W["layers"]):
+        L["attn_norm"] = 1.0 + 0.2 * synth.normal_f32(CFG["dim"], 31, 600 + 2 * l)
+        L["ffn_norm"] = 1.0 + 0.2 * synth.normal_f32(CFG["dim"], 31, 601 + 2 * l)
+    return W
+
+
 @pytest.fixture(scope="module")
 def model(qk, workloads, synth, tmp_path_factory):
     pytest.importorskip("tokenizers")
     import inferencer_jetson_amd.tokenizer as T
     tokens, merges = V.trained_vocab(T.LLAMA3_SPLIT)
-    W = workloads.llama_weights(CFG, 31)
-    for l, L in enumerate(W["layers"]):
-        L["attn_norm"] = 1.0 + 0.2 * synth.normal_f32(CFG["dim"], 31, 600 + 2 * l)
-        L["ffn_norm"] = 1.0 + 0.2 * synth.normal_f32(CFG["dim"], 31, 601 + 2 * l)
+    W = _weights(workloads, synth)
     path = tmp_path_factory.mktemp("gguf") / "llama3_small.gguf"
     gw.llama_writer(CFG, W, workloads.tensor_shape, tokens=list(tokens), merges=list(merges)).write(path)
     g = qk.GGUF(path)
@@ -184,3 +191,42 @@ def test_cli_int8_default_and_compare_output(qk, torch_gpu, model):
     steps = [l for l in lines if l.startswith("  step ")]
     assert len(steps) == 5
     assert all("baseline token" in l and "batched token" in l and "top-2 margin" in l for l in steps)
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_cli_text_matches_the_oracle(qk, torch_gpu, oracle, workloads, synth, model, int8):
+    """The command line (sequential prefill; FP32 GEMVs, or the reference's
+    default INT8 modes) against the fp64 oracle model in the same mode,
+    built from the same weights the GGUF file holds: the oracle's greedy
+    tokens, decoded, are a prefix of the printed text up to the first step
+    whose top-2 margin is below 1e-3 (FP32: where fp32 roundoff may pick the
+    other token) or 0.5 (INT8: where a code one step off a quantization
+    midpoint may), and at least three steps are compared."""
+    path, g, tok, T = model
+    W = _weights(workloads, synth)
+    ids = T.chat_prompt(tok, PROMPT)
+    n = 8
+    om = oracle.Llama(CFG, W)
+    om.set_int8(int8, int8)
+    nxt = lg = None
+    for i, t in enumerate(ids):
+        nxt, lg = om.forward(int(t), i, i + 1 == len(ids))
+    want, margins = [], []
+    for i in range(n):
+        top = np.sort(lg)[-2:]
+        want.append(int(nxt))
+        margins.append(float(top[1] - top[0]))
+        if i + 1 < n:
+            nxt, lg = om.forward(int(nxt), len(ids) + i, True)
+    del om
+    stop = tok.stop_ids()
+    clear = 0
+    while clear < n and margins[clear] > (0.5 if int8 else 1e-3) and want[clear] not in stop:
+        clear += 1
+    print("oracle tokens", want, "margins", [f"{m:.3g}" for m in margins], flush=True)
+    assert clear >= 3
+    text = b"".join(tok.decode(t) for t in want[:clear])
+    rc, out, err = _run(_cli(), ["--model", str(path), "--context", "128", "--max-tokens", str(n)] +
+                        ([] if int8 else ["--float-gemv"]) + [PROMPT])
+    assert rc == 0, err
+    assert out.startswith(text), (out, text)
