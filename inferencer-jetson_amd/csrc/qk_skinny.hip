@@ -373,6 +373,15 @@ __device__ __forceinline__ void epilogue(const SkParams &p, const int (&mi)[RT],
     }
 }
 
+// Takes the loaded words through an empty asm statement: the compiler must
+// have them in registers here (it waits for their loads here, not at a
+// later copy it would sink below other memory operations).
+__device__ __forceinline__ void own_regs(Raw &r) {
+    #pragma unroll
+    for (int k = 0; k < 7; ++k) asm volatile("" : "+v"(r.v[k].x), "+v"(r.v[k].y), "+v"(r.v[k].z), "+v"(r.v[k].w));
+    asm volatile("" : "+v"(r.d));
+}
+
 // Block b of the raw weight rows of row tile `tile` (every row tile of the
 // workgroup: RT matrices' rows), the lane's row clamped into its matrix.
 template <int TYPE, int RT>
@@ -444,6 +453,17 @@ __device__ __forceinline__ void skinny_body(const SkParams &p, float *lds) {
             for (int i = 0; i < 16; ++i) mine[i * 64] = acc[rt][i] + accmin[rt][i];
         }
         __syncthreads();
+        // The next tile's weights move into place before this tile's stores
+        // go out: the wait for them then leaves the stores in flight (vector
+        // memory counts complete in order, so a wait placed after the stores
+        // would also wait for their write-back).
+        if constexpr (LOOP) {
+            #pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                own_regs(nxt[rt]);
+                cur[rt] = nxt[rt];
+            }
+        }
         if (p.splits == 1) {
             int mi[RT], row0[RT];
             tile_rows<RT>(p, tile, mi, row0);
@@ -459,8 +479,6 @@ __device__ __forceinline__ void skinny_body(const SkParams &p, float *lds) {
         tile += stride;
         if (tile >= p.tiles) return;
         __syncthreads();   // every wave's sums read before the next tile's overwrite them
-        #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) cur[rt] = nxt[rt];
     }
 }
 
@@ -485,6 +503,132 @@ __global__ __launch_bounds__(64 * waves_max(TYPE, RT)) void skinny_i8(SkParams p
 // Workgroups of the looping kernel hold at most kLoopWaves waves (room for
 // two tiles' weights in registers).
 constexpr int kLoopWaves = 8;
+
+// Rows of at most kRowsMaxBlocks blocks, one row tile per wave: the token
+// tile's activation codes, their transposed scales and (Q4_K) the S-scale
+// products of every block sit in LDS, written once per workgroup; each wave
+// then walks its own row tiles block by block, the next block's weights in
+// flight, with no cross-wave reduction and no barrier in the loop.
+constexpr int kRowsMaxBlocks = 12;
+// A token's 256 codes of a block take 272 bytes of LDS: the lanes of a
+// half-wave (32 tokens) then start 4 banks apart instead of all in one bank.
+constexpr int kCodeStride = 272;
+
+__host__ __device__ constexpr size_t rows_lds(int nb) {
+    return static_cast<size_t>(nb) * (kToks * kCodeStride + 2 * 8 * kToks * sizeof(float));
+}
+
+template <int TYPE>
+__device__ __forceinline__ void rows_body(const SkParams &p, float *lds) {
+    const int nb = p.nb;
+    uint8_t *codes = reinterpret_cast<uint8_t *>(lds);   // [nb][32 tokens][kCodeStride]
+    float *xst = reinterpret_cast<float *>(codes + static_cast<size_t>(nb) * kToks * kCodeStride);   // [nb][8][32]
+    float *xsl = xst + nb * 8 * kToks;                                       // [nb][8][32] xscale * S
+    const int ttile = blockIdx.y;
+    const int nthreads = blockDim.x;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kh = lane >> 5, col = lane & 31;
+    const int waves = nthreads >> 6;
+    const int stride = gridDim.x * waves;
+    const int first = blockIdx.x * waves + wave;
+    const bool has_tiles = first < p.tiles;   // wave-uniform
+    const int first_c = min(first, p.tiles - 1);
+    const int n_tiles = has_tiles ? (p.tiles - 1 - first) / stride + 1 : 1;
+    const int steps = n_tiles * nb;
+    auto tile_of = [&](int k) { return first_c + min(k, steps - 1) / nb * stride; };
+    auto block_of = [&](int k) { return min(k, steps - 1) % nb; };
+    // The first two blocks' weights load while the activations are staged
+    // (a wave without tiles loads its clamped tile and discards it).
+    Raw w0[1], w1[1];
+    load_tile<TYPE, 1>(p, tile_of(0), block_of(0), col, kh, w0);
+    load_tile<TYPE, 1>(p, tile_of(1), block_of(1), col, kh, w1);
+
+    for (int i = threadIdx.x; i < nb * kToks * 16; i += nthreads) {   // 16-byte chunks
+        const int chunk = i & 15, tok = (i >> 4) & (kToks - 1), b = i >> 9;
+        const int t = min(ttile * kToks + tok, p.n_tokens - 1);
+        *reinterpret_cast<uint4 *>(codes + (b * kToks + tok) * kCodeStride + chunk * 16) =
+            *reinterpret_cast<const uint4 *>(p.xq + static_cast<int64_t>(t) * p.ldxq + b * 256 + chunk * 16);
+    }
+    for (int i = threadIdx.x; i < nb * 8 * kToks; i += nthreads) {
+        const int tok = i & (kToks - 1), sb = i >> 5;   // sb = b * 8 + sub-block
+        const int t = min(ttile * kToks + tok, p.n_tokens - 1);
+        xst[i] = p.xs[static_cast<int64_t>(t) * p.ldxs + sb];
+    }
+    __syncthreads();
+    if (TYPE == QK_TYPE_Q4_K) {
+        for (int i = threadIdx.x; i < nb * 8 * kToks; i += nthreads) {
+            const int tok = i & (kToks - 1), sb = i >> 5, b = sb >> 3, sub = sb & 7;
+            const uint4 *c = reinterpret_cast<const uint4 *>(codes + (b * kToks + tok) * kCodeStride + sub * 32);
+            int sum = 0;
+            #pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint4 v = c[h];
+                sum = __builtin_amdgcn_sdot4(static_cast<int>(v.x), 0x01010101, sum, false);
+                sum = __builtin_amdgcn_sdot4(static_cast<int>(v.y), 0x01010101, sum, false);
+                sum = __builtin_amdgcn_sdot4(static_cast<int>(v.z), 0x01010101, sum, false);
+                sum = __builtin_amdgcn_sdot4(static_cast<int>(v.w), 0x01010101, sum, false);
+            }
+            xsl[i] = static_cast<float>(sum) * xst[i];
+        }
+        __syncthreads();
+    }
+    if (!has_tiles) return;   // no barrier follows
+
+    v16f acc[1], accmin[1];
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) acc[0][i] = accmin[0][i] = 0.f;
+    // Two blocks ahead: step k computes w0 while w1 (step k + 1) and w2
+    // (step k + 2, issued now) are in flight; the last steps reload their
+    // own block, in bounds.
+    for (int k = 0; k < steps; ++k) {
+        const int b = k % nb;
+        Raw w2[1];
+        load_tile<TYPE, 1>(p, tile_of(k + 2), block_of(k + 2), col, kh, w2);
+        uint4 ca[8];
+        const uint8_t *cb = codes + (b * kToks + col) * kCodeStride;
+        #pragma unroll
+        for (int sub = 0; sub < 8; ++sub) {
+            if (is_q4<TYPE>(TYPE)) {
+                ca[sub] = *reinterpret_cast<const uint4 *>(cb + 32 * sub + 16 * kh);
+            } else {
+                const uint2 lo = *reinterpret_cast<const uint2 *>(cb + 32 * sub + 8 * kh);
+                const uint2 hi = *reinterpret_cast<const uint2 *>(cb + 32 * sub + 16 + 8 * kh);
+                ca[sub] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            }
+        }
+        float xss[8];
+        #pragma unroll
+        for (int sub = 0; sub < 8; ++sub) xss[sub] = is_q4<TYPE>(TYPE) ? xsl[(b * 8 + sub) * kToks + col] : 0.f;
+        block_i8<TYPE>(w0[0], TYPE, ca, xst + b * 8 * kToks, xss, kh, acc[0], accmin[0]);
+        own_regs(w1[0]);
+        w0[0] = w1[0];
+        w1[0] = w2[0];
+        if (b == nb - 1) {   // wave-uniform: the tile is done
+            int mi[1], row0[1];
+            tile_rows<1>(p, tile_of(k), mi, row0);
+            const SkMatrix &M = p.mat[mi[0]];
+            const int row = row0[0] + col;
+            #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int t = ttile * kToks + 8 * (i >> 2) + 4 * kh + (i & 3);
+                if (row < M.rows && t < p.n_tokens) {
+                    float *y = M.y + static_cast<int64_t>(t) * M.ldy + row;
+                    float v = acc[0][i] + accmin[0][i];
+                    if (p.epilogue == kAccumulate) v += *y;
+                    *y = v;
+                }
+                acc[0][i] = accmin[0][i] = 0.f;
+            }
+        }
+    }
+}
+
+template <int TYPE>
+__global__ __launch_bounds__(64 * kLoopWaves) void skinny_i8_rows(SkParams p) {
+    extern __shared__ __align__(16) float lds[];
+    rows_body<TYPE>(p, lds);
+}
 
 // Launches of more (row tile, token tile) units than the chip holds at
 // once, over matrices of one type: resident workgroups walk the row tiles.
@@ -561,7 +705,14 @@ int fewest_splits(int nb, int wmax) { return (nb + wmax - 1) / wmax; }
 struct SkPlan {
     int splits, waves;
     int loop_groups;   // workgroups per (split, token tile) of the looping kernel; 0: one pass
+    bool rows;         // the looping kernel is skinny_i8_rows (one row tile per wave, one split)
 };
+
+const void *rows_kernel(int type) {
+    return type == QK_TYPE_Q4_K   ? reinterpret_cast<const void *>(skinny_i8_rows<QK_TYPE_Q4_K>)
+           : type == QK_TYPE_Q6_K ? reinterpret_cast<const void *>(skinny_i8_rows<QK_TYPE_Q6_K>)
+                                  : reinterpret_cast<const void *>(skinny_i8_rows<QK_TYPE_Q6_K_SPLIT>);
+}
 
 // Splits of a row of nb blocks (one block per wave, the blocks spread
 // evenly over a workgroup's waves) for a launch of `units` (row tile, token
@@ -596,12 +747,21 @@ SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt) {
             waves = w;
         }
     }
-    if (type == 0 || best_rounds <= 1) return SkPlan{splits, waves, 0};
+    if (type == 0 || best_rounds <= 1) return SkPlan{splits, waves, 0, false};
+    const int64_t tiles = units / ttiles;
+    if (rt == 1 && nb <= kRowsMaxBlocks) {
+        // Row tiles per wave: as many 8-wave workgroups per token tile as the
+        // chip holds (one per CU with the activations' LDS).
+        const int resident = resident_blocks(rows_kernel(type), 64 * kLoopWaves, rows_lds(nb));
+        const int64_t per_tt = std::max<int64_t>(1, resident / ttiles);
+        const int64_t need = (tiles + kLoopWaves - 1) / kLoopWaves;
+        return SkPlan{1, kLoopWaves, static_cast<int>(std::min(per_tt, need)), true};
+    }
     SkPlan lp;
     lp.splits = fewest_splits(nb, kLoopWaves);
     lp.waves = (nb + lp.splits - 1) / lp.splits;
     const int resident = resident_blocks(skinny_kernel(type, rt, true), 64 * lp.waves, skinny_lds(lp.waves, rt));
-    const int64_t tiles = units / ttiles;
+    lp.rows = false;
     lp.loop_groups =
         static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(tiles, resident / (lp.splits * ttiles))));
     return lp;
@@ -692,10 +852,10 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
         if (!aligned(workspace, 16)) return fail(QK_ERR_ALIGN, std::string(where) + ": workspace not 16-byte aligned");
         p.partials = static_cast<float *>(workspace);
     }
-    const size_t lds = skinny_lds(p.waves, rt);
+    const size_t lds = plan.rows ? rows_lds(nb) : skinny_lds(p.waves, rt);
     const int groups = plan.loop_groups ? plan.loop_groups : tiles;   // workgroups per (split, token tile)
     void *args[] = {&p};
-    if (hipLaunchKernel(skinny_kernel(type, rt, plan.loop_groups > 0),
+    if (hipLaunchKernel(plan.rows ? rows_kernel(type) : skinny_kernel(type, rt, plan.loop_groups > 0),
                         dim3(static_cast<unsigned>(groups * p.splits), static_cast<unsigned>(token_tiles)),
                         dim3(64 * p.waves), args, lds, stream) != hipSuccess)
         return launch_status(where);
