@@ -398,10 +398,11 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             # FP32 (activation records), per layer: QKV, attention (one
             # workgroup per query head at these positions, no merge), o,
             # gate/up, down; then the embedding, the LM head and the greedy
-            # pick.  INT8, per layer: norm+quantize, QKV, attention, quantize,
-            # o (+add), norm+quantize, gate/up, SiLU*up+quantize, down (+add);
+            # pick.  INT8, per layer: QKV (RMSNorm + quantize staged),
+            # attention (o's input quantized), o (+add), gate/up (RMSNorm +
+            # quantize staged, SiLU*up quantized in the epilogue), down (+add);
             # then embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (6 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
+            "kernels_per_token": (5 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
             "device_bytes": mem}
 
 

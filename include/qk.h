@@ -447,7 +447,9 @@ int qk_llama_destroy(qk_llama *m);
    and the LM head (--fused-norm-quant), the attention output quantized
    before o, SiLU * up and its quantization in one launch before down, and
    the residual adds in the o / down GEMVs' epilogues -- and the other types
-   stay FP32.  Takes effect at the next qk_llama_forward. */
+   stay FP32.  (With both types enabled the driver folds the quantizations
+   into the GEMVs and the attention, with the same codes.)  Takes effect at
+   the next qk_llama_forward. */
 int qk_llama_set_int8(qk_llama *m, int q4k_int8, int q6k_int8);
 /* Device pointers to the fp32 caches, [layer][kv_heads][context][head_dim]:
    the drivers keep each KV head's rows contiguous, so the attention

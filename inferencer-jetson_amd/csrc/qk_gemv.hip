@@ -187,6 +187,9 @@ struct F32Policy {
     static constexpr bool kPrepLds = true;
     static constexpr bool kInt8 = false;
     static constexpr bool kDirect = true;   // load_direct exists (rows too long to stage)
+    // Staging inputs loaded ahead of the weights (prep_early), or none.
+    static constexpr bool kEarly = false;
+    struct Early {};
 
     struct Lane {
         int limb[4][12];
@@ -347,6 +350,8 @@ struct I8Policy {
     static constexpr bool kDirect = true;
     static constexpr bool kAccumulate = true;   // the INT8 step's residual adds
     static constexpr bool kArgmax = false;
+    static constexpr bool kEarly = false;
+    struct Early {};
     __host__ __device__ static size_t lds_bytes(int) { return 0; }
     __device__ static void prep(const GemvParams &, int, int, XGroup *) {}
 
@@ -460,6 +465,72 @@ struct I8FusedPolicy : I8Policy {
     // together, and held in registers across the sum of squares; longer rows
     // read x twice.
     static constexpr int kHeld = 4;
+
+    // The kernels that take the early form load a thread's kHeld float4 of
+    // x and of the gains (or up, or x again) before their weights: the
+    // loads return in order, so the staging then waits for these alone and
+    // overlaps the weights' arrival.  Indexes are clamped to the row and
+    // the loads are unconditional (static wait counts); rows longer than
+    // kHeld float4 per thread ignore them.
+    static constexpr bool kEarly = true;
+    struct Early {
+        float4 v[kHeld], w[kHeld];
+    };
+
+    __device__ static void early(Early &e, const GemvParams &p, int token, int cols) {
+        const float *x = static_cast<const float *>(p.x) + static_cast<int64_t>(token) * p.ldx;
+        const float *w = p.norm_w ? p.norm_w : p.up ? p.up + static_cast<int64_t>(token) * p.ldx : x;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const float4 *w4 = reinterpret_cast<const float4 *>(w);
+        const int last = (cols >> 2) - 1;
+        #pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int i = min(static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x), last);
+            e.v[k] = x4[i];
+            e.w[k] = w4[i];
+        }
+    }
+
+    // prep over what early loaded: the same values, sums and codes.
+    __device__ static void prep_early(const Early &e, const GemvParams &p, int token, int cols, XGroup *lds) {
+        const int n4 = cols >> 2;
+        const int nt = blockDim.x;
+        const int tid = threadIdx.x;
+        if (n4 > kHeld * nt) {
+            prep(p, token, cols, lds);
+            return;
+        }
+        uint32_t *q4 = reinterpret_cast<uint32_t *>(lds);
+        float *st = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + cols);
+        float *scratch = st + cols / 32;
+        float scale = 1.f;
+        if (p.norm_w) {
+            float ss = 0.f;
+            #pragma unroll
+            for (int k = 0; k < kHeld; ++k) {
+                if (tid + k * nt < n4) {
+                    ss = fmaf(e.v[k].x, e.v[k].x, ss);
+                    ss = fmaf(e.v[k].y, e.v[k].y, ss);
+                    ss = fmaf(e.v[k].z, e.v[k].z, ss);
+                    ss = fmaf(e.v[k].w, e.v[k].w, ss);
+                }
+            }
+            scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+        }
+        #pragma unroll
+        for (int k = 0; k < kHeld; ++k) {
+            const int i = tid + k * nt;
+            if (i >= n4) continue;
+            const float4 v = e.v[k], w = e.w[k];
+            float4 o = v;
+            if (p.norm_w)
+                o = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+            else if (p.up)
+                o = make_float4(silu_mul_value(v.x, w.x), silu_mul_value(v.y, w.y), silu_mul_value(v.z, w.z),
+                                silu_mul_value(v.w, w.w));
+            quantize4(o, i, q4, st);
+        }
+    }
 
     __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
         uint32_t *q4 = reinterpret_cast<uint32_t *>(lds);
@@ -681,12 +752,17 @@ __global__ __launch_bounds__(256) void gemv_wave(GemvParams p) {
     const int stride = gridDim.x * n_waves;
     const int first = blockIdx.x * n_waves + wave;
     const int last = p.total_tiles - 1;
+    typename Policy::Early e;
+    if constexpr (Policy::kEarly) Policy::early(e, p, token, p.pieces * 64);
     // The first two tiles' loads are in flight while the block prepares the
     // activations (a wave without tiles loads the last one and discards it).
     Slot a = prep<TYPE>(p, min(first, last), rit, piece, token, g, h);
     Slot b = prep<TYPE>(p, min(first + stride, last), rit, piece, token, g, h);
     if (Policy::kPrepLds) {
-        Policy::prep(p, token, p.pieces * 64, xg);
+        if constexpr (Policy::kEarly)
+            Policy::prep_early(e, p, token, p.pieces * 64, xg);
+        else
+            Policy::prep(p, token, p.pieces * 64, xg);
         __syncthreads();
     }
     typename Policy::Lane L;
@@ -1064,6 +1140,59 @@ int gcd_int(int a, int b) {
         b = t;
     }
     return a;
+}
+
+// The INT8 step's gate / up pair with SiLU(gate) * up quantized in the
+// epilogue (silu_cuda and quantize_x32_cuda's arithmetic): workgroup w owns
+// rows 32w .. 32w + 31 of both matrices -- 32 / TR tiles of TR = 64 / GROUP
+// rows each -- and its four waves take those 64 / TR tiles in turn; the
+// row sums meet in LDS and one half-wave forms and quantizes the
+// workgroup's 32 values into hq / hs (token-major, ldq / ldsc).
+template <class Policy, int TYPE, int GROUP>
+__global__ __launch_bounds__(256) void gemv_pair_quant(GemvParams p, int8_t *hq, float *hs, int ldq, int ldsc) {
+    constexpr int TR = 64 / GROUP;
+    constexpr int kHalf = 32 / TR;         // tiles per matrix
+    constexpr int kPerWave = 2 * kHalf / 4;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int token = blockIdx.y;
+    const int rit = lane / GROUP;
+    const int piece = lane & (GROUP - 1);
+    const int g = (piece >> 1) & 1, h = piece & 1;
+    XGroup *xg = reinterpret_cast<XGroup *>(qk_smem);
+    float *vals = reinterpret_cast<float *>(qk_smem + ((Policy::lds_bytes(p.pieces * 64) + 15) & ~size_t(15)));
+    const int up_begin = p.mat[1].tile_begin;
+    auto tile_at = [&](int k) {   // k < 2 * kHalf: gate tiles, then up tiles
+        const int j = min(k, 2 * kHalf - 1);
+        return (j >= kHalf ? up_begin : 0) + static_cast<int>(blockIdx.x) * kHalf + j % kHalf;
+    };
+    // The staging inputs, then up to kDepth tiles per wave (one wave per
+    // SIMD: the registers are there), are in flight before the staging.
+    typename Policy::Early e;
+    Policy::early(e, p, token, p.pieces * 64);
+    constexpr int kDepth = kPerWave < 8 ? kPerWave : 8;
+    Slot sl[kDepth];
+    #pragma unroll
+    for (int j = 0; j < kDepth; ++j) sl[j] = prep<TYPE>(p, tile_at(wave + 4 * j), rit, piece, token, g, h);
+    Policy::prep_early(e, p, token, p.pieces * 64, xg);
+    __syncthreads();
+    typename Policy::Lane L;
+    Policy::load(L, p, token, piece, xg);
+    #pragma unroll
+    for (int j = 0; j < kPerWave; ++j) {
+        Slot &cur = sl[j % kDepth];
+        const float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(cur.t.type, cur.r, L, g, h));
+        const int k = wave + 4 * j;
+        if (piece == 0) vals[(k >= kHalf ? 32 : 0) + (k % kHalf) * TR + rit] = v;
+        if (j + kDepth < kPerWave) cur = prep<TYPE>(p, tile_at(wave + 4 * (j + kDepth)), rit, piece, token, g, h);
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+        const int64_t r = static_cast<int64_t>(blockIdx.x) * 32 + threadIdx.x;
+        quantize_group_store(silu_mul_value(vals[threadIdx.x], vals[32 + threadIdx.x]), true, threadIdx.x,
+                             hq + static_cast<int64_t>(token) * ldq + r,
+                             hs + static_cast<int64_t>(token) * ldsc + blockIdx.x);
+    }
 }
 
 template <class Policy, int TYPE, int GROUP>
@@ -1683,6 +1812,64 @@ int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int
     p.up = up;
     p.accumulate = accumulate;
     return launch<I8FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "staged INT8 GEMV launch");
+}
+
+template <int TYPE>
+int launch_pair_quant_type(const GemvParams &p, int group, int n_tokens, int8_t *hq, float *hs, int ldq, int ldsc,
+                           size_t lds, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(p.mat[0].rows / 32), static_cast<unsigned>(n_tokens));
+    if (group == 4)
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 4>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+    else if (group == 8)
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 8>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+    else if (group == 16)
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 16>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+    else if (group == 32)
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 32>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+    else
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 64>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+    return launch_status("INT8 gate / up pair launch");
+}
+
+bool gemv_i8_pair_supported(int cols, int rows) {
+    const int pieces = cols / 256 * 4;
+    return cols > 0 && cols % 256 == 0 && 64 % pieces == 0 && rows > 0 && rows % 32 == 0 &&
+           gemv_i8_stageable(cols);
+}
+
+int launch_gemv_i8_pair_quant(const qk_matrix *gu, const float *x, int ldx, const float *norm_w, float eps, int cols,
+                              int n_tokens, int8_t *hq, float *hs, int ldq, int ldsc, hipStream_t stream) {
+    const int rows = gu[0].rows, type = gu[0].type;
+    if (!gemv_i8_pair_supported(cols, rows) || gu[1].rows != rows || gu[1].type != type || n_tokens > 65535)
+        return fail(QK_ERR_LIMIT, "INT8 gate / up pair: unsupported shape");
+    GemvParams p{};
+    p.x = x;
+    p.ldx = ldx;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
+    const int nb = cols / 256;
+    p.n_mats = 2;
+    p.pieces = 4 * nb;
+    p.group_lanes = p.pieces;
+    p.tile_rows = 64 / p.pieces;
+    p.chunks = 1;
+    for (int m = 0; m < 2; ++m) {
+        GemvMatrix &M = p.mat[m];
+        M.w = static_cast<const uint8_t *>(gu[m].w);
+        M.y = nullptr;
+        M.rows = rows;
+        M.type = type;
+        M.row_bytes = static_cast<int>(row_bytes(type, nb));
+        M.ldy = rows;
+        M.tile_begin = m * (rows / p.tile_rows);
+    }
+    p.total_tiles = 2 * (rows / p.tile_rows);
+    const size_t lds = ((I8FusedPolicy::lds_bytes(cols) + 15) & ~size_t(15)) + 64 * sizeof(float);
+    if (type == QK_TYPE_Q4_K)
+        return launch_pair_quant_type<QK_TYPE_Q4_K>(p, p.pieces, n_tokens, hq, hs, ldq, ldsc, lds, stream);
+    if (type == QK_TYPE_Q6_K)
+        return launch_pair_quant_type<QK_TYPE_Q6_K>(p, p.pieces, n_tokens, hq, hs, ldq, ldsc, lds, stream);
+    return launch_pair_quant_type<QK_TYPE_Q6_K_SPLIT>(p, p.pieces, n_tokens, hq, hs, ldq, ldsc, lds, stream);
 }
 
 bool gemv_i8_stageable(int cols) {

@@ -111,6 +111,13 @@ int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq
 int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int ldx, const float *norm_w, float eps,
                           const float *up, int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
 bool gemv_i8_stageable(int cols);
+// The INT8 gate / up pair (two matrices of one type and equal rows, a
+// multiple of 32) over staged inputs (RMSNorm with norm_w when given),
+// writing SiLU(gate) * up quantized per 32 into hq [token][ldq] and hs
+// [token][ldsc] instead of gate and up.  cols of 1, 2, 4, 8 or 16 blocks.
+bool gemv_i8_pair_supported(int cols, int rows);
+int launch_gemv_i8_pair_quant(const qk_matrix *gu, const float *x, int ldx, const float *norm_w, float eps, int cols,
+                              int n_tokens, int8_t *hq, float *hs, int ldq, int ldsc, hipStream_t stream);
 // INT8 product of n_tokens per-32 quantized rows with n_mats matrices on
 // the integer matrix cores (csrc/qk_skinny.hip), arguments already
 // validated: y_m[t*ldy[m] + r] overwritten (or added with accumulate); with

@@ -258,14 +258,19 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
         const qk_matrix down{L.down_type, dim, L.down, m->x};
+        const bool pair = L.gate_type == L.up_type && qk::gemv_i8_pair_supported(dim, c.hidden);
         // o reads the codes the attention wrote (or quantizes the attention's
-        // output itself); down keeps the separate SiLU * up quantization:
-        // every GEMV block would otherwise read and activate the whole
-        // 4 x hidden bytes twice.
+        // output itself); the gate / up pair quantizes SiLU(gate) * up for
+        // down in its epilogue when both are one type; down keeps its own
+        // launch (staging SiLU * up would read and activate the whole
+        // 4 x hidden bytes in every workgroup).
         if ((st = q8 ? qk::launch_gemv_i8(&o, 1, m->xq, dim, m->xscale, dim / 32, dim, 1, nullptr, 1, s)
                      : qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1, s)) ||
-            (st = qk::launch_gemv_i8_staged(gu, 2, m->x, dim, L.ffn_norm, c.eps, nullptr, dim, 1, nullptr, 0, s)) ||
-            (st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s)) ||
+            (st = pair ? qk::launch_gemv_i8_pair_quant(gu, m->x, dim, L.ffn_norm, c.eps, dim, 1, m->xq, m->xscale,
+                                                       c.hidden, c.hidden / 32, s)
+                       : qk::launch_gemv_i8_staged(gu, 2, m->x, dim, L.ffn_norm, c.eps, nullptr, dim, 1, nullptr, 0,
+                                                   s)) ||
+            (!pair && (st = qk::launch_silu_mul_quantize(m->gate, m->up, m->xq, m->xscale, c.hidden, s))) ||
             (st = qk::launch_gemv_i8(&down, 1, m->xq, c.hidden, m->xscale, c.hidden / 32, c.hidden, 1, nullptr, 1, s)) ||
             (st = trace_copy(m->trace_x ? m->trace_x + static_cast<size_t>(l) * dim : nullptr, m->x,
                              dim * sizeof(float), s)))
