@@ -95,6 +95,11 @@ struct GemvParams {
     float *arg_v;         // greedy-token epilogue: per-workgroup best value / row
     int *arg_i;
     int *grid_out;        // host: receives the launch's workgroup count (not read on the device)
+    // I8MergePolicy: the attention's unmerged split partials,
+    // [head][n_parts][split_partial_floats(part_hd)], in place of x.
+    const float *parts;
+    int n_parts;
+    int part_hd;
 };
 
 struct Raw {
@@ -639,6 +644,76 @@ struct I8FusedPolicy : I8Policy {
     __device__ static void load_direct(Lane &, const GemvParams &, int, int) {}
 };
 
+// The INT8 o projection of the one-sequence step over the attention's
+// unmerged split partials: the staging merges each head's splits (the
+// arithmetic of the attention's merge kernel, split order: the largest
+// running max, exp2 weights, fma sums, one divide) and quantizes the row per
+// 32 as I8FusedPolicy does, so the codes equal those of the merge kernel's
+// outputs through quantize_x32_kernel.  One token; rows of at most
+// kMH * 4 * blockDim.x columns; at most kMaxParts splits.
+struct I8MergePolicy : I8FusedPolicy {
+    static constexpr int kMaxParts = 8;
+    static constexpr int kMH = 2;   // float4 per thread
+    struct Early {
+        float4 acc[kMH][kMaxParts];
+        float2 ml[kMH][kMaxParts];   // running max, sum of exp
+    };
+
+    // Every load clamped (split, column) and unconditional, as in
+    // I8FusedPolicy::early.
+    __device__ static void early(Early &e, const GemvParams &p, int, int cols) {
+        const int hd = p.part_hd, ps = split_partial_floats(hd);
+        const int last = (cols >> 2) - 1;
+        #pragma unroll
+        for (int k = 0; k < kMH; ++k) {
+            const int i = min(static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x), last);
+            const int h = 4 * i / hd, c = 4 * i - h * hd;
+            const float *base = p.parts + static_cast<int64_t>(h) * p.n_parts * ps;
+            #pragma unroll
+            for (int sp = 0; sp < kMaxParts; ++sp) {
+                const float *q = base + min(sp, p.n_parts - 1) * ps;
+                e.ml[k][sp] = *reinterpret_cast<const float2 *>(q);
+                e.acc[k][sp] = *reinterpret_cast<const float4 *>(q + 4 + c);
+            }
+        }
+    }
+
+    __device__ static void prep_early(const Early &e, const GemvParams &p, int, int cols, XGroup *lds) {
+        uint32_t *q4 = reinterpret_cast<uint32_t *>(lds);
+        float *st = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + cols);
+        const int n4 = cols >> 2;
+        #pragma unroll
+        for (int k = 0; k < kMH; ++k) {
+            const int i = static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x);
+            if (i >= n4) continue;
+            float mx = -INFINITY;
+            #pragma unroll
+            for (int sp = 0; sp < kMaxParts; ++sp)
+                if (sp < p.n_parts) mx = fmaxf(mx, e.ml[k][sp].x);
+            float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+            float den = 0.f;
+            #pragma unroll
+            for (int sp = 0; sp < kMaxParts; ++sp) {
+                if (sp >= p.n_parts) continue;
+                const float w = __builtin_amdgcn_exp2f(e.ml[k][sp].x - mx);
+                den = fmaf(w, e.ml[k][sp].y, den);
+                num.x = fmaf(w, e.acc[k][sp].x, num.x);
+                num.y = fmaf(w, e.acc[k][sp].y, num.y);
+                num.z = fmaf(w, e.acc[k][sp].z, num.z);
+                num.w = fmaf(w, e.acc[k][sp].w, num.w);
+            }
+            quantize4(make_float4(num.x / den, num.y / den, num.z / den, num.w / den), i, q4, st);
+        }
+    }
+
+    // Kernels without the early form stage the same way, loads first.
+    __device__ static void prep(const GemvParams &p, int token, int cols, XGroup *lds) {
+        Early e;
+        early(e, p, token, cols);
+        prep_early(e, p, token, cols, lds);
+    }
+};
+
 // Type dispatch of one piece: TYPE is the storage type when every matrix of
 // the launch shares it, 0 for fused launches over mixed types (then `type`
 // is wave-uniform and the branch is scalar).
@@ -871,10 +946,15 @@ __global__ __launch_bounds__(256) void gemv_whole(GemvParams p) {
     auto fetch = [&](int k) {
         return fetch_whole<TYPE>(M.w + static_cast<size_t>(min(first + k * stride, last)) * tile_bytes, tile_bytes, lf);
     };
+    typename Policy::Early e;
+    if constexpr (Policy::kEarly) Policy::early(e, p, token, p.pieces * 64);
     Raw a = fetch(0);
     Raw b = fetch(1);
     if (Policy::kPrepLds) {
-        Policy::prep(p, token, p.pieces * 64, xg);
+        if constexpr (Policy::kEarly)
+            Policy::prep_early(e, p, token, p.pieces * 64, xg);
+        else
+            Policy::prep(p, token, p.pieces * 64, xg);
         __syncthreads();
     }
     typename Policy::Lane L;
@@ -1812,6 +1892,25 @@ int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int
     p.up = up;
     p.accumulate = accumulate;
     return launch<I8FusedPolicy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "staged INT8 GEMV launch");
+}
+
+bool gemv_i8_mergeable(int cols, int head_dim, int n_parts) {
+    const int pieces = cols / 256 * 4;
+    return cols > 0 && cols % 256 == 0 && cols <= I8MergePolicy::kMH * 4 * 256 && 64 % pieces == 0 && head_dim > 0 &&
+           head_dim % 4 == 0 && cols % head_dim == 0 && n_parts >= 1 && n_parts <= I8MergePolicy::kMaxParts;
+}
+
+int launch_gemv_i8_merged(const qk_matrix *mats, int n_mats, const float *parts, int n_parts, int head_dim, int cols,
+                          int accumulate, hipStream_t stream) {
+    if (!gemv_i8_mergeable(cols, head_dim, n_parts))
+        return fail(QK_ERR_LIMIT, "merged INT8 GEMV: unsupported shape");
+    GemvParams p{};
+    p.x = parts;
+    p.parts = parts;
+    p.n_parts = n_parts;
+    p.part_hd = head_dim;
+    p.accumulate = accumulate;
+    return launch<I8MergePolicy>(p, mats, n_mats, cols, 1, nullptr, stream, "merged INT8 GEMV launch");
 }
 
 template <int TYPE>

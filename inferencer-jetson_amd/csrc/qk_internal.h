@@ -116,6 +116,14 @@ bool gemv_i8_stageable(int cols);
 // writing SiLU(gate) * up quantized per 32 into hq [token][ldq] and hs
 // [token][ldsc] instead of gate and up.  cols of 1, 2, 4, 8 or 16 blocks.
 bool gemv_i8_pair_supported(int cols, int rows);
+// The INT8 GEMV (one token, 256-thread workgroups) whose input is the
+// one-sequence attention's unmerged wide-form partials (n_parts splits per
+// head of head_dim; launch_split_attention with defer_merge): each
+// workgroup merges and quantizes the row as the merge kernel and
+// quantize_x32_kernel would.  cols of 1, 2, 4 or 8 blocks, at most 8 splits.
+bool gemv_i8_mergeable(int cols, int head_dim, int n_parts);
+int launch_gemv_i8_merged(const qk_matrix *mats, int n_mats, const float *parts, int n_parts, int head_dim, int cols,
+                          int accumulate, hipStream_t stream);
 int launch_gemv_i8_pair_quant(const qk_matrix *gu, const float *x, int ldx, const float *norm_w, float eps, int cols,
                               int n_tokens, int8_t *hq, float *hs, int ldq, int ldsc, hipStream_t stream);
 // INT8 product of n_tokens per-32 quantized rows with n_mats matrices on
@@ -347,6 +355,12 @@ struct SplitAttention {
     // == 0), or NULL: the INT8 o projection's input.
     int8_t *q8_out;
     float *q8_scale;
+    // The wide form (one workgroup per query head, few tokens over short
+    // rows) takes all of a head's rows in one split unless wide_split_rows
+    // > 0 caps its rows per split.
+    int wide_split_rows;
+    // Leave split partials unmerged (no merge launch): the caller merges.
+    int defer_merge;
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
     // Cache layout: 0 the reference's [layers][cache_rows][kv_heads][head_dim],
     // 1 [layers][kv_heads][cache_rows][head_dim] (the decode drivers' own: a
@@ -377,9 +391,18 @@ int split_attention_rows(int64_t head_rows, int max_rows);
 // serves).  A call with less workspace takes fewer, longer splits, one with
 // none a single split.  Calls sharing a workspace must not overlap.
 size_t split_attention_workspace_bytes(int n_tokens, int heads, int kv_heads, int head_dim, int max_rows);
-// split_rows <= 0 takes the policy's value.  Arguments validated by the caller.
+// split_rows <= 0 takes the policy's value.  Arguments validated by the
+// caller.  splits_used (optional) receives the splits per token left for
+// the caller to merge, or 1 when the outputs are written: with a.defer_merge
+// a wide-form launch of several splits leaves its partials in the workspace,
+// split_partial_floats(head_dim) per (query head, split), split-minor, and
+// writes no outputs.
 int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
-                           hipStream_t stream);
+                           hipStream_t stream, int *splits_used = nullptr);
+// Floats of one split partial of one query head in the wide form: the
+// running max and sum of exp (base-2 units) padded to 4, then the
+// unnormalised output row of head_dim.
+constexpr int split_partial_floats(int head_dim) { return 4 + head_dim; }
 // Whether a launch of a (split_rows <= 0, gemm_rec aside) can write the
 // matrix-core GEMM's records of its outputs (a.gemm_rec).
 bool attention_gemm_records(const SplitAttention &a);

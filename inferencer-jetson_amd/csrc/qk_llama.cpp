@@ -221,8 +221,17 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     int st;
     const bool staged = m->int8_q4k && m->int8_q6k && !m->trace_q && qk::gemv_i8_stageable(dim);
     const bool q8 = c.heads * hd == dim && hd % 32 == 0;   // the attention can quantize o's input
+    // With both modes on, the attention's rows split into rounds of 128 per
+    // workgroup (at most 8 splits) and the o GEMV merges the splits while it
+    // stages its input (launch_gemv_i8_merged): the attention's CUs each
+    // stream one round of rows instead of all of a head's.  The traced step
+    // takes the same splits, merged by the merge kernel, so its codes are
+    // the staged step's.
+    const bool merge_o = m->int8_q4k && m->int8_q6k && q8 && qk::gemv_i8_stageable(dim) &&
+                         qk::gemv_i8_mergeable(dim, hd, 8);
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
     qk::SplitAttention attn{};
+    attn.wide_split_rows = merge_o ? std::max(128, ((pos + 1 + 7) / 8 + 15) / 16 * 16) : 0;
     attn.q = m->q;
     attn.k = m->k;
     attn.v = m->v;
@@ -254,18 +263,23 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
         attn.layer = l;
         attn.q8_out = q8 ? m->xq : nullptr;
         attn.q8_scale = q8 ? m->xscale : nullptr;
-        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        attn.defer_merge = merge_o;
+        int parts = 1;   // splits left for o to merge
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s, &parts))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
         const qk_matrix down{L.down_type, dim, L.down, m->x};
         const bool pair = L.gate_type == L.up_type && qk::gemv_i8_pair_supported(dim, c.hidden);
-        // o reads the codes the attention wrote (or quantizes the attention's
-        // output itself); the gate / up pair quantizes SiLU(gate) * up for
+        // o merges the attention's splits, or reads the codes the attention
+        // wrote, or quantizes the attention's output itself; the gate / up pair quantizes SiLU(gate) * up for
         // down in its epilogue when both are one type; down keeps its own
         // launch (staging SiLU * up would read and activate the whole
         // 4 x hidden bytes in every workgroup).
-        if ((st = q8 ? qk::launch_gemv_i8(&o, 1, m->xq, dim, m->xscale, dim / 32, dim, 1, nullptr, 1, s)
-                     : qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1, s)) ||
+        if ((st = parts > 1 ? qk::launch_gemv_i8_merged(&o, 1, static_cast<const float *>(m->attn_ws), parts, hd, dim,
+                                                         1, s)
+                  : q8      ? qk::launch_gemv_i8(&o, 1, m->xq, dim, m->xscale, dim / 32, dim, 1, nullptr, 1, s)
+                            : qk::launch_gemv_i8_staged(&o, 1, m->attn, dim, nullptr, 0.f, nullptr, dim, 1, nullptr, 1,
+                                                        s)) ||
             (st = pair ? qk::launch_gemv_i8_pair_quant(gu, m->x, dim, L.ffn_norm, c.eps, dim, 1, m->xq, m->xscale,
                                                        c.hidden, c.hidden / 32, s)
                        : qk::launch_gemv_i8_staged(gu, 2, m->x, dim, L.ffn_norm, c.eps, nullptr, dim, 1, nullptr, 0,

@@ -262,6 +262,7 @@ struct SplitAttnKernelArgs {
 // A split partial: max [G], sum of exp [G], padded to 16 bytes, then the
 // unnormalised output rows [G][head_dim].
 __host__ __device__ constexpr int split_header(int G) { return (2 * G + 3) & ~3; }
+static_assert(split_header(1) + 64 == split_partial_floats(64), "one-head partials: max, sum, pad, row");
 
 // Register plan of an instance: NU steps of 64/L rows per wave per round,
 // K / V buffers (8 * NU * NF VGPRs) within what the query and output rows
@@ -361,6 +362,51 @@ __device__ __forceinline__ void merge_scales(float &m, float &l, float mo, float
     fo = __builtin_amdgcn_exp2f(mo - ref);
     l = l * f + lo * fo;
     m = mn;
+}
+
+// The nsplit partials of (token b, workgroup kvh) merged in split order,
+// by 256 threads; mo: G * head_dim floats of LDS for the records.
+template <int G>
+__device__ void merge_splits(const SplitAttnKernelArgs &ka, int b, int kvh, int nsplit, float *mo) {
+    const SplitAttention &a = ka.a;
+    const int hd = a.head_dim;
+    constexpr int kHdr = split_header(G);
+    const int pstride = kHdr + G * hd;
+    const float *all = ka.partials + (static_cast<int64_t>(b) * gridDim.x + kvh) * ka.splits * pstride;
+    float *o = a.out + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
+    for (int i = threadIdx.x; i < G * hd; i += 256) {
+        const int g = i / hd;
+        float mx = -INFINITY;
+        #pragma unroll 8
+        for (int p = 0; p < nsplit; ++p) mx = fmaxf(mx, all[p * pstride + g]);
+        float num = 0.f, den = 0.f;
+        #pragma unroll 8
+        for (int p = 0; p < nsplit; ++p) {
+            const float w = __builtin_amdgcn_exp2f(all[p * pstride + g] - mx);
+            den = fmaf(w, all[p * pstride + G + g], den);
+            num = fmaf(w, all[p * pstride + kHdr + i], num);
+        }
+        o[i] = num / den;
+        if (a.rec_out || a.gemm_rec) mo[i] = num / den;
+        if (a.q8_out) {
+            // G * hd % 32 == 0: a half-wave holds one group, active together.
+            const int64_t c = static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd + i;
+            quantize_group_store(num / den, true, threadIdx.x & 31, a.q8_out + c, a.q8_scale + c / 32);
+        }
+    }
+    if (a.gemm_rec) {
+        __syncthreads();
+        write_gemm_records<G>(a, b, kvh, mo, hd);
+    }
+    if (a.rec_out) {
+        __syncthreads();
+        XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
+        const int groups = G * hd / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        for (int g0 = wave * 4; g0 < groups; g0 += 16) {   // four waves, four groups each
+            const int gi = g0 + (lane >> 4), live = gi < groups;
+            record16_quads(live ? mo[16 * gi + (lane & 15)] : 0.f, lane, rec + gi, live);
+        }
+    }
 }
 
 template <int G, int NF, int L, int NW>
@@ -613,8 +659,8 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
     }
 }
 
-// The splits of (token, KV head) with more than one: the partials merged in
-// split order.
+// The splits of (token, KV head) with more than one, when the attention
+// launch did not merge them itself.
 template <int G>
 __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka) {
     __shared__ float mo[G * 256];   // the merged outputs, for the records (head_dim <= 256)
@@ -624,44 +670,7 @@ __global__ __launch_bounds__(256) void split_merge_kernel(SplitAttnKernelArgs ka
     if (!token_ok(d, a.cache_rows, a.max_pos)) return;
     const int nsplit = (d.pos + ka.split_rows) / ka.split_rows;
     if (nsplit == 1) return;
-    const int hd = a.head_dim;
-    constexpr int kHdr = split_header(G);
-    const int pstride = kHdr + G * hd;
-    const float *all = ka.partials + (static_cast<int64_t>(b) * gridDim.x + kvh) * ka.splits * pstride;
-    float *o = a.out + static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd;
-    for (int i = threadIdx.x; i < G * hd; i += 256) {
-        const int g = i / hd;
-        float mx = -INFINITY;
-        #pragma unroll 8
-        for (int p = 0; p < nsplit; ++p) mx = fmaxf(mx, all[p * pstride + g]);
-        float num = 0.f, den = 0.f;
-        #pragma unroll 8
-        for (int p = 0; p < nsplit; ++p) {
-            const float w = __builtin_amdgcn_exp2f(all[p * pstride + g] - mx);
-            den = fmaf(w, all[p * pstride + G + g], den);
-            num = fmaf(w, all[p * pstride + kHdr + i], num);
-        }
-        o[i] = num / den;
-        if (a.rec_out || a.gemm_rec) mo[i] = num / den;
-        if (a.q8_out) {
-            // G * hd % 32 == 0: a half-wave holds one group, active together.
-            const int64_t c = static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd + i;
-            quantize_group_store(num / den, true, threadIdx.x & 31, a.q8_out + c, a.q8_scale + c / 32);
-        }
-    }
-    if (a.gemm_rec) {
-        __syncthreads();
-        write_gemm_records<G>(a, b, kvh, mo, hd);
-    }
-    if (a.rec_out) {
-        __syncthreads();
-        XGroup *rec = a.rec_out + (static_cast<int64_t>(b) * a.heads * hd + kvh * G * hd) / 16;
-        const int groups = G * hd / 16, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        for (int g0 = wave * 4; g0 < groups; g0 += 16) {   // four waves, four groups each
-            const int gi = g0 + (lane >> 4), live = gi < groups;
-            record16_quads(live ? mo[16 * gi + (lane & 15)] : 0.f, lane, rec + gi, live);
-        }
-    }
+    merge_splits<G>(ka, b, kvh, nsplit, mo);
 }
 
 // dst row i = src row idx[i] (cols floats, cols % 4 == 0, 16-byte aligned
@@ -860,7 +869,7 @@ bool attention_gemm_records(const SplitAttention &a) {
 }
 
 int launch_split_attention(const SplitAttention &a, int split_rows, void *workspace, size_t workspace_size,
-                           hipStream_t stream) {
+                           hipStream_t stream, int *splits_used) {
     const int G = a.heads / a.kv_heads;
     const void *fn = split_instance(G, a.head_dim);
     if (!fn) return fail(QK_ERR_LIMIT, "split attention: unsupported head layout");
@@ -882,7 +891,7 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
         head_split = G;
         Gk = 1;
         fn = split_instance(1, a.head_dim, true);
-        split_rows = max_rows;
+        split_rows = a.wide_split_rows > 0 ? std::min(a.wide_split_rows, max_rows) : max_rows;
     }
     // GEMM records: each workgroup's heads must fill whole 256-column blocks
     // (never so in the one-head-per-workgroup form).
@@ -920,7 +929,11 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     if (hipLaunchKernel(fn, dim3(groups, a.n_tokens, nsplit), dim3(wide ? kWideWaves * 64 : kSplitThreads), args,
                         0, stream) != hipSuccess)
         return launch_status("split attention launch");
-    if (nsplit > 1) {
+    // Deferred merges only in the wide form (its partials are one query
+    // head per workgroup).
+    const bool defer = nsplit > 1 && wide && a.defer_merge;
+    if (splits_used) *splits_used = defer ? nsplit : 1;
+    if (nsplit > 1 && !defer) {
         const void *merge = split_merge_instance(Gk);
         if (hipLaunchKernel(merge, dim3(groups, a.n_tokens), dim3(256), args, 0, stream) != hipSuccess)
             return launch_status("split attention merge launch");
