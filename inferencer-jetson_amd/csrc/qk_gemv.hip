@@ -644,38 +644,68 @@ struct I8FusedPolicy : I8Policy {
     __device__ static void load_direct(Lane &, const GemvParams &, int, int) {}
 };
 
-// The INT8 o projection of the one-sequence step over the attention's
-// unmerged split partials: the staging merges each head's splits (the
-// arithmetic of the attention's merge kernel, split order: the largest
-// running max, exp2 weights, fma sums, one divide) and quantizes the row per
-// 32 as I8FusedPolicy does, so the codes equal those of the merge kernel's
-// outputs through quantize_x32_kernel.  One token; rows of at most
-// kMH * 4 * blockDim.x columns; at most kMaxParts splits.
-struct I8MergePolicy : I8FusedPolicy {
-    static constexpr int kMaxParts = 8;
-    static constexpr int kMH = 2;   // float4 per thread
-    struct Early {
-        float4 acc[kMH][kMaxParts];
-        float2 ml[kMH][kMaxParts];   // running max, sum of exp
-    };
+// The one-sequence attention's unmerged split partials, as a GEMV that
+// stages them loads them: thread t holds float4 t + k * nt of the row (k <
+// kPartsHeld) from each of at most kMaxParts splits, with every load clamped
+// (split, column) and unconditional so the wait counts stay static.
+constexpr int kMaxParts = 8;
+constexpr int kPartsHeld = 2;
+struct PartsEarly {
+    float4 acc[kPartsHeld][kMaxParts];
+    float2 ml[kPartsHeld][kMaxParts];   // running max, sum of exp
+};
 
-    // Every load clamped (split, column) and unconditional, as in
-    // I8FusedPolicy::early.
-    __device__ static void early(Early &e, const GemvParams &p, int, int cols) {
-        const int hd = p.part_hd, ps = split_partial_floats(hd);
-        const int last = (cols >> 2) - 1;
+__device__ __forceinline__ void parts_load(PartsEarly &e, const float *parts, int n_parts, int hd, int cols, int tid,
+                                           int nt) {
+    const int ps = split_partial_floats(hd);
+    const int last = (cols >> 2) - 1;
+    #pragma unroll
+    for (int k = 0; k < kPartsHeld; ++k) {
+        const int i = min(tid + k * nt, last);
+        const int h = 4 * i / hd, c = 4 * i - h * hd;
+        const float *base = parts + static_cast<int64_t>(h) * n_parts * ps;
         #pragma unroll
-        for (int k = 0; k < kMH; ++k) {
-            const int i = min(static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x), last);
-            const int h = 4 * i / hd, c = 4 * i - h * hd;
-            const float *base = p.parts + static_cast<int64_t>(h) * p.n_parts * ps;
-            #pragma unroll
-            for (int sp = 0; sp < kMaxParts; ++sp) {
-                const float *q = base + min(sp, p.n_parts - 1) * ps;
-                e.ml[k][sp] = *reinterpret_cast<const float2 *>(q);
-                e.acc[k][sp] = *reinterpret_cast<const float4 *>(q + 4 + c);
-            }
+        for (int sp = 0; sp < kMaxParts; ++sp) {
+            const float *q = base + min(sp, n_parts - 1) * ps;
+            e.ml[k][sp] = *reinterpret_cast<const float2 *>(q);
+            e.acc[k][sp] = *reinterpret_cast<const float4 *>(q + 4 + c);
         }
+    }
+}
+
+// Float4 k of the thread's share merged: the attention merge kernel's
+// arithmetic (the largest running max, exp2 weights, fma sums in split
+// order, one divide per value).
+__device__ __forceinline__ float4 parts_merge(const PartsEarly &e, int k, int n_parts) {
+    float mx = -INFINITY;
+    #pragma unroll
+    for (int sp = 0; sp < kMaxParts; ++sp)
+        if (sp < n_parts) mx = fmaxf(mx, e.ml[k][sp].x);
+    float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
+    float den = 0.f;
+    #pragma unroll
+    for (int sp = 0; sp < kMaxParts; ++sp) {
+        if (sp >= n_parts) continue;
+        const float w = __builtin_amdgcn_exp2f(e.ml[k][sp].x - mx);
+        den = fmaf(w, e.ml[k][sp].y, den);
+        num.x = fmaf(w, e.acc[k][sp].x, num.x);
+        num.y = fmaf(w, e.acc[k][sp].y, num.y);
+        num.z = fmaf(w, e.acc[k][sp].z, num.z);
+        num.w = fmaf(w, e.acc[k][sp].w, num.w);
+    }
+    return make_float4(num.x / den, num.y / den, num.z / den, num.w / den);
+}
+
+// The INT8 o projection of the one-sequence step over the attention's
+// unmerged split partials: the staging merges each head's splits and
+// quantizes the row per 32 as I8FusedPolicy does, so the codes equal those
+// of the merge kernel's outputs through quantize_x32_kernel.  One token;
+// rows of at most kPartsHeld * 4 * blockDim.x columns.
+struct I8MergePolicy : I8FusedPolicy {
+    using Early = PartsEarly;
+
+    __device__ static void early(Early &e, const GemvParams &p, int, int cols) {
+        parts_load(e, p.parts, p.n_parts, p.part_hd, cols, threadIdx.x, blockDim.x);
     }
 
     __device__ static void prep_early(const Early &e, const GemvParams &p, int, int cols, XGroup *lds) {
@@ -683,26 +713,9 @@ struct I8MergePolicy : I8FusedPolicy {
         float *st = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + cols);
         const int n4 = cols >> 2;
         #pragma unroll
-        for (int k = 0; k < kMH; ++k) {
+        for (int k = 0; k < kPartsHeld; ++k) {
             const int i = static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x);
-            if (i >= n4) continue;
-            float mx = -INFINITY;
-            #pragma unroll
-            for (int sp = 0; sp < kMaxParts; ++sp)
-                if (sp < p.n_parts) mx = fmaxf(mx, e.ml[k][sp].x);
-            float4 num = make_float4(0.f, 0.f, 0.f, 0.f);
-            float den = 0.f;
-            #pragma unroll
-            for (int sp = 0; sp < kMaxParts; ++sp) {
-                if (sp >= p.n_parts) continue;
-                const float w = __builtin_amdgcn_exp2f(e.ml[k][sp].x - mx);
-                den = fmaf(w, e.ml[k][sp].y, den);
-                num.x = fmaf(w, e.acc[k][sp].x, num.x);
-                num.y = fmaf(w, e.acc[k][sp].y, num.y);
-                num.z = fmaf(w, e.acc[k][sp].z, num.z);
-                num.w = fmaf(w, e.acc[k][sp].w, num.w);
-            }
-            quantize4(make_float4(num.x / den, num.y / den, num.z / den, num.w / den), i, q4, st);
+            if (i < n4) quantize4(parts_merge(e, k, p.n_parts), i, q4, st);
         }
     }
 
@@ -1459,6 +1472,12 @@ struct RecParams {
     const float *gain;     // NULL: 1
     float *arg_v;          // greedy-pick partials, one per wave (NULL: none)
     int *arg_i;
+    // MERGE kernels: the input is the attention's unmerged split partials
+    // ([head][n_parts][split_partial_floats(part_hd)]), merged and made into
+    // records in LDS instead of read from rec.
+    const float *parts;
+    int n_parts;
+    int part_hd;
 };
 
 struct RecSlot {
@@ -1598,7 +1617,10 @@ __device__ __forceinline__ void record16(float x, float sq, int lane, XGroup *ds
     if (ss && lane == 0) *ss = sq;
 }
 
-template <int TYPE, int G, bool EPI, int D>
+// Columns a MERGE kernel stages (its records live in LDS).
+constexpr int kRecMergeCols = 2048;
+
+template <int TYPE, int G, bool EPI, int D, bool MERGE>
 __device__ __forceinline__ void rec_body(const RecParams &p) {
     __shared__ float part[2 * kRecRows * kRecMaxChunks];
     const int lane = threadIdx.x & 63;
@@ -1630,6 +1652,9 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
         return rec_fetch<TYPE>(p, blk, (k & smask) * step_rows + ri0, piece, g, h, !EPI && head && p.accumulate);
     };
     const int last = max(n_iter - 1, 0);
+    // MERGE: the partials' loads go out ahead of the weights'.
+    PartsEarly pe;
+    if constexpr (MERGE) parts_load(pe, p.parts, p.n_parts, p.part_hd, p.nb * 256, threadIdx.x, W * 64);
     RecSlot sl[D];
     #pragma unroll
     for (int i = 0; i < D; ++i) sl[i] = fetch(min(i, last));
@@ -1656,14 +1681,40 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
     // stay in L1 / L2 for the workgroup's other lanes), and the sums of
     // squares, with no LDS copy and no barrier before the first dot.
     F32Policy::Lane L;
-    #pragma unroll
-    for (int part_i = 0; part_i < 4; ++part_i) F32Policy::set_part(L, part_i, p.rec[F32Policy::group_of(piece, part_i)]);
+    if constexpr (MERGE) {
+        // The row merged into LDS, then its records made there (one per
+        // thread, make_group_tree: the records the attention's own epilogue
+        // would have written), then each lane's four read back.
+        __shared__ float xs[kRecMergeCols];
+        __shared__ XGroup recs[kRecMergeCols / 16];
+        const int cols = p.nb * 256, n4 = cols / 4;
+        #pragma unroll
+        for (int k = 0; k < kPartsHeld; ++k) {
+            const int i = static_cast<int>(threadIdx.x) + k * W * 64;
+            if (i < n4) reinterpret_cast<float4 *>(xs)[i] = parts_merge(pe, k, p.n_parts);
+        }
+        __syncthreads();
+        for (int gi = threadIdx.x; gi < cols / 16; gi += W * 64) {
+            float v[16];
+            load16f(xs + 16 * gi, v);
+            recs[gi] = make_group_tree(v);
+        }
+        __syncthreads();
+        #pragma unroll
+        for (int part_i = 0; part_i < 4; ++part_i) F32Policy::set_part(L, part_i, recs[F32Policy::group_of(piece, part_i)]);
+    } else {
+        #pragma unroll
+        for (int part_i = 0; part_i < 4; ++part_i)
+            F32Policy::set_part(L, part_i, p.rec[F32Policy::group_of(piece, part_i)]);
+    }
     const float *ssp = p.ss ? p.ss : reinterpret_cast<const float *>(p.rec);   // any readable address
     float ssv[kRecSsPerLane];
-    #pragma unroll
-    for (int i = 0; i < kRecSsPerLane; ++i) ssv[i] = ssp[min(lane + 64 * i, p.nb * 16 - 1)];
+    if constexpr (!MERGE) {   // (MERGE launches take no sums of squares)
+        #pragma unroll
+        for (int i = 0; i < kRecSsPerLane; ++i) ssv[i] = ssp[min(lane + 64 * i, p.nb * 16 - 1)];
+    }
     float nscale = 1.f;
-    if (p.ss) {
+    if (!MERGE && p.ss) {
         float acc = 0.f;
         #pragma unroll
         for (int i = 0; i < kRecSsPerLane; ++i) acc += lane + 64 * i < p.nb * 16 ? ssv[i] : 0.f;
@@ -1763,16 +1814,23 @@ __device__ __forceinline__ void rec_body(const RecParams &p) {
 template <int TYPE, int G, bool EPI, int D>
 __global__ __launch_bounds__(kRecMaxWaves * 64) void rec_gemv(RecParams p) {
     if constexpr (TYPE != 0) {
-        rec_body<TYPE, G, EPI, D>(p);
+        rec_body<TYPE, G, EPI, D, false>(p);
     } else {
         int m, row0;
         rec_block(p, blockIdx.x, 0, m, row0);
         const int type = __builtin_amdgcn_readfirstlane(rec_mat(p, __builtin_amdgcn_readfirstlane(m)).type);
         if (type == QK_TYPE_Q4_K)
-            rec_body<QK_TYPE_Q4_K, G, EPI, D>(p);
+            rec_body<QK_TYPE_Q4_K, G, EPI, D, false>(p);
         else
-            rec_body<QK_TYPE_Q6_K_SPLIT, G, EPI, D>(p);
+            rec_body<QK_TYPE_Q6_K_SPLIT, G, EPI, D, false>(p);
     }
+}
+
+// The one-sequence o projection over the attention's unmerged splits (one
+// matrix, one type, output records).
+template <int TYPE, int G, int D>
+__global__ __launch_bounds__(kRecMaxWaves * 64) void rec_gemv_merge(RecParams p) {
+    rec_body<TYPE, G, true, D, true>(p);
 }
 
 // Waves per workgroup W and steps S of a launch: W * S = (pair ? 2 : 1) * nb
@@ -1815,6 +1873,17 @@ template <int TYPE>
 const void *rec_kernel_t(int group, bool epi, bool deep) {
     if (deep) return epi ? rec_kernel_g<TYPE, true, 4>(group) : rec_kernel_g<TYPE, false, 4>(group);
     return epi ? rec_kernel_g<TYPE, true, 2>(group) : rec_kernel_g<TYPE, false, 2>(group);
+}
+
+const void *rec_merge_kernel(int type, int group, bool deep) {
+    if (group != 32) return nullptr;   // rows of 2048 columns
+    if (type == QK_TYPE_Q4_K)
+        return deep ? reinterpret_cast<const void *>(rec_gemv_merge<QK_TYPE_Q4_K, 32, 4>)
+                    : reinterpret_cast<const void *>(rec_gemv_merge<QK_TYPE_Q4_K, 32, 2>);
+    if (type == QK_TYPE_Q6_K_SPLIT)
+        return deep ? reinterpret_cast<const void *>(rec_gemv_merge<QK_TYPE_Q6_K_SPLIT, 32, 4>)
+                    : reinterpret_cast<const void *>(rec_gemv_merge<QK_TYPE_Q6_K_SPLIT, 32, 2>);
+    return nullptr;
 }
 
 const void *rec_kernel(int type, int group, bool epi, bool deep) {
@@ -1896,8 +1965,8 @@ int launch_gemv_i8_staged(const qk_matrix *mats, int n_mats, const float *x, int
 
 bool gemv_i8_mergeable(int cols, int head_dim, int n_parts) {
     const int pieces = cols / 256 * 4;
-    return cols > 0 && cols % 256 == 0 && cols <= I8MergePolicy::kMH * 4 * 256 && 64 % pieces == 0 && head_dim > 0 &&
-           head_dim % 4 == 0 && cols % head_dim == 0 && n_parts >= 1 && n_parts <= I8MergePolicy::kMaxParts;
+    return cols > 0 && cols % 256 == 0 && cols <= kPartsHeld * 4 * 256 && 64 % pieces == 0 && head_dim > 0 &&
+           head_dim % 4 == 0 && cols % head_dim == 0 && n_parts >= 1 && n_parts <= kMaxParts;
 }
 
 int launch_gemv_i8_merged(const qk_matrix *mats, int n_mats, const float *parts, int n_parts, int head_dim, int cols,
@@ -1984,6 +2053,12 @@ bool gemv_fusable(int cols) {
     return chunks <= kMaxChunks && F32FusedPolicy::lds_bytes(cols) + 4096 <= kMaxLds;
 }
 
+bool rec_gemv_mergeable(int cols, int head_dim) {
+    int W, S, G;
+    return cols % 256 == 0 && cols <= kRecMergeCols && rec_plan(cols / 256, false, W, S, G) && G == 32 &&
+           W * 64 * kPartsHeld * 4 >= cols && head_dim > 0 && head_dim % 4 == 0 && cols % head_dim == 0;
+}
+
 bool rec_gemv_supported(int cols, bool pair) {
     int w, s, g;
     return cols > 0 && cols % 256 == 0 && rec_plan(cols / 256, pair, w, s, g);
@@ -2046,6 +2121,28 @@ int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &
     p.arg_v = r.arg_v;
     p.arg_i = r.arg_i;
     const bool epi = (4 * nb) / G > 1 || r.rec_out || r.pair;
+    if (r.parts) {
+        // o over the attention's unmerged splits: one matrix of one type,
+        // output records, one row block per workgroup, all resident.
+        const void *fn2 = type == 0 ? nullptr : rec_merge_kernel(type, G, false);
+        if (!fn2 || !r.rec_out || r.pair || r.arg_v || r.ss || cols > kRecMergeCols ||
+            W * 64 * kPartsHeld * 4 < cols || r.n_parts < 1 || r.n_parts > kMaxParts || r.part_hd <= 0 ||
+            r.part_hd % 4 || cols % r.part_hd)
+            return fail(QK_ERR_LIMIT, "record GEMV: unsupported merged launch");
+        p.parts = r.parts;
+        p.n_parts = r.n_parts;
+        p.part_hd = r.part_hd;
+        p.rec = reinterpret_cast<const XGroup *>(r.parts);   // any readable address (the unused loads)
+        const bool deep = S > 2;
+        const void *fn = rec_merge_kernel(type, G, deep);
+        const int grid = static_cast<int>(blocks);
+        if (resident_blocks(fn, W * 64, 0) < grid)
+            return fail(QK_ERR_LIMIT, "record GEMV: merged launch does not fit in one round");
+        void *args[] = {&p};
+        if (hipLaunchKernel(fn, dim3(grid), dim3(W * 64), args, 0, stream) != hipSuccess)
+            return launch_status("merged record GEMV launch");
+        return launch_status("merged record GEMV launch");
+    }
     // One row block per workgroup when they all fit at once (always for
     // mixed types); grid-stride otherwise (the LM head), within the argmax
     // partials' buffer.  Two tiles in flight per wave when a wave has no

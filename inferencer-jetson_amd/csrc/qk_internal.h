@@ -283,6 +283,47 @@ __device__ __forceinline__ void record16_quads(float x, int lane, XGroup *dst, b
     if (store) reinterpret_cast<uint32_t *>(dst)[li] = word;
 }
 
+// record16_quads' record of 16 values made by one lane: the same maximum,
+// the sum in its xor-tree order ((v0+v8) + (v4+v12)) + ((v2+v10) + (v6+v14))
+// + ... (every lane of that butterfly ends with these bits: fp32 addition
+// commutes), the same exponent, limbs and words.
+__device__ __forceinline__ XGroup make_group_tree(const float *v) {
+    float a[8], b[4];
+    #pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = v[i] + v[i + 8];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = a[i] + a[i + 4];
+    const float sum = (b[0] + b[2]) + (b[1] + b[3]);
+    float m = fabsf(v[0]);
+    #pragma unroll
+    for (int i = 1; i < 16; ++i) m = fmaxf(m, fabsf(v[i]));
+    const bool ok = m > 0.f && isfinite(m);
+    const int e = __builtin_amdgcn_frexp_expf(m) - 1;
+    uint32_t l0[4] = {0, 0, 0, 0}, l1[4] = {0, 0, 0, 0}, l2[4] = {0, 0, 0, 0};
+    #pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int X = ok ? static_cast<int>(rintf(ldexpf(v[i], 21 - e))) : 0;
+        const int b0 = (X << 24) >> 24;
+        const int X1 = (X - b0) >> 8;
+        const int b1 = (X1 << 24) >> 24;
+        const int b2 = (X1 - b1) >> 8;
+        l0[i >> 2] |= (static_cast<uint32_t>(b0) & 0xFFu) << (8 * (i & 3));
+        l1[i >> 2] |= (static_cast<uint32_t>(b1) & 0xFFu) << (8 * (i & 3));
+        l2[i >> 2] |= (static_cast<uint32_t>(b2) & 0xFFu) << (8 * (i & 3));
+    }
+    XGroup gr;
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        gr.limb[k] = static_cast<int>(l0[k]);
+        gr.limb[4 + k] = static_cast<int>(l1[k]);
+        gr.limb[8 + k] = static_cast<int>(l2[k]);
+    }
+    gr.scale = ok ? ldexpf(1.f, e - 21) : (m == 0.f ? 0.f : __builtin_nanf(""));
+    gr.sum = sum;
+    gr.pad[0] = gr.pad[1] = 0;
+    return gr;
+}
+
 __device__ __forceinline__ XGroup make_group_regs(const float *v) {
     float m = 0.f, s = 0.f;
     #pragma unroll
@@ -559,10 +600,20 @@ struct RecGemv {
     float *arg_v = nullptr;
     int *arg_i = nullptr;
     int *arg_parts = nullptr;
+    // Instead of rec: the one-sequence attention's unmerged wide-form split
+    // partials (launch_split_attention with defer_merge), n_parts splits per
+    // head of part_hd, merged and made into records by every workgroup.
+    // One matrix of 2048 columns with rec_out, no ss, pair or greedy pick.
+    const float *parts = nullptr;
+    int n_parts = 0;
+    int part_hd = 0;
 };
 // Whether rows of cols columns have a record-GEMV launch plan, and whether
 // the matrices' types can share one launch (a pair needs one type).
 bool rec_gemv_supported(int cols, bool pair);
+// Whether a one-matrix record GEMV of cols columns can take the attention's
+// unmerged partials of head_dim (RecGemv::parts).
+bool rec_gemv_mergeable(int cols, int head_dim);
 bool rec_gemv_types(const qk_matrix *mats, int n_mats, bool pair);
 int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &r, hipStream_t stream);
 // The embedding of one token (device id) into out (cols fp32) and the

@@ -206,6 +206,12 @@ int residual_by_mode(qk_llama *m, int type, int rows, const void *w, const float
     return qk_add_f32(m->x, m->tmp, rows, s);
 }
 
+// Rows per split of the one-sequence attention when the o GEMV merges its
+// splits: one round of the wide kernel's rows (128 at head_dim 64) per
+// workgroup, longer when that would take more than the 8 splits the merging
+// GEMVs hold.
+int decode_split_rows(int rows) { return std::max(128, ((rows + 7) / 8 + 15) / 16 * 16); }
+
 // The INT8 mode of FastRunner::forward (inferencer.cu:1424-1531 with use_dp4a /
 // use_q6_dp4a and --fused-norm-quant): RMSNorm and the per-32 quantization in
 // one launch before the QKV and gate/up GEMVs, the attention output quantized
@@ -231,7 +237,7 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
                          qk::gemv_i8_mergeable(dim, hd, 8);
     if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
     qk::SplitAttention attn{};
-    attn.wide_split_rows = merge_o ? std::max(128, ((pos + 1 + 7) / 8 + 15) / 16 * 16) : 0;
+    attn.wide_split_rows = merge_o ? decode_split_rows(pos + 1) : 0;
     attn.q = m->q;
     attn.k = m->k;
     attn.v = m->v;
@@ -370,6 +376,11 @@ int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, 
     attn.cache_rows = c.context;
     attn.rows_hint = pos + 1;
     attn.pos = attn.max_pos = pos;
+    // The attention's rows split into rounds of 128 per workgroup (at most
+    // 8 splits), merged by the o GEMV, which makes the records itself.
+    const bool merge_o = c.heads * m->head_dim == dim && qk::rec_gemv_mergeable(dim, m->head_dim);
+    attn.wide_split_rows = merge_o ? decode_split_rows(pos + 1) : 0;
+    attn.defer_merge = merge_o;
     attn.n_tokens = 1;
     attn.heads = c.heads;
     attn.kv_heads = c.kv_heads;
@@ -396,9 +407,13 @@ int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, 
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
         if ((st = qk::launch_rec_gemv(qkv, 3, dim, qkv_in, s))) return st;
         attn.layer = l;
-        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
+        int parts = 1;
+        if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s, &parts))) return st;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         o_out.gain = L.ffn_norm;
+        o_out.parts = parts > 1 ? static_cast<const float *>(m->attn_ws) : nullptr;
+        o_out.n_parts = parts;
+        o_out.part_hd = m->head_dim;
         if ((st = qk::launch_rec_gemv(&o, 1, dim, o_out, s))) return st;
         const qk_matrix gu[2] = {{L.gate_type, c.hidden, L.gate, m->gate}, {L.up_type, c.hidden, L.up, m->up}};
         if ((st = qk::launch_rec_gemv(gu, 2, dim, gu_io, s))) return st;
