@@ -490,7 +490,7 @@ struct I8FusedPolicy : I8Policy {
         const int last = (cols >> 2) - 1;
         #pragma unroll
         for (int k = 0; k < kHeld; ++k) {
-            const int i = min(static_cast<int>(threadIdx.x) + k * static_cast<int>(blockDim.x), last);
+            const int i = min(static_cast<int>(threadIdx.x) + k * stage_threads(), last);
             e.v[k] = x4[i];
             e.w[k] = w4[i];
         }
@@ -499,12 +499,13 @@ struct I8FusedPolicy : I8Policy {
     // prep over what early loaded: the same values, sums and codes.
     __device__ static void prep_early(const Early &e, const GemvParams &p, int token, int cols, XGroup *lds) {
         const int n4 = cols >> 2;
-        const int nt = blockDim.x;
+        const int nt = stage_threads();
         const int tid = threadIdx.x;
         if (n4 > kHeld * nt) {
             prep(p, token, cols, lds);
             return;
         }
+        const bool stager = tid < nt;   // whole waves
         uint32_t *q4 = reinterpret_cast<uint32_t *>(lds);
         float *st = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + cols);
         float *scratch = st + cols / 32;
@@ -513,19 +514,19 @@ struct I8FusedPolicy : I8Policy {
             float ss = 0.f;
             #pragma unroll
             for (int k = 0; k < kHeld; ++k) {
-                if (tid + k * nt < n4) {
+                if (stager && tid + k * nt < n4) {
                     ss = fmaf(e.v[k].x, e.v[k].x, ss);
                     ss = fmaf(e.v[k].y, e.v[k].y, ss);
                     ss = fmaf(e.v[k].z, e.v[k].z, ss);
                     ss = fmaf(e.v[k].w, e.v[k].w, ss);
                 }
             }
-            scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+            scale = 1.0f / sqrtf(block_sum(ss, scratch, nt) / static_cast<float>(cols) + p.norm_eps);
         }
         #pragma unroll
         for (int k = 0; k < kHeld; ++k) {
             const int i = tid + k * nt;
-            if (i >= n4) continue;
+            if (!stager || i >= n4) continue;
             const float4 v = e.v[k], w = e.w[k];
             float4 o = v;
             if (p.norm_w)
@@ -568,7 +569,7 @@ struct I8FusedPolicy : I8Policy {
                     ss = fmaf(v[k].w, v[k].w, ss);
                 }
             }
-            const float scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+            const float scale = 1.0f / sqrtf(block_sum(ss, scratch, blockDim.x) / static_cast<float>(cols) + p.norm_eps);
             #pragma unroll
             for (int k = 0; k < kHeld; ++k) {
                 const int i = tid + k * nt;
@@ -590,7 +591,7 @@ struct I8FusedPolicy : I8Policy {
                 ss = fmaf(v.z, v.z, ss);
                 ss = fmaf(v.w, v.w, ss);
             }
-            scale = 1.0f / sqrtf(block_sum(ss, scratch) / static_cast<float>(cols) + p.norm_eps);
+            scale = 1.0f / sqrtf(block_sum(ss, scratch, blockDim.x) / static_cast<float>(cols) + p.norm_eps);
         }
         for (int i = tid; i < n4; i += nt) {
             const float4 v = x4[i];
@@ -607,18 +608,24 @@ struct I8FusedPolicy : I8Policy {
         }
     }
 
-    // Block sum in rmsnorm_quantize_kernel's order for 256 threads (every
-    // wave's xor tree, then (w0 + w1) + (w2 + w3)); in wave order otherwise.
-    __device__ static float block_sum(float ss, float *scratch) {
+    // Sum over the first nt threads (whole waves; every thread of the block
+    // calls it) in rmsnorm_quantize_kernel's order for 256 (every wave's xor
+    // tree, then (w0 + w1) + (w2 + w3)); in wave order otherwise.
+    __device__ static float block_sum(float ss, float *scratch, int nt) {
         #pragma unroll
         for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-        if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = ss;
+        if ((threadIdx.x & 63) == 0 && static_cast<int>(threadIdx.x) < nt) scratch[threadIdx.x >> 6] = ss;
         __syncthreads();
-        if (blockDim.x == 256) return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+        if (nt == 256) return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
         ss = 0.f;
-        for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) ss += scratch[w];
+        for (int w = 0; w < nt >> 6; ++w) ss += scratch[w];
         return ss;
     }
+
+    // Threads that stage the row in the early form: at most 256 (the
+    // separate kernel's block, so its sum order holds); the rest of a larger
+    // block waits at the barriers.
+    __device__ static int stage_threads() { return min(static_cast<int>(blockDim.x), 256); }
 
     // The lane's piece from LDS: I8Policy::load_direct's layout.
     __device__ static void load(Lane &L, const GemvParams &p, int, int piece, const XGroup *lds) {
@@ -1235,17 +1242,27 @@ int gcd_int(int a, int b) {
     return a;
 }
 
+// Waves of a gate / up pair workgroup: eight (two per SIMD: the dot
+// products of one wave's tiles overlap another's; 1B decode 0.671 -> 0.656
+// ms/token against four), fewer when the workgroup has fewer tiles (it has
+// GROUP: 2 x 32 rows of 64 / GROUP rows each).
+__host__ __device__ constexpr int pair_waves(int group) { return group < 8 ? group : 8; }
+
 // The INT8 step's gate / up pair with SiLU(gate) * up quantized in the
 // epilogue (silu_cuda and quantize_x32_cuda's arithmetic): workgroup w owns
 // rows 32w .. 32w + 31 of both matrices -- 32 / TR tiles of TR = 64 / GROUP
-// rows each -- and its four waves take those 64 / TR tiles in turn; the
-// row sums meet in LDS and one half-wave forms and quantizes the
-// workgroup's 32 values into hq / hs (token-major, ldq / ldsc).
+// rows each -- and its waves take those 64 / TR tiles in turn; the row
+// sums meet in LDS and one half-wave forms and quantizes the workgroup's
+// 32 values into hq / hs (token-major, ldq / ldsc).  The first 256 threads
+// stage the input (the separate kernel's sum order).
 template <class Policy, int TYPE, int GROUP>
-__global__ __launch_bounds__(256) void gemv_pair_quant(GemvParams p, int8_t *hq, float *hs, int ldq, int ldsc) {
+__global__ __launch_bounds__(pair_waves(GROUP) * 64) void gemv_pair_quant(GemvParams p, int8_t *hq, float *hs, int ldq,
+                                                                         int ldsc) {
     constexpr int TR = 64 / GROUP;
     constexpr int kHalf = 32 / TR;         // tiles per matrix
-    constexpr int kPerWave = 2 * kHalf / 4;
+    constexpr int NW = pair_waves(GROUP);
+    constexpr int kPerWave = 2 * kHalf / NW;
+    static_assert(kPerWave >= 1 && kPerWave * NW == 2 * kHalf, "whole tiles per wave");
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int token = blockIdx.y;
@@ -1266,7 +1283,7 @@ __global__ __launch_bounds__(256) void gemv_pair_quant(GemvParams p, int8_t *hq,
     constexpr int kDepth = kPerWave < 8 ? kPerWave : 8;
     Slot sl[kDepth];
     #pragma unroll
-    for (int j = 0; j < kDepth; ++j) sl[j] = prep<TYPE>(p, tile_at(wave + 4 * j), rit, piece, token, g, h);
+    for (int j = 0; j < kDepth; ++j) sl[j] = prep<TYPE>(p, tile_at(wave + NW * j), rit, piece, token, g, h);
     Policy::prep_early(e, p, token, p.pieces * 64, xg);
     __syncthreads();
     typename Policy::Lane L;
@@ -1275,9 +1292,9 @@ __global__ __launch_bounds__(256) void gemv_pair_quant(GemvParams p, int8_t *hq,
     for (int j = 0; j < kPerWave; ++j) {
         Slot &cur = sl[j % kDepth];
         const float v = group_sum<GROUP>(piece_dot<Policy, TYPE>(cur.t.type, cur.r, L, g, h));
-        const int k = wave + 4 * j;
+        const int k = wave + NW * j;
         if (piece == 0) vals[(k >= kHalf ? 32 : 0) + (k % kHalf) * TR + rit] = v;
-        if (j + kDepth < kPerWave) cur = prep<TYPE>(p, tile_at(wave + 4 * (j + kDepth)), rit, piece, token, g, h);
+        if (j + kDepth < kPerWave) cur = prep<TYPE>(p, tile_at(wave + NW * (j + kDepth)), rit, piece, token, g, h);
     }
     __syncthreads();
     if (threadIdx.x < 32) {
@@ -1987,15 +2004,20 @@ int launch_pair_quant_type(const GemvParams &p, int group, int n_tokens, int8_t 
                            size_t lds, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(p.mat[0].rows / 32), static_cast<unsigned>(n_tokens));
     if (group == 4)
-        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 4>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 4>), grid, dim3(pair_waves(4) * 64), lds, stream, p, hq,
+                           hs, ldq, ldsc);
     else if (group == 8)
-        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 8>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 8>), grid, dim3(pair_waves(8) * 64), lds, stream, p, hq,
+                           hs, ldq, ldsc);
     else if (group == 16)
-        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 16>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 16>), grid, dim3(pair_waves(16) * 64), lds, stream, p, hq,
+                           hs, ldq, ldsc);
     else if (group == 32)
-        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 32>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 32>), grid, dim3(pair_waves(32) * 64), lds, stream, p, hq,
+                           hs, ldq, ldsc);
     else
-        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 64>), grid, dim3(256), lds, stream, p, hq, hs, ldq, ldsc);
+        hipLaunchKernelGGL((gemv_pair_quant<I8FusedPolicy, TYPE, 64>), grid, dim3(pair_waves(64) * 64), lds, stream, p, hq,
+                           hs, ldq, ldsc);
     return launch_status("INT8 gate / up pair launch");
 }
 
