@@ -135,10 +135,23 @@ int launch_gemv_i8_pair_quant(const qk_matrix *gu, const float *x, int ldx, cons
 // launch adds: the workspace holds them (skinny_i8_workspace_bytes of the
 // launch's row tiles: sum of ceil(rows / 32), or rows / 32 for a pair).
 size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair);
+// The next RMSNorm + quantization of an accumulating one-matrix launch's
+// output rows, folded into its split reduction: x (the launch's y) as
+// rmsnorm_quantize_kernel would normalise it with w, into xq [token][ldxq]
+// and xs [token][ldxs], bit for bit.  *done is set when the launch did it
+// (it split its sums; rows of at most 4096), cleared otherwise.
+struct SkNorm {
+    const float *w = nullptr;
+    float eps = 0.f;
+    int8_t *xq = nullptr;
+    float *xs = nullptr;
+    int ldxq = 0, ldxs = 0;
+    int *done = nullptr;
+};
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
                      float *out_xs, int out_ldxq, int out_ldxs, void *workspace, size_t workspace_size,
-                     hipStream_t stream, const char *where);
+                     hipStream_t stream, const char *where, const SkNorm *norm = nullptr);
 // SiLU(gate) * up quantized per 32 values straight into xq / xscale (n a
 // multiple of 32): bit-identical to qk_silu_mul_f32 then qk_quantize_x32,
 // without the fp32 product written.  Arguments already validated.
@@ -148,6 +161,24 @@ int launch_silu_mul_quantize(const float *gate, const float *up, int8_t *xq, flo
 // SiLU(g) * u in silu_cuda's expression (inferencer.cu:1053-1057), shared by
 // every kernel that forms it so their results agree bit for bit.
 __device__ __forceinline__ float silu_mul_value(float g, float u) { return g / (1.f + expf(-g)) * u; }
+
+// Wave-wide sum (xor tree, every lane gets the total) and block-wide sum for
+// blockDim.x = 256 (every wave's tree, then (w0 + w1) + (w2 + w3)): the
+// order rmsnorm_kernel and rmsnorm_quantize_kernel sum their squares in.
+__device__ __forceinline__ float wave_sum(float v) {
+    #pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float *scratch) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
+}
 
 // quantize_x32_cuda (inferencer.cu:544-556) for the value a lane holds: the
 // 32 lanes of its half-wave form one group; lanes past the row hold 0.

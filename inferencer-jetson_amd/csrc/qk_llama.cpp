@@ -857,10 +857,14 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
         return trace_copy_2d(m->trace_q ? m->trace_q + (l * 4 + stage) * qstride : nullptr, c.layers * 4 * qstride,
                              src, cols, cols, T, s);
     };
+    // down's split reduction normalises and quantizes the next layer's
+    // input itself when it can (qk::SkNorm; the same codes): normed says it
+    // did.  A step tracing its INT8 inputs keeps the separate launch.
+    int normed = 0;
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((st = norm_quant(L.attn_norm)) || (st = trace_q(l, 0, m->xq, dim)) ||
+        if ((!normed && (st = norm_quant(L.attn_norm))) || (st = trace_q(l, 0, m->xq, dim)) ||
             (st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s)))
             return st;
         if (chained &&
@@ -893,7 +897,20 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
             return st;
         }
         const qk_matrix down{L.down_type, dim, L.down, m->x};
-        if ((st = trace_q(l, 3, m->hq, hidden)) || (st = batch_gemm_i8(m, &down, 1, m->hq, m->hs, hidden, T, true, s)) ||
+        qk::SkNorm next;
+        next.eps = c.eps;
+        next.xq = m->xq;
+        next.xs = m->xs;
+        next.ldxq = dim;
+        next.ldxs = dim / 32;
+        next.done = &normed;
+        next.w = l + 1 < c.layers ? m->layers[l + 1].attn_norm : nullptr;
+        normed = 0;
+        if ((st = trace_q(l, 3, m->hq, hidden)) ||
+            (st = T >= 8 && next.w && !m->trace_q
+                      ? qk::launch_skinny_i8(&down, 1, nullptr, m->hq, hidden, m->hs, hidden / 32, hidden, T, 1, nullptr,
+                                             nullptr, 0, 0, m->i8_ws, m->i8_ws_bytes, s, "qk_llama_batch_forward", &next)
+                      : batch_gemm_i8(m, &down, 1, m->hq, m->hs, hidden, T, true, s)) ||
             (st = batch_trace_x(m, l, T, s)))
             return st;
     }

@@ -660,6 +660,67 @@ __global__ __launch_bounds__(256) void skinny_reduce(SkParams p) {
     });
 }
 
+// float4 of a row one thread holds in skinny_reduce_norm: rows of at most
+// 4 * 256 * kNormHeld values.
+constexpr int kNormHeld = 4;
+
+// One 256-thread workgroup per token of a one-matrix accumulating launch:
+// each output of the token's row is skinny_reduce's split sum plus the
+// residual (the same additions in the same order), stored to y, and the row
+// is then normalised and quantized as rmsnorm_quantize_kernel does (thread
+// t holds float4 t, t + 256, ...; the same sum of squares, scale, codes and
+// scales), so the next projection's input needs no launch of its own.
+__global__ __launch_bounds__(256) void skinny_reduce_norm(SkParams p, int token_tiles, SkNorm nq) {
+    __shared__ float scratch[4];
+    const SkMatrix &M = p.mat[0];
+    const int t = blockIdx.x;
+    const int ttile = t / kToks, tl = t - ttile * kToks;
+    const int n4 = M.rows >> 2;
+    // Element of token tl and row r within its tile's partial sums (the
+    // epilogue's index map inverted).
+    const int ebase = (4 * (tl >> 3) + (tl & 3)) * 64 + 32 * ((tl >> 2) & 1);
+    float *y = M.y + static_cast<int64_t>(t) * M.ldy;
+    float4 v[kNormHeld];
+    float ss = 0.f;
+    #pragma unroll
+    for (int k = 0; k < kNormHeld; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= n4) continue;
+        float r[4];
+        #pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int row = 4 * i + c, tile = row / kRows;
+            const float *src = p.partials + static_cast<size_t>(tile * token_tiles + ttile) * p.splits * 1024 +
+                               ebase + (row - tile * kRows);
+            float sum = src[0];
+            #pragma unroll
+            for (int sp = 1; sp < kSplitsMax; ++sp)
+                if (sp < p.splits) sum += src[static_cast<size_t>(sp) * 1024];
+            r[c] = sum + y[row];
+        }
+        v[k] = make_float4(r[0], r[1], r[2], r[3]);
+        reinterpret_cast<float4 *>(y)[i] = v[k];
+        ss = fmaf(v[k].x, v[k].x, ss);
+        ss = fmaf(v[k].y, v[k].y, ss);
+        ss = fmaf(v[k].z, v[k].z, ss);
+        ss = fmaf(v[k].w, v[k].w, ss);
+    }
+    ss = block_sum256(ss, scratch);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(M.rows) + nq.eps);
+    const float4 *w4 = reinterpret_cast<const float4 *>(nq.w);
+    uint32_t *q4 = reinterpret_cast<uint32_t *>(nq.xq + static_cast<int64_t>(t) * nq.ldxq);
+    float *st = nq.xs + static_cast<int64_t>(t) * nq.ldxs;
+    #pragma unroll
+    for (int k = 0; k < kNormHeld; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i >= n4) continue;   // n4 is a multiple of 8: groups stay whole
+        const float4 w = w4[i];
+        quantize_quad_store(make_float4(v[k].x * scale * w.x, v[k].y * scale * w.y, v[k].z * scale * w.z,
+                                        v[k].w * scale * w.w),
+                            (i & 7) == 0, q4 + i, st + (i >> 3));
+    }
+}
+
 template <int RT, bool LOOP>
 const void *kernel_of(int type) {
     if constexpr (LOOP) {
@@ -798,8 +859,9 @@ size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair) {
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
                      float *out_xs, int out_ldxq, int out_ldxs, void *workspace, size_t workspace_size,
-                     hipStream_t stream, const char *where) {
+                     hipStream_t stream, const char *where, const SkNorm *norm) {
     const int nb = cols / 256;
+    if (norm && norm->done) *norm->done = 0;
     SkParams p{};
     p.n_mats = n_mats;
     p.xq = xq;
@@ -859,7 +921,13 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
                         dim3(static_cast<unsigned>(groups * p.splits), static_cast<unsigned>(token_tiles)),
                         dim3(64 * p.waves), args, lds, stream) != hipSuccess)
         return launch_status(where);
-    if (p.splits > 1) {
+    if (p.splits > 1 && norm && !pair && n_mats == 1 && accumulate && mats[0].rows % 32 == 0 &&
+        mats[0].rows <= 4 * 256 * kNormHeld && p.mat[0].ldy % 4 == 0 && aligned(mats[0].y, 16) && norm->w &&
+        norm->xq && norm->xs && norm->ldxq % 4 == 0 && aligned(norm->xq, 4) && aligned(norm->w, 16)) {
+        hipLaunchKernelGGL(skinny_reduce_norm, dim3(static_cast<unsigned>(n_tokens)), dim3(256), 0, stream, p,
+                           token_tiles, *norm);
+        if (norm->done) *norm->done = 1;
+    } else if (p.splits > 1) {
         const dim3 rgrid(static_cast<unsigned>(tiles), static_cast<unsigned>(token_tiles));
         if (pair)
             hipLaunchKernelGGL(skinny_reduce<2>, rgrid, dim3(256), 0, stream, p);

@@ -15,26 +15,10 @@ namespace qk {
 
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-    #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
 __device__ __forceinline__ float wave_max(float v) {
     #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
     return v;
-}
-
-// Block-wide sum for blockDim.x = 256 (4 waves); every thread gets the total.
-__device__ __forceinline__ float block_sum256(float v, float *scratch) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) scratch[wave] = v;
-    __syncthreads();
-    return (scratch[0] + scratch[1]) + (scratch[2] + scratch[3]);
 }
 
 __device__ __forceinline__ float block_max256(float v, float *scratch) {

@@ -129,6 +129,40 @@ def test_small_llama_int8_prefill_chunk_and_decodes(qk, torch_gpu, oracle, workl
     _check(rows, 1e-5, 5e-2)
 
 
+@pytest.mark.parametrize("cfg", [SMALL, dict(SMALL, dim=2048, hidden=8192, heads=32, kv_heads=8, context=128)])
+def test_folded_norm_matches_separate_launch(qk, torch_gpu, workloads, synth, cfg):
+    """From 8 tokens on, down's split reduction also normalises and
+    quantizes the next layer's input (the separate rmsnorm_quantize launch
+    folded in, the same arithmetic); a step tracing its INT8 inputs keeps
+    the separate launch.  The two give the same codes, so 3 steps' logits
+    and tokens are identical."""
+    W = _weights(workloads, synth, cfg, 19)
+    positions = [3, 10, 21, 33, 40, 47, 52, 58, 5, 9, 60, 30]
+    S, ctx = len(positions), cfg["context"]
+    _, pk, pv = batch_case(workloads, synth, cfg, 19, positions)
+    outs = []
+    for traced in (False, True):
+        br = qk.BatchRunner(cfg, W, max_tokens=S, cache_rows=S * ctx)
+        br.set_int8(True, True)
+        br.load_kv(pk, pv)
+        if traced:
+            tx = qk.DeviceBuffer(S * cfg["layers"] * cfg["dim"] * 4)
+            tq = qk.DeviceBuffer(S * cfg["layers"] * 4 * max(cfg["dim"], cfg["hidden"]))
+            br.set_trace(tx, tq)
+        tokens = [int(x) for x in synth.uniform_i32(S, 19, 30, 0, cfg["vocab"] - 1)]
+        pos, kv_row = list(positions), [s * ctx for s in range(S)]
+        got = []
+        for _ in range(3):
+            tokens = br.forward(tokens, pos, kv_row, True)
+            got.append((list(tokens), br.logits(S)))
+            pos = [p + 1 for p in pos]
+        br.close()
+        outs.append(got)
+    for (ta, la), (tb, lb) in zip(*outs):
+        assert ta == tb
+        assert np.array_equal(la, lb)
+
+
 def test_set_int8_modes(qk, torch_gpu, workloads, synth):
     """Both types or neither: a mixed request is rejected; switching back to
     FP32 gives the FP32 step's logits again."""
