@@ -139,7 +139,9 @@ size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair);
 // output rows, folded into its split reduction: x (the launch's y) as
 // rmsnorm_quantize_kernel would normalise it with w, into xq [token][ldxq]
 // and xs [token][ldxs], bit for bit.  *done is set when the launch did it
-// (it split its sums; rows of at most 4096), cleared otherwise.
+// (it split its sums; rows of at most 4096), cleared otherwise.  With
+// plan_only the launch is planned as if folding (the same split sums) but
+// reduces plainly and leaves the normalisation to the caller.
 struct SkNorm {
     const float *w = nullptr;
     float eps = 0.f;
@@ -147,6 +149,7 @@ struct SkNorm {
     float *xs = nullptr;
     int ldxq = 0, ldxs = 0;
     int *done = nullptr;
+    int plan_only = 0;
 };
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,

@@ -784,7 +784,9 @@ const void *rows_kernel(int type) {
 // workgroups instead runs the looping kernel: the fewest splits of
 // kLoopWaves-wave workgroups, as many as the chip holds, each walking its
 // share of the row tiles.
-SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt) {
+// fold: the caller folds its next RMSNorm into a split reduction, so a plan
+// without splits pays for that separate launch too.
+SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt, bool fold) {
     const int s0 = fewest_splits(nb, waves_max(type, rt));
     const int cus = std::max(1, device_info().cus);
     const void *kernel = skinny_kernel(type, rt, false);
@@ -800,7 +802,7 @@ SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt) {
         const int64_t rounds = (wgs + static_cast<int64_t>(cus) * per_cu - 1) / (static_cast<int64_t>(cus) * per_cu);
         const int load = static_cast<int>(std::min<int64_t>(per_cu, (wgs + cus - 1) / cus));   // busiest CU
         const float cost = static_cast<float>(rounds) * (kRoundUs + kWaveUs * rt * ((load * w + 3) / 4)) +
-                           (s > 1 ? kReduceUs : 0.f);
+                           (s > 1 || fold ? kReduceUs : 0.f);
         if (s == s0 || cost < best - 1e-3f) {
             best = cost;
             best_rounds = rounds;
@@ -899,7 +901,11 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
     if (token_tiles > 65535 || static_cast<int64_t>(tiles) * kSplitsMax > (1 << 30))
         return fail(QK_ERR_LIMIT, std::string(where) + ": launch too large");
     const int rt = pair ? 2 : 1;
-    const SkPlan plan = split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, token_tiles, type, rt);
+    const bool fold = norm && !pair && n_mats == 1 && accumulate && mats[0].rows % 32 == 0 &&
+                      mats[0].rows <= 4 * 256 * kNormHeld && (ldy ? ldy[0] : mats[0].rows) % 4 == 0 &&
+                      aligned(mats[0].y, 16) && norm->w && norm->xq && norm->xs && norm->ldxq % 4 == 0 &&
+                      aligned(norm->xq, 4) && aligned(norm->w, 16);
+    const SkPlan plan = split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, token_tiles, type, rt, fold);
     p.splits = plan.splits;
     p.waves = plan.waves;
     p.tiles = tiles;
@@ -921,9 +927,7 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
                         dim3(static_cast<unsigned>(groups * p.splits), static_cast<unsigned>(token_tiles)),
                         dim3(64 * p.waves), args, lds, stream) != hipSuccess)
         return launch_status(where);
-    if (p.splits > 1 && norm && !pair && n_mats == 1 && accumulate && mats[0].rows % 32 == 0 &&
-        mats[0].rows <= 4 * 256 * kNormHeld && p.mat[0].ldy % 4 == 0 && aligned(mats[0].y, 16) && norm->w &&
-        norm->xq && norm->xs && norm->ldxq % 4 == 0 && aligned(norm->xq, 4) && aligned(norm->w, 16)) {
+    if (p.splits > 1 && fold && !norm->plan_only) {
         hipLaunchKernelGGL(skinny_reduce_norm, dim3(static_cast<unsigned>(n_tokens)), dim3(256), 0, stream, p,
                            token_tiles, *norm);
         if (norm->done) *norm->done = 1;
