@@ -58,6 +58,10 @@ constexpr int kMaxChunks = 16;
 //     6 and 8).
 constexpr int kWaveBlocksPerCu = 2;
 constexpr int kWaveBlocksPerCuLong = 5;
+// The INT8 kernels' lighter arithmetic needs fewer waves per CU: Q4_K
+// 128256 x 2048, 26.45 us at 4 / CU against 26.9 at 5 (the FP32 kernel 29.0
+// at 4, 28.2 at 5).
+constexpr int kWaveBlocksPerCuLongInt8 = 4;
 constexpr int kWaveLongTiles = 16;      // tiles per wave at kWaveBlocksPerCu
 constexpr int kSplitBlocksPerCu = 2;
 constexpr int kSplitBlocksPerCuLong = 4;   // >= kWaveLongTiles tiles per wave-group at 2 / CU
@@ -1335,7 +1339,8 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         // One matrix of whole tiles: gemv_whole (scalar tile bases), else gemv_wave.
         const bool whole = TYPE != 0 && p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0;
         const void *fn = whole ? reinterpret_cast<const void *>(gemv_whole<Policy, TYPE, GROUP>) : k;
-        const int per_cu = aligned && long_launch ? kWaveBlocksPerCuLong : kWaveBlocksPerCu;
+        const int per_cu = aligned && long_launch ? (Policy::kInt8 ? kWaveBlocksPerCuLongInt8 : kWaveBlocksPerCuLong)
+                                                  : kWaveBlocksPerCu;
         const int cap = std::max(1, std::min(resident_blocks(fn, block, x_lds), per_cu * cus) / n_tokens);
         const int grid_all = std::max(1, std::min<int>((p.total_tiles + waves - 1) / waves, cap));
         // Grid-stride tiles: clamping keeps the argmax partials (one per wave)
