@@ -399,10 +399,11 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             # workgroup per query head at these positions, no merge), o,
             # gate/up, down; then the embedding, the LM head and the greedy
             # pick.  INT8, per layer: QKV (RMSNorm + quantize staged),
-            # attention (o's input quantized), o (+add), gate/up (RMSNorm +
-            # quantize staged, SiLU*up quantized in the epilogue), down (+add);
-            # then embedding, norm+quantize, LM head and two argmax stages.
-            "kernels_per_token": (5 * cfg["layers"] + 5) if int8 else (5 * cfg["layers"] + 3),
+            # attention (rows split), o (merging the splits, +add), gate/up
+            # (RMSNorm + quantize staged, SiLU*up quantized in the epilogue),
+            # down (+add); then embedding, norm+quantize, the LM head with
+            # its greedy partials and the final pick.
+            "kernels_per_token": (5 * cfg["layers"] + 4) if int8 else (5 * cfg["layers"] + 3),
             "device_bytes": mem}
 
 

@@ -445,6 +445,12 @@ struct I8Policy {
     }
 };
 
+// The INT8 LM head with the greedy-token epilogue (per-wave best row,
+// lowest index among maxima, as F32ArgPolicy).
+struct I8ArgPolicy : I8Policy {
+    static constexpr bool kArgmax = true;
+};
+
 // The INT8 step's activations quantized by the GEMV itself: every block
 // quantizes its token's fp32 row into LDS (codes, then per-32 scales, then
 // 64 bytes of reduction scratch) and the lanes read their pieces from
@@ -1322,7 +1328,8 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         // The LDS-staged kernel (INT8, split Q6_K): one matrix of whole tiles
         // at a 16-byte aligned address, in a launch long enough for its
         // pipeline to fill.
-        if constexpr (std::is_same_v<Policy, I8Policy> && TYPE == QK_TYPE_Q6_K_SPLIT) {
+        if constexpr ((std::is_same_v<Policy, I8Policy> || std::is_same_v<Policy, I8ArgPolicy>) &&
+                      TYPE == QK_TYPE_Q6_K_SPLIT) {
             if (long_launch && p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0 &&
                 (reinterpret_cast<uintptr_t>(p.mat[0].w) & 15) == 0 &&
                 p.tile_rows * p.mat[0].row_bytes <= kLdsMaxTileBytes) {
@@ -1971,6 +1978,19 @@ int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq
     p.ldscale = ldscale;
     p.accumulate = accumulate;
     return launch<I8Policy>(p, mats, n_mats, cols, n_tokens, ldy, stream, "INT8 GEMV launch");
+}
+
+int launch_gemv_i8_argmax(const qk_matrix *mat, const int8_t *xq, const float *xscale, int cols, float *arg_v,
+                          int *arg_i, int *parts, hipStream_t stream) {
+    GemvParams p{};
+    p.x = xq;
+    p.xscale = xscale;
+    p.ldx = cols;
+    p.ldscale = cols / 32;
+    p.arg_v = arg_v;
+    p.arg_i = arg_i;
+    p.grid_out = parts;
+    return launch<I8ArgPolicy>(p, mat, 1, cols, 1, nullptr, stream, "INT8 GEMV + greedy pick launch");
 }
 
 // The INT8 GEMV quantizing its own input (I8FusedPolicy): fp32 rows x of

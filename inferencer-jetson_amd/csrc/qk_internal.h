@@ -102,6 +102,11 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
 // INT8 GEMV of n_tokens quantized activation rows (xq + t*ldxq, xscale +
 // t*ldscale; y + t*ldy[m]), arguments already validated; accumulate != 0
 // adds W x into y instead of overwriting it.
+// One token's INT8 GEMV over one matrix that also leaves each wave's best
+// (value, row) in arg_v / arg_i (*parts of them, at most kArgPartsMax) for
+// launch_argmax_final: the greedy token without a pass over the outputs.
+int launch_gemv_i8_argmax(const qk_matrix *mat, const int8_t *xq, const float *xscale, int cols, float *arg_v,
+                          int *arg_i, int *parts, hipStream_t stream);
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                    int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
 // The INT8 GEMV quantizing its own fp32 input per 32 values in LDS, after

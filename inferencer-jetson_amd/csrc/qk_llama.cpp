@@ -326,6 +326,14 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
+    if (int8_type(m, out_type)) {
+        // The greedy pick in the LM head's epilogue (one pass fewer).
+        float *arg_v = static_cast<float *>(m->argmax_ws);
+        int *arg_i = reinterpret_cast<int *>(arg_v + qk::kArgPartsMax);
+        int parts = 0;
+        if ((st = qk::launch_gemv_i8_argmax(&head, m->xq, m->xscale, dim, arg_v, arg_i, &parts, s))) return st;
+        return qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s);
+    }
     if ((st = gemv_by_mode(m, &head, 1, m->xn, dim, s))) return st;
     return qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s);
 }
