@@ -401,9 +401,9 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
             # pick.  INT8, per layer: QKV (RMSNorm + quantize staged),
             # attention (rows split), o (merging the splits, +add), gate/up
             # (RMSNorm + quantize staged, SiLU*up quantized in the epilogue),
-            # down (+add); then embedding, norm+quantize, the LM head with
-            # its greedy partials and the final pick.
-            "kernels_per_token": (5 * cfg["layers"] + 4) if int8 else (5 * cfg["layers"] + 3),
+            # down (+add); then embedding, the LM head (RMSNorm + quantize
+            # staged, greedy partials) and the final pick.
+            "kernels_per_token": 5 * cfg["layers"] + 3,
             "device_bytes": mem}
 
 

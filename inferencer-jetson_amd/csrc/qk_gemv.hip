@@ -661,6 +661,12 @@ struct I8FusedPolicy : I8Policy {
     __device__ static void load_direct(Lane &, const GemvParams &, int, int) {}
 };
 
+// The INT8 LM head of the one-sequence step: RMSNorm + quantization staged
+// as I8FusedPolicy does, and the greedy-token epilogue.
+struct I8FusedArgPolicy : I8FusedPolicy {
+    static constexpr bool kArgmax = true;
+};
+
 // The one-sequence attention's unmerged split partials, as a GEMV that
 // stages them loads them: thread t holds float4 t + k * nt of the row (k <
 // kPartsHeld) from each of at most kMaxParts splits, with every load clamped
@@ -1328,7 +1334,8 @@ void launch_tiled(const GemvParams &p, int n_tokens, hipStream_t stream) {
         // The LDS-staged kernel (INT8, split Q6_K): one matrix of whole tiles
         // at a 16-byte aligned address, in a launch long enough for its
         // pipeline to fill.
-        if constexpr ((std::is_same_v<Policy, I8Policy> || std::is_same_v<Policy, I8ArgPolicy>) &&
+        if constexpr ((std::is_same_v<Policy, I8Policy> || std::is_same_v<Policy, I8ArgPolicy> ||
+                       std::is_same_v<Policy, I8FusedArgPolicy>) &&
                       TYPE == QK_TYPE_Q6_K_SPLIT) {
             if (long_launch && p.n_mats == 1 && p.mat[0].rows % p.tile_rows == 0 &&
                 (reinterpret_cast<uintptr_t>(p.mat[0].w) & 15) == 0 &&
@@ -1991,6 +1998,19 @@ int launch_gemv_i8_argmax(const qk_matrix *mat, const int8_t *xq, const float *x
     p.arg_i = arg_i;
     p.grid_out = parts;
     return launch<I8ArgPolicy>(p, mat, 1, cols, 1, nullptr, stream, "INT8 GEMV + greedy pick launch");
+}
+
+int launch_gemv_i8_staged_argmax(const qk_matrix *mat, const float *x, const float *norm_w, float eps, int cols,
+                                 float *arg_v, int *arg_i, int *parts, hipStream_t stream) {
+    GemvParams p{};
+    p.x = x;
+    p.ldx = cols;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
+    p.arg_v = arg_v;
+    p.arg_i = arg_i;
+    p.grid_out = parts;
+    return launch<I8FusedArgPolicy>(p, mat, 1, cols, 1, nullptr, stream, "staged INT8 GEMV + greedy pick launch");
 }
 
 // The INT8 GEMV quantizing its own input (I8FusedPolicy): fp32 rows x of

@@ -107,6 +107,11 @@ int launch_gemv_f32(const qk_matrix *mats, int n_mats, const float *x, int ldx, 
 // launch_argmax_final: the greedy token without a pass over the outputs.
 int launch_gemv_i8_argmax(const qk_matrix *mat, const int8_t *xq, const float *xscale, int cols, float *arg_v,
                           int *arg_i, int *parts, hipStream_t stream);
+// The same over the fp32 row x, RMSNorm'd with norm_w and quantized by every
+// workgroup (launch_gemv_i8_staged's staging; 256-thread workgroups, so the
+// codes are rmsnorm_quantize_kernel's).
+int launch_gemv_i8_staged_argmax(const qk_matrix *mat, const float *x, const float *norm_w, float eps, int cols,
+                                 float *arg_v, int *arg_i, int *parts, hipStream_t stream);
 int launch_gemv_i8(const qk_matrix *mats, int n_mats, const int8_t *xq, int ldxq, const float *xscale, int ldscale,
                    int cols, int n_tokens, const int *ldy, int accumulate, hipStream_t stream);
 // The INT8 GEMV quantizing its own fp32 input per 32 values in LDS, after

@@ -322,18 +322,26 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
             return st;
     }
     if (!need_logits) return QK_OK;
-    if ((st = norm_quant(m->w.output_norm))) return st;
     const void *out_w = m->w.output ? m->w.output : m->w.token_embd;
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
     if (int8_type(m, out_type)) {
-        // The greedy pick in the LM head's epilogue (one pass fewer).
+        // The greedy pick in the LM head's epilogue (one pass fewer); in the
+        // staged step the LM head also normalises and quantizes its input.
         float *arg_v = static_cast<float *>(m->argmax_ws);
         int *arg_i = reinterpret_cast<int *>(arg_v + qk::kArgPartsMax);
         int parts = 0;
-        if ((st = qk::launch_gemv_i8_argmax(&head, m->xq, m->xscale, dim, arg_v, arg_i, &parts, s))) return st;
+        if (staged) {
+            if ((st = qk::launch_gemv_i8_staged_argmax(&head, m->x, m->w.output_norm, c.eps, dim, arg_v, arg_i, &parts,
+                                                       s)))
+                return st;
+        } else if ((st = norm_quant(m->w.output_norm)) ||
+                   (st = qk::launch_gemv_i8_argmax(&head, m->xq, m->xscale, dim, arg_v, arg_i, &parts, s))) {
+            return st;
+        }
         return qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s);
     }
+    if ((st = norm_quant(m->w.output_norm))) return st;
     if ((st = gemv_by_mode(m, &head, 1, m->xn, dim, s))) return st;
     return qk_argmax_f32(m->logits, c.vocab, m->d_next, m->argmax_ws, s);
 }
