@@ -686,19 +686,24 @@ __global__ __launch_bounds__(256) void skinny_reduce_norm(SkParams p, int token_
     for (int k = 0; k < kNormHeld; ++k) {
         const int i = threadIdx.x + 256 * k;
         if (i >= n4) continue;
-        float r[4];
+        // Rows 4i .. 4i + 3 lie in one row tile, at consecutive elements.
+        const int tile = 4 * i / kRows;
+        const float4 *src = reinterpret_cast<const float4 *>(
+            p.partials + static_cast<size_t>(tile * token_tiles + ttile) * p.splits * 1024 + ebase + 4 * i -
+            tile * kRows);
+        float4 sum = src[0];
         #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int row = 4 * i + c, tile = row / kRows;
-            const float *src = p.partials + static_cast<size_t>(tile * token_tiles + ttile) * p.splits * 1024 +
-                               ebase + (row - tile * kRows);
-            float sum = src[0];
-            #pragma unroll
-            for (int sp = 1; sp < kSplitsMax; ++sp)
-                if (sp < p.splits) sum += src[static_cast<size_t>(sp) * 1024];
-            r[c] = sum + y[row];
+        for (int sp = 1; sp < kSplitsMax; ++sp) {
+            if (sp < p.splits) {
+                const float4 t = src[static_cast<size_t>(sp) * 256];
+                sum.x += t.x;
+                sum.y += t.y;
+                sum.z += t.z;
+                sum.w += t.w;
+            }
         }
-        v[k] = make_float4(r[0], r[1], r[2], r[3]);
+        const float4 old = reinterpret_cast<const float4 *>(y)[i];
+        v[k] = make_float4(sum.x + old.x, sum.y + old.y, sum.z + old.z, sum.w + old.w);
         reinterpret_cast<float4 *>(y)[i] = v[k];
         ss = fmaf(v[k].x, v[k].x, ss);
         ss = fmaf(v[k].y, v[k].y, ss);
