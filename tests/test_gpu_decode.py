@@ -58,6 +58,22 @@ def test_small_llama_decode(qk, torch_gpu, oracle, workloads):
     assert tg == tr
 
 
+@pytest.mark.parametrize("n_prefill", [1000, 1100])
+def test_small_llama_decode_long_context(qk, torch_gpu, oracle, workloads, n_prefill):
+    """Cache rows beyond the 1B benchmark's: at position ~1000 the attention
+    splits a head's rows eight ways and the o GEMV merges them (the most
+    partials it takes); past 1024 rows the step leaves the one-head-per-
+    workgroup form for KV-head workgroups whose splits the merge kernel
+    combines into o's records."""
+    cfg = dict(SMALL, context=1152)
+    prompt = np.array([3, 999, 17, 500], dtype=np.int32)
+    tg, tr, rep = run_decode(qk, oracle, workloads, cfg, seed=12, n_prefill=n_prefill, prompt=prompt, n_greedy=8)
+    for step, g, o, margin, err in rep:
+        print(f"step {step}: gpu {g} ref {o} top2 margin {margin:.4f} logits rel-L2 {err:.2e}")
+        assert err < 1e-4
+    assert tg == tr
+
+
 def test_llama_1b_decode_64_greedy_tokens(qk, torch_gpu, oracle, workloads):
     """The random-init Llama-3.2-1B decode workload: KV prefilled at 0..511,
     16 prompt ids at 512..527, 64 greedy tokens."""

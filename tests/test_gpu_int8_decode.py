@@ -141,6 +141,17 @@ def test_small_llama_int8_decode(qk, torch_gpu, oracle, workloads, synth, q4k, q
     _check(rows, 1e-5, 5e-2)
 
 
+@pytest.mark.parametrize("n_prefill", [1000, 1100])
+def test_small_llama_int8_decode_long_context(qk, torch_gpu, oracle, workloads, synth, n_prefill):
+    """Eight attention splits merged by the o GEMV's staging (position
+    ~1000), and past 1024 rows the KV-head split form whose merge kernel
+    quantizes o's input."""
+    prompt = np.array([3, 999, 17, 500], dtype=np.int32)
+    rows = run_int8_decode(qk, oracle, workloads, synth, dict(SMALL, context=1152), 12, n_prefill, prompt, 8, True,
+                           True)
+    _check(rows, 1e-5, 5e-2)
+
+
 def test_llama_1b_int8_decode_greedy_tokens(qk, torch_gpu, oracle, workloads, synth):
     """The random-init Llama-3.2-1B decode workload in the reference's
     default mode (both INT8 switches on): KV prefilled at 0..511, 16 prompt
