@@ -1113,12 +1113,19 @@ __global__ __launch_bounds__(256) void gemv_lds(GemvParams p) {
     // Copies of the first D - 1 tiles are in flight while the block prepares
     // the activations (indexes clamp to the last tile, so every wave issues
     // the same number of copies and its last prefetches re-read a valid tile).
+    // A staging policy's inputs load first (loads return in order: its
+    // staging then waits for them alone, not for the tile copies).
+    typename Policy::Early e;
+    if constexpr (Policy::kEarly) Policy::early(e, p, token, p.pieces * 64);
     #pragma unroll
     for (int k = 0; k < D - 1; ++k)
         copy_tile(M.w + static_cast<size_t>(min(first + k * stride, last)) * tile_bytes,
                   ring_lds + k * kLdsMaxTileBytes, chunks, lane);
     if (Policy::kPrepLds) {
-        Policy::prep(p, token, p.pieces * 64, xg);
+        if constexpr (Policy::kEarly)
+            Policy::prep_early(e, p, token, p.pieces * 64, xg);
+        else
+            Policy::prep(p, token, p.pieces * 64, xg);
         __syncthreads();
     }
     typename Policy::Lane L;
