@@ -64,16 +64,23 @@ def _weights(wl, synth, cfg, seed):
     return W
 
 
-@pytest.mark.parametrize("cfg", [SMALL, dict(SMALL, dim=2048, hidden=8192, heads=32, kv_heads=8)])
-def test_staged_quantization_matches_separate_launches(qk, torch_gpu, workloads, synth, cfg):
+WIDE = dict(SMALL, dim=2048, hidden=8192, heads=32, kv_heads=8)
+
+
+@pytest.mark.parametrize("cfg,n_prefill", [(SMALL, 20), (WIDE, 20), (dict(SMALL, context=512), 300),
+                                           (dict(WIDE, context=512), 380)])
+def test_staged_quantization_matches_separate_launches(qk, torch_gpu, workloads, synth, cfg, n_prefill):
     """Both types in INT8 mode: the step's four GEMVs quantize their own
     inputs (RMSNorm, plain, SiLU * up) instead of the separate quantization
     launches, which the step still runs while INT8 inputs are traced.  The
     codes are the same bit for bit at these widths (256-thread blocks sum the
     squares in the separate kernel's order), so 8 steps' logits and tokens
-    are identical between the two."""
+    are identical between the two.  From 128 rows on the attention splits
+    (3 and 4 splits here, a split holding only the new row among them): the
+    untraced step leaves the splits to the o GEMV's staging, the traced step
+    merges them in the merge kernel -- the same values."""
     W = _weights(workloads, synth, cfg, 17)
-    kc, vc = workloads.llama_kv_prefill(cfg, 17, 20)
+    kc, vc = workloads.llama_kv_prefill(cfg, 17, n_prefill)
     outs = []
     for traced in (False, True):
         gm = qk.Runner(cfg, W)
@@ -85,7 +92,7 @@ def test_staged_quantization_matches_separate_launches(qk, torch_gpu, workloads,
             gm.set_trace(tx, tq)
         tok, got = 5, []
         for i in range(8):
-            tok = gm.forward(tok, 20 + i, True)
+            tok = gm.forward(tok, n_prefill + i, True)
             got.append((tok, gm.logits()))
         gm.close()
         outs.append(got)
