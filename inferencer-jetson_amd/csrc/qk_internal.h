@@ -77,8 +77,11 @@ struct GemvFusion {
     int *arg_parts = nullptr;
 };
 constexpr int kArgPartsMax = 16384;
-// The argmax partials -> out[0] (the lowest row among maxima; 0 if none).
-int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream);
+// The argmax partials -> out[0] (the lowest row among maxima; 0 if none),
+// also stored to host_out[0] when given (device address of host-coherent
+// pinned memory).
+int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream,
+                        int32_t *host_out = nullptr);
 
 // dst[i][0..cols) = src[idx[i]][0..cols) (row stride ld) for i < n; idx is a
 // device array of n row indices.  cols and ld multiples of 4, src and dst

@@ -33,6 +33,12 @@ struct qk_llama {
     size_t attn_ws_bytes = 0;
     int32_t *d_next = nullptr, *d_token = nullptr;
     int32_t *h_token = nullptr;   // pinned staging for host tokens and the result
+    // The greedy token as the final pick writes it into host-coherent pinned
+    // memory (h_next; hd_next its device address): the host reads it once
+    // the stream is done, with no download launch.  next_mirrored: this
+    // step's pick wrote it.
+    int32_t *h_next = nullptr, *hd_next = nullptr;
+    bool next_mirrored = false;
     hipEvent_t upload_done = nullptr;   // the last token upload from h_token[0] has read it
     bool upload_pending = false;
     int last_next = -1;
@@ -91,6 +97,7 @@ void release(qk_llama *m) {
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_token) (void)hipHostFree(m->h_token);
+    if (m->h_next) (void)hipHostFree(m->h_next);
     if (m->upload_done) (void)hipEventDestroy(m->upload_done);
     for (void *b : m->owned) (void)hipFree(b);
     delete m;
@@ -339,7 +346,8 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
                    (st = qk::launch_gemv_i8_argmax(&head, m->xq, m->xscale, dim, arg_v, arg_i, &parts, s))) {
             return st;
         }
-        return qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s);
+        m->next_mirrored = true;
+        return qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s, m->hd_next);
     }
     if ((st = norm_quant(m->w.output_norm))) return st;
     if ((st = gemv_by_mode(m, &head, 1, m->xn, dim, s))) return st;
@@ -453,7 +461,8 @@ int forward_records(qk_llama *m, const int32_t *tok, int pos, bool need_logits, 
     const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
     const qk_matrix head{out_type, c.vocab, out_w, m->logits};
     if ((st = qk::launch_rec_gemv(&head, 1, dim, head_in, s))) return st;
-    return qk::launch_argmax_final(head_in.arg_v, head_in.arg_i, parts, m->d_next, s);
+    m->next_mirrored = true;
+    return qk::launch_argmax_final(head_in.arg_v, head_in.arg_i, parts, m->d_next, s, m->hd_next);
 }
 
 }  // namespace
@@ -547,6 +556,9 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
     }
     if (hipHostMalloc(reinterpret_cast<void **>(&m->h_token), 2 * sizeof(int32_t), hipHostMallocDefault) !=
             hipSuccess ||
+        hipHostMalloc(reinterpret_cast<void **>(&m->h_next), sizeof(int32_t),
+                      hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer(reinterpret_cast<void **>(&m->hd_next), m->h_next, 0) != hipSuccess ||
         hipEventCreateWithFlags(&m->upload_done, hipEventDisableTiming) != hipSuccess) {
         release(m);
         return qk::fail(QK_ERR_DEVICE, "qk_llama_create: cannot allocate pinned staging");
@@ -661,6 +673,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         tok = m->d_token;
     }
     m->last_next = -1;
+    m->next_mirrored = false;
     // Seven matrix products per layer (q, k, v, o, gate, up, down) and the
     // LM head, counted as the reference counts FastGPU::matvec and its fused
     // qkv / gate-up launches (inferencer.cu:1170, 1457, 1500).
@@ -738,13 +751,20 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
         const int out_type = m->w.output ? m->w.output_type : m->w.embd_type;
         const qk_matrix head{out_type, c.vocab, out_w, m->logits};
         if ((st = qk::launch_gemv_fused(&head, 1, m->x, dim, dim, 1, nullptr, out_in, s))) return st;
-        if ((st = qk::launch_argmax_final(out_in.arg_v, out_in.arg_i, parts, m->d_next, s))) return st;
+        m->next_mirrored = true;
+        if ((st = qk::launch_argmax_final(out_in.arg_v, out_in.arg_i, parts, m->d_next, s, m->hd_next))) return st;
     }
-    if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
-        hipStreamSynchronize(s) != hipSuccess)
-        return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");
+    if (m->next_mirrored) {
+        if (hipStreamSynchronize(s) != hipSuccess)
+            return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token wait failed");
+        m->last_next = *static_cast<volatile int32_t *>(m->h_next);
+    } else {
+        if (hipMemcpyAsync(m->h_token + 1, m->d_next, sizeof(int32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+            hipStreamSynchronize(s) != hipSuccess)
+            return qk::fail(QK_ERR_DEVICE, "qk_llama_forward: next token download failed");
+        m->last_next = m->h_token[1];
+    }
     m->upload_pending = false;   // the synchronisation retired every upload
-    m->last_next = m->h_token[1];
     if (next_token) *next_token = m->last_next;
     return qk::ok();
 }

@@ -715,11 +715,13 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
     }
 }
 
-// One block per row: the row's parts partials -> out[row].
-__global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int *pi, int parts, int32_t *out) {
+// One block per row: the row's parts partials -> out[row] (and host_out[row]
+// when given: host-coherent pinned memory, so the host reads the token once
+// the stream is done, with no copy launch).
+__global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int *pi, int parts, int32_t *out,
+                                                           int32_t *host_out) {
     pv += static_cast<int64_t>(blockIdx.x) * parts;
     pi += static_cast<int64_t>(blockIdx.x) * parts;
-    out += blockIdx.x;
     __shared__ float sv[4];
     __shared__ int si[4];
     float bv = -INFINITY;
@@ -752,7 +754,9 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w) arg_better(bv, bi, sv[w], si[w]);
         // All -inf (or NaN) input: fall back to index 0 like an empty tree.
-        *out = bi == 0x7FFFFFFF ? 0 : bi;
+        const int r = bi == 0x7FFFFFFF ? 0 : bi;
+        out[blockIdx.x] = r;
+        if (host_out) host_out[blockIdx.x] = r;
     }
 }
 
@@ -927,8 +931,9 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
 
 bool attention_supported(int group, int head_dim) { return split_instance(group, head_dim) != nullptr; }
 
-int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream) {
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out);
+int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream,
+                        int32_t *host_out) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out, host_out);
     return launch_status("argmax final launch");
 }
 
@@ -1147,7 +1152,7 @@ int qk_argmax_rows_f32(const float *v, int n, int64_t ldv, int rows, int32_t *ou
     float *pv = static_cast<float *>(workspace);
     int *pi = reinterpret_cast<int *>(pv + static_cast<size_t>(parts) * rows);
     hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts, rows), dim3(256), 0, qk::S(stream), v, n, ldv, pv, pi);
-    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(rows), dim3(256), 0, qk::S(stream), pv, pi, parts, out);
+    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(rows), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr);
     return qk::launch_status("qk_argmax_rows_f32 launch");
 }
 
@@ -1159,7 +1164,7 @@ int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_strea
     float *pv = static_cast<float *>(workspace);
     int *pi = reinterpret_cast<int *>(pv + parts);
     hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts), dim3(256), 0, qk::S(stream), v, n, int64_t(n), pv, pi);
-    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(1), dim3(256), 0, qk::S(stream), pv, pi, parts, out);
+    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(1), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr);
     return qk::launch_status("qk_argmax_f32 launch");
 }
 
