@@ -164,10 +164,22 @@ struct SkNorm {
     int *done = nullptr;
     int plan_only = 0;
 };
+// A storing launch (not a pair, not accumulating, no SkNorm) whose split
+// sums the consumer adds itself: the plan costs no reduction launch, and a
+// launch that splits writes no y and reports its partials' layout here
+// (splits 0: it wrote y itself).  Partial (row tile, token tile, split) is
+// 1024 floats at ((tile * token_tiles + ttile) * splits + split) * 1024, in
+// the accumulator's element order.
+struct SkDeferred {
+    const float *partials = nullptr;
+    int splits = 0, token_tiles = 0;
+    int tile_begin[QK_MAX_FUSED] = {};
+};
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
                      float *out_xs, int out_ldxq, int out_ldxs, void *workspace, size_t workspace_size,
-                     hipStream_t stream, const char *where, const SkNorm *norm = nullptr);
+                     hipStream_t stream, const char *where, const SkNorm *norm = nullptr,
+                     SkDeferred *defer = nullptr);
 // SiLU(gate) * up quantized per 32 values straight into xq / xscale (n a
 // multiple of 32): bit-identical to qk_silu_mul_f32 then qk_quantize_x32,
 // without the fp32 product written.  Arguments already validated.
@@ -449,6 +461,12 @@ struct SplitAttention {
     int wide_split_rows;
     // Leave split partials unmerged (no merge launch): the caller merges.
     int defer_merge;
+    // q, k and v as the INT8 QKV product's unreduced split sums (SkDeferred)
+    // when qkv_splits > 1, read with k set: element (token b, column c) of
+    // matrix m is the sum in split order of the partials of row tile
+    // tile0[m] + c / 32, token tile b / 32 (skinny_reduce's additions).
+    const float *qkv_parts;
+    int qkv_splits, qkv_ttiles, qkv_tile0[3];
     int layer, pos, max_pos, n_tokens, heads, kv_heads, head_dim;
     // Cache layout: 0 the reference's [layers][cache_rows][kv_heads][head_dim],
     // 1 [layers][kv_heads][cache_rows][head_dim] (the decode drivers' own: a

@@ -901,9 +901,24 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
     for (int l = 0; l < c.layers; ++l) {
         const qk_llama_layer &L = m->layers[l];
         const qk_matrix qkv[3] = {{L.q_type, dim, L.q, m->q}, {L.k_type, kv, L.k, m->k}, {L.v_type, kv, L.v, m->v}};
-        if ((!normed && (st = norm_quant(L.attn_norm))) || (st = trace_q(l, 0, m->xq, dim)) ||
-            (st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s)))
+        // A decode batch's attention reads q, k and v once, so it adds the
+        // QKV product's split sums itself (no reduction launch; the product
+        // then splits its rows over twice the workgroups).
+        qk::SkDeferred qd;
+        if ((!normed && (st = norm_quant(L.attn_norm))) || (st = trace_q(l, 0, m->xq, dim)))
             return st;
+        if (T >= 8 && !chained) {
+            const int ldy[3] = {dim, kv, kv};
+            if ((st = qk::launch_skinny_i8(qkv, 3, ldy, m->xq, dim, m->xs, dim / 32, dim, T, 0, nullptr, nullptr, 0, 0,
+                                           m->i8_ws, m->i8_ws_bytes, s, "qk_llama_batch_forward", nullptr, &qd)))
+                return st;
+        } else if ((st = batch_gemm_i8(m, qkv, 3, m->xq, m->xs, dim, T, false, s))) {
+            return st;
+        }
+        attn.qkv_parts = qd.partials;
+        attn.qkv_splits = qd.splits;
+        attn.qkv_ttiles = qd.token_tiles;
+        for (int i = 0; i < 3; ++i) attn.qkv_tile0[i] = qd.tile_begin[i];
         if (chained &&
             (st = qk::launch_rope_kv_batched(m->q, m->k, m->v, m->cosine, m->sine, m->key_cache, m->value_cache, l,
                                              m->cache_rows, m->d_desc, T, c.context, c.heads, c.kv_heads, hd, 1, s)))
@@ -918,6 +933,8 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
         if ((st = qk::launch_split_attention(attn, 0, m->attn_ws, m->attn_ws_bytes, s))) return st;
         attn.q8_out = nullptr;
         attn.q8_scale = nullptr;
+        attn.qkv_parts = nullptr;
+        attn.qkv_splits = 0;
         const qk_matrix o{L.o_type, dim, L.o, m->x};
         // (Folding the FFN's RMSNorm into o the same way makes o split its
         // sums, which it otherwise does not: no faster, 1.650 -> 1.653-1.658

@@ -791,7 +791,7 @@ const void *rows_kernel(int type) {
 // share of the row tiles.
 // fold: the caller folds its next RMSNorm into a split reduction, so a plan
 // without splits pays for that separate launch too.
-SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt, bool fold) {
+SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt, bool fold, bool deferred) {
     const int s0 = fewest_splits(nb, waves_max(type, rt));
     const int cus = std::max(1, device_info().cus);
     const void *kernel = skinny_kernel(type, rt, false);
@@ -807,7 +807,7 @@ SkPlan split_plan(int nb, int64_t units, int64_t ttiles, int type, int rt, bool 
         const int64_t rounds = (wgs + static_cast<int64_t>(cus) * per_cu - 1) / (static_cast<int64_t>(cus) * per_cu);
         const int load = static_cast<int>(std::min<int64_t>(per_cu, (wgs + cus - 1) / cus));   // busiest CU
         const float cost = static_cast<float>(rounds) * (kRoundUs + kWaveUs * rt * ((load * w + 3) / 4)) +
-                           (s > 1 || fold ? kReduceUs : 0.f);
+                           ((s > 1 && !deferred) || fold ? kReduceUs : 0.f);
         if (s == s0 || cost < best - 1e-3f) {
             best = cost;
             best_rounds = rounds;
@@ -866,9 +866,10 @@ size_t skinny_i8_workspace_bytes(int cols, int tiles, int n_tokens, bool pair) {
 int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const int8_t *xq, int ldxq,
                      const float *xscale, int ldscale, int cols, int n_tokens, int accumulate, int8_t *out_xq,
                      float *out_xs, int out_ldxq, int out_ldxs, void *workspace, size_t workspace_size,
-                     hipStream_t stream, const char *where, const SkNorm *norm) {
+                     hipStream_t stream, const char *where, const SkNorm *norm, SkDeferred *defer) {
     const int nb = cols / 256;
     if (norm && norm->done) *norm->done = 0;
+    if (defer) defer->splits = 0;
     SkParams p{};
     p.n_mats = n_mats;
     p.xq = xq;
@@ -910,7 +911,9 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
                       mats[0].rows <= 4 * 256 * kNormHeld && (ldy ? ldy[0] : mats[0].rows) % 4 == 0 &&
                       aligned(mats[0].y, 16) && norm->w && norm->xq && norm->xs && norm->ldxq % 4 == 0 &&
                       aligned(norm->xq, 4) && aligned(norm->w, 16);
-    const SkPlan plan = split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, token_tiles, type, rt, fold);
+    const bool deferrable = defer && !pair && !accumulate && !norm && n_mats <= QK_MAX_FUSED;
+    const SkPlan plan =
+        split_plan(nb, static_cast<int64_t>(tiles) * token_tiles, token_tiles, type, rt, fold, deferrable);
     p.splits = plan.splits;
     p.waves = plan.waves;
     p.tiles = tiles;
@@ -932,7 +935,13 @@ int launch_skinny_i8(const qk_matrix *mats, int n_mats, const int *ldy, const in
                         dim3(static_cast<unsigned>(groups * p.splits), static_cast<unsigned>(token_tiles)),
                         dim3(64 * p.waves), args, lds, stream) != hipSuccess)
         return launch_status(where);
-    if (p.splits > 1 && fold && !norm->plan_only) {
+    if (p.splits > 1 && deferrable && !plan.rows && !plan.loop_groups) {
+        // The consumer adds the split sums (skinny_reduce's order).
+        defer->partials = p.partials;
+        defer->splits = p.splits;
+        defer->token_tiles = token_tiles;
+        for (int i = 0; i < n_mats; ++i) defer->tile_begin[i] = p.mat[i].tile_begin;
+    } else if (p.splits > 1 && fold && !norm->plan_only) {
         hipLaunchKernelGGL(skinny_reduce_norm, dim3(static_cast<unsigned>(n_tokens)), dim3(256), 0, stream, p,
                            token_tiles, *norm);
         if (norm->done) *norm->done = 1;

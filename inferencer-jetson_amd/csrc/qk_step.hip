@@ -338,6 +338,22 @@ __device__ __forceinline__ void write_gemm_records(const SplitAttention &a, int 
     }
 }
 
+// Element (token b, column c) of matrix m (q 0, k 1, v 2) of the QKV
+// product: from its buffer (row stride ld), or, with the product's split
+// sums left unreduced, their sum in split order -- skinny_reduce's
+// additions over the partial of row tile qkv_tile0[m] + c / 32 and token
+// tile b / 32, at the accumulator's element for (token b % 32, row c % 32).
+__device__ __forceinline__ float qkv_elem(const SplitAttention &a, const float *buf, int64_t ld, int m, int b, int c) {
+    if (a.qkv_splits <= 1) return buf[b * ld + c];
+    const int tl = b & 31;
+    const int e = (4 * (tl >> 3) + (tl & 3)) * 64 + 32 * ((tl >> 2) & 1) + (c & 31);
+    const float *src =
+        a.qkv_parts + (static_cast<int64_t>(a.qkv_tile0[m] + (c >> 5)) * a.qkv_ttiles + (b >> 5)) * a.qkv_splits * 1024 + e;
+    float sum = src[0];
+    for (int sp = 1; sp < a.qkv_splits; ++sp) sum += src[static_cast<int64_t>(sp) * 1024];
+    return sum;
+}
+
 // Merge of two (max, sum) states: the scale factors of each side.
 __device__ __forceinline__ void merge_scales(float &m, float &l, float mo, float lo, float &f, float &fo) {
     const float mn = fmaxf(m, mo);
@@ -467,23 +483,24 @@ __global__ __launch_bounds__(NW * 64) void split_attention_kernel(SplitAttnKerne
     if (a.k) {
         const float *cs = a.cosine + static_cast<int64_t>(d.pos) * half;
         const float *sn = a.sine + static_cast<int64_t>(d.pos) * half;
+        const int64_t q_ld = static_cast<int64_t>(a.heads) * hd;
         for (int i = tid; i < G * half; i += kSplitThreads) {
             const int g = i / half, f = i - g * half;
             const float c = cs[f], si = sn[f];
-            const float q0 = qt[g * hd + 2 * f], q1 = qt[g * hd + 2 * f + 1];
+            const int qc = (kvh * G + g) * hd + 2 * f;
+            const float q0 = qkv_elem(a, a.q, q_ld, 0, b, qc), q1 = qkv_elem(a, a.q, q_ld, 0, b, qc + 1);
             qsf[g * HD + 2 * f] = q0 * c - q1 * si;
             qsf[g * HD + 2 * f + 1] = q0 * si + q1 * c;
         }
         if (fresh) {
-            const float *kt = a.k + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
-            const float *vt = a.v + static_cast<int64_t>(b) * kv_dim + cache_kvh * hd;
             float *kn = reinterpret_cast<float *>(knew), *vn = reinterpret_cast<float *>(vnew);
             const int64_t row = head0 + static_cast<int64_t>(d.pos) * rs;
             for (int f = tid; f < half; f += kSplitThreads) {
                 const float c = cs[f], si = sn[f];
-                const float k0 = kt[2 * f], k1 = kt[2 * f + 1];
+                const int kc = cache_kvh * hd + 2 * f;
+                const float k0 = qkv_elem(a, a.k, kv_dim, 1, b, kc), k1 = qkv_elem(a, a.k, kv_dim, 1, b, kc + 1);
                 const float kr0 = k0 * c - k1 * si, kr1 = k0 * si + k1 * c;
-                const float v0 = vt[2 * f], v1 = vt[2 * f + 1];
+                const float v0 = qkv_elem(a, a.v, kv_dim, 2, b, kc), v1 = qkv_elem(a, a.v, kv_dim, 2, b, kc + 1);
                 kn[2 * f] = kr0;
                 kn[2 * f + 1] = kr1;
                 vn[2 * f] = v0;
@@ -865,6 +882,8 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
     if (a.rec_out && a.head_dim % 16) return fail(QK_ERR_LIMIT, "split attention: records need head_dim % 16 == 0");
     if (a.q8_out && (a.head_dim % 32 || !a.q8_scale))
         return fail(QK_ERR_LIMIT, "split attention: quantized outputs need head_dim % 32 == 0 and scales");
+    if (a.qkv_splits > 1 && (!a.qkv_parts || !a.k || !a.v || a.qkv_ttiles < (a.n_tokens + 31) / 32))
+        return fail(QK_ERR_INVALID_ARG, "split attention: split QKV sums need k, v and their partials");
     const int max_rows = a.max_pos + 1;
     // Few (token, KV head) pairs over short rows: one wide workgroup each
     // reads all of its rows, and no merge kernel runs.  A CU alone streams
