@@ -94,12 +94,37 @@ __global__ __launch_bounds__(64) void q6k_split_kernel(const uint8_t *src, uint8
     }
 }
 
+// The inverse: split rows back into 210-byte GGUF blocks (one workgroup per
+// block, grid-stride).
+__global__ __launch_bounds__(64) void q6k_join_kernel(const uint8_t *src, uint8_t *dst, int nb, int64_t src_row_bytes,
+                                                      int64_t nblocks) {
+    for (int64_t blk = blockIdx.x; blk < nblocks; blk += gridDim.x) {
+        const int64_t r = blk / nb;
+        const int b = static_cast<int>(blk - r * nb);
+        const Q6Fields f = q6_fields(src + r * src_row_bytes, nb, b, true);
+        uint8_t *d = dst + blk * 210;
+        for (int u = threadIdx.x; u < 105; u += 64) {
+            const uint8_t *i = u < 64 ? f.ql + 2 * u : u < 96 ? f.qh + 2 * (u - 64) : u < 104 ? f.sc + 2 * (u - 96) : f.d;
+            const uint16_t v = static_cast<uint16_t>(load2(i));
+            __builtin_memcpy(d + 2 * u, &v, 2);
+        }
+    }
+}
+
 int grid_for(int64_t blocks) {
     int64_t cap = static_cast<int64_t>(device_info().cus) * 16;
     return static_cast<int>(blocks < cap ? (blocks > 0 ? blocks : 1) : cap);
 }
 
 }  // namespace
+
+int launch_q6k_join(const void *src, void *dst, int cols, int rows, hipStream_t stream) {
+    const int nb = cols / 256;
+    const int64_t nblocks = static_cast<int64_t>(rows) * nb;
+    hipLaunchKernelGGL(q6k_join_kernel, dim3(grid_for(nblocks)), dim3(64), 0, stream, static_cast<const uint8_t *>(src),
+                       static_cast<uint8_t *>(dst), nb, row_bytes(QK_TYPE_Q6_K_SPLIT, nb), nblocks);
+    return launch_status("Q6_K join launch");
+}
 
 int launch_embedding_records(int type, const void *w, const int32_t *token, int cols, int vocab, float *out,
                              const float *gain, XGroup *rec, float *ss, hipStream_t stream) {

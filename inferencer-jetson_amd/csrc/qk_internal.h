@@ -686,5 +686,9 @@ int launch_rec_gemv(const qk_matrix *mats, int n_mats, int cols, const RecGemv &
 // (inferencer.cu:806-819) plus the first QKV's activation records.
 int launch_embedding_records(int type, const void *w, const int32_t *token, int cols, int vocab, float *out,
                              const float *gain, XGroup *rec, float *ss, hipStream_t stream);
+// A split-layout Q6_K matrix (cols x rows) written back as GGUF blocks at
+// dst (rows * cols / 256 * 210 bytes, not overlapping src); arguments
+// already validated.
+int launch_q6k_join(const void *src, void *dst, int cols, int rows, hipStream_t stream);
 
 }  // namespace qk

@@ -806,6 +806,14 @@ struct qk_llama_batch {
     float *xs = nullptr, *hs = nullptr;
     void *i8_ws = nullptr;
     size_t i8_ws_bytes = 0;
+    // The LM head in GGUF blocks (a Q6_K head only; made from the split
+    // copy at the first enable): the multi-token INT8 product walks row tiles
+    // block by block, and in the split layout each block of a 32-row tile
+    // touches parts of ~6 cache lines per row -- about 6 MB of lines per
+    // step on an XCD, more than its 4 MB L2, so each line was fetched twice
+    // (FETCH 2.0x the matrix, 84.5 us at 32 tokens); in 210-byte blocks it is
+    // 1.11x and 77.9 us.
+    uint8_t *head_q6k = nullptr;
     // qk_llama_batch_set_trace: per token the residual after each layer
     // [token][layer][dim] and the INT8 inputs of each layer's products
     // [token][layer][4][max(dim, hidden)].
@@ -818,7 +826,8 @@ namespace {
 void release_batch(qk_llama_batch *m) {
     void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->gemm_ws, m->argmax_ws, m->attn_ws, m->d_tokens, m->d_next,
-                    m->d_rows, m->d_desc, m->rec_a, m->rec_b, m->ss, m->xq, m->hq, m->xs, m->hs, m->i8_ws};
+                    m->d_rows, m->d_desc, m->rec_a, m->rec_b, m->ss, m->xq, m->hq, m->xs, m->hs, m->i8_ws,
+                    m->head_q6k};
     for (void *b : bufs)
         if (b) (void)hipFree(b);
     if (m->h_stage) (void)hipHostFree(m->h_stage);
@@ -994,25 +1003,32 @@ int qk_llama_batch_set_int8(qk_llama_batch *m, int q4k_int8, int q6k_int8) {
         ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.dim, tiles(c.hidden), m->max_tokens, true));
         ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.hidden, tiles(c.dim), m->max_tokens, false));
         ws = std::max(ws, qk::skinny_i8_workspace_bytes(c.dim, tiles(c.vocab), m->max_tokens, false));
-        const uint64_t need = T * (c.dim + c.hidden) * (1 + sizeof(float) / 32.0) + ws + 1024;
+        const void *head = m->w.output ? m->w.output : m->w.token_embd;
+        const bool head_split = (m->w.output ? m->w.output_type : m->w.embd_type) == QK_TYPE_Q6_K_SPLIT;
+        const uint64_t head_bytes = head_split ? static_cast<uint64_t>(c.vocab) * (c.dim / 256) * 210 : 0;
+        const uint64_t need = T * (c.dim + c.hidden) * (1 + sizeof(float) / 32.0) + ws + head_bytes + 1024;
         int st;
         if ((st = check_free_memory("qk_llama_batch_set_int8", need))) return st;
-        uint64_t bytes = 0;
+        uint64_t bytes = 0, copies = 0;
         if ((st = dev_alloc(bytes, &m->xq, T * c.dim, "quantized activations")) ||
             (st = dev_alloc(bytes, &m->xs, T * (c.dim / 32), "activation scales")) ||
             (st = dev_alloc(bytes, &m->hq, T * c.hidden, "quantized hidden activations")) ||
             (st = dev_alloc(bytes, &m->hs, T * (c.hidden / 32), "hidden activation scales")) ||
-            (ws && (st = dev_alloc(bytes, reinterpret_cast<uint8_t **>(&m->i8_ws), ws, "split sums")))) {
+            (ws && (st = dev_alloc(bytes, reinterpret_cast<uint8_t **>(&m->i8_ws), ws, "split sums"))) ||
+            (head_bytes && (st = dev_alloc(copies, &m->head_q6k, head_bytes, "LM head in GGUF blocks"))) ||
+            (head_bytes && (st = qk::launch_q6k_join(head, m->head_q6k, c.dim, c.vocab, m->stream)))) {
             for (void *b : {static_cast<void *>(m->xq), static_cast<void *>(m->xs), static_cast<void *>(m->hq),
-                            static_cast<void *>(m->hs), m->i8_ws})
+                            static_cast<void *>(m->hs), m->i8_ws, static_cast<void *>(m->head_q6k)})
                 (void)hipFree(b);
             m->xq = m->hq = nullptr;
             m->xs = m->hs = nullptr;
             m->i8_ws = nullptr;
+            m->head_q6k = nullptr;
             return st;
         }
         m->i8_ws_bytes = ws;
         m->mem.buffers += bytes;
+        m->mem.weight_copies += copies;
     }
     m->int8 = q4k_int8 != 0;
     return qk::ok();
@@ -1355,9 +1371,11 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     if (m->int8) {
         // rmsnorm_cuda, then gpu.matvec's quantization and INT8 product
         // (inferencer.cu:1408-1414) for the selected rows.
+        // Over the GGUF-block copy of a Q6_K head (head_q6k).
+        const qk_matrix head_i8 = m->head_q6k ? qk_matrix{QK_TYPE_Q6_K, c.vocab, m->head_q6k, m->logits} : head;
         if ((st = qk_rmsnorm_quantize_x32(head_x, dim, m->w.output_norm, nullptr, 0, m->xq, dim, m->xs, dim / 32, dim,
                                           n_rows, c.eps, s)) ||
-            (st = batch_gemm_i8(m, &head, 1, m->xq, m->xs, dim, n_rows, false, s)))
+            (st = batch_gemm_i8(m, &head_i8, 1, m->xq, m->xs, dim, n_rows, false, s)))
             return st;
     } else if ((st = qk::launch_batched_fused(&head, 1, head_x, dim, dim, n_rows, out_in, ws, wsb, s))) {
         return st;
