@@ -890,7 +890,8 @@ int batch_gemm_i8(qk_llama_batch *m, const qk_matrix *mats, int n, const int8_t 
 // add_batch_cuda), RMSNorm and quantization, gate / up with SiLU(gate) * up
 // quantized (gate_up_batch_cuda, silu_batch_cuda, and down's quantization),
 // down added into x.
-int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention &attn, hipStream_t s) {
+int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention &attn, hipStream_t s,
+                      const float *head_norm, bool *head_normed) {
     const qk_llama_config &c = m->cfg;
     const int dim = c.dim, hidden = c.hidden, kv = m->kv_dim, hd = m->head_dim;
     int st;
@@ -970,7 +971,10 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
         next.ldxq = dim;
         next.ldxs = dim / 32;
         next.done = &normed;
-        next.w = l + 1 < c.layers ? m->layers[l + 1].attn_norm : nullptr;
+        // The last layer's reduction normalises and quantizes the LM head's
+        // input (head_norm: the output norm when the head reads every token
+        // in order).
+        next.w = l + 1 < c.layers ? m->layers[l + 1].attn_norm : head_norm;
         next.plan_only = m->trace_q != nullptr;   // the same split sums, the separate norm
         normed = 0;
         if ((st = trace_q(l, 3, m->hq, hidden)) ||
@@ -981,6 +985,7 @@ int batch_layers_int8(qk_llama_batch *m, int T, bool chained, qk::SplitAttention
             (st = batch_trace_x(m, l, T, s)))
             return st;
     }
+    *head_normed = head_norm && normed;
     return QK_OK;
 }
 
@@ -1296,7 +1301,10 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
     // layer (one more with split attention) instead of thirteen.
     const bool chain = qk::batched_chain_supported(T) && m->rec_a;
     const bool attn_records = chain && qk::attention_gemm_records(attn);
-    if (m->int8 && (st = batch_layers_int8(m, T, chained, attn, s))) return st;
+    bool head_normed = false;
+    if (m->int8 && (st = batch_layers_int8(m, T, chained, attn, s, n_rows && identity ? m->w.output_norm : nullptr,
+                                           &head_normed)))
+        return st;
     for (int l = 0; l < c.layers && !m->int8; ++l) {
         const qk_llama_layer &L = m->layers[l];
         attn_in.norm_w = L.attn_norm;
@@ -1373,8 +1381,8 @@ int qk_llama_batch_forward_rows(qk_llama_batch *m, const int32_t *tokens, const 
         // (inferencer.cu:1408-1414) for the selected rows.
         // Over the GGUF-block copy of a Q6_K head (head_q6k).
         const qk_matrix head_i8 = m->head_q6k ? qk_matrix{QK_TYPE_Q6_K, c.vocab, m->head_q6k, m->logits} : head;
-        if ((st = qk_rmsnorm_quantize_x32(head_x, dim, m->w.output_norm, nullptr, 0, m->xq, dim, m->xs, dim / 32, dim,
-                                          n_rows, c.eps, s)) ||
+        if ((!head_normed && (st = qk_rmsnorm_quantize_x32(head_x, dim, m->w.output_norm, nullptr, 0, m->xq, dim, m->xs,
+                                                           dim / 32, dim, n_rows, c.eps, s))) ||
             (st = batch_gemm_i8(m, &head_i8, 1, m->xq, m->xs, dim, n_rows, false, s)))
             return st;
     } else if ((st = qk::launch_batched_fused(&head, 1, head_x, dim, dim, n_rows, out_in, ws, wsb, s))) {
