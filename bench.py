@@ -395,15 +395,16 @@ def bench_decode_1b(torch, qk, wl, int8: bool = False) -> dict:
     return {"tokens": w.greedy_tokens, "ms_per_token": round(per_tok * 1e3, 4),
             "tokens_per_s": round(1.0 / per_tok, 1), "weight_bytes_per_token": weights,
             "GBps": round(gbps, 1), "frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
-            # FP32 (activation records), per layer: QKV, attention (one
-            # workgroup per query head at these positions, no merge), o,
-            # gate/up, down; then the embedding, the LM head and the greedy
-            # pick.  INT8, per layer: QKV (RMSNorm + quantize staged),
-            # attention (rows split), o (merging the splits, +add), gate/up
-            # (RMSNorm + quantize staged, SiLU*up quantized in the epilogue),
-            # down (+add); then embedding, the LM head (RMSNorm + quantize
-            # staged, greedy partials) and the final pick.
-            "kernels_per_token": 5 * cfg["layers"] + 3,
+            # FP32 (activation records), per layer: QKV, attention (rows
+            # split), o (merging the splits, +add), gate/up, down; then the
+            # embedding, the LM head and the greedy pick.  INT8, per layer:
+            # QKV (RMSNorm + quantize staged), attention (rows split), o
+            # (merging the splits, +add), gate/up (RMSNorm + quantize staged,
+            # SiLU*up quantized in the epilogue), down (+add); then the LM
+            # head (RMSNorm + quantize staged, greedy partials) and the final
+            # pick, which also writes the next token's embedding row (no
+            # embedding launch in a greedy step).
+            "kernels_per_token": 5 * cfg["layers"] + (2 if int8 else 3),
             "device_bytes": mem}
 
 

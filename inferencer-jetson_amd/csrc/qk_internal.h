@@ -77,11 +77,19 @@ struct GemvFusion {
     int *arg_parts = nullptr;
 };
 constexpr int kArgPartsMax = 16384;
+// The picked token's embedding row, written by the final pick for the next
+// step (out NULL: none): table rows of row_bytes, nb blocks of type.
+struct NextEmbedding {
+    const uint8_t *table = nullptr;
+    int type = 0, nb = 0;
+    int64_t row_bytes = 0;
+    float *out = nullptr;
+};
 // The argmax partials -> out[0] (the lowest row among maxima; 0 if none),
 // also stored to host_out[0] when given (device address of host-coherent
-// pinned memory).
+// pinned memory); with next, the token's embedding row into next->out.
 int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream,
-                        int32_t *host_out = nullptr);
+                        int32_t *host_out = nullptr, const NextEmbedding *next = nullptr);
 
 // dst[i][0..cols) = src[idx[i]][0..cols) (row stride ld) for i < n; idx is a
 // device array of n row indices.  cols and ld multiples of 4, src and dst

@@ -39,6 +39,12 @@ struct qk_llama {
     // step's pick wrote it.
     int32_t *h_next = nullptr, *hd_next = nullptr;
     bool next_mirrored = false;
+    // INT8 steps: the final pick also writes the picked token's embedding
+    // row into x_next; the next step, fed that token, swaps x_next in as x
+    // instead of launching the embedding (x keeps the residual stream until
+    // then, as qk_llama_residual reports it).
+    float *x_next = nullptr;
+    bool x_next_valid = false;
     hipEvent_t upload_done = nullptr;   // the last token upload from h_token[0] has read it
     bool upload_pending = false;
     int last_next = -1;
@@ -91,7 +97,7 @@ int dev_alloc(uint64_t &total, T **p, size_t count, const char *what) {
 }
 
 void release(qk_llama *m) {
-    void *bufs[] = {m->x, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
+    void *bufs[] = {m->x, m->x_next, m->xn, m->q, m->k, m->v, m->attn, m->tmp, m->gate, m->up, m->logits, m->key_cache,
                     m->value_cache, m->cosine, m->sine, m->argmax_ws, m->attn_ws, m->d_next, m->d_token,
                     m->xq, m->xscale, m->rec_norm, m->rec_attn, m->rec_ffn, m->rec_silu, m->ss_norm, m->ss_ffn};
     for (void *b : bufs)
@@ -228,7 +234,7 @@ int decode_split_rows(int rows) { return std::max(128, ((rows + 7) / 8 + 15) / 1
 // INT8 mode and no input traces, the QKV and gate/up GEMVs quantize their
 // own inputs instead (launch_gemv_i8_staged) and the attention quantizes
 // o's: the same codes, three launches per layer fewer.
-int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hipStream_t s) {
+int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, bool embedded, hipStream_t s) {
     const qk_llama_config &c = m->cfg;
     const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
     int st;
@@ -242,7 +248,10 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
     // the staged step's.
     const bool merge_o = m->int8_q4k && m->int8_q6k && q8 && qk::gemv_i8_stageable(dim) &&
                          qk::gemv_i8_mergeable(dim, hd, 8);
-    if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s))) return st;
+    if (embedded)
+        std::swap(m->x, m->x_next);   // the previous pick wrote this token's row
+    else if ((st = qk_embedding(m->w.embd_type, m->w.token_embd, tok, 1, m->x, dim, c.vocab, s)))
+        return st;
     qk::SplitAttention attn{};
     attn.wide_split_rows = merge_o ? decode_split_rows(pos + 1) : 0;
     attn.q = m->q;
@@ -347,7 +356,15 @@ int forward_int8(qk_llama *m, const int32_t *tok, int pos, bool need_logits, hip
             return st;
         }
         m->next_mirrored = true;
-        return qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s, m->hd_next);
+        qk::NextEmbedding ne;
+        ne.table = static_cast<const uint8_t *>(m->w.token_embd);
+        ne.type = m->w.embd_type;
+        ne.nb = dim / 256;
+        ne.row_bytes = qk::row_bytes(m->w.embd_type, dim / 256);
+        ne.out = m->x_next;
+        if ((st = qk::launch_argmax_final(arg_v, arg_i, parts, m->d_next, s, m->hd_next, &ne))) return st;
+        m->x_next_valid = true;
+        return QK_OK;
     }
     if ((st = norm_quant(m->w.output_norm))) return st;
     if ((st = gemv_by_mode(m, &head, 1, m->xn, dim, s))) return st;
@@ -530,7 +547,9 @@ int qk_llama_create(const qk_llama_config *cfg, const qk_llama_weights *w, qk_st
         delete m;
         return st;
     }
-    if ((st = dev_alloc(m->mem.buffers, &m->x, c.dim, "residual")) || (st = dev_alloc(m->mem.buffers, &m->xn, c.dim, "normalized state")) ||
+    if ((st = dev_alloc(m->mem.buffers, &m->x, c.dim, "residual")) ||
+        (st = dev_alloc(m->mem.buffers, &m->x_next, c.dim, "next embedding")) ||
+        (st = dev_alloc(m->mem.buffers, &m->xn, c.dim, "normalized state")) ||
         (st = dev_alloc(m->mem.buffers, &m->q, c.dim, "query")) || (st = dev_alloc(m->mem.buffers, &m->k, m->kv_dim, "key")) ||
         (st = dev_alloc(m->mem.buffers, &m->v, m->kv_dim, "value")) || (st = dev_alloc(m->mem.buffers, &m->attn, c.dim, "attention")) ||
         (st = dev_alloc(m->mem.buffers, &m->tmp, c.dim, "residual update")) || (st = dev_alloc(m->mem.buffers, &m->gate, c.hidden, "gate")) ||
@@ -660,6 +679,8 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     const int dim = c.dim, kv = m->kv_dim, hd = m->head_dim;
     int st;
     const int32_t *tok = m->d_next;
+    const bool embedded = token == m->last_next && m->x_next_valid;
+    m->x_next_valid = false;
     if (token != m->last_next) {
         // A step without logits returns before its work runs: the pinned slot
         // is rewritten only once the previous upload has read it.
@@ -679,7 +700,7 @@ int qk_llama_forward(qk_llama *m, int token, int pos, int need_logits, int *next
     // qkv / gate-up launches (inferencer.cu:1170, 1457, 1500).
     m->matrix_calls += 7ull * c.layers + (need_logits ? 1 : 0);
     if (m->int8_q4k || m->int8_q6k) {
-        if ((st = forward_int8(m, tok, pos, need_logits != 0, s))) return st;
+        if ((st = forward_int8(m, tok, pos, need_logits != 0, embedded, s))) return st;
         if (!need_logits) {
             if (next_token) *next_token = -1;
             return qk::ok();

@@ -734,9 +734,12 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *v, int
 
 // One block per row: the row's parts partials -> out[row] (and host_out[row]
 // when given: host-coherent pinned memory, so the host reads the token once
-// the stream is done, with no copy launch).
+// the stream is done, with no copy launch).  With e.out (one row), the
+// block then writes the picked token's embedding row there (embedding_kernel's
+// decode, the next step's input).
 __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, const int *pi, int parts, int32_t *out,
-                                                           int32_t *host_out) {
+                                                           int32_t *host_out, NextEmbedding e) {
+    __shared__ int picked;
     pv += static_cast<int64_t>(blockIdx.x) * parts;
     pi += static_cast<int64_t>(blockIdx.x) * parts;
     __shared__ float sv[4];
@@ -774,6 +777,16 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
         const int r = bi == 0x7FFFFFFF ? 0 : bi;
         out[blockIdx.x] = r;
         if (host_out) host_out[blockIdx.x] = r;
+        picked = r;
+    }
+    if (e.out) {
+        __syncthreads();
+        const uint8_t *row = e.table + static_cast<int64_t>(picked) * e.row_bytes;
+        for (int b = 0; b < e.nb; ++b)
+            e.out[b * 256 + threadIdx.x] = e.type == QK_TYPE_Q4_K
+                                               ? q4k_value(row + b * 144, threadIdx.x)
+                                               : q6k_value(q6_fields(row, e.nb, b, e.type == QK_TYPE_Q6_K_SPLIT),
+                                                           threadIdx.x);
     }
 }
 
@@ -951,8 +964,9 @@ int launch_split_attention(const SplitAttention &a, int split_rows, void *worksp
 bool attention_supported(int group, int head_dim) { return split_instance(group, head_dim) != nullptr; }
 
 int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream,
-                        int32_t *host_out) {
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out, host_out);
+                        int32_t *host_out, const NextEmbedding *next) {
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out, host_out,
+                       next ? *next : NextEmbedding{});
     return launch_status("argmax final launch");
 }
 
@@ -1171,7 +1185,8 @@ int qk_argmax_rows_f32(const float *v, int n, int64_t ldv, int rows, int32_t *ou
     float *pv = static_cast<float *>(workspace);
     int *pi = reinterpret_cast<int *>(pv + static_cast<size_t>(parts) * rows);
     hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts, rows), dim3(256), 0, qk::S(stream), v, n, ldv, pv, pi);
-    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(rows), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr);
+    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(rows), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr,
+                       qk::NextEmbedding{});
     return qk::launch_status("qk_argmax_rows_f32 launch");
 }
 
@@ -1183,7 +1198,8 @@ int qk_argmax_f32(const float *v, int n, int32_t *out, void *workspace, qk_strea
     float *pv = static_cast<float *>(workspace);
     int *pi = reinterpret_cast<int *>(pv + parts);
     hipLaunchKernelGGL(qk::argmax_partial_kernel, dim3(parts), dim3(256), 0, qk::S(stream), v, n, int64_t(n), pv, pi);
-    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(1), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr);
+    hipLaunchKernelGGL(qk::argmax_final_kernel, dim3(1), dim3(256), 0, qk::S(stream), pv, pi, parts, out, nullptr,
+                       qk::NextEmbedding{});
     return qk::launch_status("qk_argmax_f32 launch");
 }
 
