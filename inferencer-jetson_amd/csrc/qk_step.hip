@@ -775,18 +775,19 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const float *pv, cons
         for (int w = 1; w < 4; ++w) arg_better(bv, bi, sv[w], si[w]);
         // All -inf (or NaN) input: fall back to index 0 like an empty tree.
         const int r = bi == 0x7FFFFFFF ? 0 : bi;
-        out[blockIdx.x] = r;
-        if (host_out) host_out[blockIdx.x] = r;
+        if (blockIdx.y == 0) {
+            out[blockIdx.x] = r;
+            if (host_out) host_out[blockIdx.x] = r;
+        }
         picked = r;
     }
-    if (e.out) {
+    if (e.out) {   // workgroup (0, b) decodes block b of the picked row
         __syncthreads();
+        const int i = threadIdx.x, b = blockIdx.y;
         const uint8_t *row = e.table + static_cast<int64_t>(picked) * e.row_bytes;
-        for (int b = 0; b < e.nb; ++b)
-            e.out[b * 256 + threadIdx.x] = e.type == QK_TYPE_Q4_K
-                                               ? q4k_value(row + b * 144, threadIdx.x)
-                                               : q6k_value(q6_fields(row, e.nb, b, e.type == QK_TYPE_Q6_K_SPLIT),
-                                                           threadIdx.x);
+        e.out[b * 256 + i] = e.type == QK_TYPE_Q4_K
+                                 ? q4k_value(row + b * 144, i)
+                                 : q6k_value(q6_fields(row, e.nb, b, e.type == QK_TYPE_Q6_K_SPLIT), i);
     }
 }
 
@@ -965,7 +966,10 @@ bool attention_supported(int group, int head_dim) { return split_instance(group,
 
 int launch_argmax_final(const float *pv, const int *pi, int parts, int32_t *out, hipStream_t stream,
                         int32_t *host_out, const NextEmbedding *next) {
-    hipLaunchKernelGGL(argmax_final_kernel, dim3(1), dim3(256), 0, stream, pv, pi, parts, out, host_out,
+    // With a next embedding, one workgroup per 256-value block of the row,
+    // each repeating the (small) final pick over the partials.
+    const int blocks = next && next->out ? next->nb : 1;
+    hipLaunchKernelGGL(argmax_final_kernel, dim3(1, blocks), dim3(256), 0, stream, pv, pi, parts, out, host_out,
                        next ? *next : NextEmbedding{});
     return launch_status("argmax final launch");
 }
