@@ -54,8 +54,8 @@ def test_fused_int8_launch_matches_single_launches(qk, torch_gpu, workloads, ora
         assert t.equal(outs[j].view(t.int32), refs[j].view(t.int32)), specs[j]
 
 
-def _weights(wl, synth, cfg, seed):
-    W = wl.llama_weights(cfg, seed)
+def _weights(wl, synth, cfg, seed, embd_type=None):
+    W = wl.llama_weights(cfg, seed) if embd_type is None else wl.llama_weights(cfg, seed, embd_type=embd_type)
     dim = cfg["dim"]
     for l, L in enumerate(W["layers"]):
         L["attn_norm"] = 1.0 + 0.2 * synth.normal_f32(dim, seed, 500 + 2 * l)
@@ -101,8 +101,9 @@ def test_staged_quantization_matches_separate_launches(qk, torch_gpu, workloads,
         assert np.array_equal(la, lb)
 
 
-def run_int8_decode(qk, oracle, wl, synth, cfg, seed, n_prefill, prompt, n_greedy, q4k, q6k, unit_gains=False):
-    W = wl.llama_weights(cfg, seed) if unit_gains else _weights(wl, synth, cfg, seed)
+def run_int8_decode(qk, oracle, wl, synth, cfg, seed, n_prefill, prompt, n_greedy, q4k, q6k, unit_gains=False,
+                    embd_type=None):
+    W = wl.llama_weights(cfg, seed) if unit_gains else _weights(wl, synth, cfg, seed, embd_type)
     kc, vc = wl.llama_kv_prefill(cfg, seed, n_prefill)
     om = oracle.Llama(cfg, W)
     om.set_int8(q4k, q6k)
@@ -145,6 +146,20 @@ def _check(rows, median_bound, max_bound):
 def test_small_llama_int8_decode(qk, torch_gpu, oracle, workloads, synth, q4k, q6k):
     prompt = np.array([3, 999, 17, 500], dtype=np.int32)
     rows = run_int8_decode(qk, oracle, workloads, synth, SMALL, 11, 10, prompt, 12, q4k, q6k)
+    _check(rows, 1e-5, 5e-2)
+
+
+@pytest.mark.parametrize("q4k,q6k", [(True, True), (False, False)])
+def test_small_llama_q4k_token_table(qk, torch_gpu, oracle, workloads, synth, q4k, q6k):
+    """A Q4_K token_embd, so the tied LM head is Q4_K too: the prompt's
+    embedding launches and, on every greedy step whose token the oracle
+    also picked (teacher forcing feeds the oracle's token), the embedding
+    row the final pick wrote for that token, decoded from Q4_K blocks.  INT8
+    modes and the FP32 record step (whose first-layer records come from the
+    embedding-records launch)."""
+    prompt = np.array([3, 999, 17, 500], dtype=np.int32)
+    rows = run_int8_decode(qk, oracle, workloads, synth, SMALL, 13, 10, prompt, 12, q4k, q6k,
+                           embd_type=workloads.Q4_K)
     _check(rows, 1e-5, 5e-2)
 
 
