@@ -461,7 +461,10 @@ int qk_llama_kv_cache(qk_llama *m, float **key_cache, float **value_cache);
 int qk_llama_logits(qk_llama *m, const float **logits);
 /* Device pointer to the fp32 residual stream x (dim values) after the last
    step: the state --compare-prefill downloads from FastGPU::x
-   (inferencer.cu:1744). */
+   (inferencer.cu:1744).  Ask again after each step: a greedy INT8 step fed
+   the previous step's token swaps in the embedding row that step's final
+   pick wrote into a second buffer, so x moves between two buffers, and the
+   other one is overwritten by the next pick. */
 int qk_llama_residual(qk_llama *m, const float **x);
 /* Quantized matrix products the handle has issued since create: seven per
    layer and step (q, k, v, o, gate, up, down) plus one per LM head, the
